@@ -1,0 +1,133 @@
+/*
+ * rwkv7m_wkv.h -- C ABI of the MI355X (gfx950) WKV-7 recurrence library
+ * (librwkv7m_wkv.so).
+ *
+ * The entry points replace the three callables of the reference's FFI
+ * plugin contract, WKVFFIBackend (src/rwkv7m/kernels/wkv_ffi.py:21-34),
+ * as called by the dispatcher at src/rwkv7m/model/wkv.py:172-175 and
+ * :215-216:
+ *
+ *   forward(r, w, k, v, neg_kk, kka, S0)            -> (y, S_T)
+ *   forward_with_aux(r, w, k, v, neg_kk, kka, S0)   -> ((y, S_T), aux)
+ *   backward(r, ..., S0, dy, dS_T, *aux)            -> (dr, dw, dk, dv,
+ *                                                       dneg_kk, dkka, dS0)
+ *
+ * Conventions (the reference's layout contract, wkv.py:19-57):
+ *   - vectors r, w, k, v, neg_kk, kka, y, dy and the six vector gradients are
+ *     time-major [T][B][H][N], contiguous, all of one dtype (bf16 or fp32);
+ *   - states S0, S_T, dS_T, dS0 are [B][H][N][N] fp32, row i = value index,
+ *     column j = key index;
+ *   - w is log(-log(decay)): the recurrence applies exp(-exp(w))
+ *     (rwkv_core.py:74);
+ *   - all arithmetic on the state is fp32; y and the vector gradients are
+ *     rounded to the vector dtype (round to nearest even) once, at the store.
+ *   - aux is one fp32 buffer of checkpoints [ceil(T/ci)+1][B][H][N][N]:
+ *     entry 0 = S0, entry c = the state after token c*ci - 1, the last entry
+ *     = S_T (the format of wkv_pallas_gpu.py:83-120, :319-343).
+ *
+ * Every pointer is a device pointer; every call only enqueues work on
+ * `stream` (a hipStream_t, NULL = the null stream) and never synchronises.
+ * Calls are stateless and reentrant.  On failure a call returns a nonzero
+ * rwkv7m_status and rwkv7m_last_error() describes it (thread-local).
+ * Supported head sizes N: 1, 2, 4, 8, 16, 32, 64, 128.  The MFMA chunked
+ * kernels serve bf16 with N == 64; every other case runs the sequential
+ * kernels, with identical results to the tolerance of the contract.
+ */
+#ifndef RWKV7M_WKV_H
+#define RWKV7M_WKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum rwkv7m_dtype {
+    RWKV7M_DTYPE_F32 = 0,
+    RWKV7M_DTYPE_BF16 = 1
+} rwkv7m_dtype;
+
+typedef enum rwkv7m_status {
+    RWKV7M_OK = 0,
+    RWKV7M_ERR_INVALID_ARGUMENT = 1, /* bad shape, dtype, pointer or size */
+    RWKV7M_ERR_UNSUPPORTED = 2,      /* valid request this build cannot run */
+    RWKV7M_ERR_HIP = 3               /* a HIP runtime call or launch failed */
+} rwkv7m_status;
+
+/* Version of this ABI; bumped on any incompatible change. */
+int rwkv7m_abi_version(void);
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char *rwkv7m_last_error(void);
+
+/* Number of aux checkpoints for T tokens at interval ci: ceil(T/ci) + 1. */
+int64_t rwkv7m_wkv7_checkpoint_count(int64_t T, int64_t checkpoint_interval);
+
+/* Checkpoint interval the library uses when the caller passes 0. */
+int64_t rwkv7m_wkv7_default_checkpoint_interval(int dtype, int64_t N);
+
+/*
+ * forward: y = WKV(r, w, k, v, neg_kk, kka; S0) and S_T.
+ * Replaces WKVFFIBackend.forward (wkv_ffi.py:32; called at wkv.py:175) and
+ * the reference's inference kernel (wkv_pallas_gpu.py:123-164, :378-430).
+ * final_state may alias initial_state (in-place carry of the state).
+ */
+int rwkv7m_wkv7_forward(int dtype, int64_t T, int64_t B, int64_t H, int64_t N,
+                        const void *r, const void *w, const void *k,
+                        const void *v, const void *neg_kk, const void *kka,
+                        const float *initial_state, void *y,
+                        float *final_state, void *stream);
+
+/*
+ * forward_with_aux: as forward, and also writes the checkpoints the backward
+ * needs.  Replaces WKVFFIBackend.forward_with_aux (wkv_ffi.py:33; called at
+ * wkv.py:174) and the reference's fwd+aux kernel (wkv_pallas_gpu.py:66-120,
+ * :303-375).  checkpoint_interval = 0 selects the library default; the
+ * chunked bf16 path needs a multiple of 16.
+ * checkpoints: [rwkv7m_wkv7_checkpoint_count(T, ci)][B][H][N][N] fp32.
+ */
+int rwkv7m_wkv7_forward_with_aux(int dtype, int64_t T, int64_t B, int64_t H,
+                                 int64_t N, const void *r, const void *w,
+                                 const void *k, const void *v,
+                                 const void *neg_kk, const void *kka,
+                                 const float *initial_state, void *y,
+                                 float *final_state, float *checkpoints,
+                                 int64_t checkpoint_interval, void *stream);
+
+/*
+ * backward: the seven input cotangents from (dy, dS_T) and the aux of
+ * forward_with_aux (which must have used the same checkpoint_interval).
+ * Replaces WKVFFIBackend.backward (wkv_ffi.py:34; called at wkv.py:216) and
+ * the reference's backward kernel (wkv_pallas_gpu.py:167-282, :433-530).
+ * Vector gradients are written in the vector dtype, dS0 in fp32.
+ * dy may be NULL (treated as zeros) and so may ds_t.
+ */
+int rwkv7m_wkv7_backward(int dtype, int64_t T, int64_t B, int64_t H,
+                         int64_t N, const void *r, const void *w,
+                         const void *k, const void *v, const void *neg_kk,
+                         const void *kka, const float *initial_state,
+                         const void *dy, const float *ds_t,
+                         const float *checkpoints,
+                         int64_t checkpoint_interval, void *dr, void *dw,
+                         void *dk, void *dv, void *dneg_kk, void *dkka,
+                         float *ds0, void *stream);
+
+/*
+ * decode_inplace: one token (T = 1) for B*H states, with the fp32 state
+ * read and overwritten in place in HBM.  The T == 1 case of forward
+ * (the eager decode loop at src/rwkv7m/infer/generate.py:74-99 reaches
+ * wkv.py:175 with T = 1), with the state buffer donated.
+ * Vectors are [B][H][N] (the [1][B][H][N] slice), state [B][H][N][N].
+ */
+int rwkv7m_wkv7_decode_inplace(int dtype, int64_t B, int64_t H, int64_t N,
+                               const void *r, const void *w, const void *k,
+                               const void *v, const void *neg_kk,
+                               const void *kka, float *state, void *y,
+                               void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RWKV7M_WKV_H */

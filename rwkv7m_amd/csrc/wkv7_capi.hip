@@ -1,0 +1,280 @@
+// C ABI of librwkv7m_wkv.so (declared in include/rwkv7m_wkv.h).
+//
+// Validates every request before any launch (errors, never undefined
+// behaviour: the reference's dispatcher validates at
+// src/rwkv7m/model/wkv.py:19-57 and the native layer re-checks), then routes
+// it to the chunked MFMA kernels or the sequential kernels.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <string>
+
+#include "../../include/rwkv7m_wkv.h"
+#include "wkv7_launch.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+bool supported_n(int64_t n) {
+    return n == 1 || n == 2 || n == 4 || n == 8 || n == 16 || n == 32 ||
+           n == 64 || n == 128;
+}
+
+// Copy or clear n floats on the stream with a plain kernel (no memset nodes,
+// so a caller may capture these calls in a HIP graph).
+__global__ void fill_kernel(float* dst, const float* src, int64_t n) {
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += int64_t(gridDim.x) * blockDim.x)
+        dst[i] = src ? src[i] : 0.f;
+}
+
+int copy_or_clear(float* dst, const float* src, int64_t n,
+                  hipStream_t stream) {
+    if (n == 0 || dst == src) return RWKV7M_OK;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(fill_kernel, dim3(unsigned(blocks)), dim3(256), 0,
+                       stream, dst, src, n);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return fail(RWKV7M_ERR_HIP,
+                    std::string("fill kernel launch failed: ") +
+                        hipGetErrorString(e));
+    return RWKV7M_OK;
+}
+
+struct Dims {
+    int64_t T, B, H, N, vec_elems, state_elems;
+};
+
+int check_dims(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
+               int64_t N, Dims* out) {
+    const std::string f(fn);
+    if (dtype != RWKV7M_DTYPE_F32 && dtype != RWKV7M_DTYPE_BF16)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    f + ": WKV vectors must be bfloat16 or float32 (dtype=" +
+                        std::to_string(dtype) + ")");
+    if (T < 0 || B < 0 || H < 0 || N < 0)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    f + ": negative dimension");
+    if (!supported_n(N))
+        return fail(RWKV7M_ERR_UNSUPPORTED,
+                    f + ": head size N=" + std::to_string(N) +
+                        " is not supported (1, 2, 4, ..., 128)");
+    const int64_t lim = int64_t(1) << 40;
+    if (B > lim || H > lim || T > lim || B * H > 0x7fffffff ||
+        (B * H > 0 && T > (int64_t(1) << 46) / (B * H * N)))
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT, f + ": sizes too large");
+    out->T = T;
+    out->B = B;
+    out->H = H;
+    out->N = N;
+    out->vec_elems = T * B * H * N;
+    out->state_elems = B * H * N * N;
+    return RWKV7M_OK;
+}
+
+int need(const void* p, bool nonempty, const char* fn, const char* name) {
+    if (nonempty && p == nullptr)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": " + name + " is NULL");
+    return RWKV7M_OK;
+}
+
+#define RWKV7M_TRY(expr)              \
+    do {                              \
+        int rc_ = (expr);             \
+        if (rc_ != RWKV7M_OK) return rc_; \
+    } while (0)
+
+int hip_status(const char* what, hipError_t e) {
+    if (e == hipSuccess) return RWKV7M_OK;
+    return fail(RWKV7M_ERR_HIP, std::string(what) + ": " +
+                                    hipGetErrorString(e));
+}
+
+int64_t default_interval(int dtype, int64_t N) {
+    (void)dtype;
+    (void)N;
+    return 16;
+}
+
+int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
+                 int64_t N, const void* r, const void* w, const void* k,
+                 const void* v, const void* a, const void* b,
+                 const float* s0, void* y, float* s_t, float* ckpt,
+                 int64_t ci, hipStream_t stream) {
+    Dims d;
+    RWKV7M_TRY(check_dims(fn, dtype, T, B, H, N, &d));
+    const bool vecs = d.vec_elems > 0, st = d.state_elems > 0;
+    RWKV7M_TRY(need(r, vecs, fn, "r"));
+    RWKV7M_TRY(need(w, vecs, fn, "w"));
+    RWKV7M_TRY(need(k, vecs, fn, "k"));
+    RWKV7M_TRY(need(v, vecs, fn, "v"));
+    RWKV7M_TRY(need(a, vecs, fn, "neg_kk"));
+    RWKV7M_TRY(need(b, vecs, fn, "kka"));
+    RWKV7M_TRY(need(y, vecs, fn, "y"));
+    RWKV7M_TRY(need(s0, st, fn, "initial_state"));
+    RWKV7M_TRY(need(s_t, st, fn, "final_state"));
+    if (d.state_elems == 0) return RWKV7M_OK;
+    if (T == 0) {
+        RWKV7M_TRY(copy_or_clear(s_t, s0, d.state_elems, stream));
+        if (ckpt) RWKV7M_TRY(copy_or_clear(ckpt, s0, d.state_elems, stream));
+        return RWKV7M_OK;
+    }
+    rwkv7m::SeqFwdArgs p{};
+    p.bf16 = dtype == RWKV7M_DTYPE_BF16;
+    p.T = T;
+    p.B = B;
+    p.H = H;
+    p.N = N;
+    p.r = r;
+    p.w = w;
+    p.k = k;
+    p.v = v;
+    p.a = a;
+    p.b = b;
+    p.s0 = s0;
+    p.y = y;
+    p.s_t = s_t;
+    p.ckpt = ckpt;
+    p.ci = ci;
+    p.only_flagged = nullptr;
+    return hip_status("sequential forward launch",
+                      rwkv7m::launch_seq_forward(p, stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int rwkv7m_abi_version(void) { return 1; }
+
+const char* rwkv7m_last_error(void) { return g_last_error.c_str(); }
+
+int64_t rwkv7m_wkv7_checkpoint_count(int64_t T, int64_t checkpoint_interval) {
+    if (T < 0 || checkpoint_interval <= 0) return -1;
+    return (T + checkpoint_interval - 1) / checkpoint_interval + 1;
+}
+
+int64_t rwkv7m_wkv7_default_checkpoint_interval(int dtype, int64_t N) {
+    return default_interval(dtype, N);
+}
+
+int rwkv7m_wkv7_forward(int dtype, int64_t T, int64_t B, int64_t H, int64_t N,
+                        const void* r, const void* w, const void* k,
+                        const void* v, const void* neg_kk, const void* kka,
+                        const float* initial_state, void* y,
+                        float* final_state, void* stream) {
+    g_last_error.clear();
+    return forward_impl("rwkv7m_wkv7_forward", dtype, T, B, H, N, r, w, k, v,
+                        neg_kk, kka, initial_state, y, final_state, nullptr,
+                        0, static_cast<hipStream_t>(stream));
+}
+
+int rwkv7m_wkv7_forward_with_aux(int dtype, int64_t T, int64_t B, int64_t H,
+                                 int64_t N, const void* r, const void* w,
+                                 const void* k, const void* v,
+                                 const void* neg_kk, const void* kka,
+                                 const float* initial_state, void* y,
+                                 float* final_state, float* checkpoints,
+                                 int64_t checkpoint_interval, void* stream) {
+    g_last_error.clear();
+    const char* fn = "rwkv7m_wkv7_forward_with_aux";
+    if (checkpoint_interval < 0)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": checkpoint_interval must be >= 0");
+    const int64_t ci = checkpoint_interval == 0
+                           ? default_interval(dtype, N)
+                           : checkpoint_interval;
+    RWKV7M_TRY(need(checkpoints, B * H * N > 0, fn, "checkpoints"));
+    return forward_impl(fn, dtype, T, B, H, N, r, w, k, v, neg_kk, kka,
+                        initial_state, y, final_state, checkpoints, ci,
+                        static_cast<hipStream_t>(stream));
+}
+
+int rwkv7m_wkv7_backward(int dtype, int64_t T, int64_t B, int64_t H,
+                         int64_t N, const void* r, const void* w,
+                         const void* k, const void* v, const void* neg_kk,
+                         const void* kka, const float* initial_state,
+                         const void* dy, const float* ds_t,
+                         const float* checkpoints,
+                         int64_t checkpoint_interval, void* dr, void* dw,
+                         void* dk, void* dv, void* dneg_kk, void* dkka,
+                         float* ds0, void* stream) {
+    g_last_error.clear();
+    const char* fn = "rwkv7m_wkv7_backward";
+    (void)initial_state;  // checkpoints[0] holds it
+    Dims d;
+    RWKV7M_TRY(check_dims(fn, dtype, T, B, H, N, &d));
+    if (checkpoint_interval < 0)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": checkpoint_interval must be >= 0");
+    const int64_t ci = checkpoint_interval == 0
+                           ? default_interval(dtype, N)
+                           : checkpoint_interval;
+    const bool vecs = d.vec_elems > 0, st = d.state_elems > 0;
+    RWKV7M_TRY(need(r, vecs, fn, "r"));
+    RWKV7M_TRY(need(w, vecs, fn, "w"));
+    RWKV7M_TRY(need(k, vecs, fn, "k"));
+    RWKV7M_TRY(need(v, vecs, fn, "v"));
+    RWKV7M_TRY(need(neg_kk, vecs, fn, "neg_kk"));
+    RWKV7M_TRY(need(kka, vecs, fn, "kka"));
+    RWKV7M_TRY(need(dr, vecs, fn, "dr"));
+    RWKV7M_TRY(need(dw, vecs, fn, "dw"));
+    RWKV7M_TRY(need(dk, vecs, fn, "dk"));
+    RWKV7M_TRY(need(dv, vecs, fn, "dv"));
+    RWKV7M_TRY(need(dneg_kk, vecs, fn, "dneg_kk"));
+    RWKV7M_TRY(need(dkka, vecs, fn, "dkka"));
+    RWKV7M_TRY(need(ds0, st, fn, "ds0"));
+    RWKV7M_TRY(need(checkpoints, vecs, fn, "checkpoints"));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (d.state_elems == 0) return RWKV7M_OK;
+    if (T == 0) return copy_or_clear(ds0, ds_t, d.state_elems, s);
+    rwkv7m::SeqBwdArgs p{};
+    p.bf16 = dtype == RWKV7M_DTYPE_BF16;
+    p.T = T;
+    p.B = B;
+    p.H = H;
+    p.N = N;
+    p.r = r;
+    p.w = w;
+    p.k = k;
+    p.v = v;
+    p.a = neg_kk;
+    p.b = kka;
+    p.dy = dy;
+    p.ds_t = ds_t;
+    p.ckpt = checkpoints;
+    p.ci = ci;
+    p.dr = dr;
+    p.dw = dw;
+    p.dk = dk;
+    p.dv = dv;
+    p.da = dneg_kk;
+    p.db = dkka;
+    p.ds0 = ds0;
+    p.only_flagged = nullptr;
+    return hip_status("sequential backward launch",
+                      rwkv7m::launch_seq_backward(p, s));
+}
+
+int rwkv7m_wkv7_decode_inplace(int dtype, int64_t B, int64_t H, int64_t N,
+                               const void* r, const void* w, const void* k,
+                               const void* v, const void* neg_kk,
+                               const void* kka, float* state, void* y,
+                               void* stream) {
+    g_last_error.clear();
+    return forward_impl("rwkv7m_wkv7_decode_inplace", dtype, 1, B, H, N, r,
+                        w, k, v, neg_kk, kka, state, y, state, nullptr, 0,
+                        static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,37 @@
+// Internal launcher interface between the C ABI (wkv7_capi.hip) and the
+// kernel translation units.  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rwkv7m {
+
+struct SeqFwdArgs {
+    bool bf16;
+    int64_t T, B, H, N;
+    const void *r, *w, *k, *v, *a, *b;
+    const float* s0;
+    void* y;
+    float* s_t;
+    float* ckpt;          // nullptr: no checkpoints
+    int64_t ci;           // checkpoint interval (when ckpt != nullptr)
+    const int* only_flagged;  // nullptr: all (b,h); else run flagged only
+};
+
+struct SeqBwdArgs {
+    bool bf16;
+    int64_t T, B, H, N;
+    const void *r, *w, *k, *v, *a, *b, *dy;
+    const float* ds_t;
+    const float* ckpt;
+    int64_t ci;
+    void *dr, *dw, *dk, *dv, *da, *db;
+    float* ds0;
+    const int* only_flagged;
+};
+
+hipError_t launch_seq_forward(const SeqFwdArgs& p, hipStream_t stream);
+hipError_t launch_seq_backward(const SeqBwdArgs& p, hipStream_t stream);
+
+}  // namespace rwkv7m

@@ -1,0 +1,354 @@
+// Sequential WKV-7 kernels for gfx950: one workgroup per (batch, head).
+//
+// Each state row i is owned by G consecutive lanes, each holding C = N / G
+// contiguous columns in VGPRs, so the row-local parts of the recurrence
+// (sa = S a, y = S r, the rank-2 update) need only a G-lane butterfly.
+// Token vectors are staged through LDS in blocks.  These kernels carry the
+// fp32 path, every head size, and the exact fallback of the chunked path.
+//
+// Math (reference src/rwkv7m/model/rwkv_core.py:54-86):
+//   d = exp(-exp(w));  sa = S a;  S = S diag(d) + sa b^T + v k^T;  y = S r
+// Reverse equations (reference src/rwkv7m/kernels/wkv_pallas_gpu.py:221-257),
+// with S_{t-1} recomputed forward from checkpoints instead of divided out.
+
+#include "wkv7_common.h"
+#include "wkv7_launch.h"
+
+namespace rwkv7m {
+namespace {
+
+template <int N>
+struct SeqShape {
+    static constexpr int G = (N >= 128) ? 8 : (N >= 16 ? 16 : N);
+    static constexpr int C = N / G;
+    static constexpr int THREADS = N * G;
+    static constexpr int WAVE_LANES = THREADS < 64 ? THREADS : 64;
+    static constexpr int NWAVES = (THREADS + 63) / 64;
+    static constexpr int SUB = (N >= 128) ? 4 : (N >= 64 ? 8 : 16);
+    static constexpr int TB = 16;
+};
+
+// Forward.  ckpt == nullptr: no aux.  s_t may alias s0.
+template <int N, typename VT>
+__global__ void __launch_bounds__(SeqShape<N>::THREADS)
+wkv7_seq_fwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
+                    const VT* __restrict__ w, const VT* __restrict__ k,
+                    const VT* __restrict__ v, const VT* __restrict__ a,
+                    const VT* __restrict__ b, const float* s0, VT* y,
+                    float* s_t, float* ckpt, int64_t ci,
+                    const int* __restrict__ only_flagged) {
+    using Sh = SeqShape<N>;
+    constexpr int G = Sh::G, C = Sh::C, TB = Sh::TB, TH = Sh::THREADS;
+    constexpr int64_t NN = int64_t(N) * N;
+    __shared__ float sh[6][TB][N];  // r, decay, k, v, a, b
+    __shared__ float sh_y[TB][N];
+
+    const int64_t bh = blockIdx.x;
+    if (only_flagged && only_flagged[bh] == 0) return;
+    const int tid = threadIdx.x;
+    const int row = tid / G, col0 = (tid % G) * C;
+    const int64_t my = bh * NN + int64_t(row) * N + col0;
+
+    float S[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) S[c] = s0[my + c];
+    if (ckpt) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) ckpt[my + c] = S[c];
+    }
+    const VT* srcs[6] = {r, w, k, v, a, b};
+
+    for (int64_t t0 = 0; t0 < T; t0 += TB) {
+        const int nt = int(T - t0 < TB ? T - t0 : TB);
+        for (int e = tid; e < 6 * TB * N; e += TH) {
+            const int vec = e / (TB * N), rem = e - vec * TB * N;
+            const int u = rem / N, j = rem - u * N;
+            if (u < nt) {
+                float x = load_f(srcs[vec] + ((t0 + u) * BH + bh) * N + j);
+                if (vec == 1) x = expf(-expf(x));
+                sh[vec][u][j] = x;
+            }
+        }
+        __syncthreads();
+        for (int u = 0; u < nt; ++u) {
+            float sa = 0.f;
+#pragma unroll
+            for (int c = 0; c < C; ++c) sa += S[c] * sh[4][u][col0 + c];
+            sa = group_sum<G>(sa);
+            const float vi = sh[3][u][row];
+            float acc = 0.f;
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                S[c] = S[c] * sh[1][u][col0 + c] + sa * sh[5][u][col0 + c] +
+                       vi * sh[2][u][col0 + c];
+                acc += S[c] * sh[0][u][col0 + c];
+            }
+            acc = group_sum<G>(acc);
+            if (col0 == 0) sh_y[u][row] = acc;
+            if (ckpt) {
+                const int64_t t = t0 + u;
+                if ((t + 1) % ci == 0 || t + 1 == T) {
+                    float* dst = ckpt + ((t + ci) / ci) * BH * NN + my;
+#pragma unroll
+                    for (int c = 0; c < C; ++c) dst[c] = S[c];
+                }
+            }
+        }
+        __syncthreads();
+        for (int e = tid; e < nt * N; e += TH) {
+            const int u = e / N, i = e - u * N;
+            store_f(y + ((t0 + u) * BH + bh) * N + i, sh_y[u][i]);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) s_t[my + c] = S[c];
+}
+
+// Stage `count` tokens starting at t0 into sh[8][SUB][N]:
+// 0 r, 1 decay, 2 k, 3 v, 4 a, 5 b, 6 dy, 7 exp(w).
+template <int N, typename VT>
+__device__ __forceinline__ void stage_bwd(
+    float (*sh)[SeqShape<N>::SUB][N], int64_t t0, int count, int64_t BH,
+    int64_t bh, const VT* r, const VT* w, const VT* k, const VT* v,
+    const VT* a, const VT* b, const VT* dy) {
+    using Sh = SeqShape<N>;
+    constexpr int SUB = Sh::SUB, TH = Sh::THREADS;
+    const VT* srcs[7] = {r, w, k, v, a, b, dy};
+    for (int e = threadIdx.x; e < 7 * SUB * N; e += TH) {
+        const int vec = e / (SUB * N), rem = e - vec * SUB * N;
+        const int u = rem / N, j = rem - u * N;
+        if (u < count) {
+            const int64_t off = ((t0 + u) * BH + bh) * N + j;
+            if (vec == 1) {
+                const float ew = expf(load_f(w + off));
+                sh[1][u][j] = expf(-ew);
+                sh[7][u][j] = ew;
+            } else if (vec == 6) {
+                sh[6][u][j] = dy ? load_f(dy + off) : 0.f;
+            } else {
+                sh[vec][u][j] = load_f(srcs[vec] + off);
+            }
+        }
+    }
+}
+
+template <int N, typename VT>
+__global__ void __launch_bounds__(SeqShape<N>::THREADS)
+wkv7_seq_bwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
+                    const VT* __restrict__ w, const VT* __restrict__ k,
+                    const VT* __restrict__ v, const VT* __restrict__ a,
+                    const VT* __restrict__ b, const VT* __restrict__ dy,
+                    const float* __restrict__ ds_t,
+                    const float* __restrict__ ckpt, int64_t ci, VT* dr,
+                    VT* dw, VT* dk, VT* dv, VT* da, VT* db, float* ds0,
+                    const int* __restrict__ only_flagged) {
+    using Sh = SeqShape<N>;
+    constexpr int G = Sh::G, C = Sh::C, SUB = Sh::SUB, TH = Sh::THREADS;
+    constexpr int WL = Sh::WAVE_LANES, NW = Sh::NWAVES;
+    constexpr int64_t NN = int64_t(N) * N;
+    __shared__ float sh[8][SUB][N];
+    __shared__ float red[2][NW][5][N];
+    __shared__ float sh_dv[SUB][N];
+
+    const int64_t bh = blockIdx.x;
+    if (only_flagged && only_flagged[bh] == 0) return;
+    const int tid = threadIdx.x;
+    const int row = tid / G, col0 = (tid % G) * C;
+    const int wave = tid / 64, lane = tid % 64;
+    const int64_t my = bh * NN + int64_t(row) * N + col0;
+    VT* gout[5] = {dr, dw, db, dk, da};
+
+    float dS[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) dS[c] = ds_t ? ds_t[my + c] : 0.f;
+
+    const int64_t nint = (T + ci - 1) / ci;
+    int buf = 0;
+    for (int64_t c = nint - 1; c >= 0; --c) {
+        const int64_t ta = c * ci;
+        const int64_t tb = (ta + ci < T) ? ta + ci : T;
+        const int64_t nsub = (tb - ta + SUB - 1) / SUB;
+        for (int64_t s = nsub - 1; s >= 0; --s) {
+            float St[SUB + 1][C];
+            float sa_r[SUB];
+#pragma unroll
+            for (int cc = 0; cc < C; ++cc)
+                St[0][cc] = ckpt[c * BH * NN + my + cc];
+            const int64_t ts = ta + s * SUB;
+            // advance from the interval checkpoint to the sub-interval start
+            for (int64_t t0 = ta; t0 < ts; t0 += SUB) {
+                stage_bwd<N, VT>(sh, t0, SUB, BH, bh, r, w, k, v, a, b,
+                                 nullptr);
+                __syncthreads();
+                for (int u = 0; u < SUB; ++u) {
+                    float sa = 0.f;
+#pragma unroll
+                    for (int cc = 0; cc < C; ++cc)
+                        sa += St[0][cc] * sh[4][u][col0 + cc];
+                    sa = group_sum<G>(sa);
+                    const float vi = sh[3][u][row];
+#pragma unroll
+                    for (int cc = 0; cc < C; ++cc)
+                        St[0][cc] = St[0][cc] * sh[1][u][col0 + cc] +
+                                    sa * sh[5][u][col0 + cc] +
+                                    vi * sh[2][u][col0 + cc];
+                }
+                __syncthreads();
+            }
+            const int nt = int(tb - ts < SUB ? tb - ts : SUB);
+            stage_bwd<N, VT>(sh, ts, nt, BH, bh, r, w, k, v, a, b, dy);
+            __syncthreads();
+            // recompute the sub-interval's states: St[u] = S before token u
+#pragma unroll
+            for (int u = 0; u < SUB; ++u) {
+                if (u < nt) {
+                    float sa = 0.f;
+#pragma unroll
+                    for (int cc = 0; cc < C; ++cc)
+                        sa += St[u][cc] * sh[4][u][col0 + cc];
+                    sa = group_sum<G>(sa);
+                    sa_r[u] = sa;
+                    const float vi = sh[3][u][row];
+#pragma unroll
+                    for (int cc = 0; cc < C; ++cc)
+                        St[u + 1][cc] = St[u][cc] * sh[1][u][col0 + cc] +
+                                        sa * sh[5][u][col0 + cc] +
+                                        vi * sh[2][u][col0 + cc];
+                }
+            }
+            // reverse over the sub-interval
+#pragma unroll
+            for (int u = SUB - 1; u >= 0; --u) {
+                if (u < nt) {
+                    const float dyi = sh[6][u][row], vi = sh[3][u][row];
+                    const float sa = sa_r[u];
+                    float Gc[C];
+                    float dsa = 0.f, dvv = 0.f;
+#pragma unroll
+                    for (int cc = 0; cc < C; ++cc) {
+                        Gc[cc] = dS[cc] + dyi * sh[0][u][col0 + cc];
+                        dsa += Gc[cc] * sh[5][u][col0 + cc];
+                        dvv += Gc[cc] * sh[2][u][col0 + cc];
+                    }
+                    dsa = group_sum<G>(dsa);
+                    dvv = group_sum<G>(dvv);
+                    if (col0 == 0) sh_dv[u][row] = dvv;
+#pragma unroll
+                    for (int cc = 0; cc < C; ++cc) {
+                        float p[5];
+                        p[0] = St[u + 1][cc] * dyi;   // dr
+                        p[1] = Gc[cc] * St[u][cc];    // d decay
+                        p[2] = Gc[cc] * sa;           // dkka
+                        p[3] = Gc[cc] * vi;           // dk
+                        p[4] = St[u][cc] * dsa;       // dneg_kk
+#pragma unroll
+                        for (int q = 0; q < 5; ++q) {
+                            p[q] = cross_group_sum<G, WL>(p[q]);
+                            if (lane < G) red[buf][wave][q][col0 + cc] = p[q];
+                        }
+                        dS[cc] = Gc[cc] * sh[1][u][col0 + cc] +
+                                 dsa * sh[4][u][col0 + cc];
+                    }
+                    __syncthreads();
+                    const int64_t t = ts + u;
+                    for (int e = tid; e < 5 * N; e += TH) {
+                        const int q = e / N, j = e - q * N;
+                        float acc = 0.f;
+#pragma unroll
+                        for (int ww = 0; ww < NW; ++ww) acc += red[buf][ww][q][j];
+                        if (q == 1) acc *= -sh[7][u][j] * sh[1][u][j];
+                        store_f(gout[q] + (t * BH + bh) * N + j, acc);
+                    }
+                    buf ^= 1;
+                }
+            }
+            __syncthreads();
+            for (int e = tid; e < nt * N; e += TH) {
+                const int u = e / N, i = e - u * N;
+                store_f(dv + ((ts + u) * BH + bh) * N + i, sh_dv[u][i]);
+            }
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) ds0[my + c] = dS[c];
+}
+
+template <int N, typename VT>
+hipError_t launch_fwd_n(const SeqFwdArgs& p, hipStream_t stream) {
+    const int64_t BH = p.B * p.H;
+    hipLaunchKernelGGL((wkv7_seq_fwd_kernel<N, VT>), dim3(unsigned(BH)),
+                       dim3(SeqShape<N>::THREADS), 0, stream, p.T, BH,
+                       static_cast<const VT*>(p.r),
+                       static_cast<const VT*>(p.w),
+                       static_cast<const VT*>(p.k),
+                       static_cast<const VT*>(p.v),
+                       static_cast<const VT*>(p.a),
+                       static_cast<const VT*>(p.b), p.s0,
+                       static_cast<VT*>(p.y), p.s_t, p.ckpt, p.ci,
+                       p.only_flagged);
+    return hipGetLastError();
+}
+
+template <int N, typename VT>
+hipError_t launch_bwd_n(const SeqBwdArgs& p, hipStream_t stream) {
+    const int64_t BH = p.B * p.H;
+    hipLaunchKernelGGL((wkv7_seq_bwd_kernel<N, VT>), dim3(unsigned(BH)),
+                       dim3(SeqShape<N>::THREADS), 0, stream, p.T, BH,
+                       static_cast<const VT*>(p.r),
+                       static_cast<const VT*>(p.w),
+                       static_cast<const VT*>(p.k),
+                       static_cast<const VT*>(p.v),
+                       static_cast<const VT*>(p.a),
+                       static_cast<const VT*>(p.b),
+                       static_cast<const VT*>(p.dy), p.ds_t, p.ckpt, p.ci,
+                       static_cast<VT*>(p.dr), static_cast<VT*>(p.dw),
+                       static_cast<VT*>(p.dk), static_cast<VT*>(p.dv),
+                       static_cast<VT*>(p.da), static_cast<VT*>(p.db),
+                       p.ds0, p.only_flagged);
+    return hipGetLastError();
+}
+
+template <typename VT>
+hipError_t dispatch_fwd(const SeqFwdArgs& p, hipStream_t s) {
+    switch (p.N) {
+        case 1: return launch_fwd_n<1, VT>(p, s);
+        case 2: return launch_fwd_n<2, VT>(p, s);
+        case 4: return launch_fwd_n<4, VT>(p, s);
+        case 8: return launch_fwd_n<8, VT>(p, s);
+        case 16: return launch_fwd_n<16, VT>(p, s);
+        case 32: return launch_fwd_n<32, VT>(p, s);
+        case 64: return launch_fwd_n<64, VT>(p, s);
+        case 128: return launch_fwd_n<128, VT>(p, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <typename VT>
+hipError_t dispatch_bwd(const SeqBwdArgs& p, hipStream_t s) {
+    switch (p.N) {
+        case 1: return launch_bwd_n<1, VT>(p, s);
+        case 2: return launch_bwd_n<2, VT>(p, s);
+        case 4: return launch_bwd_n<4, VT>(p, s);
+        case 8: return launch_bwd_n<8, VT>(p, s);
+        case 16: return launch_bwd_n<16, VT>(p, s);
+        case 32: return launch_bwd_n<32, VT>(p, s);
+        case 64: return launch_bwd_n<64, VT>(p, s);
+        case 128: return launch_bwd_n<128, VT>(p, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_seq_forward(const SeqFwdArgs& p, hipStream_t stream) {
+    return p.bf16 ? dispatch_fwd<bf16_t>(p, stream)
+                  : dispatch_fwd<float>(p, stream);
+}
+
+hipError_t launch_seq_backward(const SeqBwdArgs& p, hipStream_t stream) {
+    return p.bf16 ? dispatch_bwd<bf16_t>(p, stream)
+                  : dispatch_bwd<float>(p, stream);
+}
+
+}  // namespace rwkv7m

@@ -1,0 +1,253 @@
+"""HIP (gfx950) WKV-7 backend: ctypes binding of librwkv7m_wkv.so.
+
+This is the native implementation that plugs into the reference's FFI
+registry (src/rwkv7m/kernels/wkv_ffi.py:21-67). Its three callables have the
+reference's signatures and return conventions:
+
+* ``forward(r, w, k, v, neg_kk, kka, S0) -> (y, S_T)``
+* ``forward_with_aux(...) -> ((y, S_T), aux)`` with
+  ``aux = (checkpoints, interval)``: fp32 checkpoints
+  ``[ceil(T/ci)+1, B, H, N, N]`` (entry 0 = S0, entry c = state after token
+  ``c*ci - 1``, last = S_T; the format of wkv_pallas_gpu.py:83-120) and the
+  interval as a 0-d int64 CPU tensor.
+* ``backward(r, w, k, v, neg_kk, kka, S0, dy, dS_T, *aux)`` -> seven input
+  cotangents in primal order and primal dtypes.
+
+Tensors are torch device tensors (torch supplies device memory and the
+current HIP stream; the kernels and every check of shapes and dtypes live in
+the C library). There is no CPU fallback: a missing library, a CPU tensor or
+a failed launch raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+from .wkv_ffi import WKVFFIBackend, register_wkv_ffi_backend
+
+_PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_DIR, "librwkv7m_wkv.so")
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+# Every symbol declared in include/rwkv7m_wkv.h.
+EXPORTED_SYMBOLS = (
+    "rwkv7m_abi_version",
+    "rwkv7m_last_error",
+    "rwkv7m_wkv7_checkpoint_count",
+    "rwkv7m_wkv7_default_checkpoint_interval",
+    "rwkv7m_wkv7_forward",
+    "rwkv7m_wkv7_forward_with_aux",
+    "rwkv7m_wkv7_backward",
+    "rwkv7m_wkv7_decode_inplace",
+)
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load_library(path: str | None = None):
+    """Load librwkv7m_wkv.so and declare its signatures.
+
+    Raises ``RuntimeError`` if the library has not been built.
+    """
+    global _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = path or LIB_PATH
+        if not os.path.exists(p):
+            raise RuntimeError(
+                f"HIP WKV library not found at {p}; build it with "
+                "`python -m rwkv7m_amd._build` (or __graft_entry__.build())")
+        lib = ctypes.CDLL(p)
+        i64, i32, vp = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
+        lib.rwkv7m_abi_version.restype = i32
+        lib.rwkv7m_abi_version.argtypes = []
+        lib.rwkv7m_last_error.restype = ctypes.c_char_p
+        lib.rwkv7m_last_error.argtypes = []
+        lib.rwkv7m_wkv7_checkpoint_count.restype = i64
+        lib.rwkv7m_wkv7_checkpoint_count.argtypes = [i64, i64]
+        lib.rwkv7m_wkv7_default_checkpoint_interval.restype = i64
+        lib.rwkv7m_wkv7_default_checkpoint_interval.argtypes = [i32, i64]
+        lib.rwkv7m_wkv7_forward.restype = i32
+        lib.rwkv7m_wkv7_forward.argtypes = [i32] + [i64] * 4 + [vp] * 10
+        lib.rwkv7m_wkv7_forward_with_aux.restype = i32
+        lib.rwkv7m_wkv7_forward_with_aux.argtypes = (
+            [i32] + [i64] * 4 + [vp] * 10 + [i64, vp])
+        lib.rwkv7m_wkv7_backward.restype = i32
+        lib.rwkv7m_wkv7_backward.argtypes = (
+            [i32] + [i64] * 4 + [vp] * 10 + [i64] + [vp] * 8)
+        lib.rwkv7m_wkv7_decode_inplace.restype = i32
+        lib.rwkv7m_wkv7_decode_inplace.argtypes = [i32] + [i64] * 3 + [vp] * 9
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def _check(rc: int, fn: str) -> None:
+    if rc != 0:
+        msg = load_library().rwkv7m_last_error().decode()
+        raise RuntimeError(f"{fn} failed (status {rc}): {msg}")
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return DTYPE_F32
+    if t.dtype == torch.bfloat16:
+        return DTYPE_BF16
+    raise TypeError(f"WKV vectors must be bfloat16 or float32, got {t.dtype}")
+
+
+def _dev(tensors) -> torch.device:
+    dev = tensors[0].device
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "the HIP WKV backend needs GPU tensors; got a tensor on "
+                f"{t.device} (there is no CPU fallback)")
+        if t.device != dev:
+            raise RuntimeError("all WKV tensors must be on one device")
+    return dev
+
+
+def _p(t: torch.Tensor | None):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _vecs(r, w, k, v, neg_kk, kka):
+    out = tuple(x.contiguous() for x in (r, w, k, v, neg_kk, kka))
+    if out[0].dim() != 4:
+        raise ValueError(f"r must have shape [time, batch, heads, head_size],"
+                         f" got {tuple(out[0].shape)}")
+    return out
+
+
+def default_checkpoint_interval(dtype: torch.dtype, head_size: int) -> int:
+    code = DTYPE_BF16 if dtype == torch.bfloat16 else DTYPE_F32
+    return int(load_library().rwkv7m_wkv7_default_checkpoint_interval(
+        code, head_size))
+
+
+def checkpoint_count(T: int, interval: int) -> int:
+    return int(load_library().rwkv7m_wkv7_checkpoint_count(T, interval))
+
+
+def forward(r, w, k, v, neg_kk, kka, initial_state, *, out_state=None):
+    """y, S_T = WKV(...). ``out_state`` may be ``initial_state`` (in place)."""
+    lib = load_library()
+    r, w, k, v, a, b = _vecs(r, w, k, v, neg_kk, kka)
+    s0 = initial_state.contiguous()
+    dev = _dev((r, w, k, v, a, b, s0))
+    T, B, H, N = r.shape
+    y = torch.empty_like(r)
+    s_t = out_state if out_state is not None else torch.empty_like(s0)
+    with torch.cuda.device(dev):
+        rc = lib.rwkv7m_wkv7_forward(
+            _dtype_code(r), T, B, H, N, _p(r), _p(w), _p(k), _p(v), _p(a),
+            _p(b), _p(s0), _p(y), _p(s_t), _stream(dev))
+    _check(rc, "rwkv7m_wkv7_forward")
+    return y, s_t
+
+
+def forward_with_aux(r, w, k, v, neg_kk, kka, initial_state, *,
+                     checkpoint_interval: int = 0):
+    """((y, S_T), (checkpoints, interval)) for the backward pass."""
+    lib = load_library()
+    r, w, k, v, a, b = _vecs(r, w, k, v, neg_kk, kka)
+    s0 = initial_state.contiguous()
+    dev = _dev((r, w, k, v, a, b, s0))
+    T, B, H, N = r.shape
+    ci = int(checkpoint_interval) or default_checkpoint_interval(r.dtype, N)
+    nck = checkpoint_count(T, ci)
+    y = torch.empty_like(r)
+    s_t = torch.empty_like(s0)
+    ckpt = torch.empty((nck, B, H, N, N), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.rwkv7m_wkv7_forward_with_aux(
+            _dtype_code(r), T, B, H, N, _p(r), _p(w), _p(k), _p(v), _p(a),
+            _p(b), _p(s0), _p(y), _p(s_t), _p(ckpt), ci, _stream(dev))
+    _check(rc, "rwkv7m_wkv7_forward_with_aux")
+    return (y, s_t), (ckpt, torch.tensor(ci, dtype=torch.int64))
+
+
+def backward(r, w, k, v, neg_kk, kka, initial_state, dy, ds_t, checkpoints,
+             interval):
+    """Seven input cotangents (primal order, primal dtypes)."""
+    lib = load_library()
+    r, w, k, v, a, b = _vecs(r, w, k, v, neg_kk, kka)
+    s0 = initial_state.contiguous()
+    dev = _dev((r, w, k, v, a, b, s0, checkpoints))
+    T, B, H, N = r.shape
+    ci = int(interval)
+    if checkpoints.shape != (checkpoint_count(T, ci), B, H, N, N) or \
+            checkpoints.dtype != torch.float32:
+        raise ValueError("checkpoints do not match time, shape and interval")
+    ckpt = checkpoints.contiguous()
+    dy_c = None if dy is None else dy.to(r.dtype).contiguous()
+    ds_c = None if ds_t is None else ds_t.to(torch.float32).contiguous()
+    grads = [torch.empty_like(r) for _ in range(6)]
+    ds0 = torch.empty_like(s0)
+    with torch.cuda.device(dev):
+        rc = lib.rwkv7m_wkv7_backward(
+            _dtype_code(r), T, B, H, N, _p(r), _p(w), _p(k), _p(v), _p(a),
+            _p(b), _p(s0), _p(dy_c), _p(ds_c), _p(ckpt), ci,
+            *(_p(g) for g in grads), _p(ds0), _stream(dev))
+    _check(rc, "rwkv7m_wkv7_backward")
+    return (*grads, ds0)
+
+
+def decode_inplace(r, w, k, v, neg_kk, kka, state):
+    """One-token step, state updated in place; vectors [B,H,N] or
+    [1,B,H,N]. Returns y with the vectors' shape."""
+    lib = load_library()
+    shape = r.shape
+    r, w, k, v, a, b = (x.reshape(-1, *x.shape[-3:]).contiguous()
+                        for x in (r, w, k, v, neg_kk, kka))
+    if r.shape[0] != 1 or not state.is_contiguous():
+        raise ValueError("decode_inplace takes one token and a contiguous "
+                         "state")
+    dev = _dev((r, w, k, v, a, b, state))
+    _, B, H, N = r.shape
+    y = torch.empty_like(r)
+    with torch.cuda.device(dev):
+        rc = lib.rwkv7m_wkv7_decode_inplace(
+            _dtype_code(r), B, H, N, _p(r), _p(w), _p(k), _p(v), _p(a),
+            _p(b), _p(state), _p(y), _stream(dev))
+    _check(rc, "rwkv7m_wkv7_decode_inplace")
+    return y.reshape(shape)
+
+
+def hip_wkv_ffi_backend() -> WKVFFIBackend:
+    """The HIP kernels as a reference-contract ``WKVFFIBackend``."""
+    load_library()
+    return WKVFFIBackend(
+        forward=forward,
+        forward_with_aux=forward_with_aux,
+        backward=lambda *args: backward(*args),
+    )
+
+
+def register_hip_backend(*, replace: bool = False) -> WKVFFIBackend:
+    """Register the HIP kernels as the process's WKV FFI backend; select it
+    with ``backend="ffi"`` or ``RWKV7M_WKV_BACKEND=ffi``."""
+    backend = hip_wkv_ffi_backend()
+    register_wkv_ffi_backend(backend, replace=replace)
+    return backend
+
+
+__all__ = [
+    "EXPORTED_SYMBOLS", "LIB_PATH", "backward", "checkpoint_count",
+    "decode_inplace", "default_checkpoint_interval", "forward",
+    "forward_with_aux", "hip_wkv_ffi_backend", "load_library",
+    "register_hip_backend",
+]

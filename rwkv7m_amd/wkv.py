@@ -1,0 +1,194 @@
+"""WKV-7 operator API: validation, custom VJP and backend dispatch.
+
+A torch mirror of the reference's ``src/rwkv7m/model/wkv.py``:
+
+* ``_validate_wkv_inputs`` -- wkv.py:19-57, same exception types and messages;
+* ``wkv7_reference`` -- wkv.py:60-79, the portable time-major scan of
+  ``wkv_step`` (rwkv_core.py:54-86) written with torch ops;
+* ``wkv7`` -- wkv.py:219-286, a custom-VJP op (``torch.autograd.Function``)
+  with the same positional signature ``(r, w, k, v, neg_kk, kka,
+  initial_state, backend=None, interpret=False)``, dispatching to the
+  registered FFI backend (the HIP kernels once ``register_hip_backend()`` ran)
+  or to the reference scan;
+* ``_wkv7_forward_dispatch`` / ``_wkv7_backward_dispatch`` -- wkv.py:127-216,
+  including the FFI argument order ``backward(*inputs, *cotangents, *aux)``.
+
+Layout: vectors ``[T, B, H, N]`` (bf16 or fp32, one dtype), state
+``[B, H, N, N]`` fp32; ``y`` in the vector dtype, the final state fp32.
+Only reverse-mode differentiation is supported (``torch.func.jvp`` raises).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .kernels.wkv_backend import resolve_wkv_backend
+from .kernels.wkv_ffi import require_wkv_ffi_backend
+
+_SUPPORTED_INPUT_DTYPES = (torch.bfloat16, torch.float32)
+
+
+def _validate_wkv_inputs(r, w, k, v, neg_kk, kka, initial_state):
+    vectors = {"r": r, "w": w, "k": k, "v": v, "neg_kk": neg_kk, "kka": kka}
+    if initial_state.dim() != 4:
+        raise ValueError(
+            "initial_state must have shape [batch, heads, rows, columns]"
+        )
+    if initial_state.shape[-1] != initial_state.shape[-2]:
+        raise ValueError("initial_state WKV rows and columns must be equal")
+    if initial_state.dtype != torch.float32:
+        raise TypeError(
+            f"initial_state must be float32, got {initial_state.dtype}"
+        )
+    if r.dim() != 4:
+        raise ValueError(
+            "r must have shape [time, batch, heads, head_size], "
+            f"got {tuple(r.shape)}"
+        )
+    expected_shape = (r.shape[0], *initial_state.shape[:3])
+    for name, value in vectors.items():
+        if value.dim() != 4 or tuple(value.shape) != expected_shape:
+            raise ValueError(
+                f"{name} must have shape {expected_shape}, "
+                f"got {tuple(value.shape)}"
+            )
+        if value.dtype != r.dtype:
+            raise TypeError(
+                f"all WKV vectors must use {r.dtype}, got {name}={value.dtype}"
+            )
+    if r.dtype not in _SUPPORTED_INPUT_DTYPES:
+        raise TypeError(
+            f"WKV vectors must be bfloat16 or float32, got {r.dtype}"
+        )
+
+
+def _wkv7_reference_impl(r, w, k, v, neg_kk, kka, initial_state):
+    """Time-major scan of the fp32 step (rwkv_core.py:54-86); ``y`` is cast
+    to the vector dtype once, after the scan (wkv.py:62-67)."""
+    state = initial_state.to(torch.float32)
+    ys = []
+    for t in range(r.shape[0]):
+        r_t, w_t, k_t, v_t, a_t, b_t = (
+            x[t].to(torch.float32) for x in (r, w, k, v, neg_kk, kka))
+        decay = torch.exp(-torch.exp(w_t))[..., None, :]
+        sa = (state * a_t[..., None, :]).sum(-1)
+        state = (state * decay + sa[..., :, None] * b_t[..., None, :]
+                 + v_t[..., :, None] * k_t[..., None, :])
+        ys.append((state * r_t[..., None, :]).sum(-1))
+    if ys:
+        y = torch.stack(ys)
+    else:
+        y = torch.zeros(r.shape, dtype=torch.float32, device=r.device)
+    return y.to(r.dtype), state
+
+
+def wkv7_reference(r, w, k, v, neg_kk, kka, initial_state):
+    """Execute the portable time-major WKV recurrence (wkv.py:70-79)."""
+    _validate_wkv_inputs(r, w, k, v, neg_kk, kka, initial_state)
+    return _wkv7_reference_impl(r, w, k, v, neg_kk, kka, initial_state)
+
+
+_PALLAS = ("pallas_gpu_mosaic", "pallas_gpu_triton", "pallas_tpu")
+
+
+def _no_pallas(selected: str):
+    raise NotImplementedError(
+        f"WKV backend {selected!r} is a JAX Pallas backend of the reference "
+        "and is not part of rwkv7m_amd; register the HIP kernels with "
+        "rwkv7m_amd.register_hip_backend() and select backend='ffi' "
+        "(or RWKV7M_WKV_BACKEND=ffi)"
+    )
+
+
+def _wkv7_forward_dispatch(r, w, k, v, neg_kk, kka, initial_state, *,
+                           backend, interpret, with_aux):
+    selected = resolve_wkv_backend(backend)
+    inputs = (r, w, k, v, neg_kk, kka, initial_state)
+    if selected == "reference":
+        outputs = _wkv7_reference_impl(*inputs)
+        return (outputs, ()) if with_aux else outputs
+    if selected in _PALLAS:
+        _no_pallas(selected)
+    ffi_backend = require_wkv_ffi_backend()
+    if with_aux:
+        return ffi_backend.forward_with_aux(*inputs)
+    return ffi_backend.forward(*inputs)
+
+
+def _wkv7_backward_dispatch(inputs, cotangents, aux, *, backend, interpret):
+    selected = resolve_wkv_backend(backend)
+    if selected == "reference":
+        with torch.enable_grad():
+            detached = [x.detach().requires_grad_(True) for x in inputs]
+            outs = _wkv7_reference_impl(*detached)
+            grads = torch.autograd.grad(
+                outs, detached, grad_outputs=cotangents, allow_unused=True)
+        return tuple(torch.zeros_like(x) if g is None else g.to(x.dtype)
+                     for g, x in zip(grads, inputs))
+    if selected in _PALLAS:
+        _no_pallas(selected)
+    ffi_backend = require_wkv_ffi_backend()
+    return ffi_backend.backward(*inputs, *cotangents, *aux)
+
+
+class _WKV7(torch.autograd.Function):
+    """Custom VJP of wkv7 (the jax.custom_vjp of wkv.py:219-286)."""
+
+    @staticmethod
+    def forward(ctx, r, w, k, v, neg_kk, kka, initial_state, backend,
+                interpret):
+        inputs = (r, w, k, v, neg_kk, kka, initial_state)
+        (y, final_state), aux = _wkv7_forward_dispatch(
+            *inputs, backend=backend, interpret=interpret, with_aux=True)
+        aux = tuple(aux)
+        tensor_aux = [a for a in aux if isinstance(a, torch.Tensor)]
+        ctx.save_for_backward(*inputs, *tensor_aux)
+        ctx.aux_layout = [isinstance(a, torch.Tensor) for a in aux]
+        ctx.aux_other = [a for a in aux if not isinstance(a, torch.Tensor)]
+        ctx.backend = backend
+        ctx.interpret = interpret
+        return y, final_state
+
+    @staticmethod
+    def backward(ctx, dy, ds_t):
+        saved = ctx.saved_tensors
+        inputs = saved[:7]
+        tensor_aux = iter(saved[7:])
+        other = iter(ctx.aux_other)
+        aux = tuple(next(tensor_aux) if is_t else next(other)
+                    for is_t in ctx.aux_layout)
+        r, s0 = inputs[0], inputs[6]
+        if dy is None:
+            dy = torch.zeros_like(r)
+        if ds_t is None:
+            ds_t = torch.zeros_like(s0)
+        grads = _wkv7_backward_dispatch(
+            inputs, (dy.to(r.dtype), ds_t.to(torch.float32)), aux,
+            backend=ctx.backend, interpret=ctx.interpret)
+        return (*grads, None, None)
+
+    @staticmethod
+    def jvp(ctx, *tangents):
+        raise TypeError(
+            "wkv7 supports reverse-mode differentiation only; forward-mode "
+            "autodiff (jvp) is not implemented")
+
+
+def wkv7(r, w, k, v, neg_kk, kka, initial_state, backend: str | None = None,
+         interpret: bool = False):
+    """Execute WKV-7 through the selected backend (wkv.py:219-250).
+
+    ``backend`` is normally left as ``None``/``auto``; ``"ffi"`` selects the
+    registered native backend (the HIP kernels after
+    ``rwkv7m_amd.register_hip_backend()``). ``interpret`` is accepted for
+    signature parity and only meaningful to Pallas backends.
+    """
+    _validate_wkv_inputs(r, w, k, v, neg_kk, kka, initial_state)
+    inputs = (r, w, k, v, neg_kk, kka, initial_state)
+    if torch.is_grad_enabled() and any(x.requires_grad for x in inputs):
+        return _WKV7.apply(*inputs, backend, interpret)
+    return _wkv7_forward_dispatch(*inputs, backend=backend,
+                                  interpret=interpret, with_aux=False)
+
+
+__all__ = ["wkv7", "wkv7_reference"]

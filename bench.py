@@ -1,0 +1,214 @@
+"""WKV-7 forward+backward throughput on one MI355X.
+
+One step = one pass of the hot path over one batch: ``forward_with_aux``
+(y, S_T and the checkpoints) followed by ``backward`` (all six vector
+gradients and dS0), both through the HIP backend's callables -- the
+callables the reference's FFI registry binds (src/rwkv7m/kernels/
+wkv_ffi.py:21-34).  Inputs (vectors, S0, dy, dS_T) are synthetic, with the
+model's input distributions, and resident in HBM before timing starts.
+
+The method mirrors the reference's WKV microbenchmark
+(scripts/benchmark_wkv_accelerator.py:88-97): W untimed warmup steps, then
+K steps between two device synchronisations.  Tokens/s = B*T / seconds per
+step.  Kernel durations come from HIP events recorded on the stream the
+kernels run on.  ``cpu_baseline`` times the CPU restatement of the reference
+scan (oracle/, fp32, OpenMP over (b, h)) on a bounded sample of the same
+workload on the host cores.
+
+Prints ONE JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--config", type=int, default=2,
+                   help="BASELINE config index (2 = the headline shape)")
+    p.add_argument("--chunk", type=int, default=0,
+                   help="checkpoint interval / chunk length (0 = library "
+                        "default)")
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
+                   help="target CPU-baseline sample duration (0 = skip)")
+    return p.parse_args()
+
+
+def algorithmic_bytes(T, B, H, N, eb):
+    """Compulsory HBM traffic: fwd reads 6 vectors and S0 and writes y and
+    S_T; bwd reads 6 vectors, dy, dS_T and S0 and writes 6 gradients and
+    dS0.  Checkpoint traffic is implementation overhead and not counted."""
+    V = T * B * H * N * eb
+    S = B * H * N * N * 4
+    return 7 * V + 2 * S, 13 * V + 3 * S
+
+
+def cpu_baseline(cfg, target_s):
+    """Time the CPU restatement (oracle, fp32, OpenMP over (b, h)) on the
+    config's (B, H, N) at a reduced T chosen to take about ``target_s``."""
+    import numpy as np
+
+    import oracle
+    from rwkv7m_amd.synthetic import make_inputs
+
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    B, H, N = cfg["B"], cfg["H"], cfg["N"]
+
+    def run(T):
+        inp = make_inputs(T, B, H, N, dtype=cfg["dtype"], seed=7,
+                          state_std=cfg.get("state_std", 0.0),
+                          dstate_std=cfg.get("dstate_std", 0.0),
+                          slow_decay=cfg.get("slow_decay", False))
+        arrs = {k: v.float().numpy() for k, v in inp.items()}
+        vecs = [arrs[n] for n in ("r", "w", "k", "v", "neg_kk", "kka")]
+        t0 = time.perf_counter()
+        oracle.forward(*vecs, arrs["s0"], precision="f32", threads=threads)
+        oracle.backward(*vecs, arrs["s0"], arrs["dy"], arrs["ds_t"],
+                        precision="f32", threads=threads)
+        return time.perf_counter() - t0
+
+    probe_T = 16
+    dt = run(probe_T)
+    T = int(max(probe_T, min(cfg["T"], probe_T * target_s / max(dt, 1e-6))))
+    dt = run(T)
+    return {
+        "value": B * T / dt,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"fp32 C restatement of the reference scan fwd+bwd, "
+                   f"B={B} T={T} H={H} N={N}, {dt:.1f} s on {threads} "
+                   f"threads"),
+    }
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: the WKV-7 path shards over "
+              "(batch, head) with no exchange, so each GPU runs this same "
+              "single-GPU kernel on its share; run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from rwkv7m_amd.kernels import wkv_hip
+    from rwkv7m_amd.synthetic import CONFIGS, make_inputs
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    wkv_hip.load_library()
+    cfg = dict(CONFIGS[args.config])
+    T, B, H, N, dtype = cfg["T"], cfg["B"], cfg["H"], cfg["N"], cfg["dtype"]
+    dev = torch.device("cuda:0")
+    inp = make_inputs(T, B, H, N, dtype=dtype, seed=cfg["seed"],
+                      slow_decay=cfg.get("slow_decay", False),
+                      state_std=cfg.get("state_std", 0.0),
+                      dstate_std=cfg.get("dstate_std", 0.0),
+                      device=dev, generator="torch")
+    vecs = [inp[n] for n in ("r", "w", "k", "v", "neg_kk", "kka")]
+    s0, dy, ds_t = inp["s0"], inp["dy"], inp["ds_t"]
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream(dev)
+
+    def step(evs=None):
+        if evs:
+            evs[0].record(stream)
+        (y, s_t), aux = wkv_hip.forward_with_aux(
+            *vecs, s0, checkpoint_interval=args.chunk)
+        if evs:
+            evs[1].record(stream)
+        grads = wkv_hip.backward(*vecs, s0, dy, ds_t, *aux)
+        if evs:
+            evs[2].record(stream)
+        return y, s_t, grads
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)]
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+    ms_per_step = elapsed * 1e3 / args.steps
+    eb = 2 if dtype == torch.bfloat16 else 4
+    fwd_bytes, bwd_bytes = algorithmic_bytes(T, B, H, N, eb)
+    tokens = B * T
+    value = tokens / (ms_per_step / 1e3)
+
+    dominant = "backward" if bwd_ms >= fwd_ms else "forward"
+    dom_bytes = bwd_bytes if dominant == "backward" else fwd_bytes
+    dom_ms = bwd_ms if dominant == "backward" else fwd_ms
+    achieved = dom_bytes / (dom_ms / 1e3) / 1e9
+    step_gbs = (fwd_bytes + bwd_bytes) / (ms_per_step / 1e3) / 1e9
+
+    ci = args.chunk or wkv_hip.default_checkpoint_interval(dtype, N)
+    result = {
+        "metric": "WKV-7 fwd+bwd tokens/sec at H=32,N=64,T=4096 bf16",
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if dtype == torch.bfloat16 else "f32",
+        "data": "synthetic (model input distributions, device RNG)",
+        "config": {
+            "workload": (f"config {args.config}: WKV-7 fwd+bwd B={B} T={T} "
+                         f"H={H} N={N} "
+                         f"{'bf16' if eb == 2 else 'fp32'} vectors, fp32 "
+                         f"state"),
+            "B": B, "T": T, "H": H, "N": N, "chunk": ci,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dominant,
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "algorithmic_bytes": dom_bytes,
+            "avg_ms": dom_ms,
+        },
+        "kernels_ms": {"forward": fwd_ms, "backward": bwd_ms},
+        "step_roofline_frac": step_gbs / HBM_PEAK_GBS,
+    }
+    if args.cpu_seconds > 0:
+        result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -7,7 +7,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <cstdio>
+#include <initializer_list>
 #include <string>
 
 #include "../../include/rwkv7m_wkv.h"
@@ -100,10 +102,27 @@ int hip_status(const char* what, hipError_t e) {
                                     hipGetErrorString(e));
 }
 
+// Chunk length of the MFMA kernels when the caller leaves it to the library.
+constexpr int64_t kDefaultChunk = 64;
+
 int64_t default_interval(int dtype, int64_t N) {
-    (void)dtype;
-    (void)N;
+    if (dtype == RWKV7M_DTYPE_BF16 && N == 64) return kDefaultChunk;
     return 16;
+}
+
+bool aligned16(const void* p) {
+    return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// The chunked MFMA kernels serve bf16 vectors with N = 64, a chunk length
+// (= checkpoint interval) of 16, 32 or 64, and 16-byte aligned buffers.
+bool use_chunked(int dtype, int64_t N, int64_t ci,
+                 std::initializer_list<const void*> ptrs) {
+    if (dtype != RWKV7M_DTYPE_BF16 || N != 64) return false;
+    if (ci != 16 && ci != 32 && ci != 64) return false;
+    for (const void* p : ptrs)
+        if (p && !aligned16(p)) return false;
+    return true;
 }
 
 int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
@@ -128,6 +147,27 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
         RWKV7M_TRY(copy_or_clear(s_t, s0, d.state_elems, stream));
         if (ckpt) RWKV7M_TRY(copy_or_clear(ckpt, s0, d.state_elems, stream));
         return RWKV7M_OK;
+    }
+    const int64_t L = ckpt ? ci : kDefaultChunk;
+    if (T > 1 && use_chunked(dtype, N, L, {r, w, k, v, a, b, y, s0, s_t, ckpt})) {
+        rwkv7m::ChunkFwdArgs c{};
+        c.L = int(L);
+        c.T = T;
+        c.B = B;
+        c.H = H;
+        c.r = r;
+        c.w = w;
+        c.k = k;
+        c.v = v;
+        c.a = a;
+        c.b = b;
+        c.s0 = s0;
+        c.y = y;
+        c.s_t = s_t;
+        c.ckpt = ckpt;
+        c.ckpt_every = 1;
+        return hip_status("chunked forward launch",
+                          rwkv7m::launch_chunk_forward(c, stream));
     }
     rwkv7m::SeqFwdArgs p{};
     p.bf16 = dtype == RWKV7M_DTYPE_BF16;

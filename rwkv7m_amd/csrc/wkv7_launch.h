@@ -31,6 +31,20 @@ struct SeqBwdArgs {
     const int* only_flagged;
 };
 
+// Chunked MFMA kernels: bf16 vectors, N = 64, chunk length L in {16,32,64}.
+struct ChunkFwdArgs {
+    int L;
+    int64_t T, B, H;
+    const void *r, *w, *k, *v, *a, *b;
+    const float* s0;
+    void* y;
+    float* s_t;
+    float* ckpt;          // nullptr: no checkpoints
+    int64_t ckpt_every;   // chunks per checkpoint (when ckpt != nullptr)
+};
+
+hipError_t launch_chunk_forward(const ChunkFwdArgs& p, hipStream_t stream);
+
 hipError_t launch_seq_forward(const SeqFwdArgs& p, hipStream_t stream);
 hipError_t launch_seq_backward(const SeqBwdArgs& p, hipStream_t stream);
 

@@ -1,0 +1,116 @@
+// MFMA tile helpers for gfx950 (CDNA4, wave64).
+//
+// A tile is a 16x16 fp32 accumulator held by one wave: lane l holds rows
+// 4*(l/16) + e (e = 0..3) of column l%16.  Operands are bf16 matrices in LDS
+// stored with the contraction index K contiguous: A as [m][k], B as [n][k]
+// (so every GEMM here computes A * B^T), row pitch a multiple of 8 elements
+// and rows 16-byte aligned.
+//
+// Lane layouts (checked on gfx950 hardware):
+//   v_mfma_f32_16x16x32_bf16: A lane l holds A[l%16][8*(l/16) + 0..7],
+//     B lane l holds B[8*(l/16) + 0..7][l%16], D as above.
+//   v_mfma_f32_16x16x16_bf16 (1k): the same with 4 k values per lane.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "wkv7_common.h"
+
+namespace rwkv7m {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t zero4() {
+    f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+    return z;
+}
+
+// Hardware round-to-nearest-even conversion (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ bf16_t to_bf16(float x) {
+    return __builtin_bit_cast(bf16_t, static_cast<__bf16>(x));
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return uint32_t(to_bf16(lo)) | (uint32_t(to_bf16(hi)) << 16);
+}
+
+// acc += A[0..16)[0..K) * B[0..16)[0..K)^T.  A and B point at the first row
+// of the 16-row operand blocks; lda/ldb are row pitches in elements.
+template <int K>
+__device__ __forceinline__ void mma_nt(f32x4_t& acc, const bf16_t* A, int lda,
+                                       const bf16_t* B, int ldb, int lane) {
+    static_assert(K % 16 == 0, "K must be a multiple of 16");
+    const int r = lane & 15, q = lane >> 4;
+    const bf16_t* ar = A + r * lda;
+    const bf16_t* br = B + r * ldb;
+#pragma unroll
+    for (int k0 = 0; k0 + 32 <= K; k0 += 32) {
+        const bf16x8_t a =
+            *reinterpret_cast<const bf16x8_t*>(ar + k0 + 8 * q);
+        const bf16x8_t b =
+            *reinterpret_cast<const bf16x8_t*>(br + k0 + 8 * q);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+    }
+    if constexpr (K % 32 == 16) {
+        constexpr int k0 = K - 16;
+        const s16x4_t a =
+            *reinterpret_cast<const s16x4_t*>(ar + k0 + 4 * q);
+        const s16x4_t b =
+            *reinterpret_cast<const s16x4_t*>(br + k0 + 4 * q);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
+    }
+}
+
+// Runtime-K variant (K a multiple of 16, at most KMAX).
+template <int KMAX>
+__device__ __forceinline__ void mma_nt_k(f32x4_t& acc, const bf16_t* A,
+                                         int lda, const bf16_t* B, int ldb,
+                                         int K, int lane) {
+    const int r = lane & 15, q = lane >> 4;
+    const bf16_t* ar = A + r * lda;
+    const bf16_t* br = B + r * ldb;
+    int k0 = 0;
+#pragma unroll
+    for (int it = 0; it < KMAX / 32; ++it) {
+        if (k0 + 32 <= K) {
+            const bf16x8_t a =
+                *reinterpret_cast<const bf16x8_t*>(ar + k0 + 8 * q);
+            const bf16x8_t b =
+                *reinterpret_cast<const bf16x8_t*>(br + k0 + 8 * q);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0,
+                                                          0);
+            k0 += 32;
+        }
+    }
+    if (k0 + 16 <= K) {
+        const s16x4_t a = *reinterpret_cast<const s16x4_t*>(ar + k0 + 4 * q);
+        const s16x4_t b = *reinterpret_cast<const s16x4_t*>(br + k0 + 4 * q);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
+    }
+}
+
+// Store a tile as bf16 into D[m][n] (row-major, pitch ld): 4 scattered
+// 2-byte writes per lane.
+__device__ __forceinline__ void store_tile_bf16(const f32x4_t& acc,
+                                                bf16_t* D, int ld, int lane) {
+    const int r = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) D[(4 * q + e) * ld + r] = to_bf16(acc[e]);
+}
+
+// Store a tile transposed as bf16 into D[n][m] (pitch ld, a multiple of 4):
+// the 4 rows a lane holds are contiguous there, one 8-byte write.
+__device__ __forceinline__ void store_tile_bf16_t(const f32x4_t& acc,
+                                                  bf16_t* D, int ld,
+                                                  int lane) {
+    const int r = lane & 15, q = lane >> 4;
+    uint2 p;
+    p.x = pack_bf16x2(acc[0], acc[1]);
+    p.y = pack_bf16x2(acc[2], acc[3]);
+    *reinterpret_cast<uint2*>(D + r * ld + 4 * q) = p;
+}
+
+}  // namespace rwkv7m

@@ -102,11 +102,13 @@ int hip_status(const char* what, hipError_t e) {
                                     hipGetErrorString(e));
 }
 
-// Chunk length of the MFMA kernels when the caller leaves it to the library.
+// Chunk length of the MFMA forward without checkpoints, and the default
+// checkpoint interval (= chunk length of the MFMA forward and backward).
 constexpr int64_t kDefaultChunk = 64;
+constexpr int64_t kDefaultTrainChunk = 32;
 
 int64_t default_interval(int dtype, int64_t N) {
-    if (dtype == RWKV7M_DTYPE_BF16 && N == 64) return kDefaultChunk;
+    if (dtype == RWKV7M_DTYPE_BF16 && N == 64) return kDefaultTrainChunk;
     return 16;
 }
 
@@ -278,6 +280,34 @@ int rwkv7m_wkv7_backward(int dtype, int64_t T, int64_t B, int64_t H,
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (d.state_elems == 0) return RWKV7M_OK;
     if (T == 0) return copy_or_clear(ds0, ds_t, d.state_elems, s);
+    if ((ci == 16 || ci == 32) &&
+        use_chunked(dtype, N, ci,
+                    {r, w, k, v, neg_kk, kka, dy, ds_t, checkpoints, dr, dw,
+                     dk, dv, dneg_kk, dkka, ds0})) {
+        rwkv7m::ChunkBwdArgs c{};
+        c.L = int(ci);
+        c.T = T;
+        c.B = B;
+        c.H = H;
+        c.r = r;
+        c.w = w;
+        c.k = k;
+        c.v = v;
+        c.a = neg_kk;
+        c.b = kka;
+        c.dy = dy;
+        c.ds_t = ds_t;
+        c.ckpt = checkpoints;
+        c.dr = dr;
+        c.dw = dw;
+        c.dk = dk;
+        c.dv = dv;
+        c.da = dneg_kk;
+        c.db = dkka;
+        c.ds0 = ds0;
+        return hip_status("chunked backward launch",
+                          rwkv7m::launch_chunk_backward(c, s));
+    }
     rwkv7m::SeqBwdArgs p{};
     p.bf16 = dtype == RWKV7M_DTYPE_BF16;
     p.T = T;

@@ -30,17 +30,16 @@
 // kHalfRange of log-decay on either side of g_ref: far outside the model's
 // clamped range) is run by an exact fp32 sequential loop instead.
 
-#include "wkv7_common.h"
+#include "wkv7_chunk_common.h"
 #include "wkv7_launch.h"
-#include "wkv7_mfma.h"
 
 namespace rwkv7m {
 namespace {
 
-constexpr int CN = 64;          // head size served by the chunked kernels
-constexpr int PN = CN + 8;      // LDS row pitch of K = N operands
-constexpr int NTHREADS = 256;   // 4 waves
-constexpr float kHalfRange = 40.f;
+using chunk::CN;
+using chunk::kHalfRange;
+using chunk::NTHREADS;
+using chunk::PN;
 
 template <int L>
 struct FwdSmem {
@@ -72,25 +71,6 @@ struct FwdSmem {
     float eL[CN], eRef[CN];
     int flag;
 };
-
-// Stage the chunk's six vectors into LDS (zeros past the end of the
-// sequence: a zero token with decay 1 leaves every result unchanged).
-template <int L>
-__device__ __forceinline__ void load_raw(FwdSmem<L>& sm, const bf16_t* const* src,
-                                         int64_t t0, int64_t T, int64_t BH,
-                                         int64_t bh, int tid) {
-    constexpr int ROWS = 6 * L;
-#pragma unroll
-    for (int p = 0; p < ROWS / 32; ++p) {
-        const int row = p * 32 + (tid >> 3), seg = tid & 7;
-        const int vec = row / L, t = row % L;
-        uint4 val = make_uint4(0, 0, 0, 0);
-        if (t0 + t < T)
-            val = *reinterpret_cast<const uint4*>(
-                src[vec] + ((t0 + t) * BH + bh) * CN + seg * 8);
-        *reinterpret_cast<uint4*>(&sm.raw[vec][t][seg * 8]) = val;
-    }
-}
 
 template <int L>
 __global__ void __launch_bounds__(NTHREADS)
@@ -130,7 +110,7 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         const int64_t t0 = c * L;
         const int n = int(T - t0 < L ? T - t0 : L);
         __syncthreads();  // previous chunk is done with every buffer
-        load_raw<L>(sm, src, t0, T, BH, bh, tid);
+        chunk::load_rows<L, 6>(sm.raw, src, t0, T, BH, bh, tid);
         if (tid == 0) sm.flag = 0;
         __syncthreads();
 
@@ -312,59 +292,8 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             }
             __syncthreads();
             // ---- A3: Minv = (I - Aab)^{-1} -----------------------------
-            if (wv == 0 && lane < 16 * NB) {
-                // lane = 16 * p + col: column col of diagonal block p
-                const int p = lane >> 4, col = lane & 15;
-                float x[16];
-#pragma unroll
-                for (int t = 0; t < 16; ++t) {
-                    float s = (t == col) ? 1.f : 0.f;
-#pragma unroll
-                    for (int ss = 0; ss < t; ++ss)
-                        s += sm.m.AabD[p][t][ss] * x[ss];
-                    x[t] = s;
-                }
-#pragma unroll
-                for (int t = 0; t < 16; ++t)
-                    sm.m.Minv[16 * p + t][16 * p + col] = to_bf16(x[t]);
-                uint32_t pk2[8];
-#pragma unroll
-                for (int q = 0; q < 8; ++q)
-                    pk2[q] = pack_bf16x2(x[2 * q], x[2 * q + 1]);
-                *reinterpret_cast<uint4*>(&sm.m.MinvT[16 * p + col][16 * p]) =
-                    make_uint4(pk2[0], pk2[1], pk2[2], pk2[3]);
-                *reinterpret_cast<uint4*>(
-                    &sm.m.MinvT[16 * p + col][16 * p + 8]) =
-                    make_uint4(pk2[4], pk2[5], pk2[6], pk2[7]);
-            }
-            if (NB > 1) {
-                // upper blocks of Minv are zero
-                for (int e = tid; e < L * L; e += NTHREADS) {
-                    const int tt = e / L, ss = e % L;
-                    if ((ss >> 4) > (tt >> 4)) sm.m.Minv[tt][ss] = 0;
-                }
-            }
-            __syncthreads();
-#pragma unroll
-            for (int kk = 1; kk < NB; ++kk) {
-                // blocks (p, q = p - kk), one per wave
-                const int q = wv, p = wv + kk;
-                if (p < NB) {
-                    f32x4_t z = zero4();
-                    mma_nt_k<48>(z, &sm.m.Aab[16 * p][16 * q], PL,
-                                 &sm.m.MinvT[16 * q][16 * q], PL, 16 * kk,
-                                 lane);
-                    store_tile_bf16_t(z, &sm.m.Z[wv][0][0], 24, lane);
-                    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-                    f32x4_t mq = zero4();
-                    mma_nt<16>(mq, &sm.m.Minv[16 * p][16 * p], PL,
-                               &sm.m.Z[wv][0][0], 24, lane);
-                    store_tile_bf16(mq, &sm.m.Minv[16 * p][16 * q], PL, lane);
-                    store_tile_bf16_t(mq, &sm.m.MinvT[16 * q][16 * p], PL,
-                                      lane);
-                }
-                __syncthreads();
-            }
+            chunk::build_minv<L>(sm.m.AabD, &sm.m.Aab[0][0], &sm.m.Minv[0][0],
+                                 &sm.m.MinvT[0][0], sm.m.Z, tid);
             // ---- B1: U = A~ S'^T + Aak V (stored transposed) and the
             //          state/value part of Y^T -----------------------------
             f32x4_t Yacc[NB];

@@ -45,6 +45,19 @@ struct ChunkFwdArgs {
 
 hipError_t launch_chunk_forward(const ChunkFwdArgs& p, hipStream_t stream);
 
+// Chunked backward: L in {16, 32}; ckpt holds a state every L tokens.
+struct ChunkBwdArgs {
+    int L;
+    int64_t T, B, H;
+    const void *r, *w, *k, *v, *a, *b, *dy;
+    const float* ds_t;
+    const float* ckpt;
+    void *dr, *dw, *dk, *dv, *da, *db;
+    float* ds0;
+};
+
+hipError_t launch_chunk_backward(const ChunkBwdArgs& p, hipStream_t stream);
+
 hipError_t launch_seq_forward(const SeqFwdArgs& p, hipStream_t stream);
 hipError_t launch_seq_backward(const SeqBwdArgs& p, hipStream_t stream);
 

@@ -6,10 +6,14 @@
 // (so every GEMM here computes A * B^T), row pitch a multiple of 8 elements
 // and rows 16-byte aligned.
 //
-// Lane layouts (checked on gfx950 hardware):
+// Lane layout (checked on gfx950 hardware):
 //   v_mfma_f32_16x16x32_bf16: A lane l holds A[l%16][8*(l/16) + 0..7],
 //     B lane l holds B[8*(l/16) + 0..7][l%16], D as above.
-//   v_mfma_f32_16x16x16_bf16 (1k): the same with 4 k values per lane.
+// Every product uses this one instruction.  A K step of 16 is a 16x16x32
+// step whose lanes 32..63 (k = 16..31) carry zeros: accumulating a
+// v_mfma_f32_16x16x16_bf16 onto the result of a 16x16x32 in the same
+// registers gave nondeterministic results on gfx950 with this toolchain
+// (no wait states are emitted between the two opcodes).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -20,7 +24,6 @@
 namespace rwkv7m {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f32x4_t zero4() {
@@ -56,11 +59,12 @@ __device__ __forceinline__ void mma_nt(f32x4_t& acc, const bf16_t* A, int lda,
     }
     if constexpr (K % 32 == 16) {
         constexpr int k0 = K - 16;
-        const s16x4_t a =
-            *reinterpret_cast<const s16x4_t*>(ar + k0 + 4 * q);
-        const s16x4_t b =
-            *reinterpret_cast<const s16x4_t*>(br + k0 + 4 * q);
-        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
+        bf16x8_t a = {}, b = {};
+        if (q < 2) {
+            a = *reinterpret_cast<const bf16x8_t*>(ar + k0 + 8 * q);
+            b = *reinterpret_cast<const bf16x8_t*>(br + k0 + 8 * q);
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
     }
 }
 
@@ -86,9 +90,12 @@ __device__ __forceinline__ void mma_nt_k(f32x4_t& acc, const bf16_t* A,
         }
     }
     if (k0 + 16 <= K) {
-        const s16x4_t a = *reinterpret_cast<const s16x4_t*>(ar + k0 + 4 * q);
-        const s16x4_t b = *reinterpret_cast<const s16x4_t*>(br + k0 + 4 * q);
-        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
+        bf16x8_t a = {}, b = {};
+        if (q < 2) {
+            a = *reinterpret_cast<const bf16x8_t*>(ar + k0 + 8 * q);
+            b = *reinterpret_cast<const bf16x8_t*>(br + k0 + 8 * q);
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
     }
 }
 

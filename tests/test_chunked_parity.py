@@ -139,3 +139,28 @@ def test_config4_shape_slow_decay_carry_state(hip):
     print("case:", case, flush=True)
     inp = config_inputs(4, T=2048, B=1, H=2)
     _run_case(hip, inp, 64, case)
+
+
+@pytest.mark.parametrize("ci", [16, 32, 64])
+def test_chunked_results_are_deterministic(hip, ci):
+    # The same inputs must give bit-identical outputs on every call: each
+    # workgroup owns one (batch, head) and reduces in a fixed order.
+    case = f"determinism T320 B4 H8 L{ci}"
+    print("case:", case, flush=True)
+    inp = make_inputs(320, 4, 8, 64, seed=77 + ci, state_std=0.1,
+                      dstate_std=0.1)
+    dev = {k: v.cuda() for k, v in inp.items()}
+    vecs = [dev[n] for n in NAMES]
+    first = None
+    for _ in range(6):
+        (y, s_t), aux = hip.forward_with_aux(*vecs, dev["s0"],
+                                             checkpoint_interval=ci)
+        grads = hip.backward(*vecs, dev["s0"], dev["dy"], dev["ds_t"], *aux)
+        outs = [y, s_t, aux[0], *grads]
+        torch.cuda.synchronize()
+        if first is None:
+            first = [o.clone() for o in outs]
+        else:
+            for name, a_, b_ in zip(("y", "s_t", "ckpt") + GRAD_NAMES, first,
+                                    outs):
+                assert torch.equal(a_, b_), f"{case}: {name} differs"

@@ -167,7 +167,6 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
         c.y = y;
         c.s_t = s_t;
         c.ckpt = ckpt;
-        c.ckpt_every = 1;
         return hip_status("chunked forward launch",
                           rwkv7m::launch_chunk_forward(c, stream));
     }

@@ -39,8 +39,7 @@ struct ChunkFwdArgs {
     const float* s0;
     void* y;
     float* s_t;
-    float* ckpt;          // nullptr: no checkpoints
-    int64_t ckpt_every;   // chunks per checkpoint (when ckpt != nullptr)
+    float* ckpt;  // nullptr: no checkpoints; else one per chunk (every L)
 };
 
 hipError_t launch_chunk_forward(const ChunkFwdArgs& p, hipStream_t stream);

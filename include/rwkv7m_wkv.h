@@ -21,9 +21,12 @@
  *     (rwkv_core.py:74);
  *   - all arithmetic on the state is fp32; y and the vector gradients are
  *     rounded to the vector dtype (round to nearest even) once, at the store.
- *   - aux is one fp32 buffer of checkpoints [ceil(T/ci)+1][B][H][N][N]:
+ *   - aux is one buffer of checkpoints [ceil(T/ci)+1][B][H][N][N]:
  *     entry 0 = S0, entry c = the state after token c*ci - 1, the last entry
- *     = S_T (the format of wkv_pallas_gpu.py:83-120, :319-343).
+ *     = S_T (the layout of wkv_pallas_gpu.py:83-120, :319-343).  Its element
+ *     type is rwkv7m_wkv7_checkpoint_dtype(dtype, N, ci): bf16 for bf16
+ *     vectors with N == 64 and ci in {16, 32, 64} (the MFMA path, which
+ *     only reads them as bf16 operands), fp32 otherwise.
  *
  * Every pointer is a device pointer; every call only enqueues work on
  * `stream` (a hipStream_t, NULL = the null stream) and never synchronises.
@@ -67,6 +70,11 @@ int64_t rwkv7m_wkv7_checkpoint_count(int64_t T, int64_t checkpoint_interval);
 /* Checkpoint interval the library uses when the caller passes 0. */
 int64_t rwkv7m_wkv7_default_checkpoint_interval(int dtype, int64_t N);
 
+/* Element type (an rwkv7m_dtype) of the checkpoints forward_with_aux writes
+ * and backward reads for these vectors and this interval (0 = default). */
+int rwkv7m_wkv7_checkpoint_dtype(int dtype, int64_t N,
+                                 int64_t checkpoint_interval);
+
 /*
  * forward: y = WKV(r, w, k, v, neg_kk, kka; S0) and S_T.
  * Replaces WKVFFIBackend.forward (wkv_ffi.py:32; called at wkv.py:175) and
@@ -85,14 +93,15 @@ int rwkv7m_wkv7_forward(int dtype, int64_t T, int64_t B, int64_t H, int64_t N,
  * wkv.py:174) and the reference's fwd+aux kernel (wkv_pallas_gpu.py:66-120,
  * :303-375).  checkpoint_interval = 0 selects the library default; the
  * chunked bf16 path needs a multiple of 16.
- * checkpoints: [rwkv7m_wkv7_checkpoint_count(T, ci)][B][H][N][N] fp32.
+ * checkpoints: [rwkv7m_wkv7_checkpoint_count(T, ci)][B][H][N][N] of
+ * rwkv7m_wkv7_checkpoint_dtype(dtype, N, ci).
  */
 int rwkv7m_wkv7_forward_with_aux(int dtype, int64_t T, int64_t B, int64_t H,
                                  int64_t N, const void *r, const void *w,
                                  const void *k, const void *v,
                                  const void *neg_kk, const void *kka,
                                  const float *initial_state, void *y,
-                                 float *final_state, float *checkpoints,
+                                 float *final_state, void *checkpoints,
                                  int64_t checkpoint_interval, void *stream);
 
 /*
@@ -108,7 +117,7 @@ int rwkv7m_wkv7_backward(int dtype, int64_t T, int64_t B, int64_t H,
                          const void *k, const void *v, const void *neg_kk,
                          const void *kka, const float *initial_state,
                          const void *dy, const float *ds_t,
-                         const float *checkpoints,
+                         const void *checkpoints,
                          int64_t checkpoint_interval, void *dr, void *dw,
                          void *dk, void *dv, void *dneg_kk, void *dkka,
                          float *ds0, void *stream);

@@ -112,6 +112,14 @@ int64_t default_interval(int dtype, int64_t N) {
     return 16;
 }
 
+// Checkpoints are bf16 exactly when the MFMA kernels can serve the interval
+// (they read checkpoints only as bf16 MFMA operands); the sequential kernels
+// read and write either type, so the choice does not depend on alignment.
+bool ckpt_bf16(int dtype, int64_t N, int64_t ci) {
+    return dtype == RWKV7M_DTYPE_BF16 && N == 64 &&
+           (ci == 16 || ci == 32 || ci == 64);
+}
+
 bool aligned16(const void* p) {
     return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
@@ -130,7 +138,7 @@ bool use_chunked(int dtype, int64_t N, int64_t ci,
 int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
                  int64_t N, const void* r, const void* w, const void* k,
                  const void* v, const void* a, const void* b,
-                 const float* s0, void* y, float* s_t, float* ckpt,
+                 const float* s0, void* y, float* s_t, void* ckpt,
                  int64_t ci, hipStream_t stream) {
     Dims d;
     RWKV7M_TRY(check_dims(fn, dtype, T, B, H, N, &d));
@@ -145,11 +153,7 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     RWKV7M_TRY(need(s0, st, fn, "initial_state"));
     RWKV7M_TRY(need(s_t, st, fn, "final_state"));
     if (d.state_elems == 0) return RWKV7M_OK;
-    if (T == 0) {
-        RWKV7M_TRY(copy_or_clear(s_t, s0, d.state_elems, stream));
-        if (ckpt) RWKV7M_TRY(copy_or_clear(ckpt, s0, d.state_elems, stream));
-        return RWKV7M_OK;
-    }
+    if (T == 0 && !ckpt) return copy_or_clear(s_t, s0, d.state_elems, stream);
     const int64_t L = ckpt ? ci : kDefaultChunk;
     if (T > 1 && use_chunked(dtype, N, L, {r, w, k, v, a, b, y, s0, s_t, ckpt})) {
         rwkv7m::ChunkFwdArgs c{};
@@ -186,8 +190,8 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     p.y = y;
     p.s_t = s_t;
     p.ckpt = ckpt;
+    p.ckpt_bf16 = ckpt_bf16(dtype, N, ci);
     p.ci = ci;
-    p.only_flagged = nullptr;
     return hip_status("sequential forward launch",
                       rwkv7m::launch_seq_forward(p, stream));
 }
@@ -209,6 +213,13 @@ int64_t rwkv7m_wkv7_default_checkpoint_interval(int dtype, int64_t N) {
     return default_interval(dtype, N);
 }
 
+int rwkv7m_wkv7_checkpoint_dtype(int dtype, int64_t N,
+                                 int64_t checkpoint_interval) {
+    const int64_t ci = checkpoint_interval == 0 ? default_interval(dtype, N)
+                                                : checkpoint_interval;
+    return ckpt_bf16(dtype, N, ci) ? RWKV7M_DTYPE_BF16 : RWKV7M_DTYPE_F32;
+}
+
 int rwkv7m_wkv7_forward(int dtype, int64_t T, int64_t B, int64_t H, int64_t N,
                         const void* r, const void* w, const void* k,
                         const void* v, const void* neg_kk, const void* kka,
@@ -225,7 +236,7 @@ int rwkv7m_wkv7_forward_with_aux(int dtype, int64_t T, int64_t B, int64_t H,
                                  const void* k, const void* v,
                                  const void* neg_kk, const void* kka,
                                  const float* initial_state, void* y,
-                                 float* final_state, float* checkpoints,
+                                 float* final_state, void* checkpoints,
                                  int64_t checkpoint_interval, void* stream) {
     g_last_error.clear();
     const char* fn = "rwkv7m_wkv7_forward_with_aux";
@@ -246,7 +257,7 @@ int rwkv7m_wkv7_backward(int dtype, int64_t T, int64_t B, int64_t H,
                          const void* k, const void* v, const void* neg_kk,
                          const void* kka, const float* initial_state,
                          const void* dy, const float* ds_t,
-                         const float* checkpoints,
+                         const void* checkpoints,
                          int64_t checkpoint_interval, void* dr, void* dw,
                          void* dk, void* dv, void* dneg_kk, void* dkka,
                          float* ds0, void* stream) {
@@ -322,6 +333,7 @@ int rwkv7m_wkv7_backward(int dtype, int64_t T, int64_t B, int64_t H,
     p.dy = dy;
     p.ds_t = ds_t;
     p.ckpt = checkpoints;
+    p.ckpt_bf16 = ckpt_bf16(dtype, N, ci);
     p.ci = ci;
     p.dr = dr;
     p.dw = dw;
@@ -330,7 +342,6 @@ int rwkv7m_wkv7_backward(int dtype, int64_t T, int64_t B, int64_t H,
     p.da = dneg_kk;
     p.db = dkka;
     p.ds0 = ds0;
-    p.only_flagged = nullptr;
     return hip_status("sequential backward launch",
                       rwkv7m::launch_seq_backward(p, s));
 }

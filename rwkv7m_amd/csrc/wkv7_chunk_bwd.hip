@@ -74,7 +74,7 @@ struct BwdSmem {
         struct {  // factor and matrix passes
             bf16_t raw[7][L][CN];  // r, w, k, v, neg_kk, kka, dy
             union {
-                float S0f[CN][CN];  // the next chunk's S_0, staged
+                bf16_t S0f[CN][CN];  // the next chunk's S_0, staged
                 struct {
                     bf16_t Rt[L][PN], Bt[L][PN], Kt[L][PN];  // [t][j]
                     bf16_t Aab[L][PL];
@@ -235,7 +235,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                       const bf16_t* __restrict__ b,
                       const bf16_t* __restrict__ dy,
                       const float* __restrict__ ds_t,
-                      const float* __restrict__ ckpt, bf16_t* dr, bf16_t* dw,
+                      const bf16_t* __restrict__ ckpt, bf16_t* dr, bf16_t* dw,
                       bf16_t* dk, bf16_t* dv, bf16_t* da, bf16_t* db,
                       float* ds0) {
     using Sm = BwdSmem<L>;
@@ -268,15 +268,22 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             dst[q][0] = x.x; dst[q][1] = x.y; dst[q][2] = x.z; dst[q][3] = x.w;
         }
     };
+    auto load_tiles_bf16 = [&](f32x4_t* dst, const bf16_t* p) {
+#pragma unroll
+        for (int q = 0; q < ST; ++q)
+            dst[q] = unpack4(
+                *reinterpret_cast<const uint2*>(p + sbase + toff[q]));
+    };
 
     // ---- prefetch: the next chunk's 7 vectors and S_0 --------------------
     constexpr int LOADERS = NTH;
     const int ltid = tid;
     constexpr int SEGV = 7 * L * 8;  // 16-byte segments of the 7 vectors
     constexpr int NPV = (SEGV + LOADERS - 1) / LOADERS;
-    constexpr int NPS = CN * CN * 4 / 16 / LOADERS;  // S_0 segments
+    constexpr int NPS = CN * CN * 2 / 16 / LOADERS;  // S_0 segments
+    static_assert(NPS * 16 * LOADERS == CN * CN * 2, "S_0 segments");
     uint4 prev[NPV];
-    float4 pres[NPS];
+    uint4 pres[NPS];
     auto fetch = [&](int64_t cc, int ltid) {  // chunk cc's data into registers
         const int64_t t0f = cc * L;
 #pragma unroll
@@ -292,11 +299,11 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                         base + ((t0f + t) * BH + bh) * CN + s8 * 8);
             }
         }
-        const float* cp = ckpt + cc * BH * NN + sbase;
+        const bf16_t* cp = ckpt + cc * BH * NN + sbase;
 #pragma unroll
         for (int p = 0; p < NPS; ++p)
-            pres[p] = *reinterpret_cast<const float4*>(cp +
-                                                       4 * (p * LOADERS + ltid));
+            pres[p] = *reinterpret_cast<const uint4*>(cp +
+                                                      8 * (p * LOADERS + ltid));
     };
     auto stash = [&](int ltid) {
 #pragma unroll
@@ -310,14 +317,14 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         }
 #pragma unroll
         for (int p = 0; p < NPS; ++p)
-            *reinterpret_cast<float4*>(&sm.e1.S0f[0][0] +
-                                       4 * (p * LOADERS + ltid)) = pres[p];
+            *reinterpret_cast<uint4*>(&sm.e1.S0f[0][0] +
+                                      8 * (p * LOADERS + ltid)) = pres[p];
     };
 
     f32x4_t D[ST], SL[ST], S0[ST];
     load_tiles(D, ds_t);
     const int64_t nchunks = (T + L - 1) / L;
-    load_tiles(SL, ckpt + nchunks * BH * NN);
+    load_tiles_bf16(SL, ckpt + nchunks * BH * NN);
     fetch(nchunks - 1, ltid);
     stash(ltid);
     // everything loaded before the loop has arrived (see the forward kernel)
@@ -342,11 +349,9 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         }
         // this chunk's S_0 from the staging area
 #pragma unroll
-        for (int q = 0; q < ST; ++q) {
-            const float4 x =
-                *reinterpret_cast<const float4*>(&sm.e1.S0f[0][0] + toff[q]);
-            S0[q][0] = x.x; S0[q][1] = x.y; S0[q][2] = x.z; S0[q][3] = x.w;
-        }
+        for (int q = 0; q < ST; ++q)
+            S0[q] = unpack4(
+                *reinterpret_cast<const uint2*>(&sm.e1.S0f[0][0] + toff[q]));
 
         // ---- factor pass (thread: column j = lane, tokens of group wv) ---
         const int j = lane, grp = wv;
@@ -842,7 +847,8 @@ hipError_t launch_l(const ChunkBwdArgs& p, hipStream_t stream) {
                        static_cast<const bf16_t*>(p.v),
                        static_cast<const bf16_t*>(p.a),
                        static_cast<const bf16_t*>(p.b),
-                       static_cast<const bf16_t*>(p.dy), p.ds_t, p.ckpt,
+                       static_cast<const bf16_t*>(p.dy), p.ds_t,
+                       static_cast<const bf16_t*>(p.ckpt),
                        static_cast<bf16_t*>(p.dr), static_cast<bf16_t*>(p.dw),
                        static_cast<bf16_t*>(p.dk), static_cast<bf16_t*>(p.dv),
                        static_cast<bf16_t*>(p.da), static_cast<bf16_t*>(p.db),

@@ -83,7 +83,7 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                       const bf16_t* __restrict__ v,
                       const bf16_t* __restrict__ a,
                       const bf16_t* __restrict__ b, const float* s0,
-                      bf16_t* __restrict__ y, float* s_t, float* ckpt) {
+                      bf16_t* __restrict__ y, float* s_t, bf16_t* ckpt) {
     using Sm = FwdSmem<L>;
     constexpr int NW = FWD_WAVES, NTH = NW * 64;
     constexpr int PL = Sm::PL, NB = Sm::NB, TPG = L / NW;
@@ -107,7 +107,7 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         soff[q] = sbase + (16 * ib + lr) * CN + 16 * jb + 4 * lq;
         const float4 x = *reinterpret_cast<const float4*>(s0 + soff[q]);
         S[q][0] = x.x; S[q][1] = x.y; S[q][2] = x.z; S[q][3] = x.w;
-        if (ckpt) *reinterpret_cast<float4*>(ckpt + soff[q]) = x;
+        if (ckpt) *reinterpret_cast<uint2*>(ckpt + soff[q]) = pack4(S[q]);
     }
 
     // The next chunk's six vectors are fetched into registers while the
@@ -156,8 +156,8 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
     };
     // Checkpoint tiles of the loader waves go to HBM through the store
     // waves, staged in LDS (Bh/Kh/Vt, free after B3) as [tile - 8][lane].
-    float4* ck_stage = reinterpret_cast<float4*>(&sm.Bh[0][0]);
-    static_assert(sizeof(sm.Bh) * 3 >= 8 * 64 * 16, "checkpoint staging");
+    uint2* ck_stage = reinterpret_cast<uint2*>(&sm.Bh[0][0]);
+    static_assert(sizeof(sm.Bh) * 3 >= 8 * 64 * 8, "checkpoint staging");
 
     // Pipeline: chunk c+1's vectors sit in LDS (raw) while chunk c+2's are
     // in flight to the loader waves' registers.
@@ -435,21 +435,19 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         }
         // ---- next chunk's vectors to LDS; checkpoint tiles ---------------
         const bool want_ckpt = ckpt != nullptr;
-        float* cdst = ckpt + (c + 1) * BH * CN * CN;
+        bf16_t* cdst = ckpt + (c + 1) * BH * CN * CN;
         if (loader) {
             stash();
             if (want_ckpt) {
 #pragma unroll
                 for (int q = 0; q < ST; ++q)
-                    ck_stage[(ST * wv + q - 8) * 64 + lane] =
-                        make_float4(S[q][0], S[q][1], S[q][2], S[q][3]);
+                    ck_stage[(ST * wv + q - 8) * 64 + lane] = pack4(S[q]);
             }
             if (c + 2 < nchunks) fetch(t0 + 2 * L);
         } else if (want_ckpt) {
 #pragma unroll
             for (int q = 0; q < ST; ++q)
-                *reinterpret_cast<float4*>(cdst + soff[q]) =
-                    make_float4(S[q][0], S[q][1], S[q][2], S[q][3]);
+                *reinterpret_cast<uint2*>(cdst + soff[q]) = pack4(S[q]);
         }
         if (tid == 0) sm.flag = 0;
         __syncthreads();
@@ -458,7 +456,7 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
 #pragma unroll
             for (int q = 0; q < ST; ++q) {
                 const int si = 8 + ST * wv + q, jb = si >> 2, ib = si & 3;
-                *reinterpret_cast<float4*>(
+                *reinterpret_cast<uint2*>(
                     cdst + sbase + (16 * ib + lr) * CN + 16 * jb + 4 * lq) =
                     ck_stage[(ST * wv + q) * 64 + lane];
             }
@@ -481,7 +479,8 @@ hipError_t launch_l(const ChunkFwdArgs& p, hipStream_t stream) {
                        static_cast<const bf16_t*>(p.v),
                        static_cast<const bf16_t*>(p.a),
                        static_cast<const bf16_t*>(p.b), p.s0,
-                       static_cast<bf16_t*>(p.y), p.s_t, p.ckpt);
+                       static_cast<bf16_t*>(p.y), p.s_t,
+                       static_cast<bf16_t*>(p.ckpt));
     return hipGetLastError();
 }
 

@@ -14,9 +14,9 @@ struct SeqFwdArgs {
     const float* s0;
     void* y;
     float* s_t;
-    float* ckpt;          // nullptr: no checkpoints
+    void* ckpt;           // nullptr: no checkpoints
+    bool ckpt_bf16;       // checkpoint element type: bf16 (else fp32)
     int64_t ci;           // checkpoint interval (when ckpt != nullptr)
-    const int* only_flagged;  // nullptr: all (b,h); else run flagged only
 };
 
 struct SeqBwdArgs {
@@ -24,11 +24,11 @@ struct SeqBwdArgs {
     int64_t T, B, H, N;
     const void *r, *w, *k, *v, *a, *b, *dy;
     const float* ds_t;
-    const float* ckpt;
+    const void* ckpt;
+    bool ckpt_bf16;
     int64_t ci;
     void *dr, *dw, *dk, *dv, *da, *db;
     float* ds0;
-    const int* only_flagged;
 };
 
 // Chunked MFMA kernels: bf16 vectors, N = 64, chunk length L in {16,32,64}.
@@ -39,7 +39,7 @@ struct ChunkFwdArgs {
     const float* s0;
     void* y;
     float* s_t;
-    float* ckpt;  // nullptr: no checkpoints; else one per chunk (every L)
+    void* ckpt;  // nullptr: no checkpoints; else bf16, one per chunk (every L)
 };
 
 hipError_t launch_chunk_forward(const ChunkFwdArgs& p, hipStream_t stream);
@@ -50,7 +50,7 @@ struct ChunkBwdArgs {
     int64_t T, B, H;
     const void *r, *w, *k, *v, *a, *b, *dy;
     const float* ds_t;
-    const float* ckpt;
+    const void* ckpt;  // bf16, one state every L tokens
     void *dr, *dw, *dk, *dv, *da, *db;
     float* ds0;
 };

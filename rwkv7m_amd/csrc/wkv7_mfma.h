@@ -40,6 +40,24 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return uint32_t(to_bf16(lo)) | (uint32_t(to_bf16(hi)) << 16);
 }
 
+// The 4 values of a tile lane as 4 contiguous bf16 (one 8-byte store).
+__device__ __forceinline__ uint2 pack4(const f32x4_t& x) {
+    uint2 p;
+    p.x = pack_bf16x2(x[0], x[1]);
+    p.y = pack_bf16x2(x[2], x[3]);
+    return p;
+}
+
+// Inverse of pack4 (bf16 -> fp32 is exact).
+__device__ __forceinline__ f32x4_t unpack4(uint2 p) {
+    f32x4_t x;
+    x[0] = __uint_as_float(p.x << 16);
+    x[1] = __uint_as_float(p.x & 0xffff0000u);
+    x[2] = __uint_as_float(p.y << 16);
+    x[3] = __uint_as_float(p.y & 0xffff0000u);
+    return x;
+}
+
 // acc += A[0..16)[0..K) * B[0..16)[0..K)^T.  A and B point at the first row
 // of the 16-row operand blocks; lda/ldb are row pitches in elements.
 template <int K>

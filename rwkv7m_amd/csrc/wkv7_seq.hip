@@ -28,15 +28,15 @@ struct SeqShape {
     static constexpr int TB = 16;
 };
 
-// Forward.  ckpt == nullptr: no aux.  s_t may alias s0.
-template <int N, typename VT>
+// Forward.  ckpt == nullptr: no aux.  s_t may alias s0.  CT is the
+// checkpoint element type (float or bf16_t).
+template <int N, typename VT, typename CT>
 __global__ void __launch_bounds__(SeqShape<N>::THREADS)
 wkv7_seq_fwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
                     const VT* __restrict__ w, const VT* __restrict__ k,
                     const VT* __restrict__ v, const VT* __restrict__ a,
                     const VT* __restrict__ b, const float* s0, VT* y,
-                    float* s_t, float* ckpt, int64_t ci,
-                    const int* __restrict__ only_flagged) {
+                    float* s_t, CT* ckpt, int64_t ci) {
     using Sh = SeqShape<N>;
     constexpr int G = Sh::G, C = Sh::C, TB = Sh::TB, TH = Sh::THREADS;
     constexpr int64_t NN = int64_t(N) * N;
@@ -44,7 +44,6 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
     __shared__ float sh_y[TB][N];
 
     const int64_t bh = blockIdx.x;
-    if (only_flagged && only_flagged[bh] == 0) return;
     const int tid = threadIdx.x;
     const int row = tid / G, col0 = (tid % G) * C;
     const int64_t my = bh * NN + int64_t(row) * N + col0;
@@ -54,7 +53,7 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
     for (int c = 0; c < C; ++c) S[c] = s0[my + c];
     if (ckpt) {
 #pragma unroll
-        for (int c = 0; c < C; ++c) ckpt[my + c] = S[c];
+        for (int c = 0; c < C; ++c) store_f(ckpt + my + c, S[c]);
     }
     const VT* srcs[6] = {r, w, k, v, a, b};
 
@@ -88,9 +87,9 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
             if (ckpt) {
                 const int64_t t = t0 + u;
                 if ((t + 1) % ci == 0 || t + 1 == T) {
-                    float* dst = ckpt + ((t + ci) / ci) * BH * NN + my;
+                    CT* dst = ckpt + ((t + ci) / ci) * BH * NN + my;
 #pragma unroll
-                    for (int c = 0; c < C; ++c) dst[c] = S[c];
+                    for (int c = 0; c < C; ++c) store_f(dst + c, S[c]);
                 }
             }
         }
@@ -132,16 +131,15 @@ __device__ __forceinline__ void stage_bwd(
     }
 }
 
-template <int N, typename VT>
+template <int N, typename VT, typename CT>
 __global__ void __launch_bounds__(SeqShape<N>::THREADS)
 wkv7_seq_bwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
                     const VT* __restrict__ w, const VT* __restrict__ k,
                     const VT* __restrict__ v, const VT* __restrict__ a,
                     const VT* __restrict__ b, const VT* __restrict__ dy,
                     const float* __restrict__ ds_t,
-                    const float* __restrict__ ckpt, int64_t ci, VT* dr,
-                    VT* dw, VT* dk, VT* dv, VT* da, VT* db, float* ds0,
-                    const int* __restrict__ only_flagged) {
+                    const CT* __restrict__ ckpt, int64_t ci, VT* dr,
+                    VT* dw, VT* dk, VT* dv, VT* da, VT* db, float* ds0) {
     using Sh = SeqShape<N>;
     constexpr int G = Sh::G, C = Sh::C, SUB = Sh::SUB, TH = Sh::THREADS;
     constexpr int WL = Sh::WAVE_LANES, NW = Sh::NWAVES;
@@ -151,7 +149,6 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
     __shared__ float sh_dv[SUB][N];
 
     const int64_t bh = blockIdx.x;
-    if (only_flagged && only_flagged[bh] == 0) return;
     const int tid = threadIdx.x;
     const int row = tid / G, col0 = (tid % G) * C;
     const int wave = tid / 64, lane = tid % 64;
@@ -173,7 +170,7 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
             float sa_r[SUB];
 #pragma unroll
             for (int cc = 0; cc < C; ++cc)
-                St[0][cc] = ckpt[c * BH * NN + my + cc];
+                St[0][cc] = load_f(ckpt + c * BH * NN + my + cc);
             const int64_t ts = ta + s * SUB;
             // advance from the interval checkpoint to the sub-interval start
             for (int64_t t0 = ta; t0 < ts; t0 += SUB) {
@@ -274,10 +271,10 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
     for (int c = 0; c < C; ++c) ds0[my + c] = dS[c];
 }
 
-template <int N, typename VT>
-hipError_t launch_fwd_n(const SeqFwdArgs& p, hipStream_t stream) {
+template <int N, typename VT, typename CT>
+hipError_t launch_fwd_nc(const SeqFwdArgs& p, hipStream_t stream) {
     const int64_t BH = p.B * p.H;
-    hipLaunchKernelGGL((wkv7_seq_fwd_kernel<N, VT>), dim3(unsigned(BH)),
+    hipLaunchKernelGGL((wkv7_seq_fwd_kernel<N, VT, CT>), dim3(unsigned(BH)),
                        dim3(SeqShape<N>::THREADS), 0, stream, p.T, BH,
                        static_cast<const VT*>(p.r),
                        static_cast<const VT*>(p.w),
@@ -285,15 +282,21 @@ hipError_t launch_fwd_n(const SeqFwdArgs& p, hipStream_t stream) {
                        static_cast<const VT*>(p.v),
                        static_cast<const VT*>(p.a),
                        static_cast<const VT*>(p.b), p.s0,
-                       static_cast<VT*>(p.y), p.s_t, p.ckpt, p.ci,
-                       p.only_flagged);
+                       static_cast<VT*>(p.y), p.s_t,
+                       static_cast<CT*>(p.ckpt), p.ci);
     return hipGetLastError();
 }
 
 template <int N, typename VT>
-hipError_t launch_bwd_n(const SeqBwdArgs& p, hipStream_t stream) {
+hipError_t launch_fwd_n(const SeqFwdArgs& p, hipStream_t stream) {
+    return p.ckpt_bf16 ? launch_fwd_nc<N, VT, bf16_t>(p, stream)
+                       : launch_fwd_nc<N, VT, float>(p, stream);
+}
+
+template <int N, typename VT, typename CT>
+hipError_t launch_bwd_nc(const SeqBwdArgs& p, hipStream_t stream) {
     const int64_t BH = p.B * p.H;
-    hipLaunchKernelGGL((wkv7_seq_bwd_kernel<N, VT>), dim3(unsigned(BH)),
+    hipLaunchKernelGGL((wkv7_seq_bwd_kernel<N, VT, CT>), dim3(unsigned(BH)),
                        dim3(SeqShape<N>::THREADS), 0, stream, p.T, BH,
                        static_cast<const VT*>(p.r),
                        static_cast<const VT*>(p.w),
@@ -301,12 +304,19 @@ hipError_t launch_bwd_n(const SeqBwdArgs& p, hipStream_t stream) {
                        static_cast<const VT*>(p.v),
                        static_cast<const VT*>(p.a),
                        static_cast<const VT*>(p.b),
-                       static_cast<const VT*>(p.dy), p.ds_t, p.ckpt, p.ci,
+                       static_cast<const VT*>(p.dy), p.ds_t,
+                       static_cast<const CT*>(p.ckpt), p.ci,
                        static_cast<VT*>(p.dr), static_cast<VT*>(p.dw),
                        static_cast<VT*>(p.dk), static_cast<VT*>(p.dv),
                        static_cast<VT*>(p.da), static_cast<VT*>(p.db),
-                       p.ds0, p.only_flagged);
+                       p.ds0);
     return hipGetLastError();
+}
+
+template <int N, typename VT>
+hipError_t launch_bwd_n(const SeqBwdArgs& p, hipStream_t stream) {
+    return p.ckpt_bf16 ? launch_bwd_nc<N, VT, bf16_t>(p, stream)
+                       : launch_bwd_nc<N, VT, float>(p, stream);
 }
 
 template <typename VT>

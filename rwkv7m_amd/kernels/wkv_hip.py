@@ -6,10 +6,12 @@ reference's signatures and return conventions:
 
 * ``forward(r, w, k, v, neg_kk, kka, S0) -> (y, S_T)``
 * ``forward_with_aux(...) -> ((y, S_T), aux)`` with
-  ``aux = (checkpoints, interval)``: fp32 checkpoints
+  ``aux = (checkpoints, interval)``: checkpoints
   ``[ceil(T/ci)+1, B, H, N, N]`` (entry 0 = S0, entry c = state after token
-  ``c*ci - 1``, last = S_T; the format of wkv_pallas_gpu.py:83-120) and the
-  interval as a 0-d int64 CPU tensor.
+  ``c*ci - 1``, last = S_T; the layout of wkv_pallas_gpu.py:83-120) in the
+  library's checkpoint dtype (bf16 for bf16 vectors with N = 64 and an
+  interval of 16, 32 or 64, else fp32) and the interval as a 0-d int64 CPU
+  tensor.
 * ``backward(r, w, k, v, neg_kk, kka, S0, dy, dS_T, *aux)`` -> seven input
   cotangents in primal order and primal dtypes.
 
@@ -41,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "rwkv7m_last_error",
     "rwkv7m_wkv7_checkpoint_count",
     "rwkv7m_wkv7_default_checkpoint_interval",
+    "rwkv7m_wkv7_checkpoint_dtype",
     "rwkv7m_wkv7_forward",
     "rwkv7m_wkv7_forward_with_aux",
     "rwkv7m_wkv7_backward",
@@ -75,6 +78,8 @@ def load_library(path: str | None = None):
         lib.rwkv7m_wkv7_checkpoint_count.argtypes = [i64, i64]
         lib.rwkv7m_wkv7_default_checkpoint_interval.restype = i64
         lib.rwkv7m_wkv7_default_checkpoint_interval.argtypes = [i32, i64]
+        lib.rwkv7m_wkv7_checkpoint_dtype.restype = i32
+        lib.rwkv7m_wkv7_checkpoint_dtype.argtypes = [i32, i64, i64]
         lib.rwkv7m_wkv7_forward.restype = i32
         lib.rwkv7m_wkv7_forward.argtypes = [i32] + [i64] * 4 + [vp] * 10
         lib.rwkv7m_wkv7_forward_with_aux.restype = i32
@@ -142,6 +147,15 @@ def checkpoint_count(T: int, interval: int) -> int:
     return int(load_library().rwkv7m_wkv7_checkpoint_count(T, interval))
 
 
+def checkpoint_dtype(dtype: torch.dtype, head_size: int,
+                     interval: int) -> torch.dtype:
+    """Element type of the checkpoints for these vectors and interval."""
+    code = DTYPE_BF16 if dtype == torch.bfloat16 else DTYPE_F32
+    out = int(load_library().rwkv7m_wkv7_checkpoint_dtype(
+        code, head_size, interval))
+    return torch.bfloat16 if out == DTYPE_BF16 else torch.float32
+
+
 def forward(r, w, k, v, neg_kk, kka, initial_state, *, out_state=None):
     """y, S_T = WKV(...). ``out_state`` may be ``initial_state`` (in place)."""
     lib = load_library()
@@ -171,7 +185,8 @@ def forward_with_aux(r, w, k, v, neg_kk, kka, initial_state, *,
     nck = checkpoint_count(T, ci)
     y = torch.empty_like(r)
     s_t = torch.empty_like(s0)
-    ckpt = torch.empty((nck, B, H, N, N), dtype=torch.float32, device=dev)
+    ckpt = torch.empty((nck, B, H, N, N), device=dev,
+                       dtype=checkpoint_dtype(r.dtype, N, ci))
     with torch.cuda.device(dev):
         rc = lib.rwkv7m_wkv7_forward_with_aux(
             _dtype_code(r), T, B, H, N, _p(r), _p(w), _p(k), _p(v), _p(a),
@@ -190,7 +205,7 @@ def backward(r, w, k, v, neg_kk, kka, initial_state, dy, ds_t, checkpoints,
     T, B, H, N = r.shape
     ci = int(interval)
     if checkpoints.shape != (checkpoint_count(T, ci), B, H, N, N) or \
-            checkpoints.dtype != torch.float32:
+            checkpoints.dtype != checkpoint_dtype(r.dtype, N, ci):
         raise ValueError("checkpoints do not match time, shape and interval")
     ckpt = checkpoints.contiguous()
     dy_c = None if dy is None else dy.to(r.dtype).contiguous()
@@ -247,6 +262,7 @@ def register_hip_backend(*, replace: bool = False) -> WKVFFIBackend:
 
 __all__ = [
     "EXPORTED_SYMBOLS", "LIB_PATH", "backward", "checkpoint_count",
+    "checkpoint_dtype",
     "decode_inplace", "default_checkpoint_interval", "forward",
     "forward_with_aux", "hip_wkv_ffi_backend", "load_library",
     "register_hip_backend",

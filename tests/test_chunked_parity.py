@@ -53,9 +53,11 @@ def _run_case(hip, inp, ci, case, check_grads=True):
     assert y.dtype == torch.bfloat16 and s_t.dtype == torch.float32
     _check("y", y, ey, case)
     _check("s_t", s_t, es, case)
+    # bf16 checkpoints: S0 and S_T rounded to nearest even
+    assert aux[0].dtype == torch.bfloat16
     _check("checkpoints", aux[0], eck, case)
-    assert torch.equal(aux[0][0], dev["s0"])
-    assert torch.equal(aux[0][-1], s_t)
+    assert torch.equal(aux[0][0], dev["s0"].to(torch.bfloat16))
+    assert torch.equal(aux[0][-1], s_t.to(torch.bfloat16))
     if check_grads:
         egr = oracle.backward(*host, _np(inp["s0"]), _np(inp["dy"]),
                               _np(inp["ds_t"]), threads=THREADS)
@@ -164,3 +166,64 @@ def test_chunked_results_are_deterministic(hip, ci):
             for name, a_, b_ in zip(("y", "s_t", "ckpt") + GRAD_NAMES, first,
                                     outs):
                 assert torch.equal(a_, b_), f"{case}: {name} differs"
+
+
+def _misaligned(t):
+    """A copy of t whose data starts 2 bytes past a 16-byte boundary."""
+    flat = torch.empty(t.numel() + 8, dtype=t.dtype, device=t.device)
+    out = flat[1:1 + t.numel()].view(t.shape)
+    out.copy_(t)
+    return out
+
+
+def test_sequential_kernels_share_the_bf16_checkpoint_format(hip):
+    # Misaligned vectors take the sequential kernels, which then write and
+    # read the same bf16 checkpoints as the chunked ones.
+    case = "misaligned T70 B1 H2 N64 L32"
+    print("case:", case, flush=True)
+    inp = make_inputs(70, 1, 2, 64, seed=31, state_std=0.1, dstate_std=0.1)
+    dev = {k: v.cuda() for k, v in inp.items()}
+    vecs = [_misaligned(dev[n]) for n in NAMES]
+    (y, s_t), aux = hip.forward_with_aux(*vecs, dev["s0"],
+                                         checkpoint_interval=32)
+    grads = hip.backward(*vecs, dev["s0"], _misaligned(dev["dy"]),
+                         dev["ds_t"], *aux)
+    # the aligned (chunked) forward feeding the misaligned backward, and
+    # the misaligned forward feeding the chunked backward
+    (y2, _), aux2 = hip.forward_with_aux(*[dev[n] for n in NAMES], dev["s0"],
+                                         checkpoint_interval=32)
+    grads2 = hip.backward(*[dev[n] for n in NAMES], dev["s0"], dev["dy"],
+                          dev["ds_t"], *aux)
+    grads3 = hip.backward(*vecs, dev["s0"], _misaligned(dev["dy"]),
+                          dev["ds_t"], *aux2)
+    torch.cuda.synchronize()
+    assert aux[0].dtype == torch.bfloat16
+    assert torch.equal(aux[0][0], dev["s0"].to(torch.bfloat16))
+    assert torch.equal(aux[0][-1], s_t.to(torch.bfloat16))
+    host = [_np(inp[n]) for n in NAMES]
+    ey, es, eck = oracle.forward(*host, _np(inp["s0"]),
+                                 checkpoint_interval=32, threads=THREADS)
+    egr = oracle.backward(*host, _np(inp["s0"]), _np(inp["dy"]),
+                          _np(inp["ds_t"]), threads=THREADS)
+    _check("y", y, ey, case)
+    _check("s_t", s_t, es, case)
+    _check("checkpoints", aux[0], eck, case)
+    _check("checkpoints(chunked)", aux2[0], eck, case)
+    for gs, tag in ((grads, ""), (grads2, " chunked bwd"),
+                    (grads3, " seq bwd of chunked fwd")):
+        for name, g, e in zip(GRAD_NAMES, gs, egr):
+            _check(name, g, e, case + tag)
+
+
+def test_empty_time_axis_bf16_checkpoints(hip):
+    print("case: T=0 B2 H2 N64 bf16", flush=True)
+    inp = make_inputs(0, 2, 2, 64, seed=8, state_std=0.1, dstate_std=0.1)
+    dev = {k: v.cuda() for k, v in inp.items()}
+    vecs = [dev[n] for n in NAMES]
+    (y, s_t), aux = hip.forward_with_aux(*vecs, dev["s0"])
+    grads = hip.backward(*vecs, dev["s0"], dev["dy"], dev["ds_t"], *aux)
+    torch.cuda.synchronize()
+    assert aux[0].shape == (1, 2, 2, 64, 64)
+    assert torch.equal(aux[0][0], dev["s0"].to(torch.bfloat16))
+    assert torch.equal(s_t, dev["s0"])
+    assert torch.equal(grads[-1], dev["ds_t"])

@@ -24,8 +24,10 @@
 //
 // Every product is a bf16 MFMA (v_mfma_f32_16x16x32_bf16) with fp32
 // accumulation; the state stays fp32 in MFMA accumulator registers for the
-// whole sequence.  The unit lower-triangular inverse is built from 16x16
-// diagonal blocks (fp32 forward substitution) merged with MFMA.  A chunk
+// whole sequence (the checkpoints the backward reads are its bf16 roundings,
+// one per chunk).  The unit lower-triangular inverse is built from 16x16
+// diagonal blocks, each the product (I+A)(I+A^2)(I+A^4)(I+A^8) of the
+// nilpotent strictly lower block A, merged with MFMA.  A chunk
 // whose decay range exceeds what the factored form represents (more than
 // kHalfRange of log-decay on either side of g_ref: far outside the model's
 // clamped range) is run by an exact fp32 sequential loop instead.

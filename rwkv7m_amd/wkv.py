@@ -132,31 +132,42 @@ def _wkv7_backward_dispatch(inputs, cotangents, aux, *, backend, interpret):
 
 
 class _WKV7(torch.autograd.Function):
-    """Custom VJP of wkv7 (the jax.custom_vjp of wkv.py:219-286)."""
+    """Custom VJP of wkv7 (the jax.custom_vjp of wkv.py:219-286).
+
+    Every call goes through ``apply`` so that forward-mode transforms reach
+    ``jvp`` and fail there, as jax.jvp fails on the reference's custom_vjp.
+    ``with_aux`` is decided by the caller: the backward residuals (the
+    backend's aux, e.g. state checkpoints) are only produced when a
+    gradient can be requested.
+    """
 
     @staticmethod
-    def forward(ctx, r, w, k, v, neg_kk, kka, initial_state, backend,
-                interpret):
+    def forward(r, w, k, v, neg_kk, kka, initial_state, backend, interpret,
+                with_aux):
         inputs = (r, w, k, v, neg_kk, kka, initial_state)
+        if not with_aux:
+            y, final_state = _wkv7_forward_dispatch(
+                *inputs, backend=backend, interpret=interpret,
+                with_aux=False)
+            return y, final_state, ()
         (y, final_state), aux = _wkv7_forward_dispatch(
             *inputs, backend=backend, interpret=interpret, with_aux=True)
-        aux = tuple(aux)
-        tensor_aux = [a for a in aux if isinstance(a, torch.Tensor)]
-        ctx.save_for_backward(*inputs, *tensor_aux)
-        ctx.aux_layout = [isinstance(a, torch.Tensor) for a in aux]
-        ctx.aux_other = [a for a in aux if not isinstance(a, torch.Tensor)]
-        ctx.backend = backend
-        ctx.interpret = interpret
-        return y, final_state
+        return y, final_state, tuple(aux)
 
     @staticmethod
-    def backward(ctx, dy, ds_t):
-        saved = ctx.saved_tensors
-        inputs = saved[:7]
-        tensor_aux = iter(saved[7:])
-        other = iter(ctx.aux_other)
-        aux = tuple(next(tensor_aux) if is_t else next(other)
-                    for is_t in ctx.aux_layout)
+    def setup_context(ctx, inputs, output):
+        *primal, backend, interpret, _ = inputs
+        aux = output[2]
+        ctx.save_for_backward(*primal)
+        ctx.aux = aux
+        ctx.backend = backend
+        ctx.interpret = interpret
+
+    @staticmethod
+    def backward(ctx, dy, ds_t, _aux_grad=None):
+        inputs = ctx.saved_tensors
+        aux = ctx.aux
+        ctx.aux = None
         r, s0 = inputs[0], inputs[6]
         if dy is None:
             dy = torch.zeros_like(r)
@@ -165,7 +176,7 @@ class _WKV7(torch.autograd.Function):
         grads = _wkv7_backward_dispatch(
             inputs, (dy.to(r.dtype), ds_t.to(torch.float32)), aux,
             backend=ctx.backend, interpret=ctx.interpret)
-        return (*grads, None, None)
+        return (*grads, None, None, None)
 
     @staticmethod
     def jvp(ctx, *tangents):
@@ -185,10 +196,10 @@ def wkv7(r, w, k, v, neg_kk, kka, initial_state, backend: str | None = None,
     """
     _validate_wkv_inputs(r, w, k, v, neg_kk, kka, initial_state)
     inputs = (r, w, k, v, neg_kk, kka, initial_state)
-    if torch.is_grad_enabled() and any(x.requires_grad for x in inputs):
-        return _WKV7.apply(*inputs, backend, interpret)
-    return _wkv7_forward_dispatch(*inputs, backend=backend,
-                                  interpret=interpret, with_aux=False)
+    with_aux = torch.is_grad_enabled() and any(x.requires_grad
+                                               for x in inputs)
+    y, final_state, _ = _WKV7.apply(*inputs, backend, interpret, with_aux)
+    return y, final_state
 
 
 __all__ = ["wkv7", "wkv7_reference"]

@@ -227,3 +227,37 @@ def test_empty_time_axis_bf16_checkpoints(hip):
     assert torch.equal(aux[0][0], dev["s0"].to(torch.bfloat16))
     assert torch.equal(s_t, dev["s0"])
     assert torch.equal(grads[-1], dev["ds_t"])
+
+
+def test_operator_api_through_registered_hip_backend(hip):
+    # wkv7(..., "ffi") with the HIP kernels registered: the custom VJP's
+    # residuals are the library's bf16 checkpoints (reference
+    # tests/test_wkv_pallas.py:151-198 with the native backend)
+    from rwkv7m_amd.kernels.wkv_ffi import unregister_wkv_ffi_backend
+    from rwkv7m_amd.wkv import wkv7
+    case = "wkv7 ffi T70 B2 H2 N64"
+    print("case:", case, flush=True)
+    inp = make_inputs(70, 2, 2, 64, seed=41, state_std=0.1, dstate_std=0.1)
+    dev = {k: v.cuda() for k, v in inp.items()}
+    unregister_wkv_ffi_backend()
+    hip.register_hip_backend()
+    try:
+        xs = [dev[n].clone().requires_grad_(True) for n in (*NAMES, "s0")]
+        y, s_t = wkv7(*xs, "ffi")
+        grads = torch.autograd.grad((y, s_t), xs,
+                                    grad_outputs=(dev["dy"], dev["ds_t"]))
+        with torch.no_grad():
+            y2, s_t2 = wkv7(*[dev[n] for n in (*NAMES, "s0")], "ffi")
+        torch.cuda.synchronize()
+    finally:
+        unregister_wkv_ffi_backend()
+    host = [_np(inp[n]) for n in NAMES]
+    ey, es = oracle.forward(*host, _np(inp["s0"]), threads=THREADS)
+    egr = oracle.backward(*host, _np(inp["s0"]), _np(inp["dy"]),
+                          _np(inp["ds_t"]), threads=THREADS)
+    for name, got in (("y", y), ("s_t", s_t), ("y(no grad)", y2),
+                      ("s_t(no grad)", s_t2)):
+        _check(name, got, ey if name.startswith("y") else es, case)
+    for name, g, e in zip(GRAD_NAMES, grads, egr):
+        assert g.dtype == (torch.float32 if name == "ds0" else torch.bfloat16)
+        _check(name, g, e, case)

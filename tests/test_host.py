@@ -1,0 +1,251 @@
+"""Host-side logic on the CPU: the operator API, backend policy, FFI registry,
+the C-ABI library's exports and argument checks, and the oracle against the
+committed golden fixtures.
+
+Mirrors the reference's tests/test_wkv_api.py and the registry/policy tests
+of tests/test_wkv_pallas.py:113-198 with torch in place of JAX.  Nothing here
+launches GPU work.
+"""
+
+import glob
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from rwkv7m_amd.kernels.wkv_backend import resolve_wkv_backend
+from rwkv7m_amd.kernels.wkv_ffi import (WKVFFIBackend,
+                                        register_wkv_ffi_backend,
+                                        unregister_wkv_ffi_backend)
+from rwkv7m_amd.wkv import wkv7, wkv7_reference
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
+NAMES = ("r", "w", "k", "v", "neg_kk", "kka")
+GRAD_NAMES = ("dr", "dw", "dk", "dv", "dneg_kk", "dkka", "ds0")
+
+
+def _inputs(dtype=torch.float32, time=3, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    vecs = tuple((torch.randn(time, 1, 2, 4, generator=g) * 0.1).to(dtype)
+                 for _ in range(6))
+    state = torch.randn(1, 2, 4, 4, generator=g) * 0.1
+    return (*vecs, state)
+
+
+def _np(t):
+    return t.detach().float().numpy().astype(np.float64)
+
+
+# ---------------------------------------------------------------------------
+# Operator API (reference tests/test_wkv_api.py)
+# ---------------------------------------------------------------------------
+
+def test_wkv7_reference_matches_oracle_and_dtype_contract():
+    inputs = _inputs(torch.bfloat16)
+    y, s_t = wkv7_reference(*inputs)
+    assert y.dtype == torch.bfloat16 and s_t.dtype == torch.float32
+    ey, es = oracle.forward(*(_np(x) for x in inputs))
+    np.testing.assert_allclose(_np(s_t), es, rtol=1e-5, atol=1e-6)
+    # y is rounded to bf16 once, after the fp32 scan
+    np.testing.assert_array_equal(
+        _np(y), _np(torch.from_numpy(ey).to(torch.bfloat16)))
+
+
+def test_wkv7_custom_vjp_matches_oracle_gradients():
+    inputs = [x.clone().requires_grad_(True) for x in _inputs()]
+    y, s_t = wkv7(*inputs)
+    loss = (y.square().sum() + 0.01 * s_t.square().sum())
+    grads = torch.autograd.grad(loss, inputs)
+    dy = 2 * _np(y)
+    ds_t = 0.02 * _np(s_t)
+    expected = oracle.backward(*(_np(x) for x in inputs), dy, ds_t)
+    for name, g, e in zip(GRAD_NAMES, grads, expected):
+        np.testing.assert_allclose(_np(g), e, rtol=1e-5, atol=1e-6,
+                                   err_msg=name)
+
+
+def test_wkv7_rejects_invalid_shapes_and_dtypes():
+    *vecs, s0 = _inputs()
+    with pytest.raises(TypeError, match="initial_state must be float32"):
+        wkv7_reference(*vecs, s0.to(torch.bfloat16))
+    with pytest.raises(ValueError, match="k must have shape"):
+        wkv7_reference(vecs[0], vecs[1], vecs[2][:, :, :, :-1], *vecs[3:],
+                       s0)
+    with pytest.raises(TypeError, match="bfloat16 or float32"):
+        wkv7_reference(*(x.to(torch.float16) for x in vecs), s0)
+
+
+def test_wkv7_documents_reverse_mode_only_contract():
+    inputs = [x.clone().requires_grad_(True) for x in _inputs()]
+    tangents = tuple(torch.ones_like(x) for x in inputs)
+    with pytest.raises(TypeError, match="forward-mode autodiff"):
+        torch.func.jvp(lambda *xs: wkv7(*xs), tuple(inputs), tangents)
+
+
+# ---------------------------------------------------------------------------
+# Backend policy and FFI registry (reference tests/test_wkv_pallas.py:113-198)
+# ---------------------------------------------------------------------------
+
+def test_auto_backend_is_pallas_first_and_never_selects_ffi(monkeypatch):
+    monkeypatch.delenv("RWKV7M_WKV_BACKEND", raising=False)
+    assert resolve_wkv_backend(platform="cpu") == "reference"
+    assert resolve_wkv_backend(platform="tpu") == "pallas_tpu"
+    assert resolve_wkv_backend(platform="gpu",
+                               device_kind="NVIDIA L40S") == \
+        "pallas_gpu_triton"
+    assert resolve_wkv_backend(platform="gpu",
+                               device_kind="NVIDIA H100 80GB HBM3") == \
+        "pallas_gpu_mosaic"
+
+
+def test_backend_environment_override_is_validated(monkeypatch):
+    monkeypatch.setenv("RWKV7M_WKV_BACKEND", "ffi")
+    assert resolve_wkv_backend(platform="cpu") == "ffi"
+    monkeypatch.setenv("RWKV7M_WKV_BACKEND", "not-a-backend")
+    with pytest.raises(ValueError, match="unknown WKV backend"):
+        resolve_wkv_backend(platform="cpu")
+
+
+def test_ffi_requires_explicit_registration():
+    unregister_wkv_ffi_backend()
+    with pytest.raises(RuntimeError, match="no FFI backend is registered"):
+        wkv7(*_inputs(), "ffi")
+
+
+def test_registered_ffi_satisfies_forward_and_backward_contract():
+    calls = []
+
+    def forward(*values):
+        calls.append("forward")
+        return wkv7_reference(*values)
+
+    def forward_with_aux(*values):
+        calls.append("forward_with_aux")
+        return wkv7_reference(*values), (torch.tensor(7),)
+
+    def backward(*values):
+        calls.append("backward")
+        primal, cot, aux = values[:7], values[7:9], values[9:]
+        assert len(aux) == 1 and int(aux[0]) == 7
+        with torch.enable_grad():
+            xs = [x.detach().requires_grad_(True) for x in primal]
+            outs = wkv7_reference(*xs)
+            return torch.autograd.grad(outs, xs, grad_outputs=cot)
+
+    backend = WKVFFIBackend(forward=forward,
+                            forward_with_aux=forward_with_aux,
+                            backward=backward)
+    unregister_wkv_ffi_backend()
+    register_wkv_ffi_backend(backend)
+    try:
+        with pytest.raises(RuntimeError, match="already registered"):
+            register_wkv_ffi_backend(backend)
+        register_wkv_ffi_backend(backend, replace=True)
+        inputs = _inputs()
+        with torch.no_grad():
+            actual = wkv7(*inputs, "ffi")
+        expected = wkv7_reference(*inputs)
+        assert all(torch.equal(a, e) for a, e in zip(actual, expected))
+        assert calls == ["forward"]
+
+        xs = [x.clone().requires_grad_(True) for x in inputs]
+        got = torch.autograd.grad(wkv7(*xs, "ffi")[0].sum(), xs)
+        ys = [x.clone().requires_grad_(True) for x in inputs]
+        want = torch.autograd.grad(wkv7_reference(*ys)[0].sum(), ys)
+        assert all(torch.allclose(a, b) for a, b in zip(got, want))
+        assert calls[1:] == ["forward_with_aux", "backward"]
+    finally:
+        unregister_wkv_ffi_backend()
+
+
+# ---------------------------------------------------------------------------
+# C ABI: the library loads on a host without a GPU and exports the header
+# ---------------------------------------------------------------------------
+
+def _declared_functions():
+    names = set()
+    for path in HEADERS:
+        text = open(path).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names.update(re.findall(r"\b(rwkv7m_\w+)\s*\(", text))
+    return names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from rwkv7m_amd import _build
+    from rwkv7m_amd.kernels import wkv_hip
+    if not os.path.exists(wkv_hip.LIB_PATH):
+        _build.build()
+    return wkv_hip.load_library()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from rwkv7m_amd.kernels import wkv_hip
+    declared = _declared_functions()
+    assert declared, "no declarations found in include/*.h"
+    assert declared == set(wkv_hip.EXPORTED_SYMBOLS)
+    for name in sorted(declared):
+        assert hasattr(lib, name), name
+    assert lib.rwkv7m_abi_version() == 1
+
+
+def test_library_host_queries(lib):
+    assert lib.rwkv7m_wkv7_checkpoint_count(0, 16) == 1
+    assert lib.rwkv7m_wkv7_checkpoint_count(5, 2) == 4
+    assert lib.rwkv7m_wkv7_checkpoint_count(4096, 32) == 129
+    assert lib.rwkv7m_wkv7_checkpoint_count(-1, 16) == -1
+    assert lib.rwkv7m_wkv7_checkpoint_count(5, 0) == -1
+    assert lib.rwkv7m_wkv7_default_checkpoint_interval(1, 64) == 32
+    assert lib.rwkv7m_wkv7_default_checkpoint_interval(0, 64) == 16
+    # bf16 checkpoints exactly for the MFMA-served intervals
+    for ci in (0, 16, 32, 64):
+        assert lib.rwkv7m_wkv7_checkpoint_dtype(1, 64, ci) == 1
+    for dtype, n, ci in ((1, 64, 8), (1, 64, 128), (1, 32, 16),
+                         (0, 64, 32), (0, 16, 0)):
+        assert lib.rwkv7m_wkv7_checkpoint_dtype(dtype, n, ci) == 0
+
+
+def test_library_rejects_bad_requests_before_any_device_call(lib):
+    null = [None] * 10
+    assert lib.rwkv7m_wkv7_forward(5, 1, 1, 1, 4, *null) == 1
+    assert b"bfloat16 or float32" in lib.rwkv7m_last_error()
+    assert lib.rwkv7m_wkv7_forward(0, 1, 1, 1, 48, *null) == 2
+    assert lib.rwkv7m_wkv7_forward(0, 2, 1, 1, 4, *null) == 1
+    assert b"is NULL" in lib.rwkv7m_last_error()
+    assert lib.rwkv7m_wkv7_forward_with_aux(
+        0, 2, 1, 1, 4, *null, -1, None) == 1
+    assert b"checkpoint_interval" in lib.rwkv7m_last_error()
+
+
+# ---------------------------------------------------------------------------
+# Oracle against the committed golden fixtures
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN,
+                                                               "*.npz"))),
+                         ids=os.path.basename)
+def test_oracle_reproduces_golden_fixture(path):
+    data = np.load(path)
+    bf16 = bool(data["is_bf16"])
+
+    def vec(name):
+        x = data[name]
+        return (oracle.bf16_from_bits(x) if bf16 else x).astype(np.float64)
+
+    vecs = [vec(n) for n in NAMES]
+    s0 = data["s0"].astype(np.float64)
+    y, s_t = oracle.forward(*vecs, s0)
+    np.testing.assert_allclose(y, data["y"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(s_t, data["s_t"], rtol=1e-5, atol=1e-6)
+    if "dr" in data:
+        grads = oracle.backward(*vecs, s0, vec("dy"),
+                                data["ds_t"].astype(np.float64))
+        for name, g in zip(GRAD_NAMES, grads):
+            np.testing.assert_allclose(g, data[name], rtol=1e-5, atol=1e-6,
+                                       err_msg=name)

@@ -92,9 +92,8 @@ int rwkv7m_wkv7_forward(int dtype, int64_t T, int64_t B, int64_t H, int64_t N,
  * needs.  Replaces WKVFFIBackend.forward_with_aux (wkv_ffi.py:33; called at
  * wkv.py:174) and the reference's fwd+aux kernel (wkv_pallas_gpu.py:66-120,
  * :303-375).  checkpoint_interval = 0 selects the library default; the
- * MFMA path serves bf16, N = 64 and an interval of 16, 32 or 64 (the
- * backward's MFMA path 16 or 32); other intervals run the sequential
- * kernels.
+ * MFMA path serves bf16, N = 64 and an interval of 16 or 32; other
+ * intervals run the sequential kernels.
  * checkpoints: [rwkv7m_wkv7_checkpoint_count(T, ci)][B][H][N][N] of
  * rwkv7m_wkv7_checkpoint_dtype(dtype, N, ci).
  */

@@ -104,7 +104,7 @@ int hip_status(const char* what, hipError_t e) {
 
 // Chunk length of the MFMA forward without checkpoints, and the default
 // checkpoint interval (= chunk length of the MFMA forward and backward).
-constexpr int64_t kDefaultChunk = 64;
+constexpr int64_t kDefaultChunk = 32;
 constexpr int64_t kDefaultTrainChunk = 32;
 
 int64_t default_interval(int dtype, int64_t N) {
@@ -112,8 +112,8 @@ int64_t default_interval(int dtype, int64_t N) {
     return 16;
 }
 
-// Checkpoints are bf16 exactly when the MFMA kernels can serve the interval
-// (they read checkpoints only as bf16 MFMA operands); the sequential kernels
+// Checkpoints are bf16 for the intervals of the bf16 N = 64 training path
+// (the MFMA kernels read them only as bf16 operands); the sequential kernels
 // read and write either type, so the choice does not depend on alignment.
 bool ckpt_bf16(int dtype, int64_t N, int64_t ci) {
     return dtype == RWKV7M_DTYPE_BF16 && N == 64 &&
@@ -125,11 +125,11 @@ bool aligned16(const void* p) {
 }
 
 // The chunked MFMA kernels serve bf16 vectors with N = 64, a chunk length
-// (= checkpoint interval) of 16, 32 or 64, and 16-byte aligned buffers.
+// (= checkpoint interval) of 16 or 32, and 16-byte aligned buffers.
 bool use_chunked(int dtype, int64_t N, int64_t ci,
                  std::initializer_list<const void*> ptrs) {
     if (dtype != RWKV7M_DTYPE_BF16 || N != 64) return false;
-    if (ci != 16 && ci != 32 && ci != 64) return false;
+    if (ci != 16 && ci != 32) return false;
     for (const void* p : ptrs)
         if (p && !aligned16(p)) return false;
     return true;
@@ -290,8 +290,7 @@ int rwkv7m_wkv7_backward(int dtype, int64_t T, int64_t B, int64_t H,
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (d.state_elems == 0) return RWKV7M_OK;
     if (T == 0) return copy_or_clear(ds0, ds_t, d.state_elems, s);
-    if ((ci == 16 || ci == 32) &&
-        use_chunked(dtype, N, ci,
+    if (use_chunked(dtype, N, ci,
                     {r, w, k, v, neg_kk, kka, dy, ds_t, checkpoints, dr, dw,
                      dk, dv, dneg_kk, dkka, ds0})) {
         rwkv7m::ChunkBwdArgs c{};

@@ -1,7 +1,7 @@
 // Chunked WKV-7 forward for gfx950: bf16 vectors, fp32 state, N = 64.
 //
 // One workgroup (8 waves) per (batch, head) walks the sequence in chunks of
-// L tokens (L = 16, 32 or 64).  Within a chunk the recurrence
+// L tokens (L = 16 or 32).  Within a chunk the recurrence
 // (reference src/rwkv7m/model/rwkv_core.py:54-86)
 //
 //   S_t = S_{t-1} diag(d_t) + (S_{t-1} a_t) b_t^T + v_t k_t^T,  y_t = S_t r_t
@@ -12,25 +12,38 @@
 //
 //   A~_t = a_t e^{g_{t-1}-g_ref}   R~_t = r_t e^{g_t-g_ref}
 //   B~_s = b_s e^{g_ref-g_s}       K~_s = k_s e^{g_ref-g_s}
-//   B^_s = b_s e^{g_L-g_s}         K^_s = k_s e^{g_L-g_s}
+//   B^ = B~ diag(e^{g_L-g_ref})    K^ = K~ diag(e^{g_L-g_ref})
 //
 // and the L x L matrices Aab = A~ B~^T, Aak = A~ K~^T (strictly lower),
-// Arb = R~ B~^T, Ark = R~ K~^T (lower, with diagonal).  Writing S' for the
-// chunk-start state with columns scaled by e^{g_ref}:
+// Arb = R~ B~^T, Ark = R~ K~^T (lower, with diagonal).  With S' the chunk-
+// start state with columns scaled by e^{g_ref}, Minv = (I - Aab)^{-1},
+// W = Minv A~ and U = Minv Aak V, the rows X_t = S_{t-1} a_t are
+// X = W S'^T + U, and
 //
-//   X   = (I - Aab)^{-1} (A~ S'^T + Aak V)      (X_t = S_{t-1} a_t = "sa")
-//   Y   = R~ S'^T + Arb X + Ark V
-//   S_L = S_0 diag(e^{g_L}) + X^T B^ + V^T K^
+//   Y   = Q S'^T + P                      Q = R~ + Arb W,  P = Arb U + Ark V
+//   S_L = S_0 diag(e^{g_L}) + S' M + C    M = W^T B^,      C = U^T B^ + V^T K^
+//
+// Everything but the two products with S' depends on the chunk's inputs
+// alone, so the state chain from one chunk to the next is one 64x64x64
+// product: the workgroup builds chunk c+1's Q, P, M and C while it advances
+// the state through chunk c.  Five barrier-separated phases per chunk:
+//
+//   F  c+1: factors (in-wave scan of the log-decay)  c: S' -> LDS, S e^{g_L} + C
+//   M  c+1: matrices; wave 0 starts the inverse      c: S += S' M, Y = Q S'^T + P
+//   I  c+1: wave 0 finishes Minv; Aak V; C += V^T K^; P += Ark V; next vectors
+//   W  c+1: W = Minv A~, U = Minv (Aak V)
+//   Q  c+1: Q, M; C += U^T B^; P += Arb U
 //
 // Every product is a bf16 MFMA (v_mfma_f32_16x16x32_bf16) with fp32
-// accumulation; the state stays fp32 in MFMA accumulator registers for the
-// whole sequence (the checkpoints the backward reads are its bf16 roundings,
-// one per chunk).  The unit lower-triangular inverse is built from 16x16
-// diagonal blocks, each the product (I+A)(I+A^2)(I+A^4)(I+A^8) of the
-// nilpotent strictly lower block A, merged with MFMA.  A chunk
-// whose decay range exceeds what the factored form represents (more than
-// kHalfRange of log-decay on either side of g_ref: far outside the model's
-// clamped range) is run by an exact fp32 sequential loop instead.
+// accumulation.  Operands stored with the contraction index strided are read
+// with gfx950's transposing LDS load, so no transposed copies are made.  The
+// state S, C and P stay fp32 in accumulator registers; B^ and K^ enter only
+// as the column scaling e^{g_L-g_ref} of M and C.  The 16x16 diagonal
+// blocks of Minv are the product (I+A)(I+A^2)(I+A^4)(I+A^8) of the nilpotent
+// strictly lower block A.  A chunk whose decay range exceeds what the
+// factored form represents (more than kHalfRange of log-decay on either side
+// of g_ref: far outside the model's clamped range) runs an exact fp32
+// sequential loop instead.
 
 #include "wkv7_chunk_common.h"
 #include "wkv7_launch.h"
@@ -42,43 +55,113 @@ using chunk::CN;
 using chunk::kHalfRange;
 using chunk::PN;
 
-// Waves per workgroup: 8 waves keep every value in registers (up to 256
-// VGPRs per wave); a register spill would cost far more than the fewer waves,
-// because a scratch reload waits for every HBM load and store the wave has in
-// flight (one shared counter).
 constexpr int FWD_WAVES = 8;
+constexpr int FWD_THREADS = FWD_WAVES * 64;
 
 template <int L>
 struct FwdSmem {
     static constexpr int PL = L + 8;
     static constexpr int NB = L / 16;
-    // factors, token-major [t][j]; Ybuf aliases A once A and R are dead
-    bf16_t A[L][PN], R[L][PN], Bt[L][PN], Kt[L][PN];
-    // factors and values, feature-major [j][t]
-    bf16_t Bh[CN][PL], Kh[CN][PL], Vt[CN][PL];
-    // chunk-start state (columns scaled by e^{g_ref}), [i][j]
-    bf16_t S[CN][PN];
+    // the next chunk's vectors: r, w, k, v, neg_kk, kka ([t][j])
+    bf16_t raw[6][L][PN];
     union {
-        bf16_t raw[6][L][CN];  // r, w, k, v, neg_kk, kka of the chunk
         struct {
-            bf16_t Aak[L][PL], Arb[L][PL], Ark[L][PL];
-            bf16_t Minv[L][PL], Aab[L][PL];
-            bf16_t AabTD[NB][16][24];
-            bf16_t MinvT[L][PL];
-            struct {
-                bf16_t U[CN][PL];
-                bf16_t X[CN][PL];
-            } ux;
-            bf16_t Z[4][16][24];
-        } m;
+            // factors of the chunk being prepared, token-major [t][j]
+            bf16_t At[L][PN], Rt[L][PN], Bt[L][PN], Kt[L][PN], Vc[L][PN];
+            // S' of the chunk being advanced, [i][j]
+            bf16_t Sp[CN][PN];
+        } f;
+        float fb[CN][CN + 1];  // exact fallback: the state in fp32
     };
-    float tot[FWD_WAVES][CN];
-    float eL[CN], eRef[CN];
-    int flag;
+    // L x L matrices, stored transposed: X[s][t] holds entry (t, s)
+    bf16_t Aab[L][PL], Aak[L][PL], Arb[L][PL], Ark[L][PL], MinvT[L][PL];
+    bf16_t ms[NB][4][16][24];  // inverse scratch (16x16, transposed)
+    bf16_t AakV[CN][PL];       // [i][s]
+    bf16_t Wt[CN][PL];         // [j][t] = W[t][j]
+    bf16_t Ut[CN][PL];         // [i][t] = U[t][i]
+    // the next chunk's inputs to the state step, double-buffered
+    bf16_t Q[2][L][PN];    // [t][j]
+    bf16_t Mt[2][CN][PN];  // [j][j'] = M[j'][j]
+    // e^{g_L}, e^{g_ref}, e^{g_L - g_ref} per column
+    float eL[2][CN], eRef[2][CN], eLR[2][CN];
+    int flag[2];
 };
 
+// Fragments of a contraction over K = 16 or 32 tokens.
+template <int K>
+__device__ __forceinline__ bf16x8_t fkr(const bf16_t* M, int ld, int lane) {
+    if constexpr (K == 16) return frag_kr16(M, ld, lane);
+    else return frag_kr(M, ld, lane);
+}
+template <int K>
+__device__ __forceinline__ bf16x8_t frk(const bf16_t* M, int ld, int lane) {
+    if constexpr (K == 16) return frag_rk16(M, ld, lane);
+    else return frag_rk(M, ld, lane);
+}
+
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+
+// Inclusive prefix sum over groups of L consecutive lanes (L = 16 or 32).
 template <int L>
-__global__ void __launch_bounds__(FWD_WAVES * 64)
+__device__ __forceinline__ float scan_lanes(float x) {
+#define RWKV7M_SHR(n)                                                       \
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), \
+                                                    0x110 + (n), 0xF, 0xF, \
+                                                    true))
+    RWKV7M_SHR(1);
+    RWKV7M_SHR(2);
+    RWKV7M_SHR(4);
+    RWKV7M_SHR(8);
+#undef RWKV7M_SHR
+    if constexpr (L == 32) {
+        // row_bcast:15 into rows 1 and 3 (from lane 15 of rows 0 and 2)
+        x += __int_as_float(__builtin_amdgcn_update_dpp(
+            0, __float_as_int(x), 0x142, 0xA, 0xF, false));
+    }
+    return x;
+}
+
+// Exact fp32 sequential forward over one chunk, reading the vectors from
+// HBM (the path for chunks outside the factored form's range).  S is the
+// state in LDS ([64][65]); thread: row i = tid / NW, CPT columns.
+template <int NW>
+__device__ void seq_chunk_forward(float (*S)[CN + 1], int n, int64_t t0,
+                                  int64_t BH, int64_t bh,
+                                  const chunk::VecPtrs& src,
+                                  bf16_t* __restrict__ y, int tid) {
+    constexpr int CPT = CN / NW;
+    const int i = tid / NW, c0 = CPT * (tid % NW);
+    float Sl[CPT];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) Sl[c] = S[i][c0 + c];
+    for (int t = 0; t < n; ++t) {
+        const int64_t off = ((t0 + t) * BH + bh) * CN;
+        float sa = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c)
+            sa += Sl[c] * bf16_to_f32(src.p4[off + c0 + c]);
+        sa = group_sum<NW>(sa);
+        const float vi = bf16_to_f32(src.p3[off + i]);
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int j = c0 + c;
+            const float d = expf(-expf(bf16_to_f32(src.p1[off + j])));
+            Sl[c] = Sl[c] * d + sa * bf16_to_f32(src.p5[off + j]) +
+                    vi * bf16_to_f32(src.p2[off + j]);
+            acc += Sl[c] * bf16_to_f32(src.p0[off + j]);
+        }
+        acc = group_sum<NW>(acc);
+        if (tid % NW == 0) y[off + i] = to_bf16(acc);
+    }
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) S[i][c0 + c] = Sl[c];
+}
+
+template <int L>
+__global__ void __launch_bounds__(FWD_THREADS)
 wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                       const bf16_t* __restrict__ w,
                       const bf16_t* __restrict__ k,
@@ -87,394 +170,493 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                       const bf16_t* __restrict__ b, const float* s0,
                       bf16_t* __restrict__ y, float* s_t, bf16_t* ckpt) {
     using Sm = FwdSmem<L>;
-    constexpr int NW = FWD_WAVES, NTH = NW * 64;
-    constexpr int PL = Sm::PL, NB = Sm::NB, TPG = L / NW;
-    constexpr int ST = 16 / NW;  // state tiles per wave
-    static_assert(L % NW == 0 && 16 % NW == 0, "wave layout");
+    constexpr int NW = FWD_WAVES, NTH = FWD_THREADS;
+    constexpr int PL = Sm::PL, NB = Sm::NB;
+    constexpr int CPL = L / 8;   // factor columns per lane
+    static_assert(L == 16 || L == 32, "chunk length");
     __shared__ Sm sm;
 
     const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
     const int lr = lane & 15, lq = lane >> 4;
     const int64_t bh = blockIdx.x;
     const int64_t sbase = bh * CN * CN;
+    const int64_t NN = CN * CN;
     const chunk::VecPtrs src{r, w, k, v, a, b, nullptr};
+    const int64_t nch = (T + L - 1) / L;
 
-    // State tiles of this wave: tile si = ST*wv + q covers S[i][j] with
-    // i = 16*(si & 3) + lr, j = 16*(si >> 2) + 4*lq + e (tiles of S^T).
-    f32x4_t S[ST];
-    int64_t soff[ST];
+    // ---- state: wave wv holds the S^T tiles si = 2wv, 2wv+1 --------------
+    // tile si: rows j = 16*(si >> 2) + 4*lq + e, column i = 16*(si & 3) + lr
+    f32x4_t S[2], Cacc[2], Pacc;
+    int soff[2];
 #pragma unroll
-    for (int q = 0; q < ST; ++q) {
-        const int si = ST * wv + q, jb = si >> 2, ib = si & 3;
-        soff[q] = sbase + (16 * ib + lr) * CN + 16 * jb + 4 * lq;
-        const float4 x = *reinterpret_cast<const float4*>(s0 + soff[q]);
+    for (int q = 0; q < 2; ++q) {
+        const int si = 2 * wv + q, jb = si >> 2, ib = si & 3;
+        soff[q] = (16 * ib + lr) * CN + 16 * jb + 4 * lq;
+        const float4 x =
+            *reinterpret_cast<const float4*>(s0 + sbase + soff[q]);
         S[q][0] = x.x; S[q][1] = x.y; S[q][2] = x.z; S[q][3] = x.w;
-        if (ckpt) *reinterpret_cast<uint2*>(ckpt + soff[q]) = pack4(S[q]);
+        Cacc[q] = zero4();
     }
+    Pacc = zero4();
+    // Y^T tile of this wave (all 8 waves at L = 32, waves 0..3 at L = 16):
+    // rows i = 16*yib + 4*lq + e, column t = 16*ytb + lr; yib is the i block
+    // of one of the wave's state tiles, so the two share the S' operand
+    const int yib = ((2 * wv) & 3) | ((wv >> 1) & 1), ytb = wv >> 2;
+    const bool has_y = ytb < NB;
 
-    // The next chunk's six vectors are fetched into registers while the
-    // current chunk computes (16-byte segments, 8 per 64-wide row).  Only
-    // the loader waves (upper half) load and only the store waves (lower
-    // half) store: vmcnt counts loads and stores of a wave together, so a
-    // loader wave's wait before a stash never covers stores in flight.
-    constexpr int LOADERS = NTH / 2;
-    const bool loader = tid >= LOADERS;
-    const int ltid = tid - LOADERS;
-    constexpr int SEG = 6 * L * 8;
-    constexpr int NPRE = (SEG + LOADERS - 1) / LOADERS;
+    // the matrices' and Minv's blocks above the diagonal stay zero
+    for (int e = tid; e < L * L; e += NTH) {
+        const int s = e / L, t = e % L;
+        if ((s >> 4) > (t >> 4)) {
+            sm.Aab[s][t] = 0; sm.Aak[s][t] = 0; sm.Arb[s][t] = 0;
+            sm.Ark[s][t] = 0; sm.MinvT[s][t] = 0;
+        }
+    }
+    if (tid < 2) sm.flag[tid] = 0;
+
+    // ---- the vectors, prefetched one chunk ahead into registers ----------
+    constexpr int SEG = 6 * L * 8;  // 16-byte segments of one chunk
+    constexpr int NPRE = (SEG + NTH - 1) / NTH;
     uint4 pre[NPRE];
-    // Each loader thread's segments sit at the same place of every chunk:
-    // their addresses are formed once, and a fetch only adds t0 * BH * 64.
     const bf16_t* pbase[NPRE];
     int ptok[NPRE];
 #pragma unroll
     for (int p = 0; p < NPRE; ++p) {
-        const int seg = p * LOADERS + (loader ? ltid : 0);
+        const int seg = p * NTH + tid;
         const int row = seg >> 3, s8 = seg & 7;
         const int vec = row / L, t = row % L;
-        ptok[p] = (seg < SEG) ? t : int(1 << 30);
-        pbase[p] = src.get(vec < 6 ? vec : 0) + (int64_t(t) * BH + bh) * CN + s8 * 8;
+        ptok[p] = seg < SEG ? t : (1 << 30);
+        pbase[p] = src.get(vec < 6 ? vec : 0) + (int64_t(t) * BH + bh) * CN +
+                   s8 * 8;
     }
     const int64_t chunk_stride = int64_t(L) * BH * CN;
-    auto fetch = [&](int64_t t0f) {
-        const int64_t off = (t0f / L) * chunk_stride;
+    auto fetch = [&](int64_t cc) {
 #pragma unroll
         for (int p = 0; p < NPRE; ++p) {
             pre[p] = make_uint4(0, 0, 0, 0);
-            if (t0f + ptok[p] < T)
-                pre[p] = *reinterpret_cast<const uint4*>(pbase[p] + off);
+            if (cc * L + ptok[p] < T)
+                pre[p] = *reinterpret_cast<const uint4*>(pbase[p] +
+                                                         cc * chunk_stride);
         }
     };
     auto stash = [&]() {
 #pragma unroll
         for (int p = 0; p < NPRE; ++p) {
-            const int seg = p * LOADERS + ltid;
+            const int seg = p * NTH + tid;
             if (seg < SEG) {
                 const int row = seg >> 3, s8 = seg & 7;
-                *reinterpret_cast<uint4*>(
-                    &sm.raw[row / L][row % L][s8 * 8]) = pre[p];
+                *reinterpret_cast<uint4*>(&sm.raw[row / L][row % L][s8 * 8]) =
+                    pre[p];
             }
         }
     };
-    // Checkpoint tiles of the loader waves go to HBM through the store
-    // waves, staged in LDS (Bh/Kh/Vt, free after B3) as [tile - 8][lane].
-    uint2* ck_stage = reinterpret_cast<uint2*>(&sm.Bh[0][0]);
-    static_assert(sizeof(sm.Bh) * 3 >= 8 * 64 * 8, "checkpoint staging");
-
-    // Pipeline: chunk c+1's vectors sit in LDS (raw) while chunk c+2's are
-    // in flight to the loader waves' registers.
-    const int64_t nchunks = (T + L - 1) / L;
-    if (loader) {
-        fetch(0);
-        stash();
-    }
-    // Everything loaded before the loop (state, first chunk) has arrived:
-    // without this wait the compiler guards first uses inside the loop with
-    // vmcnt waits that, in later iterations, drain the prefetch and the
-    // stores in flight.
+    fetch(0);
+    stash();
+    // everything loaded before the loop has arrived: the loop's waits then
+    // only count the prefetch and the stores
     __builtin_amdgcn_s_waitcnt(0);
-    if (loader && nchunks > 1) fetch(L);
-    if (tid == 0) sm.flag = 0;
+    if (nch > 1) fetch(1);
     __syncthreads();
-    for (int64_t c = 0; c < nchunks; ++c) {
-        const int64_t t0 = c * L;
-        const int n = int(T - t0 < L ? T - t0 : L);
 
-        // ---- A1: running log-decay and the decayed factors -------------
-        // thread: column j = lane, tokens [grp*TPG, grp*TPG + TPG)
-        const int j = lane, grp = wv;
-        float cs[TPG];
-        {
-            float run = 0.f;
-#pragma unroll
-            for (int u = 0; u < TPG; ++u) {
-                const int t = grp * TPG + u;
-                const float lam =
-                    (t < n) ? -__expf(bf16_to_f32(sm.raw[1][t][j])) : 0.f;
-                run += lam;
-                cs[u] = run;
-            }
-            sm.tot[grp][j] = run;
-        }
-        __syncthreads();
-        {
-            float off = 0.f, G = 0.f, gref = 0.f;
-#pragma unroll
-            for (int g2 = 0; g2 < NW; ++g2) {
-                const float tv = sm.tot[g2][j];
-                G += tv;
-                if (g2 < grp) off += tv;
-                if (g2 == NW / 2 - 1) gref = G;  // g at token L/2 - 1
-            }
-            if (-gref > kHalfRange || gref - G > kHalfRange) sm.flag = 1;
-            if (grp == 0) {
-                sm.eL[j] = __expf(G);
-                sm.eRef[j] = __expf(gref);
-            }
-            const float eLR = __expf(G - gref);
-            float eprev = __expf(off - gref);
-            bf16_t hb[TPG], hk[TPG], hv[TPG];
-#pragma unroll
-            for (int u = 0; u < TPG; ++u) {
-                const int t = grp * TPG + u;
-                const float g = off + cs[u];
-                const float eg = __expf(g - gref);
-                const float eng = __expf(gref - g);
-                const float egl = eLR * eng;
-                const float av = bf16_to_f32(sm.raw[4][t][j]);
-                const float rv = bf16_to_f32(sm.raw[0][t][j]);
-                const float kv = bf16_to_f32(sm.raw[2][t][j]);
-                const float bv = bf16_to_f32(sm.raw[5][t][j]);
-                sm.A[t][j] = to_bf16(av * eprev);
-                sm.R[t][j] = to_bf16(rv * eg);
-                sm.Bt[t][j] = to_bf16(bv * eng);
-                sm.Kt[t][j] = to_bf16(kv * eng);
-                hb[u] = to_bf16(bv * egl);
-                hk[u] = to_bf16(kv * egl);
-                hv[u] = sm.raw[3][t][j];
-                eprev = eg;
-            }
-            chunk::put_row<TPG>(&sm.Bh[j][grp * TPG], hb);
-            chunk::put_row<TPG>(&sm.Kh[j][grp * TPG], hk);
-            chunk::put_row<TPG>(&sm.Vt[j][grp * TPG], hv);
-        }
-        __syncthreads();
-        // read once: thread 0 clears the flag again at the end of the chunk
-        const bool fallback = sm.flag != 0;
+    // Iteration c advances the state through chunk c (c >= 0) and prepares
+    // chunk c + 1 (c + 1 < nch).
+    for (int64_t c = -1; c < nch; ++c) {
+        const bool adv = c >= 0, prep = c + 1 < nch;
+        const int cur = int(c & 1), nxt = int((c + 1) & 1);
+        const int64_t t0 = c * L;
+        const int n = adv ? int(T - t0 < L ? T - t0 : L) : 0;
+        const int n1 = prep ? int(T - t0 - L < L ? T - t0 - L : L) : 0;
+        const bool fallback = adv && sm.flag[cur] != 0;
 
         if (fallback) {
-            // ---- exact sequential fallback for this chunk -------------
-            // thread: row i = tid / NW, columns CPT*(tid % NW) .. + CPT-1
-            constexpr int CPT = CN / NW;
-            float* Sf = reinterpret_cast<float*>(&sm.A[0][0]);  // [64][65]
-            static_assert(sizeof(sm.A) * 4 + sizeof(sm.Bh) * 3 >=
-                              64 * 65 * 4, "Sf fits");
+            // ---- chunk c by the exact sequential loop -----------------
+            if (ckpt) {
 #pragma unroll
-            for (int q = 0; q < ST; ++q) {
-                const int si = ST * wv + q, jb = si >> 2, ib = si & 3;
+                for (int q = 0; q < 2; ++q)
+                    *reinterpret_cast<uint2*>(ckpt + c * BH * NN + sbase +
+                                              soff[q]) = pack4(S[q]);
+            }
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    Sf[(16 * ib + lr) * 65 + 16 * jb + 4 * lq + e] = S[q][e];
-            }
+                    sm.fb[soff[q] / CN][soff[q] % CN + e] = S[q][e];
             __syncthreads();
-            const int i = tid / NW, c0 = CPT * (tid % NW);
-            float Sl[CPT];
-#pragma unroll
-            for (int c2 = 0; c2 < CPT; ++c2) Sl[c2] = Sf[i * 65 + c0 + c2];
-            for (int t = 0; t < n; ++t) {
-                float sa = 0.f;
-#pragma unroll
-                for (int c2 = 0; c2 < CPT; ++c2)
-                    sa += Sl[c2] * bf16_to_f32(sm.raw[4][t][c0 + c2]);
-                sa = group_sum<NW>(sa);
-                const float vi = bf16_to_f32(sm.raw[3][t][i]);
-                float acc = 0.f;
-#pragma unroll
-                for (int c2 = 0; c2 < CPT; ++c2) {
-                    const int jj = c0 + c2;
-                    const float d =
-                        expf(-expf(bf16_to_f32(sm.raw[1][t][jj])));
-                    Sl[c2] = Sl[c2] * d +
-                             sa * bf16_to_f32(sm.raw[5][t][jj]) +
-                             vi * bf16_to_f32(sm.raw[2][t][jj]);
-                    acc += Sl[c2] * bf16_to_f32(sm.raw[0][t][jj]);
-                }
-                acc = group_sum<NW>(acc);
-                if (tid % NW == 0)
-                    y[((t0 + t) * BH + bh) * CN + i] = to_bf16(acc);
-            }
-#pragma unroll
-            for (int c2 = 0; c2 < CPT; ++c2) Sf[i * 65 + c0 + c2] = Sl[c2];
+            seq_chunk_forward<NW>(sm.fb, n, t0, BH, bh, src, y, tid);
             __syncthreads();
 #pragma unroll
-            for (int q = 0; q < ST; ++q) {
-                const int si = ST * wv + q, jb = si >> 2, ib = si & 3;
+            for (int q = 0; q < 2; ++q)
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    S[q][e] = Sf[(16 * ib + lr) * 65 + 16 * jb + 4 * lq + e];
+                    S[q][e] = sm.fb[soff[q] / CN][soff[q] % CN + e];
+            __syncthreads();  // fb aliases the factor arrays
+        }
+
+        // ================= phase F =======================================
+        if (adv && !fallback) {
+            // checkpoint c; S' = S e^{g_ref} to LDS; S <- S e^{g_L} + C
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int si = 2 * wv + q, jb = si >> 2, ib = si & 3;
+                if (ckpt)
+                    *reinterpret_cast<uint2*>(ckpt + c * BH * NN + sbase +
+                                              soff[q]) = pack4(S[q]);
+                const int j = 16 * jb + 4 * lq;
+                const float4 er = *reinterpret_cast<const float4*>(&sm.eRef[cur][j]);
+                const float4 el = *reinterpret_cast<const float4*>(&sm.eL[cur][j]);
+                const float4 elr = *reinterpret_cast<const float4*>(&sm.eLR[cur][j]);
+                f32x4_t sp;
+                sp[0] = S[q][0] * er.x; sp[1] = S[q][1] * er.y;
+                sp[2] = S[q][2] * er.z; sp[3] = S[q][3] * er.w;
+                S[q][0] = S[q][0] * el.x + Cacc[q][0] * elr.x;
+                S[q][1] = S[q][1] * el.y + Cacc[q][1] * elr.y;
+                S[q][2] = S[q][2] * el.z + Cacc[q][2] * elr.z;
+                S[q][3] = S[q][3] * el.w + Cacc[q][3] * elr.w;
+                store_tile_bf16_t(sp, &sm.f.Sp[16 * ib][16 * jb], PN, lane);
             }
-            __syncthreads();  // Sf (aliasing the staging area) is read
-        } else {
-            // ---- B0: scaled chunk-start state to LDS (bf16, [i][j]) ---
-#pragma unroll
-            for (int q = 0; q < ST; ++q) {
-                const int si = ST * wv + q, jb = si >> 2, ib = si & 3;
-                float er[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) er[e] = sm.eRef[16 * jb + 4 * lq + e];
-                uint2 p;
-                p.x = pack_bf16x2(S[q][0] * er[0], S[q][1] * er[1]);
-                p.y = pack_bf16x2(S[q][2] * er[2], S[q][3] * er[3]);
-                *reinterpret_cast<uint2*>(
-                    &sm.S[16 * ib + lr][16 * jb + 4 * lq]) = p;
-            }
-            // ---- A2: the four L x L matrices (lower tiles) -------------
-            constexpr int NT2 = 4 * NB * NB;
-#pragma unroll
-            for (int it = 0; it < (NT2 + NW - 1) / NW; ++it) {
-                const int ti = wv + NW * it;
-                if (ti < NT2) {
-                    const int mat = ti / (NB * NB), rem = ti % (NB * NB);
-                    const int mt = rem / NB, nt = rem % NB;
-                    bf16_t* dst = mat == 0 ? &sm.m.Aab[0][0]
-                                  : mat == 1 ? &sm.m.Aak[0][0]
-                                  : mat == 2 ? &sm.m.Arb[0][0]
-                                             : &sm.m.Ark[0][0];
-                    dst += 16 * mt * PL + 16 * nt;
-                    f32x4_t acc = zero4();
-                    if (nt <= mt) {
-                        const bf16_t* Aop = mat < 2 ? &sm.A[16 * mt][0]
-                                                    : &sm.R[16 * mt][0];
-                        const bf16_t* Bop = (mat & 1) ? &sm.Kt[16 * nt][0]
-                                                      : &sm.Bt[16 * nt][0];
-                        mma_nt<CN>(acc, Aop, PN, Bop, PN, lane);
-                        const bool strict = mat < 2;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int tt = 16 * mt + 4 * lq + e;
-                            const int ss = 16 * nt + lr;
-                            const bool keep = strict ? (ss < tt) : (ss <= tt);
-                            acc[e] = keep ? acc[e] : 0.f;
-                        }
-                        if (mat == 0 && mt == nt)
-                            store_tile_bf16_t(acc, &sm.m.AabTD[mt][0][0], 24,
-                                              lane);
-                    }
-                    store_tile_bf16(acc, dst, PL, lane);
-                }
-            }
-            __syncthreads();
-            // ---- A3 + B1: Minv = (I - Aab)^{-1} on waves 0 .. NB-1 while
-            // the other waves form U = A~ S'^T + Aak V (stored transposed)
-            // and the state/value part of Y^T.  B1 tiles 0 .. 4NB-1 are U
-            // (t block mt, i block ui), 4NB .. 8NB-1 are Y^T (i block yi,
-            // t block yt), dealt round-robin over waves NB .. NW-1.
-            constexpr int NT1 = 8 * NB, NWB = NW - NB;
-            constexpr int IT1 = (NT1 + NWB - 1) / NWB;
-            f32x4_t Yacc[IT1];
-#pragma unroll
-            for (int it = 0; it < IT1; ++it) Yacc[it] = zero4();
-            auto b1 = [&] {
-#pragma unroll
-                for (int it = 0; it < IT1; ++it) {
-                    const int ti = (wv - NB) + NWB * it;
-                    if (ti < 4 * NB) {
-                        const int mt = ti >> 2, ui = ti & 3;
-                        f32x4_t u = zero4();
-                        mma_nt<CN>(u, &sm.A[16 * mt][0], PN, &sm.S[16 * ui][0],
-                                   PN, lane);
-                        mma_nt<L>(u, &sm.m.Aak[16 * mt][0], PL,
-                                  &sm.Vt[16 * ui][0], PL, lane);
-                        store_tile_bf16_t(u, &sm.m.ux.U[16 * ui][16 * mt], PL,
-                                          lane);
-                    } else if (ti < NT1) {
-                        const int yt = (ti - 4 * NB) % NB;
-                        const int yi = (ti - 4 * NB) / NB;
-                        mma_nt<CN>(Yacc[it], &sm.S[16 * yi][0], PN,
-                                   &sm.R[16 * yt][0], PN, lane);
-                        mma_nt<L>(Yacc[it], &sm.Vt[16 * yi][0], PL,
-                                  &sm.m.Ark[16 * yt][0], PL, lane);
-                    }
+        }
+        if (prep) {
+            // factors of chunk c+1; lane = (token t, columns j0 .. j0+CPL-1).
+            // Log-decays are kept in base 2: g2 = g log2(e).
+            const int t = lane % L, grp = lane / L;
+            const int j0 = 8 * wv + CPL * grp;
+            constexpr float kLog2e = 1.4426950408889634f;
+            float rv[CPL], wl[CPL], kv[CPL], av[CPL], bv[CPL];
+            auto ld = [&](int vec, float* dst) {
+                const bf16_t* p = &sm.raw[vec][t][j0];
+                if constexpr (CPL == 4) {
+                    const uint2 u = *reinterpret_cast<const uint2*>(p);
+                    dst[0] = __uint_as_float(u.x << 16);
+                    dst[1] = __uint_as_float(u.x & 0xffff0000u);
+                    dst[2] = __uint_as_float(u.y << 16);
+                    dst[3] = __uint_as_float(u.y & 0xffff0000u);
+                } else {
+                    const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
+                    dst[0] = __uint_as_float(u << 16);
+                    dst[1] = __uint_as_float(u & 0xffff0000u);
                 }
             };
-            // product scratch in Bt/Kt (dead after A2)
-            static_assert(sizeof(sm.Bt) * 2 >= NB * 5 * 16 * 24 * 2, "W fits");
-            chunk::build_minv<L, NTH>(
-                &sm.m.Aab[0][0], sm.m.AabTD, &sm.m.Minv[0][0],
-                &sm.m.MinvT[0][0], sm.m.Z,
-                reinterpret_cast<bf16_t(*)[5][16][24]>(&sm.Bt[0][0]), tid, b1);
-            // ---- B2: X = Minv U (stored transposed) ---------------------
+            ld(0, rv); ld(1, wl); ld(2, kv); ld(4, av); ld(5, bv);
+            // v is copied as it is
+            if constexpr (CPL == 4)
+                *reinterpret_cast<uint2*>(&sm.f.Vc[t][j0]) =
+                    *reinterpret_cast<const uint2*>(&sm.raw[3][t][j0]);
+            else
+                *reinterpret_cast<uint32_t*>(&sm.f.Vc[t][j0]) =
+                    *reinterpret_cast<const uint32_t*>(&sm.raw[3][t][j0]);
+            float lam[CPL], g[CPL];
 #pragma unroll
-            for (int it = 0; it < (4 * NB + NW - 1) / NW; ++it) {
-                const int ti = wv + NW * it;
-                if (ti < 4 * NB) {
-                    const int mt = ti >> 2, xi = ti & 3;
-                    f32x4_t x = zero4();
-                    mma_nt<L>(x, &sm.m.Minv[16 * mt][0], PL,
-                              &sm.m.ux.U[16 * xi][0], PL, lane);
-                    store_tile_bf16_t(x, &sm.m.ux.X[16 * xi][16 * mt], PL,
-                                      lane);
+            for (int e = 0; e < CPL; ++e) {
+                const float l2 =
+                    -__builtin_amdgcn_exp2f(wl[e] * kLog2e) * kLog2e;
+                lam[e] = t < n1 ? l2 : 0.f;
+                g[e] = scan_lanes<L>(lam[e]);
+            }
+            bool bad = false;
+            float fA[CPL], fR[CPL], fB[CPL], fK[CPL];
+#pragma unroll
+            for (int e = 0; e < CPL; ++e) {
+                // g at tokens L/2 - 1 and L - 1 of this lane group, by
+                // ds_swizzle (bitmask mode within 32 lanes: lane | or_mask)
+                float gref, gL;
+                if constexpr (L == 32) {
+                    gref = __int_as_float(__builtin_amdgcn_ds_swizzle(
+                        __float_as_int(g[e]), 15 << 5));
+                    gL = __int_as_float(__builtin_amdgcn_ds_swizzle(
+                        __float_as_int(g[e]), 31 << 5));
+                } else {
+                    gref = __int_as_float(__builtin_amdgcn_ds_swizzle(
+                        __float_as_int(g[e]), 0x10 | (7 << 5)));
+                    gL = __int_as_float(__builtin_amdgcn_ds_swizzle(
+                        __float_as_int(g[e]), 0x10 | (15 << 5)));
+                }
+                bad |= (-gref > kHalfRange * kLog2e) ||
+                       (gref - gL > kHalfRange * kLog2e);
+                const float eg = __builtin_amdgcn_exp2f(g[e] - gref);
+                const float eng = __builtin_amdgcn_exp2f(gref - g[e]);
+                const float eprev =
+                    __builtin_amdgcn_exp2f(g[e] - lam[e] - gref);
+                fA[e] = av[e] * eprev;
+                fR[e] = rv[e] * eg;
+                fB[e] = bv[e] * eng;
+                fK[e] = kv[e] * eng;
+                if (t == 0) {
+                    sm.eL[nxt][j0 + e] = __builtin_amdgcn_exp2f(gL);
+                    sm.eRef[nxt][j0 + e] = __builtin_amdgcn_exp2f(gref);
+                    sm.eLR[nxt][j0 + e] = __builtin_amdgcn_exp2f(gL - gref);
                 }
             }
-            __syncthreads();
-            // ---- B3: Y^T += X^T Arb^T; S^T = e^{g_L} S^T + B^^T X + K^^T V
-            bf16_t(*Ybuf)[PN] = sm.A;
-            if (wv >= NB) {
-#pragma unroll
-                for (int it = 0; it < IT1; ++it) {
-                    const int ti = (wv - NB) + NWB * it;
-                    if (ti >= 4 * NB && ti < NT1) {
-                        const int yt = (ti - 4 * NB) % NB;
-                        const int yi = (ti - 4 * NB) / NB;
-                        mma_nt<L>(Yacc[it], &sm.m.ux.X[16 * yi][0], PL,
-                                  &sm.m.Arb[16 * yt][0], PL, lane);
-                        store_tile_bf16_t(Yacc[it], &Ybuf[16 * yt][16 * yi],
-                                          PN, lane);
-                    }
+            if (bad) sm.flag[nxt] = 1;
+            auto put = [&](bf16_t (*dst)[PN], const float* x) {
+                bf16_t* p = &dst[t][j0];
+                if constexpr (CPL == 4) {
+                    uint2 u;
+                    u.x = pack_bf16x2(x[0], x[1]);
+                    u.y = pack_bf16x2(x[2], x[3]);
+                    *reinterpret_cast<uint2*>(p) = u;
+                } else {
+                    *reinterpret_cast<uint32_t*>(p) = pack_bf16x2(x[0], x[1]);
                 }
-            }
-#pragma unroll
-            for (int q = 0; q < ST; ++q) {
-                const int si = ST * wv + q, jb = si >> 2, ib = si & 3;
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    S[q][e] *= sm.eL[16 * jb + 4 * lq + e];
-                mma_nt<L>(S[q], &sm.Bh[16 * jb][0], PL, &sm.m.ux.X[16 * ib][0],
-                          PL, lane);
-                mma_nt<L>(S[q], &sm.Kh[16 * jb][0], PL, &sm.Vt[16 * ib][0],
-                          PL, lane);
-            }
-            __syncthreads();
-            // ---- B4: y rows of the chunk to HBM (store waves) ---------
-            for (int sg = tid; sg < 8 * L; sg += LOADERS) {
-                if (loader) break;
-                const int t = sg >> 3, s8 = sg & 7;
-                if (t < n)
-                    *reinterpret_cast<uint4*>(
-                        y + ((t0 + t) * BH + bh) * CN + s8 * 8) =
-                        *reinterpret_cast<const uint4*>(&Ybuf[t][s8 * 8]);
-            }
+            };
+            put(sm.f.At, fA); put(sm.f.Rt, fR); put(sm.f.Bt, fB);
+            put(sm.f.Kt, fK);
         }
-        // ---- next chunk's vectors to LDS; checkpoint tiles ---------------
-        const bool want_ckpt = ckpt != nullptr;
-        bf16_t* cdst = ckpt + (c + 1) * BH * CN * CN;
-        if (loader) {
-            stash();
-            if (want_ckpt) {
-#pragma unroll
-                for (int q = 0; q < ST; ++q)
-                    ck_stage[(ST * wv + q - 8) * 64 + lane] = pack4(S[q]);
-            }
-            if (c + 2 < nchunks) fetch(t0 + 2 * L);
-        } else if (want_ckpt) {
-#pragma unroll
-            for (int q = 0; q < ST; ++q)
-                *reinterpret_cast<uint2*>(cdst + soff[q]) = pack4(S[q]);
-        }
-        if (tid == 0) sm.flag = 0;
         __syncthreads();
-        if (want_ckpt && !loader) {
-            // the store waves write the loader waves' tiles 8 .. 15
+
+        // ================= phase M =======================================
+        if (adv && !fallback) {
+            // S^T += M^T S'^T and Y^T = P^T + S' Q^T (K = 64)
 #pragma unroll
-            for (int q = 0; q < ST; ++q) {
-                const int si = 8 + ST * wv + q, jb = si >> 2, ib = si & 3;
-                *reinterpret_cast<uint2*>(
-                    cdst + sbase + (16 * ib + lr) * CN + 16 * jb + 4 * lq) =
-                    ck_stage[(ST * wv + q) * 64 + lane];
+            for (int q = 0; q < 2; ++q) {
+                const int si = 2 * wv + q, jb = si >> 2, ib = si & 3;
+#pragma unroll
+                for (int k0 = 0; k0 < CN; k0 += 32)
+                    mfma(S[q], frag_rk(&sm.Mt[cur][16 * jb][k0], PN, lane),
+                         frag_rk(&sm.f.Sp[16 * ib][k0], PN, lane));
+            }
+            if (has_y) {
+                f32x4_t yy = Pacc;
+#pragma unroll
+                for (int k0 = 0; k0 < CN; k0 += 32)
+                    mfma(yy, frag_rk(&sm.f.Sp[16 * yib][k0], PN, lane),
+                         frag_rk(&sm.Q[cur][16 * ytb][k0], PN, lane));
+                const int tt = 16 * ytb + lr;
+                if (tt < n)
+                    *reinterpret_cast<uint2*>(
+                        y + ((t0 + tt) * BH + bh) * CN + 16 * yib + 4 * lq) =
+                        pack4(yy);
             }
         }
-    }
+        if (adv && tid == 0) sm.flag[cur] = 0;
+        Pacc = zero4();
+        Cacc[0] = zero4();
+        Cacc[1] = zero4();
+        f32x4_t mi_pp[NB];
+        if (prep) {
+            if (wv == 0) {
+                // Aab lower tiles (strict), stored transposed
 #pragma unroll
-    for (int q = 0; q < ST; ++q)
-        *reinterpret_cast<float4*>(s_t + soff[q]) =
+                for (int tb = 0; tb < NB; ++tb)
+#pragma unroll
+                    for (int sb = 0; sb <= tb; ++sb) {
+                        f32x4_t acc = zero4();
+#pragma unroll
+                        for (int k0 = 0; k0 < CN; k0 += 32)
+                            mfma(acc,
+                                 frag_rk(&sm.f.At[16 * tb][k0], PN, lane),
+                                 frag_rk(&sm.f.Bt[16 * sb][k0], PN, lane));
+                        if (sb == tb) {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                acc[e] = (4 * lq + e > lr) ? acc[e] : 0.f;
+                        }
+                        store_tile_bf16_t(acc, &sm.Aab[16 * sb][16 * tb], PL,
+                                          lane);
+                    }
+                // Minv diagonal blocks p (A = Aab_pp):
+                //   A2 = A A; P = I + A + A2 + A A2; A4 = A2 A2;
+                //   P2 = P + P A4; A8 = A4 A4; Minv_pp = P2 + P2 A8
+                wave_lds_fence();
+                f32x4_t a2[NB];
+#pragma unroll
+                for (int p = 0; p < NB; ++p) {
+                    const bf16_t* Ap = &sm.Aab[16 * p][16 * p];
+                    a2[p] = zero4();
+                    mfma(a2[p], frag_kr16(Ap, PL, lane),
+                         frag_rk16(Ap, PL, lane));
+                    store_tile_bf16_t(a2[p], &sm.ms[p][0][0][0], 24, lane);
+                }
+                wave_lds_fence();
+#pragma unroll
+                for (int p = 0; p < NB; ++p) {
+                    const bf16_t* Ap = &sm.Aab[16 * p][16 * p];
+                    const f32x4_t at = unpack4(*reinterpret_cast<const uint2*>(
+                        Ap + lr * PL + 4 * lq));  // A[4lq+e][lr]
+                    f32x4_t a4 = zero4(), pp;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        pp[e] = ((4 * lq + e == lr) ? 1.f : 0.f) + at[e] +
+                                a2[p][e];
+                    mfma(pp, frag_kr16(Ap, PL, lane),
+                         frag_rk16(&sm.ms[p][0][0][0], 24, lane));
+                    mfma(a4, frag_kr16(&sm.ms[p][0][0][0], 24, lane),
+                         frag_rk16(&sm.ms[p][0][0][0], 24, lane));
+                    mi_pp[p] = pp;
+                    store_tile_bf16_t(a4, &sm.ms[p][1][0][0], 24, lane);
+                    store_tile_bf16_t(pp, &sm.ms[p][2][0][0], 24, lane);
+                }
+            } else {
+                // Aak (strict), Arb, Ark (with diagonal): lower tiles
+                constexpr int TPM = NB * (NB + 1) / 2;
+                for (int ti = wv - 1; ti < 3 * TPM; ti += NW - 1) {
+                    const int mat = ti / TPM, rem = ti % TPM;
+                    const int tb = rem < 1 ? 0 : 1;
+                    const int sb = rem - tb;
+                    const bf16_t(*Xo)[PN] = mat == 0 ? sm.f.At : sm.f.Rt;
+                    const bf16_t(*Yo)[PN] = mat == 1 ? sm.f.Bt : sm.f.Kt;
+                    bf16_t(*dst)[PL] = mat == 0   ? sm.Aak
+                                       : mat == 1 ? sm.Arb
+                                                  : sm.Ark;
+                    f32x4_t acc = zero4();
+#pragma unroll
+                    for (int k0 = 0; k0 < CN; k0 += 32)
+                        mfma(acc, frag_rk(&Xo[16 * tb][k0], PN, lane),
+                             frag_rk(&Yo[16 * sb][k0], PN, lane));
+                    if (sb == tb) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int tt = 4 * lq + e;
+                            const bool keep =
+                                mat == 0 ? (lr < tt) : (lr <= tt);
+                            acc[e] = keep ? acc[e] : 0.f;
+                        }
+                    }
+                    store_tile_bf16_t(acc, &dst[16 * sb][16 * tb], PL, lane);
+                }
+            }
+        }
+        __syncthreads();
+
+        // ================= phase I =======================================
+        if (prep && wv == 0) {
+            wave_lds_fence();
+#pragma unroll
+            for (int p = 0; p < NB; ++p) {
+                f32x4_t a8 = zero4();
+                mfma(mi_pp[p], frag_kr16(&sm.ms[p][2][0][0], 24, lane),
+                     frag_rk16(&sm.ms[p][1][0][0], 24, lane));
+                mfma(a8, frag_kr16(&sm.ms[p][1][0][0], 24, lane),
+                     frag_rk16(&sm.ms[p][1][0][0], 24, lane));
+                store_tile_bf16_t(a8, &sm.ms[p][0][0][0], 24, lane);
+                store_tile_bf16_t(mi_pp[p], &sm.ms[p][3][0][0], 24, lane);
+            }
+            wave_lds_fence();
+#pragma unroll
+            for (int p = 0; p < NB; ++p) {
+                mfma(mi_pp[p], frag_kr16(&sm.ms[p][3][0][0], 24, lane),
+                     frag_rk16(&sm.ms[p][0][0][0], 24, lane));
+                store_tile_bf16_t(mi_pp[p], &sm.MinvT[16 * p][16 * p], PL,
+                                  lane);
+            }
+            if constexpr (NB == 2) {
+                // Minv_10 = Minv_11 (Aab_10 Minv_00)
+                wave_lds_fence();
+                f32x4_t z = zero4();
+                mfma(z, frag_kr16(&sm.Aab[0][16], PL, lane),
+                     frag_rk16(&sm.MinvT[0][0], PL, lane));
+                store_tile_bf16_t(z, &sm.ms[0][1][0][0], 24, lane);
+                wave_lds_fence();
+                f32x4_t m10 = zero4();
+                mfma(m10, frag_kr16(&sm.MinvT[16][16], PL, lane),
+                     frag_rk16(&sm.ms[0][1][0][0], 24, lane));
+                store_tile_bf16_t(m10, &sm.MinvT[0][16], PL, lane);
+            }
+        }
+        // C^T += K~^T V (scaled as above), P^T += V^T Ark^T (wave 0: phase W)
+        auto c_kv = [&] {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int si = 2 * wv + q, jb = si >> 2, ib = si & 3;
+                mfma(Cacc[q], fkr<L>(&sm.f.Kt[0][16 * jb], PN, lane),
+                     fkr<L>(&sm.f.Vc[0][16 * ib], PN, lane));
+            }
+            if (has_y)
+                mfma(Pacc, fkr<L>(&sm.f.Vc[0][16 * yib], PN, lane),
+                     fkr<L>(&sm.Ark[0][16 * ytb], PL, lane));
+        };
+        if (prep && wv > 0) {
+            // Aak V -> AakV[i][s] (tiles: s block x i block)
+            for (int ti = wv - 1; ti < 4 * NB; ti += NW - 1) {
+                const int sb = ti / 4, ib = ti % 4;
+                f32x4_t acc = zero4();
+                mfma(acc, fkr<L>(&sm.Aak[0][16 * sb], PL, lane),
+                     fkr<L>(&sm.f.Vc[0][16 * ib], PN, lane));
+                store_tile_bf16_t(acc, &sm.AakV[16 * ib][16 * sb], PL, lane);
+            }
+            c_kv();
+        }
+        if (c + 2 < nch) {
+            stash();
+            if (c + 3 < nch) fetch(c + 3);
+        }
+        __syncthreads();
+
+        // ================= phase W =======================================
+        if (prep) {
+            if (wv == 0) c_kv();
+            // W = Minv A~ -> Wt[j][t]; U = Minv (Aak V) -> Ut[i][t]
+            for (int ti = wv; ti < 8 * NB; ti += NW) {
+                const bool isU = ti >= 4 * NB;
+                const int rem = ti % (4 * NB), tb = rem / 4, xb = rem % 4;
+                f32x4_t acc = zero4();
+                const bf16x8_t fa = fkr<L>(&sm.MinvT[0][16 * tb], PL, lane);
+                if (isU) {
+                    mfma(acc, fa, frk<L>(&sm.AakV[16 * xb][0], PL, lane));
+                    store_tile_bf16_t(acc, &sm.Ut[16 * xb][16 * tb], PL, lane);
+                } else {
+                    mfma(acc, fa, fkr<L>(&sm.f.At[0][16 * xb], PN, lane));
+                    store_tile_bf16_t(acc, &sm.Wt[16 * xb][16 * tb], PL, lane);
+                }
+            }
+        }
+        __syncthreads();
+
+        // ================= phase Q =======================================
+        if (prep) {
+            // Q^T = R~^T + W^T Arb^T -> Q[t][j]  (tiles: j block x t block)
+            for (int ti = wv; ti < 4 * NB; ti += NW) {
+                const int jb = ti % 4, tb = ti / 4;
+                f32x4_t acc = unpack4(*reinterpret_cast<const uint2*>(
+                    &sm.f.Rt[16 * tb + lr][16 * jb + 4 * lq]));
+                mfma(acc, frk<L>(&sm.Wt[16 * jb][0], PL, lane),
+                     fkr<L>(&sm.Arb[0][16 * tb], PL, lane));
+                store_tile_bf16_t(acc, &sm.Q[nxt][16 * tb][16 * jb], PN,
+                                  lane);
+            }
+            // M = W^T B^ = (W^T B~) diag(e^{g_L-g_ref}) -> Mt[j][j']
+            // (tiles: j' block x j block)
+            for (int ti = wv; ti < 16; ti += NW) {
+                const int jpb = ti % 4, jb = ti / 4;
+                f32x4_t acc = zero4();
+                mfma(acc, frk<L>(&sm.Wt[16 * jpb][0], PL, lane),
+                     fkr<L>(&sm.f.Bt[0][16 * jb], PN, lane));
+                const float sc = sm.eLR[nxt][16 * jb + lr];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] *= sc;
+                store_tile_bf16_t(acc, &sm.Mt[nxt][16 * jb][16 * jpb], PN,
+                                  lane);
+            }
+            // C^T += B~^T U (scaled by e^{g_L-g_ref} when applied) and
+            // P^T += U^T Arb^T
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int si = 2 * wv + q, jb = si >> 2, ib = si & 3;
+                mfma(Cacc[q], fkr<L>(&sm.f.Bt[0][16 * jb], PN, lane),
+                     frk<L>(&sm.Ut[16 * ib][0], PL, lane));
+            }
+            if (has_y)
+                mfma(Pacc, frk<L>(&sm.Ut[16 * yib][0], PL, lane),
+                     fkr<L>(&sm.Arb[0][16 * ytb], PL, lane));
+        }
+        __syncthreads();
+    }
+
+    // ---- final state -----------------------------------------------------
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        *reinterpret_cast<float4*>(s_t + sbase + soff[q]) =
             make_float4(S[q][0], S[q][1], S[q][2], S[q][3]);
+        if (ckpt)
+            *reinterpret_cast<uint2*>(ckpt + nch * BH * NN + sbase +
+                                      soff[q]) = pack4(S[q]);
+    }
 }
 
 template <int L>
 hipError_t launch_l(const ChunkFwdArgs& p, hipStream_t stream) {
     const int64_t BH = p.B * p.H;
     hipLaunchKernelGGL((wkv7_chunk_fwd_kernel<L>), dim3(unsigned(BH)),
-                       dim3(FWD_WAVES * 64), 0, stream, p.T, BH,
+                       dim3(FWD_THREADS), 0, stream, p.T, BH,
                        static_cast<const bf16_t*>(p.r),
                        static_cast<const bf16_t*>(p.w),
                        static_cast<const bf16_t*>(p.k),
@@ -492,7 +674,6 @@ hipError_t launch_chunk_forward(const ChunkFwdArgs& p, hipStream_t stream) {
     switch (p.L) {
         case 16: return launch_l<16>(p, stream);
         case 32: return launch_l<32>(p, stream);
-        case 64: return launch_l<64>(p, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -1,5 +1,12 @@
 // Pieces shared by the chunked WKV-7 forward and backward kernels (gfx950,
-// bf16 vectors, N = 64, one 4-wave workgroup per (batch, head)).
+// bf16 vectors, N = 64, one 8-wave workgroup per (batch, head), chunks of
+// L = 16 or 32 tokens).
+//
+// Conventions.  Token-major arrays are [t][j] with row pitch PN.  An L x L
+// matrix X is stored transposed: memory [s][t] holds X(t, s), pitch PL.
+// Operand fragments come from frag_rk (rows stored [row][k]) or frag_kr
+// (rows stored [k][row], transposing LDS load), so every product reads its
+// operands in whichever order they are stored.
 #pragma once
 
 #include "wkv7_common.h"
@@ -8,12 +15,14 @@
 namespace rwkv7m {
 namespace chunk {
 
-constexpr int CN = 64;          // head size served by the chunked kernels
-constexpr int PN = CN + 8;      // LDS row pitch of K = N operands
-constexpr int NTHREADS = 256;   // 4 waves
+constexpr int CN = 64;        // head size served by the chunked kernels
+constexpr int PN = CN + 8;    // LDS row pitch of 64-wide rows
+constexpr int NWAVES = 8;
+constexpr int NTHREADS = NWAVES * 64;
 // Largest log-decay span on either side of the chunk's reference point that
 // the factored form represents (e^40 keeps every factor finite in bf16).
 constexpr float kHalfRange = 40.f;
+constexpr float kLog2e = 1.4426950408889634f;
 
 // The chunk kernels' input vectors.  Pointers are picked by a switch over
 // kernel arguments (never from an indexed array) so that the compiler keeps
@@ -34,144 +43,334 @@ struct VecPtrs {
     }
 };
 
-// Stage NV time-major [T][BH][64] bf16 vectors of one chunk (L tokens from
-// t0) into dst[NV][L][64].  Rows past the end of the sequence, and vectors
-// whose pointer is null, are zeros.
-template <int L, int NV>
-__device__ __forceinline__ void load_rows(bf16_t (*dst)[L][CN],
-                                          const VecPtrs& src, int64_t t0,
-                                          int64_t T, int64_t BH, int64_t bh,
-                                          int tid) {
-    constexpr int ROWS = NV * L;
+// Fragments of a contraction over K = 16 or 32 tokens.
+template <int K>
+__device__ __forceinline__ bf16x8_t fkr(const bf16_t* M, int ld, int lane) {
+    if constexpr (K == 16) return frag_kr16(M, ld, lane);
+    else return frag_kr(M, ld, lane);
+}
+template <int K>
+__device__ __forceinline__ bf16x8_t frk(const bf16_t* M, int ld, int lane) {
+    if constexpr (K == 16) return frag_rk16(M, ld, lane);
+    else return frag_rk(M, ld, lane);
+}
+
+// LDS writes of a wave made visible to the same wave's later reads.
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+
+// Inclusive prefix sum over groups of L consecutive lanes (L = 16 or 32).
+template <int L>
+__device__ __forceinline__ float scan_lanes(float x) {
+#define RWKV7M_SHR(n)                                                       \
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), \
+                                                    0x110 + (n), 0xF, 0xF, \
+                                                    true))
+    RWKV7M_SHR(1);
+    RWKV7M_SHR(2);
+    RWKV7M_SHR(4);
+    RWKV7M_SHR(8);
+#undef RWKV7M_SHR
+    if constexpr (L == 32) {
+        // row_bcast:15 into rows 1 and 3 (from lane 15 of rows 0 and 2)
+        x += __int_as_float(__builtin_amdgcn_update_dpp(
+            0, __float_as_int(x), 0x142, 0xA, 0xF, false));
+    }
+    return x;
+}
+
+// Inclusive suffix sum over groups of L consecutive lanes (L = 16 or 32).
+template <int L>
+__device__ __forceinline__ float suffix_scan_lanes(float x, int lane) {
+#define RWKV7M_SHL(n)                                                       \
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), \
+                                                    0x100 + (n), 0xF, 0xF, \
+                                                    true))
+    RWKV7M_SHL(1);
+    RWKV7M_SHL(2);
+    RWKV7M_SHL(4);
+    RWKV7M_SHL(8);
+#undef RWKV7M_SHL
+    if constexpr (L == 32) {
+        // rows 0 and 2 add the total of rows 1 and 3 (lane 16 of each
+        // 32-lane half, by ds_swizzle in bitmask mode: lane | 16)
+        const float hi = __int_as_float(
+            __builtin_amdgcn_ds_swizzle(__float_as_int(x), 16 << 5));
+        x += (lane & 16) ? 0.f : hi;
+    }
+    return x;
+}
+
+// Value of lane t + 1 of the same group of L lanes (0 for the group's last
+// lane), by wave_shl:1.
+template <int L>
+__device__ __forceinline__ float next_token(float x, int lane) {
+    const float y = __int_as_float(__builtin_amdgcn_update_dpp(
+        0, __float_as_int(x), 0x130, 0xF, 0xF, true));
+    return (lane % L == L - 1) ? 0.f : y;
+}
+
+// ---------------------------------------------------------------------------
+// Decayed factors of one chunk.  Lane = (token t = lane % L, CPL = L/8
+// columns j0 .. j0+CPL-1 with j0 = 8*wave + CPL*(lane / L)).  The log-decay
+// is kept in base 2 (lam = log2 d_t, g its running sum over the chunk) and
+// the reference point is g_ref = g at token L/2 - 1.  Writes the token-major
+// factors
+//   A~_t = a_t 2^{g_{t-1}-g_ref}, R~_t = r_t 2^{g_t-g_ref},
+//   B~_t = b_t 2^{g_ref-g_t},     K~_t = k_t 2^{g_ref-g_t},
+// and per column 2^{g_L}, 2^{g_ref}, 2^{g_L-g_ref}; raises *flag when the
+// factored form cannot represent the chunk.  raw: the chunk's vectors
+// (r, w, k, v, neg_kk, kka, ...) as [vec][t][j]; tokens t >= n are padding.
+template <int L>
+struct LaneFactors {
+    static constexpr int CPL = L / 8;
+    int t, j0;
+    float lam[CPL], eg[CPL], eng[CPL], eprev[CPL];
+    float r[CPL], k[CPL], a[CPL], b[CPL];
+};
+
+template <int L>
+__device__ __forceinline__ void load_cols(const bf16_t* p, float* dst) {
+    if constexpr (L == 32) {
+        const uint2 u = *reinterpret_cast<const uint2*>(p);
+        dst[0] = __uint_as_float(u.x << 16);
+        dst[1] = __uint_as_float(u.x & 0xffff0000u);
+        dst[2] = __uint_as_float(u.y << 16);
+        dst[3] = __uint_as_float(u.y & 0xffff0000u);
+    } else {
+        const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
+        dst[0] = __uint_as_float(u << 16);
+        dst[1] = __uint_as_float(u & 0xffff0000u);
+    }
+}
+
+template <int L>
+__device__ __forceinline__ void store_cols(bf16_t* p, const float* x) {
+    if constexpr (L == 32) {
+        uint2 u;
+        u.x = pack_bf16x2(x[0], x[1]);
+        u.y = pack_bf16x2(x[2], x[3]);
+        *reinterpret_cast<uint2*>(p) = u;
+    } else {
+        *reinterpret_cast<uint32_t*>(p) = pack_bf16x2(x[0], x[1]);
+    }
+}
+
+template <int L>
+__device__ __forceinline__ void chunk_factors(
+    const bf16_t (*raw)[L][PN], int n, int wv, int lane, bf16_t (*At)[PN],
+    bf16_t (*Rt)[PN], bf16_t (*Bt)[PN], bf16_t (*Kt)[PN], float* eL,
+    float* eRef, float* eLR, int* flag, LaneFactors<L>& F) {
+    constexpr int CPL = L / 8;
+    const int t = lane % L, grp = lane / L;
+    const int j0 = 8 * wv + CPL * grp;
+    F.t = t;
+    F.j0 = j0;
+    float wl[CPL];
+    load_cols<L>(&raw[0][t][j0], F.r);
+    load_cols<L>(&raw[1][t][j0], wl);
+    load_cols<L>(&raw[2][t][j0], F.k);
+    load_cols<L>(&raw[4][t][j0], F.a);
+    load_cols<L>(&raw[5][t][j0], F.b);
+    float g[CPL];
 #pragma unroll
-    for (int p = 0; p < (ROWS + 31) / 32; ++p) {
-        const int row = p * 32 + (tid >> 3), seg = tid & 7;
-        if (row < ROWS) {
-            const int vec = row / L, t = row % L;
-            const bf16_t* base = src.get(vec);
-            uint4 val = make_uint4(0, 0, 0, 0);
-            if (t0 + t < T && base != nullptr)
-                val = *reinterpret_cast<const uint4*>(
-                    base + ((t0 + t) * BH + bh) * CN + seg * 8);
-            *reinterpret_cast<uint4*>(&dst[vec][t][seg * 8]) = val;
+    for (int e = 0; e < CPL; ++e) {
+        const float l2 = -__builtin_amdgcn_exp2f(wl[e] * kLog2e) * kLog2e;
+        F.lam[e] = t < n ? l2 : 0.f;
+        g[e] = scan_lanes<L>(F.lam[e]);
+    }
+    bool bad = false;
+    float fA[CPL], fR[CPL], fB[CPL], fK[CPL];
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+        // g at tokens L/2 - 1 and L - 1 of this lane group (ds_swizzle in
+        // bitmask mode within 32 lanes: (lane & and_mask) | or_mask)
+        float gref, gL;
+        if constexpr (L == 32) {
+            gref = __int_as_float(
+                __builtin_amdgcn_ds_swizzle(__float_as_int(g[e]), 15 << 5));
+            gL = __int_as_float(
+                __builtin_amdgcn_ds_swizzle(__float_as_int(g[e]), 31 << 5));
+        } else {
+            gref = __int_as_float(__builtin_amdgcn_ds_swizzle(
+                __float_as_int(g[e]), 0x10 | (7 << 5)));
+            gL = __int_as_float(__builtin_amdgcn_ds_swizzle(
+                __float_as_int(g[e]), 0x10 | (15 << 5)));
+        }
+        bad |= (-gref > kHalfRange * kLog2e) ||
+               (gref - gL > kHalfRange * kLog2e);
+        F.eg[e] = __builtin_amdgcn_exp2f(g[e] - gref);
+        F.eng[e] = __builtin_amdgcn_exp2f(gref - g[e]);
+        F.eprev[e] = __builtin_amdgcn_exp2f(g[e] - F.lam[e] - gref);
+        fA[e] = F.a[e] * F.eprev[e];
+        fR[e] = F.r[e] * F.eg[e];
+        fB[e] = F.b[e] * F.eng[e];
+        fK[e] = F.k[e] * F.eng[e];
+        if (t == 0) {
+            eL[j0 + e] = __builtin_amdgcn_exp2f(gL);
+            eRef[j0 + e] = __builtin_amdgcn_exp2f(gref);
+            eLR[j0 + e] = __builtin_amdgcn_exp2f(gL - gref);
         }
     }
+    if (bad) *flag = 1;
+    store_cols<L>(&At[t][j0], fA);
+    store_cols<L>(&Rt[t][j0], fR);
+    store_cols<L>(&Bt[t][j0], fB);
+    store_cols<L>(&Kt[t][j0], fK);
 }
 
-// Write n (1, 2, 4, 8 or 16) consecutive bf16 values to LDS with the widest
-// aligned stores (dst must be aligned to 2 * n bytes, up to 16).
-template <int n>
-__device__ __forceinline__ void put_row(bf16_t* dst, const bf16_t* v) {
-    if constexpr (n == 1) {
-        dst[0] = v[0];
-    } else if constexpr (n == 2) {
-        *reinterpret_cast<uint32_t*>(dst) = uint32_t(v[0]) | (uint32_t(v[1]) << 16);
-    } else if constexpr (n == 4) {
-        *reinterpret_cast<uint2*>(dst) =
-            make_uint2(uint32_t(v[0]) | (uint32_t(v[1]) << 16),
-                       uint32_t(v[2]) | (uint32_t(v[3]) << 16));
-    } else {
-        static_assert(n % 8 == 0, "row length");
-#pragma unroll
-        for (int q = 0; q < n / 8; ++q)
-            *reinterpret_cast<uint4*>(dst + 8 * q) = make_uint4(
-                uint32_t(v[8 * q]) | (uint32_t(v[8 * q + 1]) << 16),
-                uint32_t(v[8 * q + 2]) | (uint32_t(v[8 * q + 3]) << 16),
-                uint32_t(v[8 * q + 4]) | (uint32_t(v[8 * q + 5]) << 16),
-                uint32_t(v[8 * q + 6]) | (uint32_t(v[8 * q + 7]) << 16));
-    }
-}
-
-// Minv = (I - Aab)^{-1} for the strictly lower-triangular L x L matrix Aab.
-// Inputs: Aab (bf16, [t][s], pitch PL) and its 16x16 diagonal blocks
-// transposed (AabTD, pitch 24).  Outputs Minv ([t][s]) and MinvT ([s][t]),
-// bf16, pitch PL.  Z is a per-wave 16 x 24 scratch (L/16 - 1 waves use it),
-// W a per-block scratch of five 16 x 24 tiles.  All NTH threads of the
-// workgroup must call it; it ends with a barrier.  Waves L/16 and up, which
-// have no diagonal block, run overlap() while waves 0 .. L/16-1 invert.
-//
-// Diagonal block p (wave p): A is nilpotent (A^16 = 0), so
-//   (I - A)^{-1} = (I + A)(I + A^2)(I + A^4)(I + A^8)
-// = P + P A^4 + (P + P A^4) A^8 with P = I + A + A^2 + A^3: four dependent
-// MFMA steps (bf16 operands, fp32 accumulation).  Off-diagonal blocks:
-// Minv[p][q] = Minv[p][p] * sum_{m=q}^{p-1} Aab[p][m] Minv[m][q], by block
-// distance p - q.
-template <int L, int NTH, typename Overlap>
-__device__ __forceinline__ void build_minv(const bf16_t* Aab,
-                                           const bf16_t (*AabTD)[16][24],
-                                           bf16_t* Minv, bf16_t* MinvT,
-                                           bf16_t (*Z)[16][24],
-                                           bf16_t (*W)[5][16][24], int tid,
-                                           Overlap overlap) {
-    constexpr int PL = L + 8, NB = L / 16;
-    const int wv = tid >> 6, lane = tid & 63;
+// ---------------------------------------------------------------------------
+// The four L x L matrices (stored transposed, pitch PL = L + 8):
+//   Aab = A~ B~^T, Aak = A~ K~^T (strictly lower), Arb = R~ B~^T,
+//   Ark = R~ K~^T (lower with diagonal).
+// aab_tiles: wave 0's part (Aab), matrix_tiles: the other three, spread over
+// waves 1 .. NWAVES-1.  extra(ti) is called for job indices past the three
+// matrices' tiles (ti >= 3 * tiles per matrix), letting callers append jobs.
+template <int L>
+__device__ __forceinline__ void aab_tiles(const bf16_t (*At)[PN],
+                                          const bf16_t (*Bt)[PN],
+                                          bf16_t (*Aab)[L + 8], int lane) {
+    constexpr int NB = L / 16, PL = L + 8;
     const int lr = lane & 15, lq = lane >> 4;
-    if (wv < NB) {
-        const int p = wv;
-        const bf16_t* Ap = Aab + 16 * p * PL + 16 * p;
-        const bf16_t* ApT = &AabTD[p][0][0];
-        bf16_t(*Bf)[16][24] = W[p];
-        // A^2
-        f32x4_t a2 = zero4();
-        mma_nt<16>(a2, Ap, PL, ApT, 24, lane);
-        store_tile_bf16(a2, &Bf[0][0][0], 24, lane);    // A^2
-        store_tile_bf16_t(a2, &Bf[1][0][0], 24, lane);  // (A^2)^T
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        // A^4 and P = I + A + A^2 + A^3
-        f32x4_t a4 = zero4(), pp = zero4();
-        mma_nt<16>(a4, &Bf[0][0][0], 24, &Bf[1][0][0], 24, lane);
-        mma_nt<16>(pp, Ap, PL, &Bf[1][0][0], 24, lane);
+#pragma unroll
+    for (int tb = 0; tb < NB; ++tb)
+#pragma unroll
+        for (int sb = 0; sb <= tb; ++sb) {
+            f32x4_t acc = zero4();
+#pragma unroll
+            for (int k0 = 0; k0 < CN; k0 += 32)
+                mfma(acc, frag_rk(&At[16 * tb][k0], PN, lane),
+                     frag_rk(&Bt[16 * sb][k0], PN, lane));
+            if (sb == tb) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[e] = (4 * lq + e > lr) ? acc[e] : 0.f;
+            }
+            store_tile_bf16_t(acc, &Aab[16 * sb][16 * tb], PL, lane);
+        }
+}
+
+// A masked lower tile (tb, sb) of X Y^T over K = 64 (X, Y token-major),
+// stored transposed into dst.
+template <int L>
+__device__ __forceinline__ void lower_tile(const bf16_t (*X)[PN],
+                                           const bf16_t (*Y)[PN],
+                                           bf16_t (*dst)[L + 8], int tb,
+                                           int sb, bool strict, int lane) {
+    const int lr = lane & 15, lq = lane >> 4;
+    f32x4_t acc = zero4();
+#pragma unroll
+    for (int k0 = 0; k0 < CN; k0 += 32)
+        mfma(acc, frag_rk(&X[16 * tb][k0], PN, lane),
+             frag_rk(&Y[16 * sb][k0], PN, lane));
+    if (sb == tb) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int t = 4 * lq + e;
-            pp[e] += ((t == lr) ? 1.f : 0.f) + bf16_to_f32(Ap[t * PL + lr]) +
-                     a2[e];
-        }
-        store_tile_bf16(a4, &Bf[2][0][0], 24, lane);    // A^4
-        store_tile_bf16_t(a4, &Bf[3][0][0], 24, lane);  // (A^4)^T
-        store_tile_bf16(pp, &Bf[4][0][0], 24, lane);    // P
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        // A^8 and P2 = P + P A^4
-        f32x4_t a8 = zero4();
-        mma_nt<16>(a8, &Bf[2][0][0], 24, &Bf[3][0][0], 24, lane);
-        mma_nt<16>(pp, &Bf[4][0][0], 24, &Bf[3][0][0], 24, lane);
-        store_tile_bf16_t(a8, &Bf[0][0][0], 24, lane);  // (A^8)^T
-        store_tile_bf16(pp, &Bf[1][0][0], 24, lane);    // P2
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        // Minv_pp = P2 + P2 A^8
-        mma_nt<16>(pp, &Bf[1][0][0], 24, &Bf[0][0][0], 24, lane);
-        store_tile_bf16(pp, Minv + 16 * p * PL + 16 * p, PL, lane);
-        store_tile_bf16_t(pp, MinvT + 16 * p * PL + 16 * p, PL, lane);
-    } else {
-        overlap();
-    }
-    if (NB > 1) {
-        // zero blocks: Minv above the block diagonal, MinvT below it
-        for (int e = tid; e < L * L; e += NTH) {
-            const int a = e / L, b = e % L;
-            if ((b >> 4) > (a >> 4)) {
-                Minv[a * PL + b] = 0;
-                MinvT[b * PL + a] = 0;
-            }
+            const int tt = 4 * lq + e;
+            const bool keep = strict ? (lr < tt) : (lr <= tt);
+            acc[e] = keep ? acc[e] : 0.f;
         }
     }
-    __syncthreads();
+    store_tile_bf16_t(acc, &dst[16 * sb][16 * tb], L + 8, lane);
+}
+
+// Lower tile number rem (of NB (NB + 1) / 2) -> (tb, sb).
+__device__ __forceinline__ void lower_tile_index(int rem, int& tb, int& sb) {
+    tb = rem < 1 ? 0 : 1;
+    sb = rem - tb;
+}
+
+// ---------------------------------------------------------------------------
+// Minv = (I - Aab)^{-1} on one wave, in two halves so that a barrier can sit
+// between them.  Per diagonal block p (A = Aab_pp, nilpotent, A^16 = 0):
+//   A2 = A A; P = I + A + A2 + A A2; A4 = A2 A2;       (minv_begin)
+//   P2 = P + P A4; A8 = A4 A4; Minv_pp = P2 + P2 A8   (minv_finish)
+// i.e. (I+A)(I+A^2)(I+A^4)(I+A^8); then, for L = 32,
+//   Minv_10 = Minv_11 (Aab_10 Minv_00).
+// Aab and MinvT are stored transposed (pitch L + 8); ms is scratch.  MinvT's
+// block above the diagonal must hold zeros.
+template <int L>
+__device__ __forceinline__ void minv_begin(const bf16_t (*Aab)[L + 8],
+                                           bf16_t (*ms)[4][16][24],
+                                           f32x4_t* pp, int lane) {
+    constexpr int NB = L / 16, PL = L + 8;
+    const int lr = lane & 15, lq = lane >> 4;
+    wave_lds_fence();
+    f32x4_t a2[NB];
 #pragma unroll
-    for (int kk = 1; kk < NB; ++kk) {
-        const int q = wv, p = wv + kk;
-        if (p < NB) {
-            f32x4_t z = zero4();
-            mma_nt_k<48>(z, &Aab[16 * p * PL + 16 * q], PL,
-                         &MinvT[16 * q * PL + 16 * q], PL, 16 * kk, lane);
-            store_tile_bf16_t(z, &Z[wv][0][0], 24, lane);
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            f32x4_t mq = zero4();
-            mma_nt<16>(mq, &Minv[16 * p * PL + 16 * p], PL, &Z[wv][0][0], 24,
-                       lane);
-            store_tile_bf16(mq, &Minv[16 * p * PL + 16 * q], PL, lane);
-            store_tile_bf16_t(mq, &MinvT[16 * q * PL + 16 * p], PL, lane);
-        }
-        __syncthreads();
+    for (int p = 0; p < NB; ++p) {
+        const bf16_t* Ap = &Aab[16 * p][16 * p];
+        a2[p] = zero4();
+        mfma(a2[p], frag_kr16(Ap, PL, lane), frag_rk16(Ap, PL, lane));
+        store_tile_bf16_t(a2[p], &ms[p][0][0][0], 24, lane);
+    }
+    wave_lds_fence();
+#pragma unroll
+    for (int p = 0; p < NB; ++p) {
+        const bf16_t* Ap = &Aab[16 * p][16 * p];
+        const f32x4_t at = unpack4(
+            *reinterpret_cast<const uint2*>(Ap + lr * PL + 4 * lq));
+        f32x4_t a4 = zero4();
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            pp[p][e] = ((4 * lq + e == lr) ? 1.f : 0.f) + at[e] + a2[p][e];
+        mfma(pp[p], frag_kr16(Ap, PL, lane),
+             frag_rk16(&ms[p][0][0][0], 24, lane));
+        mfma(a4, frag_kr16(&ms[p][0][0][0], 24, lane),
+             frag_rk16(&ms[p][0][0][0], 24, lane));
+        store_tile_bf16_t(a4, &ms[p][1][0][0], 24, lane);
+        store_tile_bf16_t(pp[p], &ms[p][2][0][0], 24, lane);
+    }
+}
+
+template <int L>
+__device__ __forceinline__ void minv_finish(const bf16_t (*Aab)[L + 8],
+                                            bf16_t (*ms)[4][16][24],
+                                            bf16_t (*MinvT)[L + 8],
+                                            f32x4_t* pp, int lane) {
+    constexpr int NB = L / 16, PL = L + 8;
+    wave_lds_fence();
+#pragma unroll
+    for (int p = 0; p < NB; ++p) {
+        f32x4_t a8 = zero4();
+        mfma(pp[p], frag_kr16(&ms[p][2][0][0], 24, lane),
+             frag_rk16(&ms[p][1][0][0], 24, lane));
+        mfma(a8, frag_kr16(&ms[p][1][0][0], 24, lane),
+             frag_rk16(&ms[p][1][0][0], 24, lane));
+        store_tile_bf16_t(a8, &ms[p][0][0][0], 24, lane);
+        store_tile_bf16_t(pp[p], &ms[p][3][0][0], 24, lane);
+    }
+    wave_lds_fence();
+#pragma unroll
+    for (int p = 0; p < NB; ++p) {
+        mfma(pp[p], frag_kr16(&ms[p][3][0][0], 24, lane),
+             frag_rk16(&ms[p][0][0][0], 24, lane));
+        store_tile_bf16_t(pp[p], &MinvT[16 * p][16 * p], PL, lane);
+    }
+    if constexpr (NB == 2) {
+        wave_lds_fence();
+        f32x4_t z = zero4();
+        mfma(z, frag_kr16(&Aab[0][16], PL, lane),
+             frag_rk16(&MinvT[0][0], PL, lane));
+        store_tile_bf16_t(z, &ms[0][1][0][0], 24, lane);
+        wave_lds_fence();
+        f32x4_t m10 = zero4();
+        mfma(m10, frag_kr16(&MinvT[16][16], PL, lane),
+             frag_rk16(&ms[0][1][0][0], 24, lane));
+        store_tile_bf16_t(m10, &MinvT[0][16], PL, lane);
+    }
+}
+
+// Zero the blocks above the diagonal of n L x L matrices (stored transposed:
+// memory rows s, columns t, block s > block t).  Called once per kernel.
+template <int L>
+__device__ __forceinline__ void zero_upper(bf16_t (*const* mats)[L + 8], int n,
+                                           int tid, int nth) {
+    for (int e = tid; e < L * L; e += nth) {
+        const int s = e / L, t = e % L;
+        if ((s >> 4) > (t >> 4))
+            for (int m = 0; m < n; ++m) mats[m][s][t] = 0;
     }
 }
 

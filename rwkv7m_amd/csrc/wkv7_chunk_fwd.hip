@@ -52,11 +52,12 @@ namespace rwkv7m {
 namespace {
 
 using chunk::CN;
-using chunk::kHalfRange;
+using chunk::fkr;
+using chunk::frk;
 using chunk::PN;
 
-constexpr int FWD_WAVES = 8;
-constexpr int FWD_THREADS = FWD_WAVES * 64;
+constexpr int FWD_WAVES = chunk::NWAVES;
+constexpr int FWD_THREADS = chunk::NTHREADS;
 
 template <int L>
 struct FwdSmem {
@@ -86,42 +87,6 @@ struct FwdSmem {
     float eL[2][CN], eRef[2][CN], eLR[2][CN];
     int flag[2];
 };
-
-// Fragments of a contraction over K = 16 or 32 tokens.
-template <int K>
-__device__ __forceinline__ bf16x8_t fkr(const bf16_t* M, int ld, int lane) {
-    if constexpr (K == 16) return frag_kr16(M, ld, lane);
-    else return frag_kr(M, ld, lane);
-}
-template <int K>
-__device__ __forceinline__ bf16x8_t frk(const bf16_t* M, int ld, int lane) {
-    if constexpr (K == 16) return frag_rk16(M, ld, lane);
-    else return frag_rk(M, ld, lane);
-}
-
-__device__ __forceinline__ void wave_lds_fence() {
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-}
-
-// Inclusive prefix sum over groups of L consecutive lanes (L = 16 or 32).
-template <int L>
-__device__ __forceinline__ float scan_lanes(float x) {
-#define RWKV7M_SHR(n)                                                       \
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), \
-                                                    0x110 + (n), 0xF, 0xF, \
-                                                    true))
-    RWKV7M_SHR(1);
-    RWKV7M_SHR(2);
-    RWKV7M_SHR(4);
-    RWKV7M_SHR(8);
-#undef RWKV7M_SHR
-    if constexpr (L == 32) {
-        // row_bcast:15 into rows 1 and 3 (from lane 15 of rows 0 and 2)
-        x += __int_as_float(__builtin_amdgcn_update_dpp(
-            0, __float_as_int(x), 0x142, 0xA, 0xF, false));
-    }
-    return x;
-}
 
 // Exact fp32 sequential forward over one chunk, reading the vectors from
 // HBM (the path for chunks outside the factored form's range).  S is the
@@ -205,12 +170,10 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
     const bool has_y = ytb < NB;
 
     // the matrices' and Minv's blocks above the diagonal stay zero
-    for (int e = tid; e < L * L; e += NTH) {
-        const int s = e / L, t = e % L;
-        if ((s >> 4) > (t >> 4)) {
-            sm.Aab[s][t] = 0; sm.Aak[s][t] = 0; sm.Arb[s][t] = 0;
-            sm.Ark[s][t] = 0; sm.MinvT[s][t] = 0;
-        }
+    {
+        bf16_t(*const mats[5])[PL] = {sm.Aab, sm.Aak, sm.Arb, sm.Ark,
+                                       sm.MinvT};
+        chunk::zero_upper<L>(mats, 5, tid, NTH);
     }
     if (tid < 2) sm.flag[tid] = 0;
 
@@ -316,90 +279,19 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             }
         }
         if (prep) {
-            // factors of chunk c+1; lane = (token t, columns j0 .. j0+CPL-1).
-            // Log-decays are kept in base 2: g2 = g log2(e).
-            const int t = lane % L, grp = lane / L;
-            const int j0 = 8 * wv + CPL * grp;
-            constexpr float kLog2e = 1.4426950408889634f;
-            float rv[CPL], wl[CPL], kv[CPL], av[CPL], bv[CPL];
-            auto ld = [&](int vec, float* dst) {
-                const bf16_t* p = &sm.raw[vec][t][j0];
-                if constexpr (CPL == 4) {
-                    const uint2 u = *reinterpret_cast<const uint2*>(p);
-                    dst[0] = __uint_as_float(u.x << 16);
-                    dst[1] = __uint_as_float(u.x & 0xffff0000u);
-                    dst[2] = __uint_as_float(u.y << 16);
-                    dst[3] = __uint_as_float(u.y & 0xffff0000u);
-                } else {
-                    const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
-                    dst[0] = __uint_as_float(u << 16);
-                    dst[1] = __uint_as_float(u & 0xffff0000u);
-                }
-            };
-            ld(0, rv); ld(1, wl); ld(2, kv); ld(4, av); ld(5, bv);
-            // v is copied as it is
+            // factors of chunk c+1; v is copied as it is
+            chunk::LaneFactors<L> fl;
+            chunk::chunk_factors<L>(sm.raw, n1, wv, lane, sm.f.At, sm.f.Rt,
+                                    sm.f.Bt, sm.f.Kt, sm.eL[nxt],
+                                    sm.eRef[nxt], sm.eLR[nxt], &sm.flag[nxt],
+                                    fl);
+            const int t = fl.t, j0 = fl.j0;
             if constexpr (CPL == 4)
                 *reinterpret_cast<uint2*>(&sm.f.Vc[t][j0]) =
                     *reinterpret_cast<const uint2*>(&sm.raw[3][t][j0]);
             else
                 *reinterpret_cast<uint32_t*>(&sm.f.Vc[t][j0]) =
                     *reinterpret_cast<const uint32_t*>(&sm.raw[3][t][j0]);
-            float lam[CPL], g[CPL];
-#pragma unroll
-            for (int e = 0; e < CPL; ++e) {
-                const float l2 =
-                    -__builtin_amdgcn_exp2f(wl[e] * kLog2e) * kLog2e;
-                lam[e] = t < n1 ? l2 : 0.f;
-                g[e] = scan_lanes<L>(lam[e]);
-            }
-            bool bad = false;
-            float fA[CPL], fR[CPL], fB[CPL], fK[CPL];
-#pragma unroll
-            for (int e = 0; e < CPL; ++e) {
-                // g at tokens L/2 - 1 and L - 1 of this lane group, by
-                // ds_swizzle (bitmask mode within 32 lanes: lane | or_mask)
-                float gref, gL;
-                if constexpr (L == 32) {
-                    gref = __int_as_float(__builtin_amdgcn_ds_swizzle(
-                        __float_as_int(g[e]), 15 << 5));
-                    gL = __int_as_float(__builtin_amdgcn_ds_swizzle(
-                        __float_as_int(g[e]), 31 << 5));
-                } else {
-                    gref = __int_as_float(__builtin_amdgcn_ds_swizzle(
-                        __float_as_int(g[e]), 0x10 | (7 << 5)));
-                    gL = __int_as_float(__builtin_amdgcn_ds_swizzle(
-                        __float_as_int(g[e]), 0x10 | (15 << 5)));
-                }
-                bad |= (-gref > kHalfRange * kLog2e) ||
-                       (gref - gL > kHalfRange * kLog2e);
-                const float eg = __builtin_amdgcn_exp2f(g[e] - gref);
-                const float eng = __builtin_amdgcn_exp2f(gref - g[e]);
-                const float eprev =
-                    __builtin_amdgcn_exp2f(g[e] - lam[e] - gref);
-                fA[e] = av[e] * eprev;
-                fR[e] = rv[e] * eg;
-                fB[e] = bv[e] * eng;
-                fK[e] = kv[e] * eng;
-                if (t == 0) {
-                    sm.eL[nxt][j0 + e] = __builtin_amdgcn_exp2f(gL);
-                    sm.eRef[nxt][j0 + e] = __builtin_amdgcn_exp2f(gref);
-                    sm.eLR[nxt][j0 + e] = __builtin_amdgcn_exp2f(gL - gref);
-                }
-            }
-            if (bad) sm.flag[nxt] = 1;
-            auto put = [&](bf16_t (*dst)[PN], const float* x) {
-                bf16_t* p = &dst[t][j0];
-                if constexpr (CPL == 4) {
-                    uint2 u;
-                    u.x = pack_bf16x2(x[0], x[1]);
-                    u.y = pack_bf16x2(x[2], x[3]);
-                    *reinterpret_cast<uint2*>(p) = u;
-                } else {
-                    *reinterpret_cast<uint32_t*>(p) = pack_bf16x2(x[0], x[1]);
-                }
-            };
-            put(sm.f.At, fA); put(sm.f.Rt, fR); put(sm.f.Bt, fB);
-            put(sm.f.Kt, fK);
         }
         __syncthreads();
 
@@ -434,124 +326,29 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         f32x4_t mi_pp[NB];
         if (prep) {
             if (wv == 0) {
-                // Aab lower tiles (strict), stored transposed
-#pragma unroll
-                for (int tb = 0; tb < NB; ++tb)
-#pragma unroll
-                    for (int sb = 0; sb <= tb; ++sb) {
-                        f32x4_t acc = zero4();
-#pragma unroll
-                        for (int k0 = 0; k0 < CN; k0 += 32)
-                            mfma(acc,
-                                 frag_rk(&sm.f.At[16 * tb][k0], PN, lane),
-                                 frag_rk(&sm.f.Bt[16 * sb][k0], PN, lane));
-                        if (sb == tb) {
-#pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                acc[e] = (4 * lq + e > lr) ? acc[e] : 0.f;
-                        }
-                        store_tile_bf16_t(acc, &sm.Aab[16 * sb][16 * tb], PL,
-                                          lane);
-                    }
-                // Minv diagonal blocks p (A = Aab_pp):
-                //   A2 = A A; P = I + A + A2 + A A2; A4 = A2 A2;
-                //   P2 = P + P A4; A8 = A4 A4; Minv_pp = P2 + P2 A8
-                wave_lds_fence();
-                f32x4_t a2[NB];
-#pragma unroll
-                for (int p = 0; p < NB; ++p) {
-                    const bf16_t* Ap = &sm.Aab[16 * p][16 * p];
-                    a2[p] = zero4();
-                    mfma(a2[p], frag_kr16(Ap, PL, lane),
-                         frag_rk16(Ap, PL, lane));
-                    store_tile_bf16_t(a2[p], &sm.ms[p][0][0][0], 24, lane);
-                }
-                wave_lds_fence();
-#pragma unroll
-                for (int p = 0; p < NB; ++p) {
-                    const bf16_t* Ap = &sm.Aab[16 * p][16 * p];
-                    const f32x4_t at = unpack4(*reinterpret_cast<const uint2*>(
-                        Ap + lr * PL + 4 * lq));  // A[4lq+e][lr]
-                    f32x4_t a4 = zero4(), pp;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        pp[e] = ((4 * lq + e == lr) ? 1.f : 0.f) + at[e] +
-                                a2[p][e];
-                    mfma(pp, frag_kr16(Ap, PL, lane),
-                         frag_rk16(&sm.ms[p][0][0][0], 24, lane));
-                    mfma(a4, frag_kr16(&sm.ms[p][0][0][0], 24, lane),
-                         frag_rk16(&sm.ms[p][0][0][0], 24, lane));
-                    mi_pp[p] = pp;
-                    store_tile_bf16_t(a4, &sm.ms[p][1][0][0], 24, lane);
-                    store_tile_bf16_t(pp, &sm.ms[p][2][0][0], 24, lane);
-                }
+                chunk::aab_tiles<L>(sm.f.At, sm.f.Bt, sm.Aab, lane);
+                chunk::minv_begin<L>(sm.Aab, sm.ms, mi_pp, lane);
             } else {
                 // Aak (strict), Arb, Ark (with diagonal): lower tiles
                 constexpr int TPM = NB * (NB + 1) / 2;
                 for (int ti = wv - 1; ti < 3 * TPM; ti += NW - 1) {
-                    const int mat = ti / TPM, rem = ti % TPM;
-                    const int tb = rem < 1 ? 0 : 1;
-                    const int sb = rem - tb;
-                    const bf16_t(*Xo)[PN] = mat == 0 ? sm.f.At : sm.f.Rt;
-                    const bf16_t(*Yo)[PN] = mat == 1 ? sm.f.Bt : sm.f.Kt;
-                    bf16_t(*dst)[PL] = mat == 0   ? sm.Aak
-                                       : mat == 1 ? sm.Arb
-                                                  : sm.Ark;
-                    f32x4_t acc = zero4();
-#pragma unroll
-                    for (int k0 = 0; k0 < CN; k0 += 32)
-                        mfma(acc, frag_rk(&Xo[16 * tb][k0], PN, lane),
-                             frag_rk(&Yo[16 * sb][k0], PN, lane));
-                    if (sb == tb) {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int tt = 4 * lq + e;
-                            const bool keep =
-                                mat == 0 ? (lr < tt) : (lr <= tt);
-                            acc[e] = keep ? acc[e] : 0.f;
-                        }
-                    }
-                    store_tile_bf16_t(acc, &dst[16 * sb][16 * tb], PL, lane);
+                    const int mat = ti / TPM;
+                    int tb, sb;
+                    chunk::lower_tile_index(ti % TPM, tb, sb);
+                    chunk::lower_tile<L>(mat == 0 ? sm.f.At : sm.f.Rt,
+                                         mat == 1 ? sm.f.Bt : sm.f.Kt,
+                                         mat == 0   ? sm.Aak
+                                         : mat == 1 ? sm.Arb
+                                                    : sm.Ark,
+                                         tb, sb, mat == 0, lane);
                 }
             }
         }
         __syncthreads();
 
         // ================= phase I =======================================
-        if (prep && wv == 0) {
-            wave_lds_fence();
-#pragma unroll
-            for (int p = 0; p < NB; ++p) {
-                f32x4_t a8 = zero4();
-                mfma(mi_pp[p], frag_kr16(&sm.ms[p][2][0][0], 24, lane),
-                     frag_rk16(&sm.ms[p][1][0][0], 24, lane));
-                mfma(a8, frag_kr16(&sm.ms[p][1][0][0], 24, lane),
-                     frag_rk16(&sm.ms[p][1][0][0], 24, lane));
-                store_tile_bf16_t(a8, &sm.ms[p][0][0][0], 24, lane);
-                store_tile_bf16_t(mi_pp[p], &sm.ms[p][3][0][0], 24, lane);
-            }
-            wave_lds_fence();
-#pragma unroll
-            for (int p = 0; p < NB; ++p) {
-                mfma(mi_pp[p], frag_kr16(&sm.ms[p][3][0][0], 24, lane),
-                     frag_rk16(&sm.ms[p][0][0][0], 24, lane));
-                store_tile_bf16_t(mi_pp[p], &sm.MinvT[16 * p][16 * p], PL,
-                                  lane);
-            }
-            if constexpr (NB == 2) {
-                // Minv_10 = Minv_11 (Aab_10 Minv_00)
-                wave_lds_fence();
-                f32x4_t z = zero4();
-                mfma(z, frag_kr16(&sm.Aab[0][16], PL, lane),
-                     frag_rk16(&sm.MinvT[0][0], PL, lane));
-                store_tile_bf16_t(z, &sm.ms[0][1][0][0], 24, lane);
-                wave_lds_fence();
-                f32x4_t m10 = zero4();
-                mfma(m10, frag_kr16(&sm.MinvT[16][16], PL, lane),
-                     frag_rk16(&sm.ms[0][1][0][0], 24, lane));
-                store_tile_bf16_t(m10, &sm.MinvT[0][16], PL, lane);
-            }
-        }
+        if (prep && wv == 0)
+            chunk::minv_finish<L>(sm.Aab, sm.ms, sm.MinvT, mi_pp, lane);
         // C^T += K~^T V (scaled as above), P^T += V^T Ark^T (wave 0: phase W)
         auto c_kv = [&] {
 #pragma unroll

@@ -264,9 +264,6 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         SL[q] = unpack4(*reinterpret_cast<const uint2*>(
             ckpt + nch * BH * NN + sbase + toff[q]));
     }
-    // dV tile of this wave: rows i = 16*vib + 4*lq + e, column s = 16*vsb + lr
-    const int vib = wv & 3, vsb = wv >> 2;
-    const bool has_v = vsb < NB;
 
     if (tid == 0) sm.flag = 0;
     {
@@ -279,29 +276,30 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
     constexpr int NPRE = (SEGV + NTH - 1) / NTH;
     static_assert(CN * CN * 2 / 16 == NTH, "one S_0 segment per thread");
     uint4 pre[NPRE], pres;
-    const bf16_t* pbase[NPRE];
-    int ptok[NPRE];
-#pragma unroll
-    for (int p = 0; p < NPRE; ++p) {
-        const int seg = p * NTH + tid;
-        const int row = seg >> 3, s8 = seg & 7;
-        const int vec = row / L, t = row % L;
-        const bf16_t* base = src.get(vec < 7 ? vec : 0);
-        ptok[p] = (seg < SEGV && base != nullptr) ? t : (1 << 30);
-        pbase[p] = (base != nullptr ? base : r) +
-                   (int64_t(t) * BH + bh) * CN + s8 * 8;
-    }
-    const int64_t chunk_stride = int64_t(L) * BH * CN;
-    const bf16_t* const sbase_ck = ckpt + sbase + 8 * tid;
-    auto fetch = [&](int64_t cc) {
+    // part p < NPRE: one 16-byte segment of the vectors; part NPRE: S_0
+    // (addresses are formed at each fetch: kept across the loop they would
+    // hold registers for the whole run)
+    auto fetch_part = [&](int64_t cc, int part, int tidv) {
 #pragma unroll
         for (int p = 0; p < NPRE; ++p) {
-            pre[p] = make_uint4(0, 0, 0, 0);
-            if (cc * L + ptok[p] < T)
-                pre[p] = *reinterpret_cast<const uint4*>(pbase[p] +
-                                                         cc * chunk_stride);
+            if (p == part) {
+                const int seg = p * NTH + tidv;
+                const int row = seg >> 3, s8 = seg & 7;
+                const int vec = row / L, t = row % L;
+                const bf16_t* base = src.get(vec);
+                pre[p] = make_uint4(0, 0, 0, 0);
+                if (seg < SEGV && base != nullptr && cc * L + t < T)
+                    pre[p] = *reinterpret_cast<const uint4*>(
+                        base + ((cc * L + t) * BH + bh) * CN + s8 * 8);
+            }
         }
-        pres = *reinterpret_cast<const uint4*>(sbase_ck + cc * BH * NN);
+        if (part == NPRE)
+            pres = *reinterpret_cast<const uint4*>(
+                ckpt + cc * BH * NN + sbase + 8 * tidv);
+    };
+    auto fetch = [&](int64_t cc, int tidv) {
+#pragma unroll
+        for (int p = 0; p <= NPRE; ++p) fetch_part(cc, p, tidv);
     };
     auto stash = [&]() {
 #pragma unroll
@@ -315,13 +313,29 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         }
         *reinterpret_cast<uint4*>(&sm.S0s[tid >> 3][8 * (tid & 7)]) = pres;
     };
-    fetch(nch - 1);
+    fetch(nch - 1, tid);
     stash();
     // everything loaded before the loop has arrived: the loop's waits then
     // only count the prefetch and the stores
     __builtin_amdgcn_s_waitcnt(0);
-    if (nch > 1) fetch(nch - 2);
     __syncthreads();
+
+    // Each chunk's HBM traffic is spread over its phases instead of one
+    // burst per chunk: the previous chunk's vectors are fetched a part per
+    // phase (2 .. 6) and stashed in phase 7, and the gradients computed in
+    // phase 7 (kept as bf16 pairs) are stored during phases 2 .. 4 of the
+    // next chunk.
+    // The gradients computed in phase 7 wait in registers (bf16 pairs) and
+    // are stored during phases 2 .. 4 of the next chunk.
+    uint32_t pend[5][CPL / 2];  // dr, dw, dk, dneg_kk, dkka
+    uint2 pend_dv = make_uint2(0, 0);
+    int64_t pend_off = -1, pend_voff = -1;  // -1: nothing to store
+    auto store_pair = [&](bf16_t* dst, const uint32_t* val) {
+        if constexpr (CPL == 4)
+            *reinterpret_cast<uint2*>(dst) = make_uint2(val[0], val[1]);
+        else
+            *reinterpret_cast<uint32_t*>(dst) = val[0];
+    };
 
     for (int64_t c = nch - 1; c >= 0; --c) {
         const int64_t t0 = c * L;
@@ -331,6 +345,17 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         int tid_it = threadIdx.x;
         asm volatile("" : "+v"(tid_it));
         const int tid = tid_it, lane = tid & 63, lr = lane & 15, lq = lane >> 4;
+        const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+        // dV tile of this wave: rows i = 16*vib + 4*lq + e, column
+        // s = 16*vsb + lr
+        const int vib = wv & 3, vsb = wv >> 2;
+        const bool has_v = vsb < NB;
+        int toff[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int si = 2 * wv + q, jb = si >> 2, ib = si & 3;
+            toff[q] = (16 * ib + lr) * CN + 16 * jb + 4 * lq;
+        }
 
         // ================= 1: factors; S_0 tiles =========================
         chunk::LaneFactors<L> fl;
@@ -357,6 +382,17 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
 
         if (fallback) {
             // ---- exact sequential reverse pass for this chunk -------------
+            if (pend_off >= 0) {
+                store_pair(dr + pend_off, pend[0]);
+                store_pair(dw + pend_off, pend[1]);
+                store_pair(dk + pend_off, pend[2]);
+                store_pair(da + pend_off, pend[3]);
+                store_pair(db + pend_off, pend[4]);
+            }
+            if (pend_voff >= 0)
+                *reinterpret_cast<uint2*>(dv + pend_voff) = pend_dv;
+            pend_off = pend_voff = -1;
+            if (c >= 1) fetch(c - 1, tid);
 #pragma unroll
             for (int q = 0; q < 2; ++q)
 #pragma unroll
@@ -369,6 +405,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             seq_chunk_backward<L, NW>(sm.raw, n, sm.fb.Sf, sm.fb.Df, sm.fb.red,
                                       t0, BH, bh, dr, dw, dk, dv, da, db, tid);
             __syncthreads();
+            if (c >= 1) stash();
 #pragma unroll
             for (int q = 0; q < 2; ++q)
 #pragma unroll
@@ -376,6 +413,11 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                     D[q][e] = sm.fb.Df[(toff[q] / CN) * 65 + toff[q] % CN + e];
         } else {
             // ================= 2 ==========================================
+            if (pend_off >= 0) {
+                store_pair(dr + pend_off, pend[0]);
+                store_pair(dw + pend_off, pend[1]);
+            }
+            if (c >= 1) fetch_part(c - 1, 0, tid);
             // S' = S_0 e^{g_ref} and D' = D e^{g_L - g_ref} ([i][j]);
             // sum_i D[i][j] S_L[i][j] per column (the decay's tail)
             {
@@ -399,7 +441,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                     for (int e = 0; e < 4; ++e) tl[e] += D[q][e] * SL[q][e];
                 }
 #pragma unroll
-                for (int e = 0; e < 4; ++e) tl[e] = group_sum<16>(tl[e]);
+                for (int e = 0; e < 4; ++e) tl[e] = chunk::row_sum16(tl[e]);
                 if (lr == 0) {
                     const int j = 16 * ((2 * wv) >> 2) + 4 * lq;
                     *reinterpret_cast<float4*>(&sm.part[wv & 1][j]) =
@@ -441,6 +483,11 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             __syncthreads();
 
             // ================= 3 ==========================================
+            if (pend_off >= 0) {
+                store_pair(dk + pend_off, pend[2]);
+                store_pair(da + pend_off, pend[3]);
+            }
+            if (c >= 1) fetch_part(c - 1, 1, tid);
             if (wv == 0) {
                 chunk::minv_finish<L>(sm.m.Aab, sm.m.ms, sm.m.MinvT, mi_pp,
                                       lane);
@@ -475,6 +522,10 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             __syncthreads();
 
             // ================= 4 ==========================================
+            if (pend_off >= 0) store_pair(db + pend_off, pend[4]);
+            if (pend_voff >= 0)
+                *reinterpret_cast<uint2*>(dv + pend_voff) = pend_dv;
+            if (c >= 1 && NPRE > 2) fetch_part(c - 1, 2, tid);
             // X = Minv U -> X[t][i]; dU = Minv^T dX -> dU[t][i]
             for (int ti = wv; ti < 8 * NB; ti += NW) {
                 const bool isdU = ti >= 4 * NB;
@@ -493,6 +544,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             __syncthreads();
 
             // ================= 5 ==========================================
+            if (c >= 1 && NPRE > 3) fetch_part(c - 1, 3, tid);
             // dArb = dY X^T (with diagonal), dAab = dU X^T, dAak = dU V^T
             // (strict)
             for (int ti = wv; ti < 3 * TPM; ti += NW) {
@@ -542,10 +594,12 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             __syncthreads();
 
             // ================= 6 ==========================================
+            if (c >= 1) fetch_part(c - 1, NPRE, tid);
+            if (c >= 1 && NPRE == 2) fetch_part(c - 1, 2, tid);
             // transposed tiles of dR~, dA~, dB~, dK~ -> g[t][j] (fp32)
             // (tiles: gradient x t block x j block)
             constexpr int NTG = 16 * NB;
-#pragma unroll
+#pragma unroll 1
             for (int it = 0; it < NTG / NW; ++it) {
                 const int ti = wv + NW * it;
                 const int gsel = ti / (4 * NB), rem = ti % (4 * NB);
@@ -642,32 +696,37 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                     dwv[e] = (chunk::suffix_scan_lanes<L>(f, lane) + tail) *
                              fl.lam[e] * kLn2;
                 }
-                if (t < n) {
-                    const int64_t off = ((t0 + t) * BH + bh) * CN + j0;
-                    chunk::store_cols<L>(dr + off, drv);
-                    chunk::store_cols<L>(dw + off, dwv);
-                    chunk::store_cols<L>(dk + off, dkv);
-                    chunk::store_cols<L>(da + off, dav);
-                    chunk::store_cols<L>(db + off, dbv);
+#pragma unroll
+                for (int h = 0; h < CPL / 2; ++h) {
+                    pend[0][h] = pack_bf16x2(drv[2 * h], drv[2 * h + 1]);
+                    pend[1][h] = pack_bf16x2(dwv[2 * h], dwv[2 * h + 1]);
+                    pend[2][h] = pack_bf16x2(dkv[2 * h], dkv[2 * h + 1]);
+                    pend[3][h] = pack_bf16x2(dav[2 * h], dav[2 * h + 1]);
+                    pend[4][h] = pack_bf16x2(dbv[2 * h], dbv[2 * h + 1]);
                 }
+                pend_off = t < n ? ((t0 + t) * BH + bh) * CN + j0 : -1;
                 const int s = 16 * vsb + lr;
-                if (has_v && s < n)
-                    *reinterpret_cast<uint2*>(
-                        dv + ((t0 + s) * BH + bh) * CN + 16 * vib + 4 * lq) =
-                        pack4(dvt);
+                pend_dv = pack4(dvt);
+                pend_voff = (has_v && s < n)
+                                ? ((t0 + s) * BH + bh) * CN + 16 * vib + 4 * lq
+                                : -1;
             }
             D[0] = Dn[0];
             D[1] = Dn[1];
         }
-        // ---- the previous chunk's data to LDS (the fallback path); the
-        // one before in flight
-        if (fallback && c >= 1) stash();
         SL[0] = S0[0];
         SL[1] = S0[1];
         if (tid == 0) sm.flag = 0;
-        if (c >= 2) fetch(c - 2);
         __syncthreads();
     }
+    if (pend_off >= 0) {
+        store_pair(dr + pend_off, pend[0]);
+        store_pair(dw + pend_off, pend[1]);
+        store_pair(dk + pend_off, pend[2]);
+        store_pair(da + pend_off, pend[3]);
+        store_pair(db + pend_off, pend[4]);
+    }
+    if (pend_voff >= 0) *reinterpret_cast<uint2*>(dv + pend_voff) = pend_dv;
 #pragma unroll
     for (int q = 0; q < 2; ++q)
         *reinterpret_cast<float4*>(ds0 + sbase + toff[q]) =

@@ -102,6 +102,20 @@ __device__ __forceinline__ float suffix_scan_lanes(float x, int lane) {
     return x;
 }
 
+// Sum over each row of 16 lanes, in every lane of the row (DPP row_ror).
+__device__ __forceinline__ float row_sum16(float x) {
+#define RWKV7M_ROR(n)                                                       \
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), \
+                                                    0x120 + (n), 0xF, 0xF, \
+                                                    false))
+    RWKV7M_ROR(8);
+    RWKV7M_ROR(4);
+    RWKV7M_ROR(2);
+    RWKV7M_ROR(1);
+#undef RWKV7M_ROR
+    return x;
+}
+
 // Value of lane t + 1 of the same group of L lanes (0 for the group's last
 // lane), by wave_shl:1.
 template <int L>

@@ -86,8 +86,10 @@ struct BwdSmem {
             float Sf[CN * 65], Df[CN * 65], red[BWD_WAVES * 5 * CN];
         } fb;
     };
-    float eL[CN], eRef[CN], eLR[CN];
-    float part[2][CN];  // sum_i D S_L over the two halves of i
+    alignas(16) float eL[CN];
+    alignas(16) float eRef[CN];
+    alignas(16) float eLR[CN];
+    alignas(16) float part[2][CN];  // sum_i D S_L over the two halves of i
     int flag;
 };
 
@@ -321,12 +323,11 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
     __syncthreads();
 
     // Each chunk's HBM traffic is spread over its phases instead of one
-    // burst per chunk: the previous chunk's vectors are fetched a part per
-    // phase (2 .. 6) and stashed in phase 7, and the gradients computed in
-    // phase 7 (kept as bf16 pairs) are stored during phases 2 .. 4 of the
-    // next chunk.
-    // The gradients computed in phase 7 wait in registers (bf16 pairs) and
-    // are stored during phases 2 .. 4 of the next chunk.
+    // burst per chunk: the previous chunk's S_0 (phase 2) and vectors (a
+    // part per phase, 3 .. 5) are fetched early enough to have arrived by
+    // the stash in phase 7, and the gradients computed in phase 7 wait in
+    // registers (bf16 pairs) and are stored during phases 2 .. 4 of the next
+    // chunk.
     uint32_t pend[5][CPL / 2];  // dr, dw, dk, dneg_kk, dkka
     uint2 pend_dv = make_uint2(0, 0);
     int64_t pend_off = -1, pend_voff = -1;  // -1: nothing to store
@@ -406,6 +407,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                                       t0, BH, bh, dr, dw, dk, dv, da, db, tid);
             __syncthreads();
             if (c >= 1) stash();
+            chunk::wait_vmem();
 #pragma unroll
             for (int q = 0; q < 2; ++q)
 #pragma unroll
@@ -417,7 +419,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                 store_pair(dr + pend_off, pend[0]);
                 store_pair(dw + pend_off, pend[1]);
             }
-            if (c >= 1) fetch_part(c - 1, 0, tid);
+            if (c >= 1) fetch_part(c - 1, NPRE, tid);  // S_0 first
             // S' = S_0 e^{g_ref} and D' = D e^{g_L - g_ref} ([i][j]);
             // sum_i D[i][j] S_L[i][j] per column (the decay's tail)
             {
@@ -487,7 +489,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                 store_pair(dk + pend_off, pend[2]);
                 store_pair(da + pend_off, pend[3]);
             }
-            if (c >= 1) fetch_part(c - 1, 1, tid);
+            if (c >= 1) fetch_part(c - 1, 0, tid);
             if (wv == 0) {
                 chunk::minv_finish<L>(sm.m.Aab, sm.m.ms, sm.m.MinvT, mi_pp,
                                       lane);
@@ -525,11 +527,14 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             if (pend_off >= 0) store_pair(db + pend_off, pend[4]);
             if (pend_voff >= 0)
                 *reinterpret_cast<uint2*>(dv + pend_voff) = pend_dv;
-            if (c >= 1 && NPRE > 2) fetch_part(c - 1, 2, tid);
-            // X = Minv U -> X[t][i]; dU = Minv^T dX -> dU[t][i]
-            for (int ti = wv; ti < 8 * NB; ti += NW) {
-                const bool isdU = ti >= 4 * NB;
-                const int rem = ti % (4 * NB), tb = rem / 4, ib = rem % 4;
+            if (c >= 1) fetch_part(c - 1, 1, tid);
+            // X = Minv U -> X[t][i]; dU = Minv^T dX -> dU[t][i].  NB = 2:
+            // every wave one X and one dU tile (t block wv / 4, i block
+            // wv % 4); NB = 1: waves 0-3 X, waves 4-7 dU.
+#pragma unroll
+            for (int it = 0; it < NB; ++it) {
+                const bool isdU = NB == 2 ? it == 1 : wv >= 4;
+                const int tb = NB == 2 ? wv >> 2 : 0, ib = wv & 3;
                 f32x4_t acc = zero4();
                 if (!isdU) {
                     mfma(acc, frk<L>(&sm.m.Ut[16 * ib][0], PL, lane),
@@ -544,6 +549,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             __syncthreads();
 
             // ================= 5 ==========================================
+            if (c >= 1 && NPRE > 2) fetch_part(c - 1, 2, tid);
             if (c >= 1 && NPRE > 3) fetch_part(c - 1, 3, tid);
             // dArb = dY X^T (with diagonal), dAab = dU X^T, dAak = dU V^T
             // (strict)
@@ -594,16 +600,9 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             __syncthreads();
 
             // ================= 6 ==========================================
-            if (c >= 1) fetch_part(c - 1, NPRE, tid);
-            if (c >= 1 && NPRE == 2) fetch_part(c - 1, 2, tid);
-            // transposed tiles of dR~, dA~, dB~, dK~ -> g[t][j] (fp32)
-            // (tiles: gradient x t block x j block)
-            constexpr int NTG = 16 * NB;
-#pragma unroll 1
-            for (int it = 0; it < NTG / NW; ++it) {
-                const int ti = wv + NW * it;
-                const int gsel = ti / (4 * NB), rem = ti % (4 * NB);
-                const int tb = rem / 4, jb = rem % 4;
+            // one transposed tile (t block tb, j block jb) of dR~, dA~, dB~
+            // or dK~ (gsel 0 .. 3)
+            auto grad_tile = [&](int gsel, int tb, int jb) {
                 f32x4_t acc = zero4();
                 float(*gdst)[CN + 4];
                 if (gsel == 0) {
@@ -654,6 +653,21 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                 *reinterpret_cast<float4*>(
                     &gdst[16 * tb + lr][16 * jb + 4 * lq]) =
                     make_float4(acc[0], acc[1], acc[2], acc[3]);
+            };
+            // transposed tiles of dR~, dA~, dB~, dK~ -> g[t][j] (fp32).
+            // NB = 2: every wave the (t block wv / 4, j block wv % 4) tile of
+            // all four, two at a time; NB = 1: two of the four (wv / 4 picks
+            // which), j block wv % 4.
+            if constexpr (NB == 2) {
+                const int tb = wv >> 2, jb = wv & 3;
+                grad_tile(0, tb, jb);
+                grad_tile(1, tb, jb);
+                __builtin_amdgcn_sched_barrier(0);
+                grad_tile(2, tb, jb);
+                grad_tile(3, tb, jb);
+            } else {
+                grad_tile(wv >> 2, 0, wv & 3);
+                grad_tile(2 + (wv >> 2), 0, wv & 3);
             }
             __syncthreads();
 
@@ -662,6 +676,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             // to LDS first, so that waiting for their loads does not also wait
             // for this chunk's stores (one counter covers loads and stores).
             if (c >= 1) stash();
+            chunk::wait_vmem();
             {
                 const int t = fl.t, j0 = fl.j0;
                 float gRv[CPL], gAv[CPL], gBv[CPL], gKv[CPL];

@@ -60,6 +60,26 @@ __device__ __forceinline__ void wave_lds_fence() {
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 }
 
+// s_waitcnt vmcnt(0): every vector memory access of this wave has completed.
+// Placed where the loads of a conditional prefetch are known to be consumed:
+// the compiler's wait insertion does not correlate the prefetch's condition
+// with the consumer's, and would otherwise treat the registers those loads
+// wrote as still pending and wait for all outstanding loads and stores
+// (a full HBM round trip) when it next reuses them.
+__device__ __forceinline__ void wait_vmem() {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt 0, expcnt 7, lgkmcnt 15
+}
+
+// Keeps a cross-lane result (DPP, ds_swizzle) where it is computed, with
+// every lane active.  A cross-lane value consumed only under a condition,
+// such as select(first token, v, previous lane's value), may otherwise be
+// moved into a branch, where the lanes outside the branch no longer supply
+// their values.
+__device__ __forceinline__ float pin_lanes(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 // Inclusive prefix sum over groups of L consecutive lanes (L = 16 or 32).
 template <int L>
 __device__ __forceinline__ float scan_lanes(float x) {
@@ -95,8 +115,8 @@ __device__ __forceinline__ float suffix_scan_lanes(float x, int lane) {
     if constexpr (L == 32) {
         // rows 0 and 2 add the total of rows 1 and 3 (lane 16 of each
         // 32-lane half, by ds_swizzle in bitmask mode: lane | 16)
-        const float hi = __int_as_float(
-            __builtin_amdgcn_ds_swizzle(__float_as_int(x), 16 << 5));
+        const float hi = pin_lanes(__int_as_float(
+            __builtin_amdgcn_ds_swizzle(__float_as_int(x), 16 << 5)));
         x += (lane & 16) ? 0.f : hi;
     }
     return x;
@@ -120,9 +140,17 @@ __device__ __forceinline__ float row_sum16(float x) {
 // lane), by wave_shl:1.
 template <int L>
 __device__ __forceinline__ float next_token(float x, int lane) {
-    const float y = __int_as_float(__builtin_amdgcn_update_dpp(
-        0, __float_as_int(x), 0x130, 0xF, 0xF, true));
+    const float y = pin_lanes(__int_as_float(__builtin_amdgcn_update_dpp(
+        0, __float_as_int(x), 0x130, 0xF, 0xF, true)));
     return (lane % L == L - 1) ? 0.f : y;
+}
+
+// Value of lane l - 1 (wave_shr:1; lane 0 receives 0).  Lanes at the start
+// of a group of L lanes receive the previous group's last value, which
+// callers replace.
+__device__ __forceinline__ float prev_lane(float x) {
+    return pin_lanes(__int_as_float(__builtin_amdgcn_update_dpp(
+        0, __float_as_int(x), 0x138, 0xF, 0xF, true)));
 }
 
 // ---------------------------------------------------------------------------
@@ -171,6 +199,15 @@ __device__ __forceinline__ void store_cols(bf16_t* p, const float* x) {
     }
 }
 
+// CPL consecutive floats (16-byte or 8-byte aligned) in one LDS write.
+template <int CPL>
+__device__ __forceinline__ void store_f32(float* p, const float* x) {
+    if constexpr (CPL == 4)
+        *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+    else
+        *reinterpret_cast<float2*>(p) = make_float2(x[0], x[1]);
+}
+
 template <int L>
 __device__ __forceinline__ void chunk_factors(
     const bf16_t (*raw)[L][PN], int n, int wv, int lane, bf16_t (*At)[PN],
@@ -188,14 +225,23 @@ __device__ __forceinline__ void chunk_factors(
     load_cols<L>(&raw[4][t][j0], F.a);
     load_cols<L>(&raw[5][t][j0], F.b);
     float g[CPL];
+    const bool valid = t < n;
 #pragma unroll
     for (int e = 0; e < CPL; ++e) {
-        const float l2 = -__builtin_amdgcn_exp2f(wl[e] * kLog2e) * kLog2e;
-        F.lam[e] = t < n ? l2 : 0.f;
+        // log2 d_t = -e^{w} log2(e); padding tokens (t >= n) decay by nothing
+        const float ew = __builtin_amdgcn_exp2f(
+            valid ? wl[e] * kLog2e : -__builtin_inff());
+        F.lam[e] = -ew * kLog2e;
         g[e] = scan_lanes<L>(F.lam[e]);
     }
-    bool bad = false;
-    float fA[CPL], fR[CPL], fB[CPL], fK[CPL];
+    // Four exponentials per element.  A~'s factor 2^{g_{t-1}-g_ref} is the
+    // previous token's 2^{g_t-g_ref} (one lane over), except at t = 0 where
+    // it is 2^{-g_ref}.  That value comes from a fourth exponential whose
+    // argument depends on the token: t = 0 takes -g_ref, t = 1 and t = 2
+    // take the per-column g_ref and g_L.  2^{g_L-g_ref} is 2^{g_t-g_ref} at
+    // t = L - 1.
+    float lo = 0.f;  // min over columns of g_ref and g_L - g_ref
+    float fA[CPL], fR[CPL], fB[CPL], fK[CPL], sp[CPL];
 #pragma unroll
     for (int e = 0; e < CPL; ++e) {
         // g at tokens L/2 - 1 and L - 1 of this lane group (ds_swizzle in
@@ -212,26 +258,27 @@ __device__ __forceinline__ void chunk_factors(
             gL = __int_as_float(__builtin_amdgcn_ds_swizzle(
                 __float_as_int(g[e]), 0x10 | (15 << 5)));
         }
-        bad |= (-gref > kHalfRange * kLog2e) ||
-               (gref - gL > kHalfRange * kLog2e);
-        F.eg[e] = __builtin_amdgcn_exp2f(g[e] - gref);
-        F.eng[e] = __builtin_amdgcn_exp2f(gref - g[e]);
-        F.eprev[e] = __builtin_amdgcn_exp2f(g[e] - F.lam[e] - gref);
+        lo = fminf(lo, fminf(gref, gL - gref));
+        const float dg = g[e] - gref;
+        F.eg[e] = __builtin_amdgcn_exp2f(dg);
+        F.eng[e] = __builtin_amdgcn_exp2f(-dg);
+        sp[e] = __builtin_amdgcn_exp2f(t == 0 ? -gref : t == 1 ? gref : gL);
+        const float pe = prev_lane(F.eg[e]);  // every lane takes part
+        F.eprev[e] = t == 0 ? sp[e] : pe;
         fA[e] = F.a[e] * F.eprev[e];
         fR[e] = F.r[e] * F.eg[e];
         fB[e] = F.b[e] * F.eng[e];
         fK[e] = F.k[e] * F.eng[e];
-        if (t == 0) {
-            eL[j0 + e] = __builtin_amdgcn_exp2f(gL);
-            eRef[j0 + e] = __builtin_amdgcn_exp2f(gref);
-            eLR[j0 + e] = __builtin_amdgcn_exp2f(gL - gref);
-        }
     }
-    if (bad) *flag = 1;
+    // the factored form needs g_ref >= -H and g_L - g_ref >= -H
+    if (lo < -kHalfRange * kLog2e) *flag = 1;
     store_cols<L>(&At[t][j0], fA);
     store_cols<L>(&Rt[t][j0], fR);
     store_cols<L>(&Bt[t][j0], fB);
     store_cols<L>(&Kt[t][j0], fK);
+    if (t == 1) store_f32<CPL>(&eRef[j0], sp);
+    if (t == 2) store_f32<CPL>(&eL[j0], sp);
+    if (t == L - 1) store_f32<CPL>(&eLR[j0], F.eg);
 }
 
 // ---------------------------------------------------------------------------

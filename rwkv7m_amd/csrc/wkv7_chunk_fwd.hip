@@ -84,7 +84,9 @@ struct FwdSmem {
     bf16_t Q[2][L][PN];    // [t][j]
     bf16_t Mt[2][CN][PN];  // [j][j'] = M[j'][j]
     // e^{g_L}, e^{g_ref}, e^{g_L - g_ref} per column
-    float eL[2][CN], eRef[2][CN], eLR[2][CN];
+    alignas(16) float eL[2][CN];
+    alignas(16) float eRef[2][CN];
+    alignas(16) float eLR[2][CN];
     int flag[2];
 };
 

@@ -3,7 +3,8 @@
 // Validates every request before any launch (errors, never undefined
 // behaviour: the reference's dispatcher validates at
 // src/rwkv7m/model/wkv.py:19-57 and the native layer re-checks), then routes
-// it to the chunked MFMA kernels or the sequential kernels.
+// it to the chunked MFMA kernels, the single-token kernel or the sequential
+// kernels.
 
 #include <hip/hip_runtime.h>
 
@@ -124,15 +125,19 @@ bool aligned16(const void* p) {
     return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
+bool all_aligned16(std::initializer_list<const void*> ptrs) {
+    for (const void* p : ptrs)
+        if (p && !aligned16(p)) return false;
+    return true;
+}
+
 // The chunked MFMA kernels serve bf16 vectors with N = 64, a chunk length
 // (= checkpoint interval) of 16 or 32, and 16-byte aligned buffers.
 bool use_chunked(int dtype, int64_t N, int64_t ci,
                  std::initializer_list<const void*> ptrs) {
     if (dtype != RWKV7M_DTYPE_BF16 || N != 64) return false;
     if (ci != 16 && ci != 32) return false;
-    for (const void* p : ptrs)
-        if (p && !aligned16(p)) return false;
-    return true;
+    return all_aligned16(ptrs);
 }
 
 int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
@@ -192,6 +197,9 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     p.ckpt = ckpt;
     p.ckpt_bf16 = ckpt_bf16(dtype, N, ci);
     p.ci = ci;
+    if (T == 1 && !ckpt && N == 64 &&
+        all_aligned16({r, w, k, v, a, b, y, s0, s_t}))
+        return hip_status("decode launch", rwkv7m::launch_decode(p, stream));
     return hip_status("sequential forward launch",
                       rwkv7m::launch_seq_forward(p, stream));
 }

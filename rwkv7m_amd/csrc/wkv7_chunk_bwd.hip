@@ -659,12 +659,53 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             // all four, two at a time; NB = 1: two of the four (wv / 4 picks
             // which), j block wv % 4.
             if constexpr (NB == 2) {
+                // the two tiles of a pair share their S' or D' fragments and
+                // the factor fragments (loaded once)
                 const int tb = wv >> 2, jb = wv & 3;
-                grad_tile(0, tb, jb);
-                grad_tile(1, tb, jb);
+                auto store_g = [&](float(*gdst)[CN + 4], const f32x4_t& acc) {
+                    *reinterpret_cast<float4*>(
+                        &gdst[16 * tb + lr][16 * jb + 4 * lq]) =
+                        make_float4(acc[0], acc[1], acc[2], acc[3]);
+                };
+                {
+                    // dR~ = dY S' + dArb B~ + dArk K~,
+                    // dA~ = dU S' + dAab B~ + dAak K~
+                    f32x4_t aR = zero4(), aA = zero4();
+#pragma unroll
+                    for (int k0 = 0; k0 < CN; k0 += 32) {
+                        const bf16x8_t sp = frag_kr(&sm.Sp[k0][16 * jb], PN, lane);
+                        mfma(aR, sp, frag_rk(&sm.raw[6][16 * tb][k0], PN, lane));
+                        mfma(aA, sp, frag_rk(&sm.dU[16 * tb][k0], PN, lane));
+                    }
+                    const bf16x8_t fb = fkr<L>(&sm.Bt[0][16 * jb], PN, lane);
+                    const bf16x8_t fk = fkr<L>(&sm.Kt[0][16 * jb], PN, lane);
+                    mfma(aR, fb, fkr<L>(&sm.dArb[0][16 * tb], PL, lane));
+                    mfma(aA, fb, fkr<L>(&sm.dAab[0][16 * tb], PL, lane));
+                    mfma(aR, fk, fkr<L>(&sm.dArk[0][16 * tb], PL, lane));
+                    mfma(aA, fk, fkr<L>(&sm.dAak[0][16 * tb], PL, lane));
+                    store_g(sm.g.gR, aR);
+                    store_g(sm.g.gA, aA);
+                }
                 __builtin_amdgcn_sched_barrier(0);
-                grad_tile(2, tb, jb);
-                grad_tile(3, tb, jb);
+                {
+                    // dB~ = dAab^T A~ + dArb^T R~ + X D',
+                    // dK~ = dAak^T A~ + dArk^T R~ + V D'
+                    f32x4_t aB = zero4(), aK = zero4();
+                    const bf16x8_t fa = fkr<L>(&sm.At[0][16 * jb], PN, lane);
+                    const bf16x8_t fr = fkr<L>(&sm.Rt[0][16 * jb], PN, lane);
+                    mfma(aB, fa, frk<L>(&sm.dAab[16 * tb][0], PL, lane));
+                    mfma(aK, fa, frk<L>(&sm.dAak[16 * tb][0], PL, lane));
+                    mfma(aB, fr, frk<L>(&sm.dArb[16 * tb][0], PL, lane));
+                    mfma(aK, fr, frk<L>(&sm.dArk[16 * tb][0], PL, lane));
+#pragma unroll
+                    for (int k0 = 0; k0 < CN; k0 += 32) {
+                        const bf16x8_t dl = frag_kr(&sm.Dl[k0][16 * jb], PN, lane);
+                        mfma(aB, dl, frag_rk(&sm.X[16 * tb][k0], PN, lane));
+                        mfma(aK, dl, frag_rk(&sm.raw[3][16 * tb][k0], PN, lane));
+                    }
+                    store_g(sm.g.gB, aB);
+                    store_g(sm.g.gK, aK);
+                }
             } else {
                 grad_tile(wv >> 2, 0, wv & 3);
                 grad_tile(2 + (wv >> 2), 0, wv & 3);

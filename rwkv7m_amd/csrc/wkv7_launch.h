@@ -58,6 +58,9 @@ struct ChunkBwdArgs {
 hipError_t launch_chunk_backward(const ChunkBwdArgs& p, hipStream_t stream);
 
 hipError_t launch_seq_forward(const SeqFwdArgs& p, hipStream_t stream);
+
+// One token (T = 1) for N = 64 without checkpoints; s_t may alias s0.
+hipError_t launch_decode(const SeqFwdArgs& p, hipStream_t stream);
 hipError_t launch_seq_backward(const SeqBwdArgs& p, hipStream_t stream);
 
 }  // namespace rwkv7m

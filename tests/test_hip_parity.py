@@ -158,6 +158,49 @@ def test_decode_inplace_matches_oracle_over_steps(hip):
     _assert_close("state", state, es, 2e-2)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16],
+                         ids=["f32", "bf16"])
+def test_decode_kernel_many_heads(hip, dtype):
+    """The single-token kernel (N = 64) at 1024 heads, in place, against
+    the oracle; then against the sequential kernel on the same step (a
+    T = 1 forward with checkpoints takes the sequential kernel)."""
+    print(f"case: decode B64 H16 N64 {dtype}", flush=True)
+    inp = make_inputs(1, 64, 16, 64, dtype=dtype, seed=21, state_std=0.1)
+    ey, es = oracle.forward(*[_np(inp[n]) for n in NAMES], _np(inp["s0"]))
+    dev = _to_dev(inp)
+    state = dev["s0"].clone()
+    y = hip.decode_inplace(*(dev[n][0] for n in NAMES), state)
+    torch.cuda.synchronize()
+    _assert_close("y", y[None], ey, TOL[dtype])
+    _assert_close("state", state, es, 1e-5)
+    (ys, ss), _ = hip.forward_with_aux(*(dev[n] for n in NAMES), dev["s0"],
+                                       checkpoint_interval=1)
+    torch.cuda.synchronize()
+    _assert_close("y vs sequential", y[None], _np(ys), TOL[dtype])
+    _assert_close("state vs sequential", state, _np(ss), 1e-6)
+
+
+def test_decode_kernel_closed_form(hip):
+    """d = 1 (w -> -inf) and a = b = 0: one step is S + v k^T exactly
+    enough to compare at fp32 rounding, and y = (S + v k^T) r."""
+    print("case: decode closed form B3 H5 N64 f32", flush=True)
+    g = torch.Generator().manual_seed(22)
+    B, H, N = 3, 5, 64
+    s0 = torch.randn(B, H, N, N, generator=g)
+    k = torch.randn(1, B, H, N, generator=g)
+    v = torch.randn(1, B, H, N, generator=g)
+    r = torch.randn(1, B, H, N, generator=g)
+    w = torch.full((1, B, H, N), -1e4)
+    z = torch.zeros(1, B, H, N)
+    es = (s0.double() + v[0].double()[..., :, None] * k[0].double()[..., None, :])
+    ey = torch.einsum("bhij,bhj->bhi", es, r[0].double())
+    state = s0.cuda()
+    y = hip.decode_inplace(*(x.cuda() for x in (r, w, k, v, z, z)), state)
+    torch.cuda.synchronize()
+    _assert_close("state", state, es.numpy(), 1e-6)
+    _assert_close("y", y[0], ey.numpy(), 1e-5)
+
+
 def test_forward_state_in_place_alias(hip):
     print("case: forward with out_state aliasing S0", flush=True)
     inp = _to_dev(make_inputs(9, 2, 2, 64, seed=6, state_std=0.1))

@@ -39,7 +39,8 @@ def parse_args():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--config", type=int, default=2,
-                   help="BASELINE config index (2 = the headline shape)")
+                   help="BASELINE config index (2 = the headline shape; "
+                        "3 = the decode loop)")
     p.add_argument("--chunk", type=int, default=0,
                    help="checkpoint interval / chunk length (0 = library "
                         "default)")
@@ -120,6 +121,105 @@ def cpu_baseline(cfg, target_s):
     }
 
 
+def decode_cpu_baseline(cfg, target_s):
+    """Time the CPU restatement (oracle, fp32, OpenMP over (b, h)) of one
+    decode step at the config's (B, H, N), repeated for about target_s."""
+    import oracle
+    from rwkv7m_amd.synthetic import make_inputs
+
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    B, H, N = cfg["B"], cfg["H"], cfg["N"]
+    inp = make_inputs(1, B, H, N, dtype=cfg["dtype"], seed=7,
+                      state_std=cfg.get("state_std", 0.0))
+    arrs = {k: v.float().numpy() for k, v in inp.items()}
+    vecs = [arrs[n] for n in ("r", "w", "k", "v", "neg_kk", "kka")]
+    reps, dt = 0, 0.0
+    while reps == 0 or dt < 0.8 * target_s:
+        t0 = time.perf_counter()
+        oracle.forward(*vecs, arrs["s0"], precision="f32", threads=threads)
+        dt += time.perf_counter() - t0
+        reps += 1
+    return {
+        "value": reps * B / dt,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"fp32 C restatement of one reference step, B={B} H={H} "
+                   f"N={N}, {reps} step(s), {dt:.1f} s on {threads} "
+                   f"threads"),
+    }
+
+
+def bench_decode(args, cfg, inp, stream):
+    """Config 3: the reference's eager decode loop
+    (src/rwkv7m/infer/generate.py:74-99) -- one WKV call per token with the
+    whole state, updated in place, fresh vectors each step.  A step is one
+    ``decode_inplace`` call; tokens/s = B per step."""
+    import torch
+
+    from rwkv7m_amd.kernels import wkv_hip
+    from rwkv7m_amd.synthetic import make_inputs
+
+    B, H, N, dtype = cfg["B"], cfg["H"], cfg["N"], cfg["dtype"]
+    nsteps = args.warmup + args.steps
+    seq = make_inputs(nsteps, B, H, N, dtype=dtype, seed=cfg["seed"],
+                      device=stream.device, generator="torch")
+    vecs = [seq[n] for n in ("r", "w", "k", "v", "neg_kk", "kka")]
+    state = inp["s0"].clone()
+    for t in range(args.warmup):
+        wkv_hip.decode_inplace(*(x[t] for x in vecs), state)
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)]
+           for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        t = args.warmup + i
+        evs[i][0].record(stream)
+        wkv_hip.decode_inplace(*(x[t] for x in vecs), state)
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kern_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    ms_per_step = elapsed * 1e3 / args.steps
+    eb = 2 if dtype == torch.bfloat16 else 4
+    step_bytes = 2 * B * H * N * N * 4 + 7 * B * H * N * eb
+    achieved = step_bytes / (kern_ms / 1e3) / 1e9
+    result = {
+        "metric": "WKV-7 decode tokens/sec at B=256,H=64,N=64 (in place)",
+        "value": B / (ms_per_step / 1e3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if eb == 2 else "f32",
+        "data": "synthetic (model input distributions, device RNG)",
+        "config": {
+            "workload": (f"config {args.config}: WKV-7 decode B={B} H={H} "
+                         f"N={N}, one token per step, state in place"),
+            "B": B, "T": 1, "H": H, "N": N,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": measured_traffic("decode", args.config, 0),
+            "algorithmic_bytes": step_bytes,
+            "avg_ms": kern_ms,
+        },
+        "kernels_ms": {"decode": kern_ms},
+    }
+    result["cpu_baseline"] = (decode_cpu_baseline(cfg, args.cpu_seconds)
+                              if args.cpu_seconds > 0 else None)
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -152,6 +252,8 @@ def main():
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream(dev)
+    if T == 1:
+        return bench_decode(args, cfg, inp, stream)
     if args.copy_probe > 0:
         n = args.copy_probe * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device=dev)

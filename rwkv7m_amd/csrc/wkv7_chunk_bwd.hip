@@ -33,9 +33,9 @@
 // decay.  Seven barrier-separated phases per chunk:
 //
 //   1  factors; S_0 tiles
-//   2  S', D' to LDS; sum_i D S_L; Aab and the inverse's first half (wave
-//      0); Aak, Arb, Ark, dArk
-//   3  the inverse's second half (wave 0); U, dX
+//   2  S', D' to LDS; sum_i D S_L; the inverse (wave 0, in registers);
+//      Aak, Arb, Ark, dArk
+//   3  U, dX
 //   4  X, dU
 //   5  dArb, dAab, dAak; dV (to HBM); D_0
 //   6  dR~, dA~, dB~, dK~ (fp32 to LDS)
@@ -74,9 +74,8 @@ struct BwdSmem {
     bf16_t dArb[L][PL], dArk[L][PL], dAab[L][PL], dAak[L][PL];
     union {
         struct {  // phases 2 .. 5
-            bf16_t Aab[L][PL], Aak[L][PL], Arb[L][PL], Ark[L][PL];
+            bf16_t Aak[L][PL], Arb[L][PL], Ark[L][PL];
             bf16_t MinvT[L][PL];
-            bf16_t ms[NB][4][16][24];
             bf16_t Ut[CN][PL], dXt[CN][PL];  // [i][t]
         } m;
         struct {  // phases 6, 7: dR~, dA~, dB~, dK~ ([t][j])
@@ -450,10 +449,8 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                         make_float4(tl[0], tl[1], tl[2], tl[3]);
                 }
             }
-            f32x4_t mi_pp[NB];
             if (wv == 0) {
-                chunk::aab_tiles<L>(sm.At, sm.Bt, sm.m.Aab, lane);
-                chunk::minv_begin<L>(sm.m.Aab, sm.m.ms, mi_pp, lane);
+                chunk::minv_regs<L>(sm.At, sm.Bt, sm.m.MinvT, lane);
             } else {
                 // Aak (strict), Arb, Ark (with diagonal), dArk = dY V^T
                 // (with diagonal); the matrices' blocks above the diagonal
@@ -490,15 +487,15 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                 store_pair(da + pend_off, pend[3]);
             }
             if (c >= 1) fetch_part(c - 1, 0, tid);
-            if (wv == 0) {
-                chunk::minv_finish<L>(sm.m.Aab, sm.m.ms, sm.m.MinvT, mi_pp,
-                                      lane);
-            } else {
+            {
                 // U = A~ S'^T + Aak V -> Ut[i][t];
-                // dX = B~ D'^T + Arb^T dY -> dXt[i][t]   (t block x i block)
-                for (int ti = wv - 1; ti < 8 * NB; ti += NW - 1) {
-                    const bool isX = ti >= 4 * NB;
-                    const int rem = ti % (4 * NB), tb = rem / 4, ib = rem % 4;
+                // dX = B~ D'^T + Arb^T dY -> dXt[i][t].  NB = 2: every wave
+                // the U and the dX tile (t block wv / 4, i block wv % 4);
+                // NB = 1: waves 0-3 U, waves 4-7 dX.
+#pragma unroll
+                for (int it = 0; it < NB; ++it) {
+                    const bool isX = NB == 2 ? it == 1 : wv >= 4;
+                    const int tb = NB == 2 ? wv >> 2 : 0, ib = wv & 3;
                     f32x4_t acc = zero4();
                     if (!isX) {
 #pragma unroll

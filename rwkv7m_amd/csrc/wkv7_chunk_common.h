@@ -285,32 +285,8 @@ __device__ __forceinline__ void chunk_factors(
 // The four L x L matrices (stored transposed, pitch PL = L + 8):
 //   Aab = A~ B~^T, Aak = A~ K~^T (strictly lower), Arb = R~ B~^T,
 //   Ark = R~ K~^T (lower with diagonal).
-// aab_tiles: wave 0's part (Aab), matrix_tiles: the other three, spread over
-// waves 1 .. NWAVES-1.  extra(ti) is called for job indices past the three
-// matrices' tiles (ti >= 3 * tiles per matrix), letting callers append jobs.
-template <int L>
-__device__ __forceinline__ void aab_tiles(const bf16_t (*At)[PN],
-                                          const bf16_t (*Bt)[PN],
-                                          bf16_t (*Aab)[L + 8], int lane) {
-    constexpr int NB = L / 16, PL = L + 8;
-    const int lr = lane & 15, lq = lane >> 4;
-#pragma unroll
-    for (int tb = 0; tb < NB; ++tb)
-#pragma unroll
-        for (int sb = 0; sb <= tb; ++sb) {
-            f32x4_t acc = zero4();
-#pragma unroll
-            for (int k0 = 0; k0 < CN; k0 += 32)
-                mfma(acc, frag_rk(&At[16 * tb][k0], PN, lane),
-                     frag_rk(&Bt[16 * sb][k0], PN, lane));
-            if (sb == tb) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    acc[e] = (4 * lq + e > lr) ? acc[e] : 0.f;
-            }
-            store_tile_bf16_t(acc, &Aab[16 * sb][16 * tb], PL, lane);
-        }
-}
+// Aab is consumed only by the inverse (minv_regs), which forms it in
+// registers; the other three are stored by lower_tile.
 
 // A masked lower tile (tb, sb) of X Y^T over K = 64 (X, Y token-major),
 // stored transposed into dst.
@@ -343,82 +319,103 @@ __device__ __forceinline__ void lower_tile_index(int rem, int& tb, int& sb) {
 }
 
 // ---------------------------------------------------------------------------
-// Minv = (I - Aab)^{-1} on one wave, in two halves so that a barrier can sit
-// between them.  Per diagonal block p (A = Aab_pp, nilpotent, A^16 = 0):
-//   A2 = A A; P = I + A + A2 + A A2; A4 = A2 A2;       (minv_begin)
-//   P2 = P + P A4; A8 = A4 A4; Minv_pp = P2 + P2 A8   (minv_finish)
-// i.e. (I+A)(I+A^2)(I+A^4)(I+A^8); then, for L = 32,
-//   Minv_10 = Minv_11 (Aab_10 Minv_00).
-// Aab and MinvT are stored transposed (pitch L + 8); ms is scratch.  MinvT's
-// block above the diagonal must hold zeros.
-template <int L>
-__device__ __forceinline__ void minv_begin(const bf16_t (*Aab)[L + 8],
-                                           bf16_t (*ms)[4][16][24],
-                                           f32x4_t* pp, int lane) {
-    constexpr int NB = L / 16, PL = L + 8;
-    const int lr = lane & 15, lq = lane >> 4;
-    wave_lds_fence();
-    f32x4_t a2[NB];
-#pragma unroll
-    for (int p = 0; p < NB; ++p) {
-        const bf16_t* Ap = &Aab[16 * p][16 * p];
-        a2[p] = zero4();
-        mfma(a2[p], frag_kr16(Ap, PL, lane), frag_rk16(Ap, PL, lane));
-        store_tile_bf16_t(a2[p], &ms[p][0][0][0], 24, lane);
-    }
-    wave_lds_fence();
-#pragma unroll
-    for (int p = 0; p < NB; ++p) {
-        const bf16_t* Ap = &Aab[16 * p][16 * p];
-        const f32x4_t at = unpack4(
-            *reinterpret_cast<const uint2*>(Ap + lr * PL + 4 * lq));
-        f32x4_t a4 = zero4();
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            pp[p][e] = ((4 * lq + e == lr) ? 1.f : 0.f) + at[e] + a2[p][e];
-        mfma(pp[p], frag_kr16(Ap, PL, lane),
-             frag_rk16(&ms[p][0][0][0], 24, lane));
-        mfma(a4, frag_kr16(&ms[p][0][0][0], 24, lane),
-             frag_rk16(&ms[p][0][0][0], 24, lane));
-        store_tile_bf16_t(a4, &ms[p][1][0][0], 24, lane);
-        store_tile_bf16_t(pp[p], &ms[p][2][0][0], 24, lane);
-    }
+// A 16 x 16 matrix as a v_mfma_f32_16x16x32_bf16 operand, straight from an
+// accumulator tile.  D(M), the accumulator layout, has lane l holding
+// M[4 (l/16) + e][l % 16] (e = 0..3).  kq(D(M)) puts those four values, as
+// bf16, in operand slots 8 (l/16) + e and zeros in slots 8 (l/16) + 4..7:
+// the contraction index k = 4 (l/16) + e occupies the same slot in either
+// operand, so kq(D(M)) serves as M for the B operand (k x n) and as M^T for
+// the A operand (m x k):
+//   mfma(kq(D(N)), kq(D(M))) accumulates N^T M.
+// Products then chain in registers; a transpose costs a second product.
+__device__ __forceinline__ bf16x8_t kq(const f32x4_t& d) {
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    const u32x4_t u = {pack_bf16x2(d[0], d[1]), pack_bf16x2(d[2], d[3]), 0u,
+                       0u};
+    return __builtin_bit_cast(bf16x8_t, u);
 }
 
+// Minv = (I - Aab)^{-1} of a chunk on one wave, entirely in registers, from
+// the token-major factors A~, B~; stored transposed into MinvT (whose blocks
+// above the diagonal must hold zeros).  Per diagonal block p, A = Aab_pp is
+// strictly lower (A^16 = 0) and
+//   Minv_pp = (I + A)(I + A^2)(I + A^4)(I + A^8)
+//           = Q2 + Q2 A^8,  Q2 = Q1 + Q1 A^4,  Q1 = I + A + A^2 + A A^2,
+// each product carried together with its transpose (the A operand of a kq
+// product is a transpose).  For L = 32, Minv_10 = Minv_11 (Aab_10 Minv_00).
+// Every product is bf16 x bf16 with fp32 accumulation, as in the rest of
+// the chunk.
 template <int L>
-__device__ __forceinline__ void minv_finish(const bf16_t (*Aab)[L + 8],
-                                            bf16_t (*ms)[4][16][24],
-                                            bf16_t (*MinvT)[L + 8],
-                                            f32x4_t* pp, int lane) {
+__device__ __forceinline__ void minv_regs(const bf16_t (*At)[PN],
+                                          const bf16_t (*Bt)[PN],
+                                          bf16_t (*MinvT)[L + 8], int lane) {
     constexpr int NB = L / 16, PL = L + 8;
-    wave_lds_fence();
+    const int lr = lane & 15, lq = lane >> 4;
+    // A and A^T of each diagonal block (masked products over K = 64) and,
+    // for L = 32, Aab_10^T = B~_0 A~_1^T
+    f32x4_t dA[NB], dAT[NB], dA10T = zero4();
 #pragma unroll
     for (int p = 0; p < NB; ++p) {
-        f32x4_t a8 = zero4();
-        mfma(pp[p], frag_kr16(&ms[p][2][0][0], 24, lane),
-             frag_rk16(&ms[p][1][0][0], 24, lane));
-        mfma(a8, frag_kr16(&ms[p][1][0][0], 24, lane),
-             frag_rk16(&ms[p][1][0][0], 24, lane));
-        store_tile_bf16_t(a8, &ms[p][0][0][0], 24, lane);
-        store_tile_bf16_t(pp[p], &ms[p][3][0][0], 24, lane);
-    }
-    wave_lds_fence();
+        dA[p] = zero4();
+        dAT[p] = zero4();
 #pragma unroll
-    for (int p = 0; p < NB; ++p) {
-        mfma(pp[p], frag_kr16(&ms[p][3][0][0], 24, lane),
-             frag_rk16(&ms[p][0][0][0], 24, lane));
-        store_tile_bf16_t(pp[p], &MinvT[16 * p][16 * p], PL, lane);
+        for (int k0 = 0; k0 < CN; k0 += 32) {
+            const bf16x8_t fa = frag_rk(&At[16 * p][k0], PN, lane);
+            const bf16x8_t fb = frag_rk(&Bt[16 * p][k0], PN, lane);
+            mfma(dA[p], fa, fb);
+            mfma(dAT[p], fb, fa);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int row = 4 * lq + e;
+            dA[p][e] = row > lr ? dA[p][e] : 0.f;
+            dAT[p][e] = lr > row ? dAT[p][e] : 0.f;
+        }
     }
     if constexpr (NB == 2) {
-        wave_lds_fence();
-        f32x4_t z = zero4();
-        mfma(z, frag_kr16(&Aab[0][16], PL, lane),
-             frag_rk16(&MinvT[0][0], PL, lane));
-        store_tile_bf16_t(z, &ms[0][1][0][0], 24, lane);
-        wave_lds_fence();
-        f32x4_t m10 = zero4();
-        mfma(m10, frag_kr16(&MinvT[16][16], PL, lane),
-             frag_rk16(&ms[0][1][0][0], 24, lane));
+#pragma unroll
+        for (int k0 = 0; k0 < CN; k0 += 32)
+            mfma(dA10T, frag_rk(&Bt[0][k0], PN, lane),
+                 frag_rk(&At[16][k0], PN, lane));
+    }
+    f32x4_t dM[NB], dM1T = zero4();
+#pragma unroll
+    for (int p = 0; p < NB; ++p) {
+        const bf16x8_t pA = kq(dA[p]), pT = kq(dAT[p]);
+        f32x4_t x2 = zero4(), t2 = zero4();
+        mfma(x2, pT, pA);  // A A
+        mfma(t2, pA, pT);  // A^T A^T
+        const bf16x8_t px2 = kq(x2), pt2 = kq(t2);
+        f32x4_t q1, q1t;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float one = (4 * lq + e == lr) ? 1.f : 0.f;
+            q1[e] = one + dA[p][e] + x2[e];
+            q1t[e] = one + dAT[p][e] + t2[e];
+        }
+        mfma(q1, pT, px2);   // + A A^2
+        mfma(q1t, px2, pT);  // + (A^2)^T A^T
+        f32x4_t x4 = zero4(), t4 = zero4();
+        mfma(x4, pt2, px2);  // A^2 A^2
+        mfma(t4, px2, pt2);  // (A^2)^T (A^2)^T
+        const bf16x8_t pq1t = kq(q1t), px4 = kq(x4), pt4 = kq(t4);
+        f32x4_t q2 = q1, q2t = q1t, x8 = zero4();
+        mfma(q2, pq1t, px4);   // + Q1 A^4
+        mfma(q2t, px4, pq1t);  // + (A^4)^T Q1^T
+        mfma(x8, pt4, px4);    // A^4 A^4
+        const bf16x8_t pq2t = kq(q2t), px8 = kq(x8);
+        dM[p] = q2;
+        mfma(dM[p], pq2t, px8);  // + Q2 A^8
+        if (NB == 2 && p == 1) {
+            dM1T = q2t;
+            mfma(dM1T, px8, pq2t);  // + (A^8)^T Q2^T
+        }
+        store_tile_bf16_t(dM[p], &MinvT[16 * p][16 * p], PL, lane);
+    }
+    if constexpr (NB == 2) {
+        f32x4_t z = zero4(), m10 = zero4();
+        mfma(z, kq(dA10T), kq(dM[0]));  // Aab_10 Minv_00
+        mfma(m10, kq(dM1T), kq(z));     // Minv_11 (Aab_10 Minv_00)
         store_tile_bf16_t(m10, &MinvT[0][16], PL, lane);
     }
 }

@@ -29,8 +29,8 @@
 // the state through chunk c.  Five barrier-separated phases per chunk:
 //
 //   F  c+1: factors (in-wave scan of the log-decay)  c: S' -> LDS, S e^{g_L} + C
-//   M  c+1: matrices; wave 0 starts the inverse      c: S += S' M, Y = Q S'^T + P
-//   I  c+1: wave 0 finishes Minv; Aak V; C += V^T K^; P += Ark V; next vectors
+//   M  c+1: matrices; wave 0 the inverse             c: S += S' M, Y = Q S'^T + P
+//   I  c+1: Aak V; C += V^T K^; P += Ark V; next vectors
 //   W  c+1: W = Minv A~, U = Minv (Aak V)
 //   Q  c+1: Q, M; C += U^T B^; P += Arb U
 //
@@ -38,9 +38,9 @@
 // accumulation.  Operands stored with the contraction index strided are read
 // with gfx950's transposing LDS load, so no transposed copies are made.  The
 // state S, C and P stay fp32 in accumulator registers; B^ and K^ enter only
-// as the column scaling e^{g_L-g_ref} of M and C.  The 16x16 diagonal
-// blocks of Minv are the product (I+A)(I+A^2)(I+A^4)(I+A^8) of the nilpotent
-// strictly lower block A.  A chunk whose decay range exceeds what the
+// as the column scaling e^{g_L-g_ref} of M and C.  Minv is formed in one
+// wave's registers (the 16x16 diagonal blocks as the product
+// (I+A)(I+A^2)(I+A^4)(I+A^8) of the nilpotent strictly lower block A).  A chunk whose decay range exceeds what the
 // factored form represents (more than kHalfRange of log-decay on either side
 // of g_ref: far outside the model's clamped range) runs an exact fp32
 // sequential loop instead.
@@ -75,8 +75,7 @@ struct FwdSmem {
         float fb[CN][CN + 1];  // exact fallback: the state in fp32
     };
     // L x L matrices, stored transposed: X[s][t] holds entry (t, s)
-    bf16_t Aab[L][PL], Aak[L][PL], Arb[L][PL], Ark[L][PL], MinvT[L][PL];
-    bf16_t ms[NB][4][16][24];  // inverse scratch (16x16, transposed)
+    bf16_t Aak[L][PL], Arb[L][PL], Ark[L][PL], MinvT[L][PL];
     bf16_t AakV[CN][PL];       // [i][s]
     bf16_t Wt[CN][PL];         // [j][t] = W[t][j]
     bf16_t Ut[CN][PL];         // [i][t] = U[t][i]
@@ -173,9 +172,8 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
 
     // the matrices' and Minv's blocks above the diagonal stay zero
     {
-        bf16_t(*const mats[5])[PL] = {sm.Aab, sm.Aak, sm.Arb, sm.Ark,
-                                       sm.MinvT};
-        chunk::zero_upper<L>(mats, 5, tid, NTH);
+        bf16_t(*const mats[4])[PL] = {sm.Aak, sm.Arb, sm.Ark, sm.MinvT};
+        chunk::zero_upper<L>(mats, 4, tid, NTH);
     }
     if (tid < 2) sm.flag[tid] = 0;
 
@@ -325,11 +323,9 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         Pacc = zero4();
         Cacc[0] = zero4();
         Cacc[1] = zero4();
-        f32x4_t mi_pp[NB];
         if (prep) {
             if (wv == 0) {
-                chunk::aab_tiles<L>(sm.f.At, sm.f.Bt, sm.Aab, lane);
-                chunk::minv_begin<L>(sm.Aab, sm.ms, mi_pp, lane);
+                chunk::minv_regs<L>(sm.f.At, sm.f.Bt, sm.MinvT, lane);
             } else {
                 // Aak (strict), Arb, Ark (with diagonal): lower tiles
                 constexpr int TPM = NB * (NB + 1) / 2;
@@ -349,10 +345,17 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         __syncthreads();
 
         // ================= phase I =======================================
-        if (prep && wv == 0)
-            chunk::minv_finish<L>(sm.Aab, sm.ms, sm.MinvT, mi_pp, lane);
-        // C^T += K~^T V (scaled as above), P^T += V^T Ark^T (wave 0: phase W)
-        auto c_kv = [&] {
+        if (prep) {
+            // Aak V -> AakV[i][s]: one tile (s block wv / 4, i block wv % 4)
+            // per wave (NB = 2) or per wave 0..3 (NB = 1)
+            if (NB == 2 || wv < 4) {
+                const int sb = wv >> 2, ib = wv & 3;
+                f32x4_t acc = zero4();
+                mfma(acc, fkr<L>(&sm.Aak[0][16 * sb], PL, lane),
+                     fkr<L>(&sm.f.Vc[0][16 * ib], PN, lane));
+                store_tile_bf16_t(acc, &sm.AakV[16 * ib][16 * sb], PL, lane);
+            }
+            // C^T += K~^T V (scaled as above), P^T += V^T Ark^T
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 const int si = 2 * wv + q, jb = si >> 2, ib = si & 3;
@@ -362,17 +365,6 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             if (has_y)
                 mfma(Pacc, fkr<L>(&sm.f.Vc[0][16 * yib], PN, lane),
                      fkr<L>(&sm.Ark[0][16 * ytb], PL, lane));
-        };
-        if (prep && wv > 0) {
-            // Aak V -> AakV[i][s] (tiles: s block x i block)
-            for (int ti = wv - 1; ti < 4 * NB; ti += NW - 1) {
-                const int sb = ti / 4, ib = ti % 4;
-                f32x4_t acc = zero4();
-                mfma(acc, fkr<L>(&sm.Aak[0][16 * sb], PL, lane),
-                     fkr<L>(&sm.f.Vc[0][16 * ib], PN, lane));
-                store_tile_bf16_t(acc, &sm.AakV[16 * ib][16 * sb], PL, lane);
-            }
-            c_kv();
         }
         if (c + 2 < nch) {
             stash();
@@ -382,7 +374,6 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
 
         // ================= phase W =======================================
         if (prep) {
-            if (wv == 0) c_kv();
             // W = Minv A~ -> Wt[j][t]; U = Minv (Aak V) -> Ut[i][t]
             for (int ti = wv; ti < 8 * NB; ti += NW) {
                 const bool isU = ti >= 4 * NB;

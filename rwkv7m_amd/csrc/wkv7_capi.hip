@@ -132,11 +132,13 @@ bool all_aligned16(std::initializer_list<const void*> ptrs) {
 }
 
 // The chunked MFMA kernels serve bf16 vectors with N = 64, a chunk length
-// (= checkpoint interval) of 16 or 32, and 16-byte aligned buffers.
-bool use_chunked(int dtype, int64_t N, int64_t ci,
+// (= checkpoint interval) of 16 or 32, 16-byte aligned buffers, and chunks
+// whose element span L * B*H * N stays below 2^31 (32-bit lane offsets).
+bool use_chunked(int dtype, int64_t N, int64_t ci, int64_t BH,
                  std::initializer_list<const void*> ptrs) {
     if (dtype != RWKV7M_DTYPE_BF16 || N != 64) return false;
     if (ci != 16 && ci != 32) return false;
+    if (BH * N * ci >= (int64_t(1) << 31)) return false;
     return all_aligned16(ptrs);
 }
 
@@ -160,7 +162,8 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     if (d.state_elems == 0) return RWKV7M_OK;
     if (T == 0 && !ckpt) return copy_or_clear(s_t, s0, d.state_elems, stream);
     const int64_t L = ckpt ? ci : kDefaultChunk;
-    if (T > 1 && use_chunked(dtype, N, L, {r, w, k, v, a, b, y, s0, s_t, ckpt})) {
+    if (T > 1 &&
+        use_chunked(dtype, N, L, B * H, {r, w, k, v, a, b, y, s0, s_t, ckpt})) {
         rwkv7m::ChunkFwdArgs c{};
         c.L = int(L);
         c.T = T;
@@ -298,7 +301,7 @@ int rwkv7m_wkv7_backward(int dtype, int64_t T, int64_t B, int64_t H,
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (d.state_elems == 0) return RWKV7M_OK;
     if (T == 0) return copy_or_clear(ds0, ds_t, d.state_elems, s);
-    if (use_chunked(dtype, N, ci,
+    if (use_chunked(dtype, N, ci, B * H,
                     {r, w, k, v, neg_kk, kka, dy, ds_t, checkpoints, dr, dw,
                      dk, dv, dneg_kk, dkka, ds0})) {
         rwkv7m::ChunkBwdArgs c{};

@@ -273,30 +273,42 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
     }
 
     // ---- the chunk's vectors and S_0, prefetched one chunk ahead --------
+    // HBM addresses are a per-chunk scalar base plus a 32-bit per-lane
+    // offset (t * BH * CN + column; the host keeps L * BH * CN below 2^31).
     constexpr int SEGV = 7 * L * 8;  // 16-byte segments of the 7 vectors
     constexpr int NPRE = (SEGV + NTH - 1) / NTH;
     static_assert(CN * CN * 2 / 16 == NTH, "one S_0 segment per thread");
+    static_assert((8 * L) % 64 == 0 && SEGV % 64 == 0,
+                  "each wave loads from one vector");
+    const uint32_t BHCN = uint32_t(BH) * CN;
+    // part p of this wave: one vector (the same for all 64 lanes), or none
+    const bf16_t* vp[NPRE];
+#pragma unroll
+    for (int p = 0; p < NPRE; ++p) {
+        const int wseg = __builtin_amdgcn_readfirstlane((p * NTH + tid) & ~63);
+        vp[p] = wseg < SEGV ? src.get(wseg / (8 * L)) : nullptr;
+    }
     uint4 pre[NPRE], pres;
     // part p < NPRE: one 16-byte segment of the vectors; part NPRE: S_0
-    // (addresses are formed at each fetch: kept across the loop they would
-    // hold registers for the whole run)
+    // (lane offsets are formed at each fetch: kept across the loop they
+    // would hold registers for the whole run)
     auto fetch_part = [&](int64_t cc, int part, int tidv) {
+        const int64_t cbase = (cc * L * BH + bh) * CN;
+        const int ncc = int(T - cc * L < L ? T - cc * L : L);
 #pragma unroll
         for (int p = 0; p < NPRE; ++p) {
             if (p == part) {
-                const int seg = p * NTH + tidv;
-                const int row = seg >> 3, s8 = seg & 7;
-                const int vec = row / L, t = row % L;
-                const bf16_t* base = src.get(vec);
+                const uint32_t seg = uint32_t(p * NTH + tidv);
+                const uint32_t t = (seg >> 3) & (L - 1), s8 = seg & 7;
                 pre[p] = make_uint4(0, 0, 0, 0);
-                if (seg < SEGV && base != nullptr && cc * L + t < T)
+                if (vp[p] != nullptr && int(t) < ncc)
                     pre[p] = *reinterpret_cast<const uint4*>(
-                        base + ((cc * L + t) * BH + bh) * CN + s8 * 8);
+                        (vp[p] + cbase) + (t * BHCN + s8 * 8));
             }
         }
         if (part == NPRE)
             pres = *reinterpret_cast<const uint4*>(
-                ckpt + cc * BH * NN + sbase + 8 * tidv);
+                (ckpt + cc * BH * NN + sbase) + uint32_t(8 * tidv));
     };
     auto fetch = [&](int64_t cc, int tidv) {
 #pragma unroll
@@ -329,12 +341,24 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
     // chunk.
     uint32_t pend[5][CPL / 2];  // dr, dw, dk, dneg_kk, dkka
     uint2 pend_dv = make_uint2(0, 0);
-    int64_t pend_off = -1, pend_voff = -1;  // -1: nothing to store
-    auto store_pair = [&](bf16_t* dst, const uint32_t* val) {
-        if constexpr (CPL == 4)
-            *reinterpret_cast<uint2*>(dst) = make_uint2(val[0], val[1]);
-        else
-            *reinterpret_cast<uint32_t*>(dst) = val[0];
+    // the pending chunk's scalar base (-1: nothing pending) and the lane's
+    // offsets and in-range flags for the five gradients and dV
+    int64_t pend_cbase = -1;
+    uint32_t pend_lane = 0, pend_vlane = 0;
+    bool pend_ok = false, pend_vok = false;
+    auto store_pair = [&](bf16_t* g, const uint32_t* val) {
+        if (pend_ok) {
+            bf16_t* dst = (g + pend_cbase) + pend_lane;
+            if constexpr (CPL == 4)
+                *reinterpret_cast<uint2*>(dst) = make_uint2(val[0], val[1]);
+            else
+                *reinterpret_cast<uint32_t*>(dst) = val[0];
+        }
+    };
+    auto store_dv = [&]() {
+        if (pend_vok)
+            *reinterpret_cast<uint2*>((dv + pend_cbase) + pend_vlane) =
+                pend_dv;
     };
 
     for (int64_t c = nch - 1; c >= 0; --c) {
@@ -382,16 +406,15 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
 
         if (fallback) {
             // ---- exact sequential reverse pass for this chunk -------------
-            if (pend_off >= 0) {
-                store_pair(dr + pend_off, pend[0]);
-                store_pair(dw + pend_off, pend[1]);
-                store_pair(dk + pend_off, pend[2]);
-                store_pair(da + pend_off, pend[3]);
-                store_pair(db + pend_off, pend[4]);
+            if (pend_cbase >= 0) {
+                store_pair(dr, pend[0]);
+                store_pair(dw, pend[1]);
+                store_pair(dk, pend[2]);
+                store_pair(da, pend[3]);
+                store_pair(db, pend[4]);
+                store_dv();
             }
-            if (pend_voff >= 0)
-                *reinterpret_cast<uint2*>(dv + pend_voff) = pend_dv;
-            pend_off = pend_voff = -1;
+            pend_cbase = -1;
             if (c >= 1) fetch(c - 1, tid);
 #pragma unroll
             for (int q = 0; q < 2; ++q)
@@ -414,9 +437,9 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                     D[q][e] = sm.fb.Df[(toff[q] / CN) * 65 + toff[q] % CN + e];
         } else {
             // ================= 2 ==========================================
-            if (pend_off >= 0) {
-                store_pair(dr + pend_off, pend[0]);
-                store_pair(dw + pend_off, pend[1]);
+            if (pend_cbase >= 0) {
+                store_pair(dr, pend[0]);
+                store_pair(dw, pend[1]);
             }
             if (c >= 1) fetch_part(c - 1, NPRE, tid);  // S_0 first
             // S' = S_0 e^{g_ref} and D' = D e^{g_L - g_ref} ([i][j]);
@@ -482,9 +505,9 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             __syncthreads();
 
             // ================= 3 ==========================================
-            if (pend_off >= 0) {
-                store_pair(dk + pend_off, pend[2]);
-                store_pair(da + pend_off, pend[3]);
+            if (pend_cbase >= 0) {
+                store_pair(dk, pend[2]);
+                store_pair(da, pend[3]);
             }
             if (c >= 1) fetch_part(c - 1, 0, tid);
             {
@@ -521,9 +544,10 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             __syncthreads();
 
             // ================= 4 ==========================================
-            if (pend_off >= 0) store_pair(db + pend_off, pend[4]);
-            if (pend_voff >= 0)
-                *reinterpret_cast<uint2*>(dv + pend_voff) = pend_dv;
+            if (pend_cbase >= 0) {
+                store_pair(db, pend[4]);
+                store_dv();
+            }
             if (c >= 1) fetch_part(c - 1, 1, tid);
             // X = Minv U -> X[t][i]; dU = Minv^T dX -> dU[t][i].  NB = 2:
             // every wave one X and one dU tile (t block wv / 4, i block
@@ -757,12 +781,13 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                     pend[3][h] = pack_bf16x2(dav[2 * h], dav[2 * h + 1]);
                     pend[4][h] = pack_bf16x2(dbv[2 * h], dbv[2 * h + 1]);
                 }
-                pend_off = t < n ? ((t0 + t) * BH + bh) * CN + j0 : -1;
+                pend_cbase = (t0 * BH + bh) * CN;
+                pend_ok = t < n;
+                pend_lane = uint32_t(t) * BHCN + j0;
                 const int s = 16 * vsb + lr;
                 pend_dv = pack4(dvt);
-                pend_voff = (has_v && s < n)
-                                ? ((t0 + s) * BH + bh) * CN + 16 * vib + 4 * lq
-                                : -1;
+                pend_vok = has_v && s < n;
+                pend_vlane = uint32_t(s) * BHCN + 16 * vib + 4 * lq;
             }
             D[0] = Dn[0];
             D[1] = Dn[1];
@@ -772,14 +797,14 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         if (tid == 0) sm.flag = 0;
         __syncthreads();
     }
-    if (pend_off >= 0) {
-        store_pair(dr + pend_off, pend[0]);
-        store_pair(dw + pend_off, pend[1]);
-        store_pair(dk + pend_off, pend[2]);
-        store_pair(da + pend_off, pend[3]);
-        store_pair(db + pend_off, pend[4]);
+    if (pend_cbase >= 0) {
+        store_pair(dr, pend[0]);
+        store_pair(dw, pend[1]);
+        store_pair(dk, pend[2]);
+        store_pair(da, pend[3]);
+        store_pair(db, pend[4]);
+        store_dv();
     }
-    if (pend_voff >= 0) *reinterpret_cast<uint2*>(dv + pend_voff) = pend_dv;
 #pragma unroll
     for (int q = 0; q < 2; ++q)
         *reinterpret_cast<float4*>(ds0 + sbase + toff[q]) =

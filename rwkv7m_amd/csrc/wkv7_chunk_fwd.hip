@@ -178,28 +178,32 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
     if (tid < 2) sm.flag[tid] = 0;
 
     // ---- the vectors, prefetched one chunk ahead into registers ----------
+    // HBM addresses are a per-chunk scalar base plus a 32-bit per-lane
+    // offset (t * BH * CN + column; the host keeps L * BH * CN below 2^31).
     constexpr int SEG = 6 * L * 8;  // 16-byte segments of one chunk
     constexpr int NPRE = (SEG + NTH - 1) / NTH;
-    uint4 pre[NPRE];
-    const bf16_t* pbase[NPRE];
-    int ptok[NPRE];
+    static_assert((8 * L) % 64 == 0 && SEG % 64 == 0,
+                  "each wave loads from one vector");
+    const uint32_t BHCN = uint32_t(BH) * CN;
+    // part p of this wave: one vector (the same for all 64 lanes), or none
+    const bf16_t* vp[NPRE];
 #pragma unroll
     for (int p = 0; p < NPRE; ++p) {
-        const int seg = p * NTH + tid;
-        const int row = seg >> 3, s8 = seg & 7;
-        const int vec = row / L, t = row % L;
-        ptok[p] = seg < SEG ? t : (1 << 30);
-        pbase[p] = src.get(vec < 6 ? vec : 0) + (int64_t(t) * BH + bh) * CN +
-                   s8 * 8;
+        const int wseg = __builtin_amdgcn_readfirstlane((p * NTH + tid) & ~63);
+        vp[p] = wseg < SEG ? src.get(wseg / (8 * L)) : nullptr;
     }
-    const int64_t chunk_stride = int64_t(L) * BH * CN;
+    uint4 pre[NPRE];
     auto fetch = [&](int64_t cc) {
+        const int64_t cbase = (cc * L * BH + bh) * CN;
+        const int ncc = int(T - cc * L < L ? T - cc * L : L);
 #pragma unroll
         for (int p = 0; p < NPRE; ++p) {
+            const uint32_t seg = uint32_t(p * NTH + tid);
+            const uint32_t t = (seg >> 3) & (L - 1), s8 = seg & 7;
             pre[p] = make_uint4(0, 0, 0, 0);
-            if (cc * L + ptok[p] < T)
-                pre[p] = *reinterpret_cast<const uint4*>(pbase[p] +
-                                                         cc * chunk_stride);
+            if (vp[p] != nullptr && int(t) < ncc)
+                pre[p] = *reinterpret_cast<const uint4*>(
+                    (vp[p] + cbase) + (t * BHCN + s8 * 8));
         }
     };
     auto stash = [&]() {
@@ -315,7 +319,8 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                 const int tt = 16 * ytb + lr;
                 if (tt < n)
                     *reinterpret_cast<uint2*>(
-                        y + ((t0 + tt) * BH + bh) * CN + 16 * yib + 4 * lq) =
+                        (y + (t0 * BH + bh) * CN) +
+                        (uint32_t(tt) * BHCN + 16 * yib + 4 * lq)) =
                         pack4(yy);
             }
         }

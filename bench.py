@@ -252,8 +252,6 @@ def main():
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream(dev)
-    if T == 1:
-        return bench_decode(args, cfg, inp, stream)
     if args.copy_probe > 0:
         n = args.copy_probe * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device=dev)
@@ -261,6 +259,8 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if T == 1:
+        return bench_decode(args, cfg, inp, stream)
 
     def step(evs=None):
         if evs:

@@ -67,9 +67,16 @@ struct BwdSmem {
     bf16_t raw[7][L][PN];
     bf16_t S0s[CN][PN];  // the next chunk's S_0 checkpoint (staging), [i][j]
     bf16_t At[L][PN], Rt[L][PN], Bt[L][PN], Kt[L][PN];  // factors, [t][j]
-    bf16_t Sp[CN][PN];  // S' = S_0 diag(e^{g_ref}), [i][j]
-    bf16_t Dl[CN][PN];  // D' = D diag(e^{g_L - g_ref}), [i][j]
-    bf16_t X[L][PN], dU[L][PN];  // [t][i]
+    union {
+        struct {
+            bf16_t Sp[CN][PN];  // S' = S_0 diag(e^{g_ref}), [i][j]
+            bf16_t Dl[CN][PN];  // D' = D diag(e^{g_L - g_ref}), [i][j]
+            bf16_t X[L][PN], dU[L][PN];  // [t][i]
+        };
+        // phase 7 to the next chunk's phase 1: the chunk's gradients
+        // dr, dw, dk, dneg_kk, dkka, dv (bf16, [t][j]) on their way to HBM
+        bf16_t stg[6][L][PN];
+    };
     // cotangents of the L x L matrices, stored transposed
     bf16_t dArb[L][PL], dArk[L][PL], dAab[L][PL], dAak[L][PL];
     union {
@@ -234,7 +241,8 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                       float* ds0) {
     using Sm = BwdSmem<L>;
     constexpr int NW = BWD_WAVES, NTH = BWD_THREADS;
-    constexpr int PL = Sm::PL, NB = Sm::NB, CPL = L / 8;
+    constexpr int PL = Sm::PL, NB = Sm::NB;
+    constexpr int CPL = chunk::LaneFactors<L, NW>::CPL;
     constexpr int TPM = NB * (NB + 1) / 2;  // lower tiles of an L x L matrix
     static_assert(L == 16 || L == 32, "chunk length");
     __shared__ Sm sm;
@@ -336,29 +344,34 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
     // Each chunk's HBM traffic is spread over its phases instead of one
     // burst per chunk: the previous chunk's S_0 (phase 2) and vectors (a
     // part per phase, 3 .. 5) are fetched early enough to have arrived by
-    // the stash in phase 7, and the gradients computed in phase 7 wait in
-    // registers (bf16 pairs) and are stored during phases 2 .. 4 of the next
-    // chunk.
-    uint32_t pend[5][CPL / 2];  // dr, dw, dk, dneg_kk, dkka
-    uint2 pend_dv = make_uint2(0, 0);
-    // the pending chunk's scalar base (-1: nothing pending) and the lane's
-    // offsets and in-range flags for the five gradients and dV
-    int64_t pend_cbase = -1;
-    uint32_t pend_lane = 0, pend_vlane = 0;
-    bool pend_ok = false, pend_vok = false;
-    auto store_pair = [&](bf16_t* g, const uint32_t* val) {
-        if (pend_ok) {
-            bf16_t* dst = (g + pend_cbase) + pend_lane;
-            if constexpr (CPL == 4)
-                *reinterpret_cast<uint2*>(dst) = make_uint2(val[0], val[1]);
-            else
-                *reinterpret_cast<uint32_t*>(dst) = val[0];
+    // the stash in phase 7.  The gradients computed in phase 7 are staged in
+    // LDS (stg) and written at the start of the next chunk as whole 128-byte
+    // token rows, 16 bytes a lane: a lane's own elements would give every
+    // store 32 rows of 8 or 16 bytes each.
+    constexpr int SEGG = 6 * L * 8;  // 16-byte segments of the staged rows
+    constexpr int NFL = (SEGG + NTH - 1) / NTH;
+    static_assert((8 * L) % 64 == 0, "each wave stores one gradient");
+    int64_t pend_cbase = -1;  // the staged chunk's scalar base (-1: none)
+    int pend_n = 0;           // its valid tokens
+    auto flush = [&](int tidv) {
+#pragma unroll
+        for (int p = 0; p < NFL; ++p) {
+            const int seg = p * NTH + tidv;
+            const int wseg = __builtin_amdgcn_readfirstlane(seg & ~63);
+            const int g = wseg / (8 * L);
+            const uint32_t t = (uint32_t(seg) >> 3) & (L - 1), s8 = seg & 7;
+            if (wseg < SEGG && int(t) < pend_n) {
+                bf16_t* dst = g == 0   ? dr
+                              : g == 1 ? dw
+                              : g == 2 ? dk
+                              : g == 3 ? da
+                              : g == 4 ? db
+                                       : dv;
+                *reinterpret_cast<uint4*>((dst + pend_cbase) +
+                                          (t * BHCN + s8 * 8)) =
+                    *reinterpret_cast<const uint4*>(&sm.stg[g][t][8 * s8]);
+            }
         }
-    };
-    auto store_dv = [&]() {
-        if (pend_vok)
-            *reinterpret_cast<uint2*>((dv + pend_cbase) + pend_vlane) =
-                pend_dv;
     };
 
     for (int64_t c = nch - 1; c >= 0; --c) {
@@ -382,17 +395,13 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         }
 
         // ================= 1: factors; S_0 tiles =========================
-        chunk::LaneFactors<L> fl;
-        chunk::chunk_factors<L>(sm.raw, n, wv, lane, sm.At, sm.Rt, sm.Bt,
-                                sm.Kt, sm.eL, sm.eRef, sm.eLR, &sm.flag, fl);
-        // r, k, neg_kk, kka of the lane's elements as bf16 pairs, for the
+        if (pend_cbase >= 0) flush(tid);  // the previous chunk's gradients
+        chunk::LaneFactors<L, NW> fl;
+        chunk::chunk_factors<L, NW>(sm.raw, n, wv, lane, sm.At, sm.Rt, sm.Bt,
+                                    sm.Kt, sm.eL, sm.eRef, sm.eLR, &sm.flag,
+                                    fl);
+        // fl keeps r, k, neg_kk, kka of the lane's elements (fp32) for the
         // decay gradient after the chunk's vectors have been replaced
-        uint32_t prk[CPL], pab[CPL];
-#pragma unroll
-        for (int e = 0; e < CPL; ++e) {
-            prk[e] = pack_bf16x2(fl.r[e], fl.k[e]);
-            pab[e] = pack_bf16x2(fl.a[e], fl.b[e]);
-        }
         f32x4_t S0[2];
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
@@ -406,14 +415,6 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
 
         if (fallback) {
             // ---- exact sequential reverse pass for this chunk -------------
-            if (pend_cbase >= 0) {
-                store_pair(dr, pend[0]);
-                store_pair(dw, pend[1]);
-                store_pair(dk, pend[2]);
-                store_pair(da, pend[3]);
-                store_pair(db, pend[4]);
-                store_dv();
-            }
             pend_cbase = -1;
             if (c >= 1) fetch(c - 1, tid);
 #pragma unroll
@@ -437,10 +438,6 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                     D[q][e] = sm.fb.Df[(toff[q] / CN) * 65 + toff[q] % CN + e];
         } else {
             // ================= 2 ==========================================
-            if (pend_cbase >= 0) {
-                store_pair(dr, pend[0]);
-                store_pair(dw, pend[1]);
-            }
             if (c >= 1) fetch_part(c - 1, NPRE, tid);  // S_0 first
             // S' = S_0 e^{g_ref} and D' = D e^{g_L - g_ref} ([i][j]);
             // sum_i D[i][j] S_L[i][j] per column (the decay's tail)
@@ -505,10 +502,6 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             __syncthreads();
 
             // ================= 3 ==========================================
-            if (pend_cbase >= 0) {
-                store_pair(dk, pend[2]);
-                store_pair(da, pend[3]);
-            }
             if (c >= 1) fetch_part(c - 1, 0, tid);
             {
                 // U = A~ S'^T + Aak V -> Ut[i][t];
@@ -544,10 +537,6 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             __syncthreads();
 
             // ================= 4 ==========================================
-            if (pend_cbase >= 0) {
-                store_pair(db, pend[4]);
-                store_dv();
-            }
             if (c >= 1) fetch_part(c - 1, 1, tid);
             // X = Minv U -> X[t][i]; dU = Minv^T dX -> dU[t][i].  NB = 2:
             // every wave one X and one dU tile (t block wv / 4, i block
@@ -748,14 +737,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                 };
                 ldg(sm.g.gR, gRv); ldg(sm.g.gA, gAv);
                 ldg(sm.g.gB, gBv); ldg(sm.g.gK, gKv);
-                float rv[CPL], kv[CPL], av[CPL], bv[CPL];
-#pragma unroll
-                for (int e = 0; e < CPL; ++e) {
-                    rv[e] = __uint_as_float(prk[e] << 16);
-                    kv[e] = __uint_as_float(prk[e] & 0xffff0000u);
-                    av[e] = __uint_as_float(pab[e] << 16);
-                    bv[e] = __uint_as_float(pab[e] & 0xffff0000u);
-                }
+                const float *rv = fl.r, *kv = fl.k, *av = fl.a, *bv = fl.b;
                 float drv[CPL], dav[CPL], dbv[CPL], dkv[CPL], dwv[CPL];
                 constexpr float kLn2 = 0.6931471805599453f;
 #pragma unroll
@@ -773,21 +755,18 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                     dwv[e] = (chunk::suffix_scan_lanes<L>(f, lane) + tail) *
                              fl.lam[e] * kLn2;
                 }
-#pragma unroll
-                for (int h = 0; h < CPL / 2; ++h) {
-                    pend[0][h] = pack_bf16x2(drv[2 * h], drv[2 * h + 1]);
-                    pend[1][h] = pack_bf16x2(dwv[2 * h], dwv[2 * h + 1]);
-                    pend[2][h] = pack_bf16x2(dkv[2 * h], dkv[2 * h + 1]);
-                    pend[3][h] = pack_bf16x2(dav[2 * h], dav[2 * h + 1]);
-                    pend[4][h] = pack_bf16x2(dbv[2 * h], dbv[2 * h + 1]);
-                }
+                // stage the gradients (the rows of padding tokens are
+                // staged but never written out)
+                chunk::store_cols<CPL>(&sm.stg[0][t][j0], drv);
+                chunk::store_cols<CPL>(&sm.stg[1][t][j0], dwv);
+                chunk::store_cols<CPL>(&sm.stg[2][t][j0], dkv);
+                chunk::store_cols<CPL>(&sm.stg[3][t][j0], dav);
+                chunk::store_cols<CPL>(&sm.stg[4][t][j0], dbv);
+                if (has_v)
+                    store_tile_bf16_t(dvt, &sm.stg[5][16 * vsb][16 * vib], PN,
+                                      lane);
                 pend_cbase = (t0 * BH + bh) * CN;
-                pend_ok = t < n;
-                pend_lane = uint32_t(t) * BHCN + j0;
-                const int s = 16 * vsb + lr;
-                pend_dv = pack4(dvt);
-                pend_vok = has_v && s < n;
-                pend_vlane = uint32_t(s) * BHCN + 16 * vib + 4 * lq;
+                pend_n = n;
             }
             D[0] = Dn[0];
             D[1] = Dn[1];
@@ -797,14 +776,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         if (tid == 0) sm.flag = 0;
         __syncthreads();
     }
-    if (pend_cbase >= 0) {
-        store_pair(dr, pend[0]);
-        store_pair(dw, pend[1]);
-        store_pair(dk, pend[2]);
-        store_pair(da, pend[3]);
-        store_pair(db, pend[4]);
-        store_dv();
-    }
+    if (pend_cbase >= 0) flush(tid);
 #pragma unroll
     for (int q = 0; q < 2; ++q)
         *reinterpret_cast<float4*>(ds0 + sbase + toff[q]) =

@@ -154,76 +154,83 @@ __device__ __forceinline__ float prev_lane(float x) {
 }
 
 // ---------------------------------------------------------------------------
-// Decayed factors of one chunk.  Lane = (token t = lane % L, CPL = L/8
-// columns j0 .. j0+CPL-1 with j0 = 8*wave + CPL*(lane / L)).  The log-decay
-// is kept in base 2 (lam = log2 d_t, g its running sum over the chunk) and
-// the reference point is g_ref = g at token L/2 - 1.  Writes the token-major
-// factors
+// Decayed factors of one chunk, computed by NW waves.  Lane = (token
+// t = lane % L, CPL = L * CN / (64 * NW) columns j0 .. j0+CPL-1 with
+// j0 = (CN / NW) * wave + CPL * (lane / L)).  The log-decay is kept in base
+// 2 (lam = log2 d_t, g its running sum over the chunk) and the reference
+// point is g_ref = g at token L/2 - 1.  Writes the token-major factors
 //   A~_t = a_t 2^{g_{t-1}-g_ref}, R~_t = r_t 2^{g_t-g_ref},
 //   B~_t = b_t 2^{g_ref-g_t},     K~_t = k_t 2^{g_ref-g_t},
 // and per column 2^{g_L}, 2^{g_ref}, 2^{g_L-g_ref}; raises *flag when the
 // factored form cannot represent the chunk.  raw: the chunk's vectors
 // (r, w, k, v, neg_kk, kka, ...) as [vec][t][j]; tokens t >= n are padding.
-template <int L>
+template <int L, int NW>
 struct LaneFactors {
-    static constexpr int CPL = L / 8;
+    static constexpr int CPL = L * CN / (64 * NW);
+    static_assert(CPL == 1 || CPL == 2 || CPL == 4, "columns per lane");
     int t, j0;
     float lam[CPL], eg[CPL], eng[CPL], eprev[CPL];
     float r[CPL], k[CPL], a[CPL], b[CPL];
 };
 
-template <int L>
+template <int CPL>
 __device__ __forceinline__ void load_cols(const bf16_t* p, float* dst) {
-    if constexpr (L == 32) {
+    if constexpr (CPL == 4) {
         const uint2 u = *reinterpret_cast<const uint2*>(p);
         dst[0] = __uint_as_float(u.x << 16);
         dst[1] = __uint_as_float(u.x & 0xffff0000u);
         dst[2] = __uint_as_float(u.y << 16);
         dst[3] = __uint_as_float(u.y & 0xffff0000u);
-    } else {
+    } else if constexpr (CPL == 2) {
         const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
         dst[0] = __uint_as_float(u << 16);
         dst[1] = __uint_as_float(u & 0xffff0000u);
+    } else {
+        dst[0] = bf16_to_f32(*p);
     }
 }
 
-template <int L>
+template <int CPL>
 __device__ __forceinline__ void store_cols(bf16_t* p, const float* x) {
-    if constexpr (L == 32) {
+    if constexpr (CPL == 4) {
         uint2 u;
         u.x = pack_bf16x2(x[0], x[1]);
         u.y = pack_bf16x2(x[2], x[3]);
         *reinterpret_cast<uint2*>(p) = u;
-    } else {
+    } else if constexpr (CPL == 2) {
         *reinterpret_cast<uint32_t*>(p) = pack_bf16x2(x[0], x[1]);
+    } else {
+        *p = to_bf16(x[0]);
     }
 }
 
-// CPL consecutive floats (16-byte or 8-byte aligned) in one LDS write.
+// CPL consecutive floats (aligned to their size) in one LDS write.
 template <int CPL>
 __device__ __forceinline__ void store_f32(float* p, const float* x) {
     if constexpr (CPL == 4)
         *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
-    else
+    else if constexpr (CPL == 2)
         *reinterpret_cast<float2*>(p) = make_float2(x[0], x[1]);
+    else
+        *p = x[0];
 }
 
-template <int L>
+template <int L, int NW>
 __device__ __forceinline__ void chunk_factors(
     const bf16_t (*raw)[L][PN], int n, int wv, int lane, bf16_t (*At)[PN],
     bf16_t (*Rt)[PN], bf16_t (*Bt)[PN], bf16_t (*Kt)[PN], float* eL,
-    float* eRef, float* eLR, int* flag, LaneFactors<L>& F) {
-    constexpr int CPL = L / 8;
+    float* eRef, float* eLR, int* flag, LaneFactors<L, NW>& F) {
+    constexpr int CPL = LaneFactors<L, NW>::CPL;
     const int t = lane % L, grp = lane / L;
-    const int j0 = 8 * wv + CPL * grp;
+    const int j0 = (CN / NW) * wv + CPL * grp;
     F.t = t;
     F.j0 = j0;
     float wl[CPL];
-    load_cols<L>(&raw[0][t][j0], F.r);
-    load_cols<L>(&raw[1][t][j0], wl);
-    load_cols<L>(&raw[2][t][j0], F.k);
-    load_cols<L>(&raw[4][t][j0], F.a);
-    load_cols<L>(&raw[5][t][j0], F.b);
+    load_cols<CPL>(&raw[0][t][j0], F.r);
+    load_cols<CPL>(&raw[1][t][j0], wl);
+    load_cols<CPL>(&raw[2][t][j0], F.k);
+    load_cols<CPL>(&raw[4][t][j0], F.a);
+    load_cols<CPL>(&raw[5][t][j0], F.b);
     float g[CPL];
     const bool valid = t < n;
 #pragma unroll
@@ -272,10 +279,10 @@ __device__ __forceinline__ void chunk_factors(
     }
     // the factored form needs g_ref >= -H and g_L - g_ref >= -H
     if (lo < -kHalfRange * kLog2e) *flag = 1;
-    store_cols<L>(&At[t][j0], fA);
-    store_cols<L>(&Rt[t][j0], fR);
-    store_cols<L>(&Bt[t][j0], fB);
-    store_cols<L>(&Kt[t][j0], fK);
+    store_cols<CPL>(&At[t][j0], fA);
+    store_cols<CPL>(&Rt[t][j0], fR);
+    store_cols<CPL>(&Bt[t][j0], fB);
+    store_cols<CPL>(&Kt[t][j0], fK);
     if (t == 1) store_f32<CPL>(&eRef[j0], sp);
     if (t == 2) store_f32<CPL>(&eL[j0], sp);
     if (t == L - 1) store_f32<CPL>(&eLR[j0], F.eg);
@@ -319,20 +326,25 @@ __device__ __forceinline__ void lower_tile_index(int rem, int& tb, int& sb) {
 }
 
 // ---------------------------------------------------------------------------
-// A 16 x 16 matrix as a v_mfma_f32_16x16x32_bf16 operand, straight from an
-// accumulator tile.  D(M), the accumulator layout, has lane l holding
-// M[4 (l/16) + e][l % 16] (e = 0..3).  kq(D(M)) puts those four values, as
-// bf16, in operand slots 8 (l/16) + e and zeros in slots 8 (l/16) + 4..7:
-// the contraction index k = 4 (l/16) + e occupies the same slot in either
-// operand, so kq(D(M)) serves as M for the B operand (k x n) and as M^T for
-// the A operand (m x k):
-//   mfma(kq(D(N)), kq(D(M))) accumulates N^T M.
+// A 16 x 16 matrix as an operand of v_mfma_f32_16x16x16_bf16, straight from
+// an accumulator tile.  D(M), the accumulator layout, has lane l holding
+// M[4 (l/16) + e][l % 16] (e = 0..3); the 16x16x16 operands take, in lane l,
+// A[l % 16][4 (l/16) + e] and B[4 (l/16) + e][l % 16].  So kq(D(M)), the
+// lane's four values as bf16, is M as the B operand and M^T as the A
+// operand:
+//   mfma16(acc, kq(D(N)), kq(D(M))) accumulates N^T M.
 // Products then chain in registers; a transpose costs a second product.
-__device__ __forceinline__ bf16x8_t kq(const f32x4_t& d) {
-    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-    const u32x4_t u = {pack_bf16x2(d[0], d[1]), pack_bf16x2(d[2], d[3]), 0u,
-                       0u};
-    return __builtin_bit_cast(bf16x8_t, u);
+// These products never accumulate onto a 16x16x32 result (their
+// accumulators start from zero, from VALU sums or from 16x16x16 results).
+__device__ __forceinline__ i16x4_t kq(const f32x4_t& d) {
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    const u32x2_t u = {pack_bf16x2(d[0], d[1]), pack_bf16x2(d[2], d[3])};
+    return __builtin_bit_cast(i16x4_t, u);
+}
+
+__device__ __forceinline__ void mfma16(f32x4_t& acc, const i16x4_t& a,
+                                       const i16x4_t& b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc, 0, 0, 0);
 }
 
 // Minv = (I - Aab)^{-1} of a chunk on one wave, entirely in registers, from
@@ -381,11 +393,11 @@ __device__ __forceinline__ void minv_regs(const bf16_t (*At)[PN],
     f32x4_t dM[NB], dM1T = zero4();
 #pragma unroll
     for (int p = 0; p < NB; ++p) {
-        const bf16x8_t pA = kq(dA[p]), pT = kq(dAT[p]);
+        const i16x4_t pA = kq(dA[p]), pT = kq(dAT[p]);
         f32x4_t x2 = zero4(), t2 = zero4();
-        mfma(x2, pT, pA);  // A A
-        mfma(t2, pA, pT);  // A^T A^T
-        const bf16x8_t px2 = kq(x2), pt2 = kq(t2);
+        mfma16(x2, pT, pA);  // A A
+        mfma16(t2, pA, pT);  // A^T A^T
+        const i16x4_t px2 = kq(x2), pt2 = kq(t2);
         f32x4_t q1, q1t;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -393,29 +405,29 @@ __device__ __forceinline__ void minv_regs(const bf16_t (*At)[PN],
             q1[e] = one + dA[p][e] + x2[e];
             q1t[e] = one + dAT[p][e] + t2[e];
         }
-        mfma(q1, pT, px2);   // + A A^2
-        mfma(q1t, px2, pT);  // + (A^2)^T A^T
+        mfma16(q1, pT, px2);   // + A A^2
+        mfma16(q1t, px2, pT);  // + (A^2)^T A^T
         f32x4_t x4 = zero4(), t4 = zero4();
-        mfma(x4, pt2, px2);  // A^2 A^2
-        mfma(t4, px2, pt2);  // (A^2)^T (A^2)^T
-        const bf16x8_t pq1t = kq(q1t), px4 = kq(x4), pt4 = kq(t4);
+        mfma16(x4, pt2, px2);  // A^2 A^2
+        mfma16(t4, px2, pt2);  // (A^2)^T (A^2)^T
+        const i16x4_t pq1t = kq(q1t), px4 = kq(x4), pt4 = kq(t4);
         f32x4_t q2 = q1, q2t = q1t, x8 = zero4();
-        mfma(q2, pq1t, px4);   // + Q1 A^4
-        mfma(q2t, px4, pq1t);  // + (A^4)^T Q1^T
-        mfma(x8, pt4, px4);    // A^4 A^4
-        const bf16x8_t pq2t = kq(q2t), px8 = kq(x8);
+        mfma16(q2, pq1t, px4);   // + Q1 A^4
+        mfma16(q2t, px4, pq1t);  // + (A^4)^T Q1^T
+        mfma16(x8, pt4, px4);    // A^4 A^4
+        const i16x4_t pq2t = kq(q2t), px8 = kq(x8);
         dM[p] = q2;
-        mfma(dM[p], pq2t, px8);  // + Q2 A^8
+        mfma16(dM[p], pq2t, px8);  // + Q2 A^8
         if (NB == 2 && p == 1) {
             dM1T = q2t;
-            mfma(dM1T, px8, pq2t);  // + (A^8)^T Q2^T
+            mfma16(dM1T, px8, pq2t);  // + (A^8)^T Q2^T
         }
         store_tile_bf16_t(dM[p], &MinvT[16 * p][16 * p], PL, lane);
     }
     if constexpr (NB == 2) {
         f32x4_t z = zero4(), m10 = zero4();
-        mfma(z, kq(dA10T), kq(dM[0]));  // Aab_10 Minv_00
-        mfma(m10, kq(dM1T), kq(z));     // Minv_11 (Aab_10 Minv_00)
+        mfma16(z, kq(dA10T), kq(dM[0]));  // Aab_10 Minv_00
+        mfma16(m10, kq(dM1T), kq(z));     // Minv_11 (Aab_10 Minv_00)
         store_tile_bf16_t(m10, &MinvT[0][16], PL, lane);
     }
 }

@@ -284,8 +284,8 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
         }
         if (prep) {
             // factors of chunk c+1; v is copied as it is
-            chunk::LaneFactors<L> fl;
-            chunk::chunk_factors<L>(sm.raw, n1, wv, lane, sm.f.At, sm.f.Rt,
+            chunk::LaneFactors<L, NW> fl;
+            chunk::chunk_factors<L, NW>(sm.raw, n1, wv, lane, sm.f.At, sm.f.Rt,
                                     sm.f.Bt, sm.f.Kt, sm.eL[nxt],
                                     sm.eRef[nxt], sm.eLR[nxt], &sm.flag[nxt],
                                     fl);

@@ -9,11 +9,13 @@
 // Lane layout (checked on gfx950 hardware):
 //   v_mfma_f32_16x16x32_bf16: A lane l holds A[l%16][8*(l/16) + 0..7],
 //     B lane l holds B[8*(l/16) + 0..7][l%16], D as above.
-// Every product uses this one instruction.  A K step of 16 is a 16x16x32
-// step whose lanes 32..63 (k = 16..31) carry zeros: accumulating a
+// Tile products from LDS use this instruction.  A K step of 16 is a
+// 16x16x32 step whose lanes 32..63 (k = 16..31) carry zeros: accumulating a
 // v_mfma_f32_16x16x16_bf16 onto the result of a 16x16x32 in the same
 // registers gave nondeterministic results on gfx950 with this toolchain
-// (no wait states are emitted between the two opcodes).
+// (no wait states are emitted between the two opcodes).  The 16x16x16 form
+// is used only for products chained in registers whose accumulators never
+// hold a 16x16x32 result (the triangular inverse).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -125,74 +127,6 @@ __device__ __forceinline__ bf16x8_t frag_kr16(const bf16_t* M, int ld,
 __device__ __forceinline__ void mfma(f32x4_t& acc, const bf16x8_t& a,
                                      const bf16x8_t& b) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
-}
-
-// acc += A[0..16)[0..K) * B[0..16)[0..K)^T.  A and B point at the first row
-// of the 16-row operand blocks; lda/ldb are row pitches in elements.
-template <int K>
-__device__ __forceinline__ void mma_nt(f32x4_t& acc, const bf16_t* A, int lda,
-                                       const bf16_t* B, int ldb, int lane) {
-    static_assert(K % 16 == 0, "K must be a multiple of 16");
-    const int r = lane & 15, q = lane >> 4;
-    const bf16_t* ar = A + r * lda;
-    const bf16_t* br = B + r * ldb;
-#pragma unroll
-    for (int k0 = 0; k0 + 32 <= K; k0 += 32) {
-        const bf16x8_t a =
-            *reinterpret_cast<const bf16x8_t*>(ar + k0 + 8 * q);
-        const bf16x8_t b =
-            *reinterpret_cast<const bf16x8_t*>(br + k0 + 8 * q);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
-    }
-    if constexpr (K % 32 == 16) {
-        constexpr int k0 = K - 16;
-        bf16x8_t a = {}, b = {};
-        if (q < 2) {
-            a = *reinterpret_cast<const bf16x8_t*>(ar + k0 + 8 * q);
-            b = *reinterpret_cast<const bf16x8_t*>(br + k0 + 8 * q);
-        }
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
-    }
-}
-
-// Runtime-K variant (K a multiple of 16, at most KMAX).
-template <int KMAX>
-__device__ __forceinline__ void mma_nt_k(f32x4_t& acc, const bf16_t* A,
-                                         int lda, const bf16_t* B, int ldb,
-                                         int K, int lane) {
-    const int r = lane & 15, q = lane >> 4;
-    const bf16_t* ar = A + r * lda;
-    const bf16_t* br = B + r * ldb;
-    int k0 = 0;
-#pragma unroll
-    for (int it = 0; it < KMAX / 32; ++it) {
-        if (k0 + 32 <= K) {
-            const bf16x8_t a =
-                *reinterpret_cast<const bf16x8_t*>(ar + k0 + 8 * q);
-            const bf16x8_t b =
-                *reinterpret_cast<const bf16x8_t*>(br + k0 + 8 * q);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0,
-                                                          0);
-            k0 += 32;
-        }
-    }
-    if (k0 + 16 <= K) {
-        bf16x8_t a = {}, b = {};
-        if (q < 2) {
-            a = *reinterpret_cast<const bf16x8_t*>(ar + k0 + 8 * q);
-            b = *reinterpret_cast<const bf16x8_t*>(br + k0 + 8 * q);
-        }
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
-    }
-}
-
-// Store a tile as bf16 into D[m][n] (row-major, pitch ld): 4 scattered
-// 2-byte writes per lane.
-__device__ __forceinline__ void store_tile_bf16(const f32x4_t& acc,
-                                                bf16_t* D, int ld, int lane) {
-    const int r = lane & 15, q = lane >> 4;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) D[(4 * q + e) * ld + r] = to_bf16(acc[e]);
 }
 
 // Store a tile transposed as bf16 into D[n][m] (pitch ld, a multiple of 4):

@@ -44,6 +44,10 @@ def parse_args():
     p.add_argument("--chunk", type=int, default=0,
                    help="checkpoint interval / chunk length (0 = library "
                         "default)")
+    p.add_argument("--layout", choices=("tbhn", "bthn"), default="tbhn",
+                   help="vector layout: time-major [T,B,H,N] (the "
+                        "reference's WKV contract) or batch-major "
+                        "[B,T,H,N] (the _bthn entry points)")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="target CPU-baseline sample duration (0 = skip)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -62,7 +66,7 @@ def algorithmic_bytes(T, B, H, N, eb):
     return 7 * V + 2 * S, 13 * V + 3 * S
 
 
-def measured_traffic(kernel, config, chunk):
+def measured_traffic(kernel, config, chunk, layout="tbhn"):
     """HBM bytes per launch of ``kernel`` from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE measurement, or None if none matches."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
@@ -73,7 +77,8 @@ def measured_traffic(kernel, config, chunk):
         return None
     for row in rows:
         if (row.get("kernel") == kernel and row.get("config") == config
-                and row.get("chunk") == chunk):
+                and row.get("chunk") == chunk
+                and row.get("layout", "tbhn") == layout):
             return row.get("bytes_per_launch")
     return None
 
@@ -261,15 +266,22 @@ def main():
         del src, dst
     if T == 1:
         return bench_decode(args, cfg, inp, stream)
+    if args.layout == "bthn":
+        # batch-major copies, made before the timed region
+        vecs = [x.transpose(0, 1).contiguous() for x in vecs]
+        dy = dy.transpose(0, 1).contiguous()
+        del inp
+        torch.cuda.synchronize()
 
     def step(evs=None):
         if evs:
             evs[0].record(stream)
         (y, s_t), aux = wkv_hip.forward_with_aux(
-            *vecs, s0, checkpoint_interval=args.chunk)
+            *vecs, s0, checkpoint_interval=args.chunk, layout=args.layout)
         if evs:
             evs[1].record(stream)
-        grads = wkv_hip.backward(*vecs, s0, dy, ds_t, *aux)
+        grads = wkv_hip.backward(*vecs, s0, dy, ds_t, *aux,
+                                 layout=args.layout)
         if evs:
             evs[2].record(stream)
         return y, s_t, grads
@@ -318,9 +330,11 @@ def main():
         "config": {
             "workload": (f"config {args.config}: WKV-7 fwd+bwd B={B} T={T} "
                          f"H={H} N={N} "
-                         f"{'bf16' if eb == 2 else 'fp32'} vectors, fp32 "
-                         f"state"),
+                         f"{'bf16' if eb == 2 else 'fp32'} vectors "
+                         f"({'time' if args.layout == 'tbhn' else 'batch'}"
+                         f"-major), fp32 state"),
             "B": B, "T": T, "H": H, "N": N, "chunk": ci,
+            "layout": args.layout,
         },
         "roofline": {
             "bound": "hbm",
@@ -329,7 +343,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": measured_traffic(dominant, args.config, ci),
+            "traffic": measured_traffic(dominant, args.config, ci,
+                                        args.layout),
             "algorithmic_bytes": dom_bytes,
             "avg_ms": dom_ms,
         },

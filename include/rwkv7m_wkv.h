@@ -124,6 +124,38 @@ int rwkv7m_wkv7_backward(int dtype, int64_t T, int64_t B, int64_t H,
                          float *ds0, void *stream);
 
 /*
+ * Batch-major variants: the same three calls, with the token vectors (r,
+ * w, k, v, neg_kk, kka, y, dy and the six vector gradients) laid out
+ * [B][T][H][N] instead of [T][B][H][N].  States and checkpoints keep their
+ * layouts.  The reference's model keeps its activations batch-major and
+ * transposes to and from the time-major WKV layout around every call
+ * (src/rwkv7m/model/nnx_model.py:695-698 before, :709-711 after); these
+ * entry points take the batch-major tensors as they are.  Results equal
+ * those of the time-major calls on the transposed tensors.
+ */
+int rwkv7m_wkv7_forward_bthn(int dtype, int64_t T, int64_t B, int64_t H,
+                             int64_t N, const void *r, const void *w,
+                             const void *k, const void *v, const void *neg_kk,
+                             const void *kka, const float *initial_state,
+                             void *y, float *final_state, void *stream);
+
+int rwkv7m_wkv7_forward_with_aux_bthn(
+    int dtype, int64_t T, int64_t B, int64_t H, int64_t N, const void *r,
+    const void *w, const void *k, const void *v, const void *neg_kk,
+    const void *kka, const float *initial_state, void *y, float *final_state,
+    void *checkpoints, int64_t checkpoint_interval, void *stream);
+
+int rwkv7m_wkv7_backward_bthn(int dtype, int64_t T, int64_t B, int64_t H,
+                              int64_t N, const void *r, const void *w,
+                              const void *k, const void *v, const void *neg_kk,
+                              const void *kka, const float *initial_state,
+                              const void *dy, const float *ds_t,
+                              const void *checkpoints,
+                              int64_t checkpoint_interval, void *dr, void *dw,
+                              void *dk, void *dv, void *dneg_kk, void *dkka,
+                              float *ds0, void *stream);
+
+/*
  * decode_inplace: one token (T = 1) for B*H states, with the fp32 state
  * read and overwritten in place in HBM.  The T == 1 case of forward
  * (the eager decode loop at src/rwkv7m/infer/generate.py:74-99 reaches

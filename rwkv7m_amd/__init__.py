@@ -19,7 +19,7 @@ from .kernels import (
     resolve_wkv_backend,
     unregister_wkv_ffi_backend,
 )
-from .wkv import wkv7, wkv7_reference
+from .wkv import wkv7, wkv7_batch_major, wkv7_reference
 
 __all__ = [
     "WKVBackend",
@@ -32,5 +32,6 @@ __all__ = [
     "resolve_wkv_backend",
     "unregister_wkv_ffi_backend",
     "wkv7",
+    "wkv7_batch_major",
     "wkv7_reference",
 ]

@@ -125,6 +125,23 @@ bool aligned16(const void* p) {
     return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
+// Token vectors' layout: time-major [T][B][H][N] (the reference's) or
+// batch-major [B][T][H][N].
+rwkv7m::VecLayout vec_layout(bool batch_major, int64_t T, int64_t B,
+                             int64_t H, int64_t N) {
+    rwkv7m::VecLayout l;
+    l.H = H;
+    if (batch_major) {
+        l.ts = H * N;
+        l.bs = T * H * N;
+    } else {
+        l.ts = B * H * N;
+        l.bs = H * N;
+    }
+    (void)B;
+    return l;
+}
+
 bool all_aligned16(std::initializer_list<const void*> ptrs) {
     for (const void* p : ptrs)
         if (p && !aligned16(p)) return false;
@@ -133,12 +150,13 @@ bool all_aligned16(std::initializer_list<const void*> ptrs) {
 
 // The chunked MFMA kernels serve bf16 vectors with N = 64, a chunk length
 // (= checkpoint interval) of 16 or 32, 16-byte aligned buffers, and chunks
-// whose element span L * B*H * N stays below 2^31 (32-bit lane offsets).
-bool use_chunked(int dtype, int64_t N, int64_t ci, int64_t BH,
+// whose element span L * (token stride) stays below 2^31 (32-bit lane
+// offsets).
+bool use_chunked(int dtype, int64_t N, int64_t ci, int64_t token_stride,
                  std::initializer_list<const void*> ptrs) {
     if (dtype != RWKV7M_DTYPE_BF16 || N != 64) return false;
     if (ci != 16 && ci != 32) return false;
-    if (BH * N * ci >= (int64_t(1) << 31)) return false;
+    if (token_stride * ci >= (int64_t(1) << 31)) return false;
     return all_aligned16(ptrs);
 }
 
@@ -146,7 +164,7 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
                  int64_t N, const void* r, const void* w, const void* k,
                  const void* v, const void* a, const void* b,
                  const float* s0, void* y, float* s_t, void* ckpt,
-                 int64_t ci, hipStream_t stream) {
+                 int64_t ci, hipStream_t stream, bool batch_major) {
     Dims d;
     RWKV7M_TRY(check_dims(fn, dtype, T, B, H, N, &d));
     const bool vecs = d.vec_elems > 0, st = d.state_elems > 0;
@@ -162,13 +180,15 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     if (d.state_elems == 0) return RWKV7M_OK;
     if (T == 0 && !ckpt) return copy_or_clear(s_t, s0, d.state_elems, stream);
     const int64_t L = ckpt ? ci : kDefaultChunk;
+    const rwkv7m::VecLayout lay = vec_layout(batch_major, T, B, H, N);
     if (T > 1 &&
-        use_chunked(dtype, N, L, B * H, {r, w, k, v, a, b, y, s0, s_t, ckpt})) {
+        use_chunked(dtype, N, L, lay.ts, {r, w, k, v, a, b, y, s0, s_t, ckpt})) {
         rwkv7m::ChunkFwdArgs c{};
         c.L = int(L);
         c.T = T;
         c.B = B;
         c.H = H;
+        c.lay = lay;
         c.r = r;
         c.w = w;
         c.k = k;
@@ -188,6 +208,7 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     p.B = B;
     p.H = H;
     p.N = N;
+    p.lay = lay;
     p.r = r;
     p.w = w;
     p.k = k;
@@ -205,6 +226,118 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
         return hip_status("decode launch", rwkv7m::launch_decode(p, stream));
     return hip_status("sequential forward launch",
                       rwkv7m::launch_seq_forward(p, stream));
+}
+
+int backward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
+                         int64_t N, const void* r, const void* w,
+                         const void* k, const void* v, const void* neg_kk,
+                         const void* kka, const float* initial_state,
+                         const void* dy, const float* ds_t,
+                         const void* checkpoints,
+                         int64_t checkpoint_interval, void* dr, void* dw,
+                         void* dk, void* dv, void* dneg_kk, void* dkka,
+                         float* ds0, hipStream_t s, bool batch_major) {
+    (void)initial_state;  // checkpoints[0] holds it
+    Dims d;
+    RWKV7M_TRY(check_dims(fn, dtype, T, B, H, N, &d));
+    if (checkpoint_interval < 0)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": checkpoint_interval must be >= 0");
+    const int64_t ci = checkpoint_interval == 0
+                           ? default_interval(dtype, N)
+                           : checkpoint_interval;
+    const bool vecs = d.vec_elems > 0, st = d.state_elems > 0;
+    RWKV7M_TRY(need(r, vecs, fn, "r"));
+    RWKV7M_TRY(need(w, vecs, fn, "w"));
+    RWKV7M_TRY(need(k, vecs, fn, "k"));
+    RWKV7M_TRY(need(v, vecs, fn, "v"));
+    RWKV7M_TRY(need(neg_kk, vecs, fn, "neg_kk"));
+    RWKV7M_TRY(need(kka, vecs, fn, "kka"));
+    RWKV7M_TRY(need(dr, vecs, fn, "dr"));
+    RWKV7M_TRY(need(dw, vecs, fn, "dw"));
+    RWKV7M_TRY(need(dk, vecs, fn, "dk"));
+    RWKV7M_TRY(need(dv, vecs, fn, "dv"));
+    RWKV7M_TRY(need(dneg_kk, vecs, fn, "dneg_kk"));
+    RWKV7M_TRY(need(dkka, vecs, fn, "dkka"));
+    RWKV7M_TRY(need(ds0, st, fn, "ds0"));
+    RWKV7M_TRY(need(checkpoints, vecs, fn, "checkpoints"));
+    if (d.state_elems == 0) return RWKV7M_OK;
+    if (T == 0) return copy_or_clear(ds0, ds_t, d.state_elems, s);
+    const rwkv7m::VecLayout lay = vec_layout(batch_major, T, B, H, N);
+    if (use_chunked(dtype, N, ci, lay.ts,
+                    {r, w, k, v, neg_kk, kka, dy, ds_t, checkpoints, dr, dw,
+                     dk, dv, dneg_kk, dkka, ds0})) {
+        rwkv7m::ChunkBwdArgs c{};
+        c.L = int(ci);
+        c.T = T;
+        c.B = B;
+        c.H = H;
+        c.lay = lay;
+        c.r = r;
+        c.w = w;
+        c.k = k;
+        c.v = v;
+        c.a = neg_kk;
+        c.b = kka;
+        c.dy = dy;
+        c.ds_t = ds_t;
+        c.ckpt = checkpoints;
+        c.dr = dr;
+        c.dw = dw;
+        c.dk = dk;
+        c.dv = dv;
+        c.da = dneg_kk;
+        c.db = dkka;
+        c.ds0 = ds0;
+        return hip_status("chunked backward launch",
+                          rwkv7m::launch_chunk_backward(c, s));
+    }
+    rwkv7m::SeqBwdArgs p{};
+    p.bf16 = dtype == RWKV7M_DTYPE_BF16;
+    p.T = T;
+    p.B = B;
+    p.H = H;
+    p.N = N;
+    p.lay = lay;
+    p.r = r;
+    p.w = w;
+    p.k = k;
+    p.v = v;
+    p.a = neg_kk;
+    p.b = kka;
+    p.dy = dy;
+    p.ds_t = ds_t;
+    p.ckpt = checkpoints;
+    p.ckpt_bf16 = ckpt_bf16(dtype, N, ci);
+    p.ci = ci;
+    p.dr = dr;
+    p.dw = dw;
+    p.dk = dk;
+    p.dv = dv;
+    p.da = dneg_kk;
+    p.db = dkka;
+    p.ds0 = ds0;
+    return hip_status("sequential backward launch",
+                      rwkv7m::launch_seq_backward(p, s));
+}
+
+int forward_aux_impl(const char* fn, int dtype, int64_t T, int64_t B,
+                     int64_t H, int64_t N, const void* r, const void* w,
+                     const void* k, const void* v, const void* neg_kk,
+                     const void* kka, const float* initial_state, void* y,
+                     float* final_state, void* checkpoints,
+                     int64_t checkpoint_interval, hipStream_t stream,
+                     bool batch_major) {
+    if (checkpoint_interval < 0)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": checkpoint_interval must be >= 0");
+    const int64_t ci = checkpoint_interval == 0
+                           ? default_interval(dtype, N)
+                           : checkpoint_interval;
+    RWKV7M_TRY(need(checkpoints, B * H * N > 0, fn, "checkpoints"));
+    return forward_impl(fn, dtype, T, B, H, N, r, w, k, v, neg_kk, kka,
+                        initial_state, y, final_state, checkpoints, ci, stream,
+                        batch_major);
 }
 
 }  // namespace
@@ -239,7 +372,18 @@ int rwkv7m_wkv7_forward(int dtype, int64_t T, int64_t B, int64_t H, int64_t N,
     g_last_error.clear();
     return forward_impl("rwkv7m_wkv7_forward", dtype, T, B, H, N, r, w, k, v,
                         neg_kk, kka, initial_state, y, final_state, nullptr,
-                        0, static_cast<hipStream_t>(stream));
+                        0, static_cast<hipStream_t>(stream), false);
+}
+
+int rwkv7m_wkv7_forward_bthn(int dtype, int64_t T, int64_t B, int64_t H,
+                             int64_t N, const void* r, const void* w,
+                             const void* k, const void* v, const void* neg_kk,
+                             const void* kka, const float* initial_state,
+                             void* y, float* final_state, void* stream) {
+    g_last_error.clear();
+    return forward_impl("rwkv7m_wkv7_forward_bthn", dtype, T, B, H, N, r, w,
+                        k, v, neg_kk, kka, initial_state, y, final_state,
+                        nullptr, 0, static_cast<hipStream_t>(stream), true);
 }
 
 int rwkv7m_wkv7_forward_with_aux(int dtype, int64_t T, int64_t B, int64_t H,
@@ -250,17 +394,22 @@ int rwkv7m_wkv7_forward_with_aux(int dtype, int64_t T, int64_t B, int64_t H,
                                  float* final_state, void* checkpoints,
                                  int64_t checkpoint_interval, void* stream) {
     g_last_error.clear();
-    const char* fn = "rwkv7m_wkv7_forward_with_aux";
-    if (checkpoint_interval < 0)
-        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
-                    std::string(fn) + ": checkpoint_interval must be >= 0");
-    const int64_t ci = checkpoint_interval == 0
-                           ? default_interval(dtype, N)
-                           : checkpoint_interval;
-    RWKV7M_TRY(need(checkpoints, B * H * N > 0, fn, "checkpoints"));
-    return forward_impl(fn, dtype, T, B, H, N, r, w, k, v, neg_kk, kka,
-                        initial_state, y, final_state, checkpoints, ci,
-                        static_cast<hipStream_t>(stream));
+    return forward_aux_impl("rwkv7m_wkv7_forward_with_aux", dtype, T, B, H, N,
+                            r, w, k, v, neg_kk, kka, initial_state, y,
+                            final_state, checkpoints, checkpoint_interval,
+                            static_cast<hipStream_t>(stream), false);
+}
+
+int rwkv7m_wkv7_forward_with_aux_bthn(
+    int dtype, int64_t T, int64_t B, int64_t H, int64_t N, const void* r,
+    const void* w, const void* k, const void* v, const void* neg_kk,
+    const void* kka, const float* initial_state, void* y, float* final_state,
+    void* checkpoints, int64_t checkpoint_interval, void* stream) {
+    g_last_error.clear();
+    return forward_aux_impl("rwkv7m_wkv7_forward_with_aux_bthn", dtype, T, B,
+                            H, N, r, w, k, v, neg_kk, kka, initial_state, y,
+                            final_state, checkpoints, checkpoint_interval,
+                            static_cast<hipStream_t>(stream), true);
 }
 
 int rwkv7m_wkv7_backward(int dtype, int64_t T, int64_t B, int64_t H,
@@ -273,87 +422,27 @@ int rwkv7m_wkv7_backward(int dtype, int64_t T, int64_t B, int64_t H,
                          void* dk, void* dv, void* dneg_kk, void* dkka,
                          float* ds0, void* stream) {
     g_last_error.clear();
-    const char* fn = "rwkv7m_wkv7_backward";
-    (void)initial_state;  // checkpoints[0] holds it
-    Dims d;
-    RWKV7M_TRY(check_dims(fn, dtype, T, B, H, N, &d));
-    if (checkpoint_interval < 0)
-        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
-                    std::string(fn) + ": checkpoint_interval must be >= 0");
-    const int64_t ci = checkpoint_interval == 0
-                           ? default_interval(dtype, N)
-                           : checkpoint_interval;
-    const bool vecs = d.vec_elems > 0, st = d.state_elems > 0;
-    RWKV7M_TRY(need(r, vecs, fn, "r"));
-    RWKV7M_TRY(need(w, vecs, fn, "w"));
-    RWKV7M_TRY(need(k, vecs, fn, "k"));
-    RWKV7M_TRY(need(v, vecs, fn, "v"));
-    RWKV7M_TRY(need(neg_kk, vecs, fn, "neg_kk"));
-    RWKV7M_TRY(need(kka, vecs, fn, "kka"));
-    RWKV7M_TRY(need(dr, vecs, fn, "dr"));
-    RWKV7M_TRY(need(dw, vecs, fn, "dw"));
-    RWKV7M_TRY(need(dk, vecs, fn, "dk"));
-    RWKV7M_TRY(need(dv, vecs, fn, "dv"));
-    RWKV7M_TRY(need(dneg_kk, vecs, fn, "dneg_kk"));
-    RWKV7M_TRY(need(dkka, vecs, fn, "dkka"));
-    RWKV7M_TRY(need(ds0, st, fn, "ds0"));
-    RWKV7M_TRY(need(checkpoints, vecs, fn, "checkpoints"));
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    if (d.state_elems == 0) return RWKV7M_OK;
-    if (T == 0) return copy_or_clear(ds0, ds_t, d.state_elems, s);
-    if (use_chunked(dtype, N, ci, B * H,
-                    {r, w, k, v, neg_kk, kka, dy, ds_t, checkpoints, dr, dw,
-                     dk, dv, dneg_kk, dkka, ds0})) {
-        rwkv7m::ChunkBwdArgs c{};
-        c.L = int(ci);
-        c.T = T;
-        c.B = B;
-        c.H = H;
-        c.r = r;
-        c.w = w;
-        c.k = k;
-        c.v = v;
-        c.a = neg_kk;
-        c.b = kka;
-        c.dy = dy;
-        c.ds_t = ds_t;
-        c.ckpt = checkpoints;
-        c.dr = dr;
-        c.dw = dw;
-        c.dk = dk;
-        c.dv = dv;
-        c.da = dneg_kk;
-        c.db = dkka;
-        c.ds0 = ds0;
-        return hip_status("chunked backward launch",
-                          rwkv7m::launch_chunk_backward(c, s));
-    }
-    rwkv7m::SeqBwdArgs p{};
-    p.bf16 = dtype == RWKV7M_DTYPE_BF16;
-    p.T = T;
-    p.B = B;
-    p.H = H;
-    p.N = N;
-    p.r = r;
-    p.w = w;
-    p.k = k;
-    p.v = v;
-    p.a = neg_kk;
-    p.b = kka;
-    p.dy = dy;
-    p.ds_t = ds_t;
-    p.ckpt = checkpoints;
-    p.ckpt_bf16 = ckpt_bf16(dtype, N, ci);
-    p.ci = ci;
-    p.dr = dr;
-    p.dw = dw;
-    p.dk = dk;
-    p.dv = dv;
-    p.da = dneg_kk;
-    p.db = dkka;
-    p.ds0 = ds0;
-    return hip_status("sequential backward launch",
-                      rwkv7m::launch_seq_backward(p, s));
+    return backward_impl("rwkv7m_wkv7_backward", dtype, T, B, H, N, r, w, k, v,
+                         neg_kk, kka, initial_state, dy, ds_t, checkpoints,
+                         checkpoint_interval, dr, dw, dk, dv, dneg_kk, dkka,
+                         ds0, static_cast<hipStream_t>(stream), false);
+}
+
+int rwkv7m_wkv7_backward_bthn(int dtype, int64_t T, int64_t B, int64_t H,
+                              int64_t N, const void* r, const void* w,
+                              const void* k, const void* v, const void* neg_kk,
+                              const void* kka, const float* initial_state,
+                              const void* dy, const float* ds_t,
+                              const void* checkpoints,
+                              int64_t checkpoint_interval, void* dr, void* dw,
+                              void* dk, void* dv, void* dneg_kk, void* dkka,
+                              float* ds0, void* stream) {
+    g_last_error.clear();
+    return backward_impl("rwkv7m_wkv7_backward_bthn", dtype, T, B, H, N, r, w,
+                         k, v, neg_kk, kka, initial_state, dy, ds_t,
+                         checkpoints, checkpoint_interval, dr, dw, dk, dv,
+                         dneg_kk, dkka, ds0, static_cast<hipStream_t>(stream),
+                         true);
 }
 
 int rwkv7m_wkv7_decode_inplace(int dtype, int64_t B, int64_t H, int64_t N,
@@ -364,7 +453,7 @@ int rwkv7m_wkv7_decode_inplace(int dtype, int64_t B, int64_t H, int64_t N,
     g_last_error.clear();
     return forward_impl("rwkv7m_wkv7_decode_inplace", dtype, 1, B, H, N, r,
                         w, k, v, neg_kk, kka, state, y, state, nullptr, 0,
-                        static_cast<hipStream_t>(stream));
+                        static_cast<hipStream_t>(stream), false);
 }
 
 }  // extern "C"

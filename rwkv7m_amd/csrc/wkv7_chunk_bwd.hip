@@ -106,7 +106,7 @@ struct BwdSmem {
 template <int L, int NW>
 __device__ void seq_chunk_backward(const bf16_t (*raw)[L][PN], int n,
                                    const float* Sf, float* Df, float* red,
-                                   int64_t t0, int64_t BH, int64_t bh,
+                                   int64_t t0, int64_t tstr, int64_t hoff,
                                    bf16_t* dr, bf16_t* dw, bf16_t* dk,
                                    bf16_t* dv, bf16_t* da, bf16_t* db,
                                    int tid) {
@@ -176,7 +176,7 @@ __device__ void seq_chunk_backward(const bf16_t (*raw)[L][PN], int n,
                 }
                 dsa = group_sum<NW>(dsa);
                 dvv = group_sum<NW>(dvv);
-                if (qq == 0) dv[((t0 + t) * BH + bh) * CN + i] = to_bf16(dvv);
+                if (qq == 0) dv[(t0 + t) * tstr + hoff + i] = to_bf16(dvv);
 #pragma unroll
                 for (int c = 0; c < CPT; ++c) {
                     float p[5];
@@ -198,7 +198,7 @@ __device__ void seq_chunk_backward(const bf16_t (*raw)[L][PN], int n,
 #pragma unroll
                     for (int w2 = 0; w2 < NTH / 64; ++w2)
                         s += red[(w2 * 5 + q) * CN + jj];
-                    const int64_t off = ((t0 + t) * BH + bh) * CN + jj;
+                    const int64_t off = (t0 + t) * tstr + hoff + jj;
                     if (q == 0) {
                         dr[off] = to_bf16(s);
                     } else if (q == 1) {
@@ -228,7 +228,8 @@ __device__ void seq_chunk_backward(const bf16_t (*raw)[L][PN], int n,
 
 template <int L>
 __global__ void __launch_bounds__(BWD_THREADS)
-wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
+wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
+                      const bf16_t* __restrict__ r,
                       const bf16_t* __restrict__ w,
                       const bf16_t* __restrict__ k,
                       const bf16_t* __restrict__ v,
@@ -251,6 +252,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
     const int lr = lane & 15, lq = lane >> 4;
     const int64_t bh = blockIdx.x;
     const int64_t sbase = bh * CN * CN;
+    const int64_t hoff = lay.head(bh, CN);  // the head's vector offset
     const int64_t NN = CN * CN;
     const chunk::VecPtrs src{r, w, k, v, a, b, dy};
     const int64_t nch = (T + L - 1) / L;
@@ -282,13 +284,14 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
 
     // ---- the chunk's vectors and S_0, prefetched one chunk ahead --------
     // HBM addresses are a per-chunk scalar base plus a 32-bit per-lane
-    // offset (t * BH * CN + column; the host keeps L * BH * CN below 2^31).
+    // offset (t * ts + column, ts the token stride; the host keeps L * ts
+    // below 2^31).
     constexpr int SEGV = 7 * L * 8;  // 16-byte segments of the 7 vectors
     constexpr int NPRE = (SEGV + NTH - 1) / NTH;
     static_assert(CN * CN * 2 / 16 == NTH, "one S_0 segment per thread");
     static_assert((8 * L) % 64 == 0 && SEGV % 64 == 0,
                   "each wave loads from one vector");
-    const uint32_t BHCN = uint32_t(BH) * CN;
+    const uint32_t TS = uint32_t(lay.ts);
     // part p of this wave: one vector (the same for all 64 lanes), or none
     const bf16_t* vp[NPRE];
 #pragma unroll
@@ -301,7 +304,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
     // (lane offsets are formed at each fetch: kept across the loop they
     // would hold registers for the whole run)
     auto fetch_part = [&](int64_t cc, int part, int tidv) {
-        const int64_t cbase = (cc * L * BH + bh) * CN;
+        const int64_t cbase = cc * L * lay.ts + hoff;
         const int ncc = int(T - cc * L < L ? T - cc * L : L);
 #pragma unroll
         for (int p = 0; p < NPRE; ++p) {
@@ -311,7 +314,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                 pre[p] = make_uint4(0, 0, 0, 0);
                 if (vp[p] != nullptr && int(t) < ncc)
                     pre[p] = *reinterpret_cast<const uint4*>(
-                        (vp[p] + cbase) + (t * BHCN + s8 * 8));
+                        (vp[p] + cbase) + (t * TS + s8 * 8));
             }
         }
         if (part == NPRE)
@@ -368,7 +371,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                               : g == 4 ? db
                                        : dv;
                 *reinterpret_cast<uint4*>((dst + pend_cbase) +
-                                          (t * BHCN + s8 * 8)) =
+                                          (t * TS + s8 * 8)) =
                     *reinterpret_cast<const uint4*>(&sm.stg[g][t][8 * s8]);
             }
         }
@@ -427,7 +430,8 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                 }
             __syncthreads();
             seq_chunk_backward<L, NW>(sm.raw, n, sm.fb.Sf, sm.fb.Df, sm.fb.red,
-                                      t0, BH, bh, dr, dw, dk, dv, da, db, tid);
+                                      t0, lay.ts, hoff, dr, dw, dk, dv, da, db,
+                                      tid);
             __syncthreads();
             if (c >= 1) stash();
             chunk::wait_vmem();
@@ -765,7 +769,7 @@ wkv7_chunk_bwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                 if (has_v)
                     store_tile_bf16_t(dvt, &sm.stg[5][16 * vsb][16 * vib], PN,
                                       lane);
-                pend_cbase = (t0 * BH + bh) * CN;
+                pend_cbase = t0 * lay.ts + hoff;
                 pend_n = n;
             }
             D[0] = Dn[0];
@@ -787,7 +791,7 @@ template <int L>
 hipError_t launch_l(const ChunkBwdArgs& p, hipStream_t stream) {
     const int64_t BH = p.B * p.H;
     hipLaunchKernelGGL((wkv7_chunk_bwd_kernel<L>), dim3(unsigned(BH)),
-                       dim3(BWD_THREADS), 0, stream, p.T, BH,
+                       dim3(BWD_THREADS), 0, stream, p.T, BH, p.lay,
                        static_cast<const bf16_t*>(p.r),
                        static_cast<const bf16_t*>(p.w),
                        static_cast<const bf16_t*>(p.k),

@@ -94,7 +94,7 @@ struct FwdSmem {
 // state in LDS ([64][65]); thread: row i = tid / NW, CPT columns.
 template <int NW>
 __device__ void seq_chunk_forward(float (*S)[CN + 1], int n, int64_t t0,
-                                  int64_t BH, int64_t bh,
+                                  int64_t tstr, int64_t hoff,
                                   const chunk::VecPtrs& src,
                                   bf16_t* __restrict__ y, int tid) {
     constexpr int CPT = CN / NW;
@@ -103,7 +103,7 @@ __device__ void seq_chunk_forward(float (*S)[CN + 1], int n, int64_t t0,
 #pragma unroll
     for (int c = 0; c < CPT; ++c) Sl[c] = S[i][c0 + c];
     for (int t = 0; t < n; ++t) {
-        const int64_t off = ((t0 + t) * BH + bh) * CN;
+        const int64_t off = (t0 + t) * tstr + hoff;
         float sa = 0.f;
 #pragma unroll
         for (int c = 0; c < CPT; ++c)
@@ -128,7 +128,8 @@ __device__ void seq_chunk_forward(float (*S)[CN + 1], int n, int64_t t0,
 
 template <int L>
 __global__ void __launch_bounds__(FWD_THREADS)
-wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
+wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, VecLayout lay,
+                      const bf16_t* __restrict__ r,
                       const bf16_t* __restrict__ w,
                       const bf16_t* __restrict__ k,
                       const bf16_t* __restrict__ v,
@@ -146,6 +147,7 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
     const int lr = lane & 15, lq = lane >> 4;
     const int64_t bh = blockIdx.x;
     const int64_t sbase = bh * CN * CN;
+    const int64_t hoff = lay.head(bh, CN);  // the head's vector offset
     const int64_t NN = CN * CN;
     const chunk::VecPtrs src{r, w, k, v, a, b, nullptr};
     const int64_t nch = (T + L - 1) / L;
@@ -179,12 +181,13 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
 
     // ---- the vectors, prefetched one chunk ahead into registers ----------
     // HBM addresses are a per-chunk scalar base plus a 32-bit per-lane
-    // offset (t * BH * CN + column; the host keeps L * BH * CN below 2^31).
+    // offset (t * ts + column, ts the token stride; the host keeps L * ts
+    // below 2^31).
     constexpr int SEG = 6 * L * 8;  // 16-byte segments of one chunk
     constexpr int NPRE = (SEG + NTH - 1) / NTH;
     static_assert((8 * L) % 64 == 0 && SEG % 64 == 0,
                   "each wave loads from one vector");
-    const uint32_t BHCN = uint32_t(BH) * CN;
+    const uint32_t TS = uint32_t(lay.ts);
     // part p of this wave: one vector (the same for all 64 lanes), or none
     const bf16_t* vp[NPRE];
 #pragma unroll
@@ -194,7 +197,7 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
     }
     uint4 pre[NPRE];
     auto fetch = [&](int64_t cc) {
-        const int64_t cbase = (cc * L * BH + bh) * CN;
+        const int64_t cbase = cc * L * lay.ts + hoff;
         const int ncc = int(T - cc * L < L ? T - cc * L : L);
 #pragma unroll
         for (int p = 0; p < NPRE; ++p) {
@@ -203,7 +206,7 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
             pre[p] = make_uint4(0, 0, 0, 0);
             if (vp[p] != nullptr && int(t) < ncc)
                 pre[p] = *reinterpret_cast<const uint4*>(
-                    (vp[p] + cbase) + (t * BHCN + s8 * 8));
+                    (vp[p] + cbase) + (t * TS + s8 * 8));
         }
     };
     auto stash = [&]() {
@@ -249,7 +252,7 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                 for (int e = 0; e < 4; ++e)
                     sm.fb[soff[q] / CN][soff[q] % CN + e] = S[q][e];
             __syncthreads();
-            seq_chunk_forward<NW>(sm.fb, n, t0, BH, bh, src, y, tid);
+            seq_chunk_forward<NW>(sm.fb, n, t0, lay.ts, hoff, src, y, tid);
             __syncthreads();
 #pragma unroll
             for (int q = 0; q < 2; ++q)
@@ -319,8 +322,8 @@ wkv7_chunk_fwd_kernel(int64_t T, int64_t BH, const bf16_t* __restrict__ r,
                 const int tt = 16 * ytb + lr;
                 if (tt < n)
                     *reinterpret_cast<uint2*>(
-                        (y + (t0 * BH + bh) * CN) +
-                        (uint32_t(tt) * BHCN + 16 * yib + 4 * lq)) =
+                        (y + (t0 * lay.ts + hoff)) +
+                        (uint32_t(tt) * TS + 16 * yib + 4 * lq)) =
                         pack4(yy);
             }
         }
@@ -451,7 +454,7 @@ template <int L>
 hipError_t launch_l(const ChunkFwdArgs& p, hipStream_t stream) {
     const int64_t BH = p.B * p.H;
     hipLaunchKernelGGL((wkv7_chunk_fwd_kernel<L>), dim3(unsigned(BH)),
-                       dim3(FWD_THREADS), 0, stream, p.T, BH,
+                       dim3(FWD_THREADS), 0, stream, p.T, BH, p.lay,
                        static_cast<const bf16_t*>(p.r),
                        static_cast<const bf16_t*>(p.w),
                        static_cast<const bf16_t*>(p.k),

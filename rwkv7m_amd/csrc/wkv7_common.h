@@ -29,6 +29,17 @@ __device__ __forceinline__ void store_f(bf16_t* p, float x) {
     *p = f32_to_bf16(x);
 }
 
+// Element layout of the token vectors [T, B, H, N] or [B, T, H, N]: element
+// (t, b, h, j) sits at t * ts + b * bs + h * N + j.  Time-major (the
+// reference's layout): ts = B*H*N, bs = H*N.  Batch-major: ts = H*N,
+// bs = T*H*N.  States are [B][H][N][N] in both.
+struct VecLayout {
+    int64_t ts, bs, H;
+    __device__ __forceinline__ int64_t head(int64_t bh, int64_t N) const {
+        return (bh / H) * bs + (bh % H) * N;
+    }
+};
+
 // Sum over aligned groups of G consecutive lanes (G a power of two <= 64).
 template <int G>
 __device__ __forceinline__ float group_sum(float x) {

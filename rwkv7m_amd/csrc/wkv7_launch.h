@@ -5,11 +5,14 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "wkv7_common.h"
+
 namespace rwkv7m {
 
 struct SeqFwdArgs {
     bool bf16;
     int64_t T, B, H, N;
+    VecLayout lay;  // token vectors' layout
     const void *r, *w, *k, *v, *a, *b;
     const float* s0;
     void* y;
@@ -22,6 +25,7 @@ struct SeqFwdArgs {
 struct SeqBwdArgs {
     bool bf16;
     int64_t T, B, H, N;
+    VecLayout lay;
     const void *r, *w, *k, *v, *a, *b, *dy;
     const float* ds_t;
     const void* ckpt;
@@ -35,6 +39,7 @@ struct SeqBwdArgs {
 struct ChunkFwdArgs {
     int L;
     int64_t T, B, H;
+    VecLayout lay;
     const void *r, *w, *k, *v, *a, *b;
     const float* s0;
     void* y;
@@ -48,6 +53,7 @@ hipError_t launch_chunk_forward(const ChunkFwdArgs& p, hipStream_t stream);
 struct ChunkBwdArgs {
     int L;
     int64_t T, B, H;
+    VecLayout lay;
     const void *r, *w, *k, *v, *a, *b, *dy;
     const float* ds_t;
     const void* ckpt;  // bf16, one state every L tokens

@@ -32,7 +32,8 @@ struct SeqShape {
 // checkpoint element type (float or bf16_t).
 template <int N, typename VT, typename CT>
 __global__ void __launch_bounds__(SeqShape<N>::THREADS)
-wkv7_seq_fwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
+wkv7_seq_fwd_kernel(int64_t T, int64_t BH, VecLayout lay,
+                    const VT* __restrict__ r,
                     const VT* __restrict__ w, const VT* __restrict__ k,
                     const VT* __restrict__ v, const VT* __restrict__ a,
                     const VT* __restrict__ b, const float* s0, VT* y,
@@ -47,6 +48,7 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
     const int tid = threadIdx.x;
     const int row = tid / G, col0 = (tid % G) * C;
     const int64_t my = bh * NN + int64_t(row) * N + col0;
+    const int64_t hoff = lay.head(bh, N);
 
     float S[C];
 #pragma unroll
@@ -63,7 +65,7 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
             const int vec = e / (TB * N), rem = e - vec * TB * N;
             const int u = rem / N, j = rem - u * N;
             if (u < nt) {
-                float x = load_f(srcs[vec] + ((t0 + u) * BH + bh) * N + j);
+                float x = load_f(srcs[vec] + (t0 + u) * lay.ts + hoff + j);
                 if (vec == 1) x = expf(-expf(x));
                 sh[vec][u][j] = x;
             }
@@ -96,7 +98,7 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
         __syncthreads();
         for (int e = tid; e < nt * N; e += TH) {
             const int u = e / N, i = e - u * N;
-            store_f(y + ((t0 + u) * BH + bh) * N + i, sh_y[u][i]);
+            store_f(y + (t0 + u) * lay.ts + hoff + i, sh_y[u][i]);
         }
     }
 #pragma unroll
@@ -107,8 +109,8 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
 // 0 r, 1 decay, 2 k, 3 v, 4 a, 5 b, 6 dy, 7 exp(w).
 template <int N, typename VT>
 __device__ __forceinline__ void stage_bwd(
-    float (*sh)[SeqShape<N>::SUB][N], int64_t t0, int count, int64_t BH,
-    int64_t bh, const VT* r, const VT* w, const VT* k, const VT* v,
+    float (*sh)[SeqShape<N>::SUB][N], int64_t t0, int count, int64_t tstr,
+    int64_t hoff, const VT* r, const VT* w, const VT* k, const VT* v,
     const VT* a, const VT* b, const VT* dy) {
     using Sh = SeqShape<N>;
     constexpr int SUB = Sh::SUB, TH = Sh::THREADS;
@@ -117,7 +119,7 @@ __device__ __forceinline__ void stage_bwd(
         const int vec = e / (SUB * N), rem = e - vec * SUB * N;
         const int u = rem / N, j = rem - u * N;
         if (u < count) {
-            const int64_t off = ((t0 + u) * BH + bh) * N + j;
+            const int64_t off = (t0 + u) * tstr + hoff + j;
             if (vec == 1) {
                 const float ew = expf(load_f(w + off));
                 sh[1][u][j] = expf(-ew);
@@ -133,7 +135,8 @@ __device__ __forceinline__ void stage_bwd(
 
 template <int N, typename VT, typename CT>
 __global__ void __launch_bounds__(SeqShape<N>::THREADS)
-wkv7_seq_bwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
+wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
+                    const VT* __restrict__ r,
                     const VT* __restrict__ w, const VT* __restrict__ k,
                     const VT* __restrict__ v, const VT* __restrict__ a,
                     const VT* __restrict__ b, const VT* __restrict__ dy,
@@ -153,6 +156,7 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
     const int row = tid / G, col0 = (tid % G) * C;
     const int wave = tid / 64, lane = tid % 64;
     const int64_t my = bh * NN + int64_t(row) * N + col0;
+    const int64_t hoff = lay.head(bh, N);
     VT* gout[5] = {dr, dw, db, dk, da};
 
     float dS[C];
@@ -174,8 +178,8 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
             const int64_t ts = ta + s * SUB;
             // advance from the interval checkpoint to the sub-interval start
             for (int64_t t0 = ta; t0 < ts; t0 += SUB) {
-                stage_bwd<N, VT>(sh, t0, SUB, BH, bh, r, w, k, v, a, b,
-                                 nullptr);
+                stage_bwd<N, VT>(sh, t0, SUB, lay.ts, hoff, r, w, k, v, a,
+                                 b, nullptr);
                 __syncthreads();
                 for (int u = 0; u < SUB; ++u) {
                     float sa = 0.f;
@@ -193,7 +197,8 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
                 __syncthreads();
             }
             const int nt = int(tb - ts < SUB ? tb - ts : SUB);
-            stage_bwd<N, VT>(sh, ts, nt, BH, bh, r, w, k, v, a, b, dy);
+            stage_bwd<N, VT>(sh, ts, nt, lay.ts, hoff, r, w, k, v, a, b,
+                             dy);
             __syncthreads();
             // recompute the sub-interval's states: St[u] = S before token u
 #pragma unroll
@@ -254,7 +259,7 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
 #pragma unroll
                         for (int ww = 0; ww < NW; ++ww) acc += red[buf][ww][q][j];
                         if (q == 1) acc *= -sh[7][u][j] * sh[1][u][j];
-                        store_f(gout[q] + (t * BH + bh) * N + j, acc);
+                        store_f(gout[q] + t * lay.ts + hoff + j, acc);
                     }
                     buf ^= 1;
                 }
@@ -262,7 +267,7 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, const VT* __restrict__ r,
             __syncthreads();
             for (int e = tid; e < nt * N; e += TH) {
                 const int u = e / N, i = e - u * N;
-                store_f(dv + ((ts + u) * BH + bh) * N + i, sh_dv[u][i]);
+                store_f(dv + (ts + u) * lay.ts + hoff + i, sh_dv[u][i]);
             }
             __syncthreads();
         }
@@ -275,7 +280,7 @@ template <int N, typename VT, typename CT>
 hipError_t launch_fwd_nc(const SeqFwdArgs& p, hipStream_t stream) {
     const int64_t BH = p.B * p.H;
     hipLaunchKernelGGL((wkv7_seq_fwd_kernel<N, VT, CT>), dim3(unsigned(BH)),
-                       dim3(SeqShape<N>::THREADS), 0, stream, p.T, BH,
+                       dim3(SeqShape<N>::THREADS), 0, stream, p.T, BH, p.lay,
                        static_cast<const VT*>(p.r),
                        static_cast<const VT*>(p.w),
                        static_cast<const VT*>(p.k),
@@ -297,7 +302,7 @@ template <int N, typename VT, typename CT>
 hipError_t launch_bwd_nc(const SeqBwdArgs& p, hipStream_t stream) {
     const int64_t BH = p.B * p.H;
     hipLaunchKernelGGL((wkv7_seq_bwd_kernel<N, VT, CT>), dim3(unsigned(BH)),
-                       dim3(SeqShape<N>::THREADS), 0, stream, p.T, BH,
+                       dim3(SeqShape<N>::THREADS), 0, stream, p.T, BH, p.lay,
                        static_cast<const VT*>(p.r),
                        static_cast<const VT*>(p.w),
                        static_cast<const VT*>(p.k),

@@ -15,6 +15,14 @@ reference's signatures and return conventions:
 * ``backward(r, w, k, v, neg_kk, kka, S0, dy, dS_T, *aux)`` -> seven input
   cotangents in primal order and primal dtypes.
 
+Vectors are time-major ``[T, B, H, N]`` (the reference's layout contract,
+src/rwkv7m/model/wkv.py:19-57). ``layout="bthn"`` on forward,
+forward_with_aux and backward takes batch-major ``[B, T, H, N]`` vectors
+instead (the model's own activation layout, which the reference transposes
+around every call at src/rwkv7m/model/nnx_model.py:695-698 and :709-711);
+states and checkpoints keep their layouts, and the outputs follow the
+vectors' layout.
+
 Tensors are torch device tensors (torch supplies device memory and the
 current HIP stream; the kernels and every check of shapes and dtypes live in
 the C library). There is no CPU fallback: a missing library, a CPU tensor or
@@ -47,8 +55,13 @@ EXPORTED_SYMBOLS = (
     "rwkv7m_wkv7_forward",
     "rwkv7m_wkv7_forward_with_aux",
     "rwkv7m_wkv7_backward",
+    "rwkv7m_wkv7_forward_bthn",
+    "rwkv7m_wkv7_forward_with_aux_bthn",
+    "rwkv7m_wkv7_backward_bthn",
     "rwkv7m_wkv7_decode_inplace",
 )
+
+LAYOUTS = ("tbhn", "bthn")
 
 _lib = None
 _lock = threading.Lock()
@@ -80,14 +93,16 @@ def load_library(path: str | None = None):
         lib.rwkv7m_wkv7_default_checkpoint_interval.argtypes = [i32, i64]
         lib.rwkv7m_wkv7_checkpoint_dtype.restype = i32
         lib.rwkv7m_wkv7_checkpoint_dtype.argtypes = [i32, i64, i64]
-        lib.rwkv7m_wkv7_forward.restype = i32
-        lib.rwkv7m_wkv7_forward.argtypes = [i32] + [i64] * 4 + [vp] * 10
-        lib.rwkv7m_wkv7_forward_with_aux.restype = i32
-        lib.rwkv7m_wkv7_forward_with_aux.argtypes = (
-            [i32] + [i64] * 4 + [vp] * 10 + [i64, vp])
-        lib.rwkv7m_wkv7_backward.restype = i32
-        lib.rwkv7m_wkv7_backward.argtypes = (
-            [i32] + [i64] * 4 + [vp] * 10 + [i64] + [vp] * 8)
+        for sfx in ("", "_bthn"):
+            fwd = getattr(lib, "rwkv7m_wkv7_forward" + sfx)
+            fwd.restype = i32
+            fwd.argtypes = [i32] + [i64] * 4 + [vp] * 10
+            aux = getattr(lib, "rwkv7m_wkv7_forward_with_aux" + sfx)
+            aux.restype = i32
+            aux.argtypes = [i32] + [i64] * 4 + [vp] * 10 + [i64, vp]
+            bwd = getattr(lib, "rwkv7m_wkv7_backward" + sfx)
+            bwd.restype = i32
+            bwd.argtypes = [i32] + [i64] * 4 + [vp] * 10 + [i64] + [vp] * 8
         lib.rwkv7m_wkv7_decode_inplace.restype = i32
         lib.rwkv7m_wkv7_decode_inplace.argtypes = [i32] + [i64] * 3 + [vp] * 9
         if path is None:
@@ -132,9 +147,20 @@ def _stream(dev: torch.device):
 def _vecs(r, w, k, v, neg_kk, kka):
     out = tuple(x.contiguous() for x in (r, w, k, v, neg_kk, kka))
     if out[0].dim() != 4:
-        raise ValueError(f"r must have shape [time, batch, heads, head_size],"
-                         f" got {tuple(out[0].shape)}")
+        raise ValueError(f"r must have shape [time, batch, heads, head_size]"
+                         f" (or [batch, time, ...]), got {tuple(out[0].shape)}")
     return out
+
+
+def _layout(layout: str, r: torch.Tensor):
+    """(entry-point suffix, T, B, H, N) of vectors in ``layout``."""
+    if layout == "tbhn":
+        T, B, H, N = r.shape
+        return "", T, B, H, N
+    if layout == "bthn":
+        B, T, H, N = r.shape
+        return "_bthn", T, B, H, N
+    raise ValueError(f"layout must be one of {LAYOUTS}, got {layout!r}")
 
 
 def default_checkpoint_interval(dtype: torch.dtype, head_size: int) -> int:
@@ -156,53 +182,56 @@ def checkpoint_dtype(dtype: torch.dtype, head_size: int,
     return torch.bfloat16 if out == DTYPE_BF16 else torch.float32
 
 
-def forward(r, w, k, v, neg_kk, kka, initial_state, *, out_state=None):
+def forward(r, w, k, v, neg_kk, kka, initial_state, *, out_state=None,
+            layout: str = "tbhn"):
     """y, S_T = WKV(...). ``out_state`` may be ``initial_state`` (in place)."""
     lib = load_library()
     r, w, k, v, a, b = _vecs(r, w, k, v, neg_kk, kka)
     s0 = initial_state.contiguous()
     dev = _dev((r, w, k, v, a, b, s0))
-    T, B, H, N = r.shape
+    sfx, T, B, H, N = _layout(layout, r)
     y = torch.empty_like(r)
     s_t = out_state if out_state is not None else torch.empty_like(s0)
+    fn = "rwkv7m_wkv7_forward" + sfx
     with torch.cuda.device(dev):
-        rc = lib.rwkv7m_wkv7_forward(
+        rc = getattr(lib, fn)(
             _dtype_code(r), T, B, H, N, _p(r), _p(w), _p(k), _p(v), _p(a),
             _p(b), _p(s0), _p(y), _p(s_t), _stream(dev))
-    _check(rc, "rwkv7m_wkv7_forward")
+    _check(rc, fn)
     return y, s_t
 
 
 def forward_with_aux(r, w, k, v, neg_kk, kka, initial_state, *,
-                     checkpoint_interval: int = 0):
+                     checkpoint_interval: int = 0, layout: str = "tbhn"):
     """((y, S_T), (checkpoints, interval)) for the backward pass."""
     lib = load_library()
     r, w, k, v, a, b = _vecs(r, w, k, v, neg_kk, kka)
     s0 = initial_state.contiguous()
     dev = _dev((r, w, k, v, a, b, s0))
-    T, B, H, N = r.shape
+    sfx, T, B, H, N = _layout(layout, r)
     ci = int(checkpoint_interval) or default_checkpoint_interval(r.dtype, N)
     nck = checkpoint_count(T, ci)
     y = torch.empty_like(r)
     s_t = torch.empty_like(s0)
     ckpt = torch.empty((nck, B, H, N, N), device=dev,
                        dtype=checkpoint_dtype(r.dtype, N, ci))
+    fn = "rwkv7m_wkv7_forward_with_aux" + sfx
     with torch.cuda.device(dev):
-        rc = lib.rwkv7m_wkv7_forward_with_aux(
+        rc = getattr(lib, fn)(
             _dtype_code(r), T, B, H, N, _p(r), _p(w), _p(k), _p(v), _p(a),
             _p(b), _p(s0), _p(y), _p(s_t), _p(ckpt), ci, _stream(dev))
-    _check(rc, "rwkv7m_wkv7_forward_with_aux")
+    _check(rc, fn)
     return (y, s_t), (ckpt, torch.tensor(ci, dtype=torch.int64))
 
 
 def backward(r, w, k, v, neg_kk, kka, initial_state, dy, ds_t, checkpoints,
-             interval):
+             interval, *, layout: str = "tbhn"):
     """Seven input cotangents (primal order, primal dtypes)."""
     lib = load_library()
     r, w, k, v, a, b = _vecs(r, w, k, v, neg_kk, kka)
     s0 = initial_state.contiguous()
     dev = _dev((r, w, k, v, a, b, s0, checkpoints))
-    T, B, H, N = r.shape
+    sfx, T, B, H, N = _layout(layout, r)
     ci = int(interval)
     if checkpoints.shape != (checkpoint_count(T, ci), B, H, N, N) or \
             checkpoints.dtype != checkpoint_dtype(r.dtype, N, ci):
@@ -212,12 +241,13 @@ def backward(r, w, k, v, neg_kk, kka, initial_state, dy, ds_t, checkpoints,
     ds_c = None if ds_t is None else ds_t.to(torch.float32).contiguous()
     grads = [torch.empty_like(r) for _ in range(6)]
     ds0 = torch.empty_like(s0)
+    fn = "rwkv7m_wkv7_backward" + sfx
     with torch.cuda.device(dev):
-        rc = lib.rwkv7m_wkv7_backward(
+        rc = getattr(lib, fn)(
             _dtype_code(r), T, B, H, N, _p(r), _p(w), _p(k), _p(v), _p(a),
             _p(b), _p(s0), _p(dy_c), _p(ds_c), _p(ckpt), ci,
             *(_p(g) for g in grads), _p(ds0), _stream(dev))
-    _check(rc, "rwkv7m_wkv7_backward")
+    _check(rc, fn)
     return (*grads, ds0)
 
 
@@ -261,7 +291,7 @@ def register_hip_backend(*, replace: bool = False) -> WKVFFIBackend:
 
 
 __all__ = [
-    "EXPORTED_SYMBOLS", "LIB_PATH", "backward", "checkpoint_count",
+    "EXPORTED_SYMBOLS", "LAYOUTS", "LIB_PATH", "backward", "checkpoint_count",
     "checkpoint_dtype",
     "decode_inplace", "default_checkpoint_interval", "forward",
     "forward_with_aux", "hip_wkv_ffi_backend", "load_library",

@@ -11,7 +11,10 @@ A torch mirror of the reference's ``src/rwkv7m/model/wkv.py``:
   registered FFI backend (the HIP kernels once ``register_hip_backend()`` ran)
   or to the reference scan;
 * ``_wkv7_forward_dispatch`` / ``_wkv7_backward_dispatch`` -- wkv.py:127-216,
-  including the FFI argument order ``backward(*inputs, *cotangents, *aux)``.
+  including the FFI argument order ``backward(*inputs, *cotangents, *aux)``;
+* ``wkv7_batch_major`` -- the call as the reference's time-mix layer makes it
+  on its batch-major activations (nnx_model.py:695-698, :709-711), without
+  materialising the transposes when the HIP kernels serve it.
 
 Layout: vectors ``[T, B, H, N]`` (bf16 or fp32, one dtype), state
 ``[B, H, N, N]`` fp32; ``y`` in the vector dtype, the final state fp32.
@@ -202,4 +205,96 @@ def wkv7(r, w, k, v, neg_kk, kka, initial_state, backend: str | None = None,
     return y, final_state
 
 
-__all__ = ["wkv7", "wkv7_reference"]
+# ---------------------------------------------------------------------------
+# Batch-major call: the model's own [B, T, H, N] activations
+# ---------------------------------------------------------------------------
+
+def _validate_batch_major(r, w, k, v, neg_kk, kka, initial_state):
+    if r.dim() != 4:
+        raise ValueError(
+            "r must have shape [batch, time, heads, head_size], "
+            f"got {tuple(r.shape)}"
+        )
+    # the time-major checks on views with the first two axes swapped
+    swapped = [x.transpose(0, 1) if x.dim() >= 2 else x
+               for x in (r, w, k, v, neg_kk, kka)]
+    try:
+        _validate_wkv_inputs(*swapped, initial_state)
+    except ValueError as exc:
+        expected = (initial_state.shape[0], r.shape[1],
+                    *initial_state.shape[1:3])
+        raise ValueError(
+            f"batch-major WKV vectors must all have shape {expected} "
+            f"[batch, time, heads, head_size]: {exc}") from exc
+
+
+class _WKV7BatchMajor(torch.autograd.Function):
+    """Custom VJP of the batch-major call on the HIP kernels: forward,
+    forward_with_aux and backward with ``layout="bthn"``, so no transposed
+    copy of the vectors, y or the vector gradients is ever made."""
+
+    @staticmethod
+    def forward(r, w, k, v, neg_kk, kka, initial_state, with_aux):
+        from .kernels import wkv_hip
+        inputs = (r, w, k, v, neg_kk, kka, initial_state)
+        if not with_aux:
+            y, final_state = wkv_hip.forward(*inputs, layout="bthn")
+            return y, final_state, ()
+        (y, final_state), aux = wkv_hip.forward_with_aux(*inputs,
+                                                         layout="bthn")
+        return y, final_state, tuple(aux)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        ctx.save_for_backward(*inputs[:7])
+        ctx.aux = output[2]
+
+    @staticmethod
+    def backward(ctx, dy, ds_t, _aux_grad=None):
+        from .kernels import wkv_hip
+        inputs = ctx.saved_tensors
+        aux = ctx.aux
+        ctx.aux = None
+        grads = wkv_hip.backward(*inputs, dy, ds_t, *aux, layout="bthn")
+        return (*grads, None)
+
+    @staticmethod
+    def jvp(ctx, *tangents):
+        raise TypeError(
+            "wkv7 supports reverse-mode differentiation only; forward-mode "
+            "autodiff (jvp) is not implemented")
+
+
+def _hip_backend_registered() -> bool:
+    from .kernels import wkv_ffi, wkv_hip
+    backend = wkv_ffi._registered_backend
+    return backend is not None and backend.forward is wkv_hip.forward
+
+
+def wkv7_batch_major(r, w, k, v, neg_kk, kka, initial_state,
+                     backend: str | None = None, interpret: bool = False):
+    """WKV-7 on batch-major vectors ``[B, T, H, N]``; ``y`` is batch-major,
+    the states ``[B, H, N, N]`` fp32 as in ``wkv7``.
+
+    Equal to swapping the first two axes of the six vectors, calling
+    ``wkv7`` and swapping ``y`` back -- what the reference's time-mix layer
+    does around every call (src/rwkv7m/model/nnx_model.py:695-698,
+    :709-711).  With the HIP backend registered and selected, the kernels
+    read and write the batch-major tensors directly (the library's
+    ``_bthn`` entry points) and the transposes are never materialised; any
+    other backend runs behind the transposes.
+    """
+    _validate_batch_major(r, w, k, v, neg_kk, kka, initial_state)
+    selected = resolve_wkv_backend(backend)
+    if selected == "ffi" and _hip_backend_registered():
+        inputs = (r, w, k, v, neg_kk, kka, initial_state)
+        with_aux = torch.is_grad_enabled() and any(x.requires_grad
+                                                   for x in inputs)
+        y, final_state, _ = _WKV7BatchMajor.apply(*inputs, with_aux)
+        return y, final_state
+    swapped = [x.transpose(0, 1) for x in (r, w, k, v, neg_kk, kka)]
+    y, final_state = wkv7(*swapped, initial_state, backend, interpret)
+    return y.transpose(0, 1), final_state
+
+
+__all__ = ["wkv7", "wkv7_batch_major", "wkv7_reference"]

@@ -20,7 +20,7 @@ from rwkv7m_amd.kernels.wkv_backend import resolve_wkv_backend
 from rwkv7m_amd.kernels.wkv_ffi import (WKVFFIBackend,
                                         register_wkv_ffi_backend,
                                         unregister_wkv_ffi_backend)
-from rwkv7m_amd.wkv import wkv7, wkv7_reference
+from rwkv7m_amd.wkv import wkv7, wkv7_batch_major, wkv7_reference
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLDEN = os.path.join(ROOT, "tests", "golden")
@@ -163,6 +163,79 @@ def test_registered_ffi_satisfies_forward_and_backward_contract():
         unregister_wkv_ffi_backend()
 
 
+def _batch_inputs(dtype=torch.float32, seed=3):
+    """Batch-major [B=2, T=5, H=2, N=4] vectors and a [2, 2, 4, 4] state."""
+    g = torch.Generator().manual_seed(seed)
+    vecs = tuple((torch.randn(2, 5, 2, 4, generator=g) * 0.3).to(dtype)
+                 for _ in range(6))
+    return (*vecs, torch.randn(2, 2, 4, 4, generator=g) * 0.1)
+
+
+def test_wkv7_batch_major_equals_transposes_around_wkv7():
+    # the reference's time-mix layer: swap axes 0 and 1 of the six vectors,
+    # call wkv7, swap y back (nnx_model.py:695-698, :709-711)
+    inputs = _batch_inputs()
+    y, s_t = wkv7_batch_major(*inputs, "reference")
+    ty, ts = wkv7_reference(*(x.transpose(0, 1) for x in inputs[:6]),
+                            inputs[6])
+    assert y.shape == inputs[0].shape
+    assert torch.equal(y, ty.transpose(0, 1)) and torch.equal(s_t, ts)
+    # against the oracle on the time-major copies
+    ey, es = oracle.forward(*(_np(x.transpose(0, 1)) for x in inputs[:6]),
+                            _np(inputs[6]))
+    np.testing.assert_allclose(_np(y.transpose(0, 1)), ey, rtol=1e-5,
+                               atol=1e-6)
+    np.testing.assert_allclose(_np(s_t), es, rtol=1e-5, atol=1e-6)
+
+    xs = [x.clone().requires_grad_(True) for x in inputs]
+    y, s_t = wkv7_batch_major(*xs, "reference")
+    got = torch.autograd.grad((y * y).sum() + s_t.sum(), xs)
+    zs = [x.clone().requires_grad_(True) for x in inputs]
+    ty, ts = wkv7_reference(*(z.transpose(0, 1) for z in zs[:6]), zs[6])
+    want = torch.autograd.grad((ty * ty).sum() + ts.sum(), zs)
+    for a, b in zip(got, want):
+        assert a.shape == b.shape and torch.allclose(a, b, atol=1e-6)
+
+
+def test_wkv7_batch_major_other_ffi_backends_get_time_major_vectors():
+    # an FFI backend other than the HIP kernels sees the reference's
+    # time-major contract: the transposes run around it
+    shapes = []
+
+    def forward(*values):
+        shapes.append(tuple(values[0].shape))
+        return wkv7_reference(*values)
+
+    backend = WKVFFIBackend(forward=forward,
+                            forward_with_aux=lambda *a: (forward(*a), ()),
+                            backward=None)
+    unregister_wkv_ffi_backend()
+    register_wkv_ffi_backend(backend)
+    try:
+        inputs = _batch_inputs()
+        with torch.no_grad():
+            y, s_t = wkv7_batch_major(*inputs, "ffi")
+        assert shapes == [(5, 2, 2, 4)]
+        ey, es = wkv7_batch_major(*inputs, "reference")
+        assert torch.equal(y, ey) and torch.equal(s_t, es)
+    finally:
+        unregister_wkv_ffi_backend()
+
+
+def test_wkv7_batch_major_validates_batch_major_shapes():
+    inputs = list(_batch_inputs())
+    with pytest.raises(ValueError, match="batch, time, heads"):
+        wkv7_batch_major(inputs[0][0], *inputs[1:], "reference")
+    bad = inputs.copy()
+    bad[3] = bad[3][:, :4]
+    with pytest.raises(ValueError, match=r"\(2, 5, 2, 4\)"):
+        wkv7_batch_major(*bad, "reference")
+    bad = inputs.copy()
+    bad[2] = bad[2].to(torch.bfloat16)
+    with pytest.raises(TypeError, match="all WKV vectors"):
+        wkv7_batch_major(*bad, "reference")
+
+
 # ---------------------------------------------------------------------------
 # C ABI: the library loads on a host without a GPU and exports the header
 # ---------------------------------------------------------------------------
@@ -221,6 +294,15 @@ def test_library_rejects_bad_requests_before_any_device_call(lib):
     assert lib.rwkv7m_wkv7_forward_with_aux(
         0, 2, 1, 1, 4, *null, -1, None) == 1
     assert b"checkpoint_interval" in lib.rwkv7m_last_error()
+    # the batch-major entry points check the same things and name themselves
+    assert lib.rwkv7m_wkv7_forward_bthn(0, 2, 1, 1, 4, *null) == 1
+    assert b"rwkv7m_wkv7_forward_bthn" in lib.rwkv7m_last_error()
+    assert lib.rwkv7m_wkv7_forward_with_aux_bthn(
+        1, 2, 1, 1, 4, *null, 0, None) == 1
+    assert b"checkpoints is NULL" in lib.rwkv7m_last_error()
+    assert lib.rwkv7m_wkv7_backward_bthn(
+        0, 2, 1, 1, 4, *null, -1, *([None] * 8)) == 1
+    assert b"rwkv7m_wkv7_backward_bthn" in lib.rwkv7m_last_error()
 
 
 # ---------------------------------------------------------------------------

@@ -103,9 +103,10 @@ int hip_status(const char* what, hipError_t e) {
                                     hipGetErrorString(e));
 }
 
-// Chunk length of the MFMA forward without checkpoints, and the default
-// checkpoint interval (= chunk length of the MFMA forward and backward).
-constexpr int64_t kDefaultChunk = 32;
+// Chunk length of the MFMA forward without checkpoints (16: the
+// wave-per-chunk kernel), and the default checkpoint interval (= chunk
+// length of the MFMA forward and backward).
+constexpr int64_t kDefaultChunk = 16;
 constexpr int64_t kDefaultTrainChunk = 32;
 
 int64_t default_interval(int dtype, int64_t N) {
@@ -199,6 +200,9 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
         c.y = y;
         c.s_t = s_t;
         c.ckpt = ckpt;
+        if (L == 16)
+            return hip_status("wave forward launch",
+                              rwkv7m::launch_wave_forward(c, stream));
         return hip_status("chunked forward launch",
                           rwkv7m::launch_chunk_forward(c, stream));
     }

@@ -49,6 +49,9 @@ struct ChunkFwdArgs {
 
 hipError_t launch_chunk_forward(const ChunkFwdArgs& p, hipStream_t stream);
 
+// Wave-per-chunk forward: L = 16 (checkpoints, if any, every 16 tokens).
+hipError_t launch_wave_forward(const ChunkFwdArgs& p, hipStream_t stream);
+
 // Chunked backward: L in {16, 32}; ckpt holds a state every L tokens.
 struct ChunkBwdArgs {
     int L;

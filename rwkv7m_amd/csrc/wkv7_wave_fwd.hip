@@ -1,0 +1,663 @@
+// Chunked WKV-7 forward for gfx950 with the state rows split over waves:
+// bf16 vectors, fp32 state, N = 64, chunks of 16 tokens.
+//
+// The recurrence (reference src/rwkv7m/model/rwkv_core.py:54-86)
+//
+//   S_t = S_{t-1} diag(d_t) + (S_{t-1} a_t) b_t^T + v_t k_t^T,  y_t = S_t r_t
+//
+// acts on each row i of the state separately: row i needs only v_t[i] of
+// the value side and yields only y_t[i].  Over a chunk, in the closed form
+// of the chunked kernels (wkv7_chunk_common.h),
+//
+//   S_L = S_0 diag(2^{g_L}) + bf16(S_0) M^ + C,   Y^T = bf16(S_0) Q^^T + P^T
+//
+// with M^ = diag(2^{g_ref}) W^T B^ and Q^ = diag(2^{g_ref}) (R~ + Arb W)^T
+// depending on the chunk's key-side vectors only, and C = U^T B^ + V^T K^,
+// P = Arb U + Ark V linear in the value rows.
+//
+// One workgroup of 8 waves per (batch, head):
+//   * waves 4..7, the producers: producer p builds chunks p, p + 4, ...:
+//     the decayed factors, the 16 x 16 matrices, the inverse, W, U, M^ and
+//     Q^, all in registers, and hands them to a ring of three LDS slots;
+//   * waves 0..3, the chains: chain ib holds rows 16 ib .. 16 ib + 15 of the
+//     fp32 state in registers for the whole sequence and, chunk after
+//     chunk, takes the slot, forms its rows of C and P, advances its rows
+//     (8 MFMAs) and writes its rows of y.
+// The four chains run independent recurrences; each one's step per chunk is
+// short, so the kernel runs at the producers' rate.
+//
+// Register layouts (lane l, r = l % 16, q = l / 16).  A 16 x 16 accumulator
+// tile D(X) holds X[4q + e][r] (e = 0..3).  As operands of
+// v_mfma_f32_16x16x16_bf16, the lane's four values (kq) are X as the B
+// operand and X^T as the A operand.  Token-major matrices X[t][j] (16 x 64)
+// come two ways:
+//   T layout: lane holds X[r][16 kb + 4q + e] (kb = 0..3): the tiles
+//             D((X^T)_kb), for products contracting over j;
+//   J layout: lane holds X[4q + e][16 jb + r]: the tiles D(X_jb), for
+//             products contracting over t.
+// Vectors arrive in the T layout; A~, B^, K^ and V are turned into the J
+// layout through a per-producer LDS buffer and gfx950's transposing LDS
+// load.  Products over K = 64 pair two T tiles into one
+// v_mfma_f32_16x16x32_bf16 operand (the same slot order on both sides).  A
+// chain's state rows sit in the accumulator layout D(S^T_{j'b, ib}), which
+// is at the same time the bf16 operand layout of the state step.  A
+// 16x16x16 product never accumulates onto a 16x16x32 result or the other way
+// round: every such hand-over goes through a VALU operation.
+
+#include "wkv7_chunk_common.h"
+#include "wkv7_launch.h"
+
+namespace rwkv7m {
+namespace {
+
+using chunk::kHalfRange;
+using chunk::kLog2e;
+using chunk::kq;
+using chunk::mfma16;
+
+constexpr int WN = 64;       // head size
+constexpr int WL = 16;       // tokens per chunk
+constexpr int NCHAIN = 4;    // chain waves (16 state rows each)
+constexpr int NPROD = 8;     // producer waves
+constexpr int NSLOT = 3;     // hand-over ring
+constexpr int WTHREADS = 64 * (NCHAIN + NPROD);
+constexpr int XPITCH = WN + 8;  // bf16 transpose buffer row pitch
+// Bound on the polls of one hand-over (each poll sleeps ~64 cycles).  A wave
+// waits for at most a few other chunks; the bound is orders of magnitude
+// above that and only guarantees that every wave exits.
+constexpr int kPollLimit = 1 << 20;
+
+typedef short i16x8_t __attribute__((ext_vector_type(8)));
+
+// Per producer: the next chunk's six vectors as loaded, and, once the
+// factors are formed, the four J-layout matrices on their way through the
+// transposing read.  raw[p][h][s][u] holds the 16-byte segment s (columns
+// 8s .. 8s + 7) of token 8h + u: the T-layout reads of one vector are then
+// one address plus constant offsets.
+union ProdStage {
+    uint4 raw[6][2][8][8];
+    bf16_t xp[4][WL][XPITCH];  // A~, B^, K^, V ([t][j])
+};
+
+// One chunk's hand-over from a producer to the chains, as register images
+// (element [..][lane] is that lane's operand).
+struct Slot {
+    bf16x8_t M[4][2][64];  // A operands of M^^T: tiles (2jp, j'b), (2jp+1, j'b)
+    bf16x8_t Q[2][64];     // B operands of Q^^T: tiles 2jp, 2jp + 1
+    i16x4_t B[4][64];      // B^ (J layout)
+    i16x4_t K[4][64];      // K^ (J layout)
+    i16x4_t U[4][64];      // D(U_ib)
+    i16x4_t V[4][64];      // V (J layout)
+    i16x4_t Arb[64];       // D(Arb^T)
+    i16x4_t Ark[64];       // D(Ark^T)
+    float eL[WN];          // 2^{g_L} per column
+    int exact;             // the chunk needs the exact sequential pass
+};
+
+struct WaveFwdSmem {
+    Slot slot[NSLOT];
+    ProdStage st[NPROD];
+    float eref[NPROD][WN];  // per producer: 2^{g_ref} per column
+    float eL[NPROD][WN];    // per producer: 2^{g_L} per column
+    int ready[NSLOT];       // chunk held by the slot (-1: none yet)
+    int done[NSLOT];        // chains finished with the slot, over all uses
+};
+
+__device__ __forceinline__ bf16x8_t pk8(const i16x4_t& lo, const i16x4_t& hi) {
+    const i16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// Value of lane n of each 16-lane row, in every lane of the row.
+template <int N>
+__device__ __forceinline__ float row_bcast(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(
+        0, __float_as_int(x), 0x150 + N, 0xF, 0xF, false));
+}
+
+// The previous lane's value within each row; the row's first lane keeps
+// `first`.
+__device__ __forceinline__ float row_prev(float x, float first) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(
+        __float_as_int(first), __float_as_int(x), 0x111, 0xF, 0xF, false));
+}
+
+// X[4q + e][16 jb + r] (e = 0..3) of a [t][j] matrix in LDS (the J layout)
+// by one transposing read: lane s of each 16-lane group addresses row
+// 4q + s / 4, columns 16 jb + 4 (s % 4) .. + 3.
+__device__ __forceinline__ i16x4_t read_j(const bf16_t (*X)[XPITCH], int jb,
+                                          int lane) {
+    const int s = lane & 15, q = lane >> 4;
+    const bf16_t* p = &X[4 * q + (s >> 2)][16 * jb + 4 * (s & 3)];
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p));
+}
+
+// Keep X[4q + e][r] where (row_below: r < 4q + e; else 4q + e < r), with
+// equality kept unless strict.
+__device__ __forceinline__ f32x4_t mask4(f32x4_t x, int r, int q, bool strict,
+                                         bool row_below) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int m = 4 * q + e;
+        const bool keep = row_below ? (strict ? r < m : r <= m)
+                                    : (strict ? m < r : m <= r);
+        x[e] = keep ? x[e] : 0.f;
+    }
+    return x;
+}
+
+// Hand-over words in LDS are read and written as relaxed workgroup-scope
+// atomics: a volatile access would also make the wave wait for all its
+// outstanding global stores.  Ordering against the data they guard comes
+// from an explicit lgkmcnt(0) before each write and from the polling
+// reads' own completion before the guarded reads are issued.
+__device__ __forceinline__ int lds_load(int* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_store(int* p, int x) {
+    __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Poll an LDS word until pred(value) holds (bounded).
+template <typename Pred>
+__device__ __forceinline__ void poll(int* p, Pred pred) {
+    for (int it = 0; it < kPollLimit; ++it) {
+        if (pred(__builtin_amdgcn_readfirstlane(lds_load(p)))) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("" ::: "memory");
+}
+
+struct FwdArgs {
+    int64_t T, BH;
+    VecLayout lay;
+    const bf16_t *r, *w, *k, *v, *a, *b;
+    const float* s0;
+    bf16_t* y;
+    float* s_t;
+    bf16_t* ckpt;
+};
+
+// ---------------------------------------------------------------------------
+// Producer p: chunks p, p + NPROD, ...
+__device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
+                                        int p, int lane) {
+    const int lr = lane & 15, lq = lane >> 4;
+    const int64_t bh = blockIdx.x;
+    const int64_t hoff = A.lay.head(bh, WN);
+    const int64_t T = A.T;
+    const int64_t nch = (T + WL - 1) / WL;
+    const uint32_t TS = uint32_t(A.lay.ts);
+    const chunk::VecPtrs src{A.r, A.w, A.k, A.v, A.a, A.b, nullptr};
+    ProdStage& stg = sm.st[p];
+    bf16_t (*const xp)[WL][XPITCH] = stg.xp;
+    int* const vdone = sm.done;
+    int* const vready = sm.ready;
+
+    // A chunk's vectors go straight to the stage in LDS (16 bytes per lane,
+    // global_load_lds_dwordx4, which writes lane l's data at 16 l): lane l
+    // of load (vector, h) fetches segment l / 8 of token 8h + l % 8.  Tokens
+    // past the end re-read the last token (zeroed when read).
+    const int ldu = lane & 7, ldseg = lane >> 3;
+    auto fetch = [&](int64_t c) {
+        const int64_t cbase = c * WL * A.lay.ts + hoff;
+        const int n = int(T - c * WL < WL ? T - c * WL : WL);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int t = 8 * h + ldu;
+            const uint32_t off = uint32_t(t < n ? t : n - 1) * TS + 8 * ldseg;
+#pragma unroll
+            for (int vv = 0; vv < 6; ++vv)
+                __builtin_amdgcn_global_load_lds(
+                    (const void __attribute__((address_space(1)))*)(
+                        (src.get(vv) + cbase) + off),
+                    (void __attribute__((address_space(3)))*)(
+                        &stg.raw[vv][h][0][0]),
+                    16, 0, 0);
+        }
+    };
+    // the T layout read of vector vv: token lr, columns 16 kb + 4 lq .. + 3
+    // (segment 2 kb + lq / 2, half lq % 2)
+    const bf16_t* const rbase = reinterpret_cast<const bf16_t*>(
+        &stg.raw[0][lr >> 3][lq >> 1][lr & 7]) + 4 * (lq & 1);
+    auto read_t = [&](int vv, int kb) -> uint2 {
+        return *reinterpret_cast<const uint2*>(rbase + vv * (2 * 8 * 8 * 8) +
+                                               kb * (2 * 8 * 8));
+    };
+    if (p < nch) fetch(p);
+
+    for (int64_t c = p; c < nch; c += NPROD) {
+        const int n = int(T - c * WL < WL ? T - c * WL : WL);
+        const bool valid = lr < n;
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this chunk's vectors
+        asm volatile("" ::: "memory");
+        uint2 raw[6][4];
+#pragma unroll
+        for (int vv = 0; vv < 6; ++vv)
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) raw[vv][kb] = read_t(vv, kb);
+        if (n < WL) {
+#pragma unroll
+            for (int vv = 0; vv < 6; ++vv)
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+                    raw[vv][kb] = valid ? raw[vv][kb] : make_uint2(0, 0);
+        }
+
+        // ---- factors (T layout, fp32) --------------------------------------
+        // lam = log2 d_t, g its running sum over the chunk, g_ref = g at
+        // token 7, g_L = g at token 15 (padding tokens decay by nothing)
+        f32x4_t fA[4], fR[4], fB[4], fK[4];
+        float lo = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const f32x4_t wr = unpack4(raw[1][kb]);
+            const f32x4_t ar = unpack4(raw[4][kb]), br = unpack4(raw[5][kb]);
+            const f32x4_t rr = unpack4(raw[0][kb]), kr = unpack4(raw[2][kb]);
+            f32x4_t sLR, sp4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float ew = __builtin_amdgcn_exp2f(
+                    valid ? wr[e] * kLog2e : -__builtin_inff());
+                const float g = chunk::scan_lanes<16>(-ew * kLog2e);
+                const float gref = row_bcast<7>(g), gL = row_bcast<15>(g);
+                lo = fminf(lo, fminf(gref, gL - gref));
+                const float dg = g - gref;
+                const float eg = __builtin_amdgcn_exp2f(dg);
+                const float eng = __builtin_amdgcn_exp2f(-dg);
+                // token 0: 2^{-g_ref} (its A~ factor); tokens 1, 2: the
+                // column's 2^{g_ref}, 2^{g_L}
+                const float sp = __builtin_amdgcn_exp2f(
+                    lr == 0 ? -gref : lr == 1 ? gref : gL);
+                const float eprev = row_prev(eg, sp);
+                sp4[e] = sp;
+                sLR[e] = chunk::pin_lanes(row_bcast<15>(eg));
+                fA[kb][e] = ar[e] * eprev;
+                fR[kb][e] = rr[e] * eg;
+                fB[kb][e] = br[e] * eng;
+                fK[kb][e] = kr[e] * eng;
+            }
+            // per-column 2^{g_ref} (token 1) and 2^{g_L} (token 2)
+            if (lr == 1)
+                *reinterpret_cast<f32x4_t*>(&sm.eref[p][16 * kb + 4 * lq]) = sp4;
+            if (lr == 2)
+                *reinterpret_cast<f32x4_t*>(&sm.eL[p][16 * kb + 4 * lq]) = sp4;
+            f32x4_t bh4, kh4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                bh4[e] = fB[kb][e] * sLR[e];
+                kh4[e] = fK[kb][e] * sLR[e];
+            }
+            *reinterpret_cast<uint2*>(&xp[0][lr][16 * kb + 4 * lq]) =
+                pack4(fA[kb]);
+            *reinterpret_cast<uint2*>(&xp[1][lr][16 * kb + 4 * lq]) =
+                pack4(bh4);
+            *reinterpret_cast<uint2*>(&xp[2][lr][16 * kb + 4 * lq]) =
+                pack4(kh4);
+            *reinterpret_cast<uint2*>(&xp[3][lr][16 * kb + 4 * lq]) =
+                raw[3][kb];
+        }
+        // the factored form needs g_ref >= -H and g_L - g_ref >= -H
+        const bool exact =
+            __builtin_amdgcn_ballot_w64(lo < -kHalfRange * kLog2e) != 0;
+
+        i16x4_t tA[4], tR[4], tB[4], tK[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            tA[kb] = kq(fA[kb]);
+            tR[kb] = kq(fR[kb]);
+            tB[kb] = kq(fB[kb]);
+            tK[kb] = kq(fK[kb]);
+        }
+
+        // ---- the 16 x 16 matrices (K = 64) ---------------------------------
+        // D(Aab), D(Aab^T) for the inverse; D(Aak^T), D(Arb^T), D(Ark^T)
+        f32x4_t mA = zero4(), mAT = zero4(), mAakT = zero4(), mArbT = zero4(),
+                mArkT = zero4();
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            const bf16x8_t a8 = pk8(tA[2 * kp], tA[2 * kp + 1]);
+            const bf16x8_t b8 = pk8(tB[2 * kp], tB[2 * kp + 1]);
+            const bf16x8_t k8 = pk8(tK[2 * kp], tK[2 * kp + 1]);
+            const bf16x8_t r8 = pk8(tR[2 * kp], tR[2 * kp + 1]);
+            mfma(mA, a8, b8);     // Aab[t][s] = A~_t . B~_s
+            mfma(mAT, b8, a8);    // Aab^T
+            mfma(mAakT, k8, a8);  // Aak^T[u][s] = K~_u . A~_s
+            mfma(mArbT, b8, r8);  // Arb^T[s][t] = B~_s . R~_t
+            mfma(mArkT, k8, r8);  // Ark^T[s][t] = K~_s . R~_t
+        }
+        mA = mask4(mA, lr, lq, true, true);          // s < t
+        mAT = mask4(mAT, lr, lq, true, false);       // s < t
+        mAakT = mask4(mAakT, lr, lq, true, false);   // u < s
+        mArbT = mask4(mArbT, lr, lq, false, false);  // s <= t
+        mArkT = mask4(mArkT, lr, lq, false, false);
+
+        // ---- Minv = (I - Aab)^{-1} = (I + A)(I + A^2)(I + A^4)(I + A^8) ----
+        f32x4_t dMT;
+        {
+            const i16x4_t pA = kq(mA), pT = kq(mAT);
+            f32x4_t x2 = zero4(), t2 = zero4();
+            mfma16(x2, pT, pA);  // A A
+            mfma16(t2, pA, pT);  // A^T A^T
+            const i16x4_t px2 = kq(x2), pt2 = kq(t2);
+            f32x4_t q1t;  // Q1^T = I + A^T + (A^2)^T + (A^2)^T A^T
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float one = (4 * lq + e == lr) ? 1.f : 0.f;
+                q1t[e] = one + mAT[e] + t2[e];
+            }
+            mfma16(q1t, px2, pT);
+            f32x4_t x4 = zero4(), t4 = zero4();
+            mfma16(x4, pt2, px2);  // A^4
+            mfma16(t4, px2, pt2);  // (A^4)^T
+            const i16x4_t pq1t = kq(q1t), px4 = kq(x4), pt4 = kq(t4);
+            f32x4_t q2t = q1t, x8 = zero4();
+            mfma16(q2t, px4, pq1t);  // (Q1 + Q1 A^4)^T
+            mfma16(x8, pt4, px4);    // A^8
+            dMT = q2t;
+            mfma16(dMT, kq(x8), kq(q2t));  // Minv^T = (Q2 + Q2 A^8)^T
+        }
+
+        // ---- products over the chunk (K = 16) ------------------------------
+        const i16x4_t kMinv = kq(dMT);  // A operand: Minv
+        const i16x4_t kAak = kq(mAakT), kArbT = kq(mArbT),
+                      kArkT = kq(mArkT);
+        chunk::wave_lds_fence();
+        i16x4_t jA[4], jB[4], jK[4], jV[4];
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            jA[jb] = read_j(xp[0], jb, lane);
+            jB[jb] = read_j(xp[1], jb, lane);
+            jK[jb] = read_j(xp[2], jb, lane);
+            jV[jb] = read_j(xp[3], jb, lane);
+        }
+
+        // 2^{g_ref} of column 16 jb + lr (W's columns in the J layout) and
+        // of rows 16 jb + 4 lq + e (the T layout): folded into W and R~, so
+        // that the state enters the chains as bf16(S_0)
+        float erj[4];
+        f32x4_t ert[4];
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            erj[jb] = sm.eref[p][16 * jb + lr];
+            ert[jb] = *reinterpret_cast<const f32x4_t*>(
+                &sm.eref[p][16 * jb + 4 * lq]);
+        }
+        i16x4_t kW[4], kU[4], kQ[4];
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            f32x4_t x = zero4();
+            mfma16(x, kMinv, jA[jb]);  // W = Minv A~ : D(W_jb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] *= erj[jb];
+            kW[jb] = kq(x);            // W diag(2^{g_ref})
+            f32x4_t av = zero4();
+            mfma16(av, kAak, jV[jb]);  // Aak V : D((Aak V)_ib)
+            f32x4_t u = zero4();
+            mfma16(u, kMinv, kq(av));  // U = Minv Aak V : D(U_ib)
+            kU[jb] = kq(u);
+        }
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            // Q^ = diag(2^{g_ref}) R~^T + (W diag(2^{g_ref}))^T Arb^T
+            f32x4_t x = unpack4(__builtin_bit_cast(uint2, tR[jb]));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] *= ert[jb][e];
+            mfma16(x, kW[jb], kArbT);
+            kQ[jb] = kq(x);
+        }
+
+        // M^ = (W diag(2^{g_ref}))^T B^ : D(M^_{jb, j'b}), as the chains'
+        // A operands (tiles 2jp, 2jp + 1 of column block j'b)
+        bf16x8_t M8[4][2];
+#pragma unroll
+        for (int jpb = 0; jpb < 4; ++jpb) {
+            i16x4_t m4[4];
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+                f32x4_t x = zero4();
+                mfma16(x, kW[jb], jB[jpb]);
+                m4[jb] = kq(x);
+            }
+            M8[jpb][0] = pk8(m4[0], m4[1]);
+            M8[jpb][1] = pk8(m4[2], m4[3]);
+        }
+
+        // ---- hand the chunk to the chains ---------------------------------
+        const int s = int(c % NSLOT);
+        const int uses = int(c / NSLOT);  // earlier uses of this slot
+        poll(vdone + s, [&](int d) { return d >= NCHAIN * uses; });
+        Slot& sl = sm.slot[s];
+#pragma unroll
+        for (int jpb = 0; jpb < 4; ++jpb) {
+            sl.M[jpb][0][lane] = M8[jpb][0];
+            sl.M[jpb][1][lane] = M8[jpb][1];
+        }
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            sl.B[jb][lane] = jB[jb];
+            sl.K[jb][lane] = jK[jb];
+            sl.U[jb][lane] = kU[jb];
+            sl.V[jb][lane] = jV[jb];
+        }
+        sl.Q[0][lane] = pk8(kQ[0], kQ[1]);
+        sl.Q[1][lane] = pk8(kQ[2], kQ[3]);
+        sl.Arb[lane] = kArbT;
+        sl.Ark[lane] = kArkT;
+        if (lane < 16)
+            *reinterpret_cast<f32x4_t*>(&sl.eL[4 * lane]) =
+                *reinterpret_cast<const f32x4_t*>(&sm.eL[p][4 * lane]);
+        if (lane == 0) sl.exact = exact ? 1 : 0;
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        asm volatile("" ::: "memory");
+        if (lane == 0) lds_store(vready + s, int(c));
+        // the producer's next chunk: its loads are issued only now, so that
+        // no wait on them delays a hand-over (producers have time to spare)
+        if (c + NPROD < nch) fetch(c + NPROD);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Chain ib: state rows 16 ib .. 16 ib + 15 through every chunk.
+__device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
+                                      int ib, int lane) {
+    const int lr = lane & 15, lq = lane >> 4;
+    const int64_t bh = blockIdx.x;
+    const int64_t sbase = bh * WN * WN;
+    const int64_t hoff = A.lay.head(bh, WN);
+    const int64_t T = A.T;
+    const int64_t nch = (T + WL - 1) / WL;
+    const int64_t NN = WN * WN;
+    const uint32_t TS = uint32_t(A.lay.ts);
+    int* const vready = sm.ready;
+    const int row = 16 * ib + lr;  // the lane's state row
+
+    // the chains are the serial path: they take issue priority over the
+    // producers sharing their SIMDs
+    __builtin_amdgcn_s_setprio(2);
+    // S tiles D(S^T_{j'b, ib}): lane holds S[row][16 j'b + 4 lq + e]
+    f32x4_t S[4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+        S[jb] = *reinterpret_cast<const f32x4_t*>(A.s0 + sbase + row * WN +
+                                                  16 * jb + 4 * lq);
+    // the loop's only global memory operations are stores: with the state
+    // loads complete here, no wait for those stores lands inside the loop
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+
+    for (int64_t c = 0; c < nch; ++c) {
+        const int64_t t0 = c * WL;
+        const int n = int(T - t0 < WL ? T - t0 : WL);
+
+        // per-lane store offsets, recomputed in every iteration rather than
+        // kept as 64-bit addresses across the loop
+        uint32_t yoff = uint32_t(lr) * TS + 16 * ib + 4 * lq;
+        uint32_t coff = uint32_t(row) * WN + 4 * lq;
+        asm volatile("" : "+v"(yoff), "+v"(coff));
+
+        // bf16(S_0): the operand of the state step and checkpoint c
+        i16x4_t sb[4];
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) sb[jb] = kq(S[jb]);
+        const bf16x8_t Sb0 = pk8(sb[0], sb[1]), Sb1 = pk8(sb[2], sb[3]);
+
+        const int s = int(c % NSLOT);
+        poll(vready + s, [&](int x) { return x == int(c); });
+        const Slot& sl = sm.slot[s];
+        bf16x8_t M[4][2], Q[2];
+        i16x4_t B[4], K[4];
+        f32x4_t eL[4];
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            M[jb][0] = sl.M[jb][0][lane];
+            M[jb][1] = sl.M[jb][1][lane];
+            B[jb] = sl.B[jb][lane];
+            K[jb] = sl.K[jb][lane];
+            eL[jb] = *reinterpret_cast<const f32x4_t*>(&sl.eL[16 * jb + 4 * lq]);
+        }
+        Q[0] = sl.Q[0][lane];
+        Q[1] = sl.Q[1][lane];
+        const i16x4_t U = sl.U[ib][lane], V = sl.V[ib][lane];
+        const i16x4_t Arb = sl.Arb[lane], Ark = sl.Ark[lane];
+        const int exact = __builtin_amdgcn_readfirstlane(sl.exact);
+        // the slot's data is in registers: release it to the producers
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        asm volatile("" ::: "memory");
+        if (lane == 0)
+            __hip_atomic_fetch_add(&sm.done[s], 1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+
+        if (!exact) {
+            // S_L^T = S_0^T diag(2^{g_L}) + C^T + M^^T bf16(S_0)^T, rows of
+            // block ib; C^T_{j'b, ib} = B^^T U + K^^T V
+#pragma unroll
+            for (int jpb = 0; jpb < 4; ++jpb) {
+                f32x4_t cc = zero4();
+                mfma16(cc, B[jpb], U);
+                mfma16(cc, K[jpb], V);
+                f32x4_t acc;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[e] = S[jpb][e] * eL[jpb][e] + cc[e];
+                mfma(acc, M[jpb][0], Sb0);
+                mfma(acc, M[jpb][1], Sb1);
+                S[jpb] = acc;
+            }
+            // Y^T_ib = bf16(S_0) Q^^T + U^T Arb^T + V^T Ark^T, stored as
+            // y[t][16 ib + 4 lq ..]
+            f32x4_t pp = zero4();
+            mfma16(pp, U, Arb);
+            mfma16(pp, V, Ark);
+            f32x4_t yy = zero4();
+            mfma(yy, Sb0, Q[0]);
+            mfma(yy, Sb1, Q[1]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) yy[e] += pp[e];
+            if (lr < n)
+                *reinterpret_cast<uint2*>((A.y + (t0 * A.lay.ts + hoff)) +
+                                          yoff) = pack4(yy);
+            if (A.ckpt) {
+#pragma unroll
+                for (int jb = 0; jb < 4; ++jb)
+                    *reinterpret_cast<i16x4_t*>(
+                        (A.ckpt + (c * A.BH * NN + sbase)) + (coff + 16 * jb)) =
+                        sb[jb];
+            }
+        } else {
+            if (A.ckpt) {
+#pragma unroll
+                for (int jb = 0; jb < 4; ++jb)
+                    *reinterpret_cast<i16x4_t*>(
+                        (A.ckpt + (c * A.BH * NN + sbase)) + (coff + 16 * jb)) =
+                        sb[jb];
+            }
+            // exact fp32 sequential pass over the chunk for the rows of
+            // block ib (a chunk outside the factored form's range, far
+            // beyond the model's clamped decays): sums over the lane's 16
+            // columns, then over the four lanes of the row (lq = 0..3)
+            for (int t = 0; t < n; ++t) {
+                const int64_t off = (t0 + t) * A.lay.ts + hoff;
+                float sa = 0.f;
+#pragma unroll
+                for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        sa += S[jb][e] *
+                              bf16_to_f32(A.a[off + 16 * jb + 4 * lq + e]);
+                sa += __shfl_xor(sa, 16);
+                sa += __shfl_xor(sa, 32);
+                const float vi = bf16_to_f32(A.v[off + row]);
+                float acc = 0.f;
+#pragma unroll
+                for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int64_t j = off + 16 * jb + 4 * lq + e;
+                        const float d = expf(-expf(bf16_to_f32(A.w[j])));
+                        S[jb][e] = S[jb][e] * d + sa * bf16_to_f32(A.b[j]) +
+                                   vi * bf16_to_f32(A.k[j]);
+                        acc += S[jb][e] * bf16_to_f32(A.r[j]);
+                    }
+                acc += __shfl_xor(acc, 16);
+                acc += __shfl_xor(acc, 32);
+                if (lq == 0) A.y[off + row] = to_bf16(acc);
+            }
+        }
+    }
+
+    // final state (fp32) and the last checkpoint
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+        *reinterpret_cast<float4*>(A.s_t + sbase + row * WN + 16 * jb +
+                                   4 * lq) =
+            make_float4(S[jb][0], S[jb][1], S[jb][2], S[jb][3]);
+        if (A.ckpt)
+            *reinterpret_cast<uint2*>(A.ckpt + nch * A.BH * NN + sbase +
+                                      row * WN + 16 * jb + 4 * lq) =
+                pack4(S[jb]);
+    }
+}
+
+__global__ void __launch_bounds__(WTHREADS)
+wkv7_wave_fwd_kernel(FwdArgs A) {
+    __shared__ WaveFwdSmem sm;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // the wave index, in a scalar register: every chunk index, token offset
+    // and base address derived from it stays scalar
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (tid < NSLOT) {
+        sm.ready[tid] = -1;
+        sm.done[tid] = 0;
+    }
+    __syncthreads();
+    if (wv < NCHAIN)
+        chain(A, sm, wv, lane);
+    else
+        produce(A, sm, wv - NCHAIN, lane);
+}
+
+}  // namespace
+
+hipError_t launch_wave_forward(const ChunkFwdArgs& p, hipStream_t stream) {
+    if (p.L != WL) return hipErrorInvalidValue;
+    FwdArgs A;
+    A.T = p.T;
+    A.BH = p.B * p.H;
+    A.lay = p.lay;
+    A.r = static_cast<const bf16_t*>(p.r);
+    A.w = static_cast<const bf16_t*>(p.w);
+    A.k = static_cast<const bf16_t*>(p.k);
+    A.v = static_cast<const bf16_t*>(p.v);
+    A.a = static_cast<const bf16_t*>(p.a);
+    A.b = static_cast<const bf16_t*>(p.b);
+    A.s0 = p.s0;
+    A.y = static_cast<bf16_t*>(p.y);
+    A.s_t = p.s_t;
+    A.ckpt = static_cast<bf16_t*>(p.ckpt);
+    if (A.BH <= 0) return hipSuccess;
+    hipLaunchKernelGGL(wkv7_wave_fwd_kernel, dim3(unsigned(A.BH)),
+                       dim3(WTHREADS), 0, stream, A);
+    return hipGetLastError();
+}
+
+}  // namespace rwkv7m

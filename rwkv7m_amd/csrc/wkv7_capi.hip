@@ -200,11 +200,8 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
         c.y = y;
         c.s_t = s_t;
         c.ckpt = ckpt;
-        if (L == 16)
-            return hip_status("wave forward launch",
-                              rwkv7m::launch_wave_forward(c, stream));
         return hip_status("chunked forward launch",
-                          rwkv7m::launch_chunk_forward(c, stream));
+                          rwkv7m::launch_wave_forward(c, stream));
     }
     rwkv7m::SeqFwdArgs p{};
     p.bf16 = dtype == RWKV7M_DTYPE_BF16;

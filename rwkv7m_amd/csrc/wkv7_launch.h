@@ -35,7 +35,7 @@ struct SeqBwdArgs {
     float* ds0;
 };
 
-// Chunked MFMA kernels: bf16 vectors, N = 64, chunk length L in {16,32,64}.
+// MFMA forward: bf16 vectors, N = 64; L is the checkpoint interval.
 struct ChunkFwdArgs {
     int L;
     int64_t T, B, H;
@@ -47,9 +47,8 @@ struct ChunkFwdArgs {
     void* ckpt;  // nullptr: no checkpoints; else bf16, one per chunk (every L)
 };
 
-hipError_t launch_chunk_forward(const ChunkFwdArgs& p, hipStream_t stream);
-
-// Wave-per-chunk forward: L = 16 (checkpoints, if any, every 16 tokens).
+// The forward runs in 16-token chunks (wkv7_wave_fwd.hip); L in {16, 32, 64}
+// is the checkpoint interval (checkpoints every L / 16 chunks).
 hipError_t launch_wave_forward(const ChunkFwdArgs& p, hipStream_t stream);
 
 // Chunked backward: L in {16, 32}; ckpt holds a state every L tokens.

@@ -175,7 +175,8 @@ struct FwdArgs {
     const float* s0;
     bf16_t* y;
     float* s_t;
-    bf16_t* ckpt;
+    bf16_t* ckpt;  // nullptr, or bf16 checkpoints every cstride chunks
+    int cstride;   // checkpoint interval / 16
 };
 
 // ---------------------------------------------------------------------------
@@ -556,20 +557,20 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
             if (lr < n)
                 *reinterpret_cast<uint2*>((A.y + (t0 * A.lay.ts + hoff)) +
                                           yoff) = pack4(yy);
-            if (A.ckpt) {
+            if (A.ckpt && c % A.cstride == 0) {
 #pragma unroll
                 for (int jb = 0; jb < 4; ++jb)
                     *reinterpret_cast<i16x4_t*>(
-                        (A.ckpt + (c * A.BH * NN + sbase)) + (coff + 16 * jb)) =
-                        sb[jb];
+                        (A.ckpt + ((c / A.cstride) * A.BH * NN + sbase)) +
+                        (coff + 16 * jb)) = sb[jb];
             }
         } else {
-            if (A.ckpt) {
+            if (A.ckpt && c % A.cstride == 0) {
 #pragma unroll
                 for (int jb = 0; jb < 4; ++jb)
                     *reinterpret_cast<i16x4_t*>(
-                        (A.ckpt + (c * A.BH * NN + sbase)) + (coff + 16 * jb)) =
-                        sb[jb];
+                        (A.ckpt + ((c / A.cstride) * A.BH * NN + sbase)) +
+                        (coff + 16 * jb)) = sb[jb];
             }
             // exact fp32 sequential pass over the chunk for the rows of
             // block ib (a chunk outside the factored form's range, far
@@ -612,7 +613,10 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
                                    4 * lq) =
             make_float4(S[jb][0], S[jb][1], S[jb][2], S[jb][3]);
         if (A.ckpt)
-            *reinterpret_cast<uint2*>(A.ckpt + nch * A.BH * NN + sbase +
+            *reinterpret_cast<uint2*>(A.ckpt +
+                                      ((nch + A.cstride - 1) / A.cstride) *
+                                          A.BH * NN +
+                                      sbase +
                                       row * WN + 16 * jb + 4 * lq) =
                 pack4(S[jb]);
     }
@@ -639,7 +643,9 @@ wkv7_wave_fwd_kernel(FwdArgs A) {
 }  // namespace
 
 hipError_t launch_wave_forward(const ChunkFwdArgs& p, hipStream_t stream) {
-    if (p.L != WL) return hipErrorInvalidValue;
+    // p.L: the checkpoint interval, a multiple of the 16-token chunk
+    if (p.L % WL != 0 || p.L / WL < 1 || p.L / WL > 4)
+        return hipErrorInvalidValue;
     FwdArgs A;
     A.T = p.T;
     A.BH = p.B * p.H;
@@ -654,6 +660,7 @@ hipError_t launch_wave_forward(const ChunkFwdArgs& p, hipStream_t stream) {
     A.y = static_cast<bf16_t*>(p.y);
     A.s_t = p.s_t;
     A.ckpt = static_cast<bf16_t*>(p.ckpt);
+    A.cstride = p.L / WL;
     if (A.BH <= 0) return hipSuccess;
     hipLaunchKernelGGL(wkv7_wave_fwd_kernel, dim3(unsigned(A.BH)),
                        dim3(WTHREADS), 0, stream, A);

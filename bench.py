@@ -48,6 +48,10 @@ def parse_args():
                    help="vector layout: time-major [T,B,H,N] (the "
                         "reference's WKV contract) or batch-major "
                         "[B,T,H,N] (the _bthn entry points)")
+    p.add_argument("--path", choices=("wkv", "timemix"), default="wkv",
+                   help="wkv: the WKV-7 call (the headline); timemix: the "
+                        "fused time-mix section around it (producers, "
+                        "batch-major WKV, consumer), forward and backward")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="target CPU-baseline sample duration (0 = skip)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -224,6 +228,199 @@ def bench_decode(args, cfg, inp, stream):
                               if args.cpu_seconds > 0 else None)
     print(json.dumps(result), flush=True)
 
+def timemix_cpu_baseline(cfg, target_s):
+    """Time the CPU restatements of the time-mix section on the host cores:
+    the numpy producers/consumer oracle (fp32 arrays) around the C WKV
+    oracle (fp32, OpenMP over (b, h)), forward and backward, on the
+    config's (B, H, N) at a reduced T."""
+    import numpy as np
+
+    import oracle
+    from oracle import timemix_oracle as tmo
+
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    B, H, N = cfg["B"], cfg["H"], cfg["N"]
+    C = H * N
+    rng = np.random.default_rng(7)
+
+    def run(T):
+        rows = B * T
+        f = {n: rng.standard_normal((rows, C), dtype=np.float32)
+             for n in ("w_raw", "k", "a", "r", "v", "g", "dout")}
+        par = np.ones(C, np.float32)
+        s0 = np.zeros((B, H, N, N), np.float32)
+
+        def tmaj(x):
+            return np.ascontiguousarray(
+                x.reshape(B, T, H, N).transpose(1, 0, 2, 3))
+
+        def bmaj(x):
+            return x.transpose(1, 0, 2, 3).reshape(rows, C)
+
+        t0 = time.perf_counter()
+        w, kp, nkk, kka = tmo.wkv_inputs(f["w_raw"], f["k"], f["a"], par,
+                                         par, N)
+        vecs = [tmaj(x) for x in (f["r"], w, kp, f["v"], nkk, kka)]
+        y, _ = oracle.forward(*vecs, s0, precision="f32", threads=threads)
+        args = (bmaj(y), f["r"], kp, f["v"], f["g"], par, par, par)
+        tmo.wkv_output(*args, N)
+        dy, _, dk_c, *_ = tmo.wkv_output_backward(*args, f["dout"], N)
+        g = oracle.backward(*vecs, s0, tmaj(dy), s0, precision="f32",
+                            threads=threads)
+        tmo.wkv_inputs_backward(f["w_raw"], f["k"], f["a"], par, par,
+                                bmaj(g[1]), bmaj(g[2]) + dk_c, bmaj(g[4]),
+                                bmaj(g[5]), N)
+        return time.perf_counter() - t0
+
+    probe_T = 16
+    dt = run(probe_T)
+    T = int(max(probe_T, min(cfg["T"], probe_T * target_s / max(dt, 1e-6))))
+    reps, dt = 0, 0.0
+    while reps == 0 or dt < 0.8 * target_s:
+        dt += run(T)
+        reps += 1
+    return {
+        "value": reps * B * T / dt,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"numpy time-mix producers/consumer (fp32) around the "
+                   f"fp32 C WKV restatement, fwd+bwd, B={B} T={T} H={H} "
+                   f"N={N}, {reps} run(s), {dt:.1f} s on {threads} threads"),
+    }
+
+
+def bench_timemix(args, cfg):
+    """The fused WKV section of the time mix (src/rwkv7m/model/
+    nnx_model.py:630-727 without the projections) on batch-major [B, T, C]
+    activations: producers, batch-major WKV forward_with_aux, consumer, then
+    consumer, WKV and producer backward and the two cotangent sums of r and
+    v -- the calls ``rwkv7m_amd.time_mix_wkv`` makes.  Each stage is
+    bracketed by HIP events on the launch stream; the algorithmic bytes of a
+    fused kernel are its activation reads and writes."""
+    import torch
+
+    from rwkv7m_amd.kernels import timemix_hip, wkv_hip
+
+    T, B, H, N, dtype = cfg["T"], cfg["B"], cfg["H"], cfg["N"], cfg["dtype"]
+    C = H * N
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(cfg["seed"])
+
+    def act(scale=1.0, shift=0.0):
+        return (torch.randn(B, T, C, generator=gen, device=dev) * scale +
+                shift).to(dtype)
+
+    x = {"r": act(), "w_raw": act(0.5, -0.5), "k": act(), "v": act(),
+         "a": torch.sigmoid(act().float()).to(dtype), "g": act(),
+         "dout": act()}
+    par = {"k_k": torch.full((C,), 0.7, device=dev),
+           "k_a": torch.full((C,), 1.02, device=dev),
+           "r_k": torch.full((C,), -0.04, device=dev),
+           "scale": torch.full((C,), 0.8, device=dev),
+           "bias": torch.zeros(C, device=dev)}
+    s0 = torch.zeros(B, H, N, N, device=dev)
+    ds_t = torch.zeros_like(s0)
+    hv = (B, T, H, N)
+    stream = torch.cuda.current_stream(dev)
+    torch.cuda.synchronize()
+    stages = ("inputs_fwd", "wkv_fwd", "output_fwd", "output_bwd", "wkv_bwd",
+              "inputs_bwd", "sums")
+
+    def step(evs=None):
+        def mark(i):
+            if evs:
+                evs[i].record(stream)
+        mark(0)
+        w, kp, nkk, kka = (t.view(hv) for t in timemix_hip.inputs_forward(
+            x["w_raw"], x["k"], x["a"], par["k_k"], par["k_a"], N))
+        mark(1)
+        r_h, v_h = x["r"].view(hv), x["v"].view(hv)
+        vecs = (r_h, w, kp, v_h, nkk, kka, s0)
+        (y, s_t), aux = wkv_hip.forward_with_aux(*vecs, layout="bthn")
+        mark(2)
+        out = timemix_hip.output_forward(y, r_h, kp, v_h, x["g"],
+                                         par["r_k"], par["scale"],
+                                         par["bias"], N)
+        mark(3)
+        dy, dr_c, dk_c, dv_c, dg, *pg = timemix_hip.output_backward(
+            y, r_h, kp, v_h, x["g"], par["r_k"], par["scale"], par["bias"],
+            x["dout"], N)
+        mark(4)
+        dr, dw, dk_w, dv, dnkk, dkka, ds0 = wkv_hip.backward(
+            *vecs, dy, ds_t, *aux, layout="bthn")
+        mark(5)
+        gi = timemix_hip.inputs_backward(
+            x["w_raw"], x["k"], x["a"], par["k_k"], par["k_a"], dw, dk_w,
+            dnkk, dkka, N, dk_out2=dk_c)
+        mark(6)
+        dr = dr + dr_c
+        dv = dv + dv_c
+        mark(7)
+        return out, s_t, dr, dv, dg, gi, pg, ds0
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(8)]
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    stage_ms = {name: sum(e[j].elapsed_time(e[j + 1]) for e in evs) /
+                args.steps for j, name in enumerate(stages)}
+    ms_per_step = elapsed * 1e3 / args.steps
+    eb = 2 if dtype == torch.bfloat16 else 4
+    M = B * T * C * eb
+    moved = {"inputs_fwd": 7 * M, "output_fwd": 6 * M, "output_bwd": 11 * M,
+             "inputs_bwd": 11 * M}
+    kernels = {name: {"ms": stage_ms[name],
+                      "algorithmic_bytes": moved[name],
+                      "GB/s": moved[name] / (stage_ms[name] / 1e3) / 1e9}
+               for name in moved}
+    dominant = max(moved, key=lambda n: stage_ms[n])
+    ach = kernels[dominant]["GB/s"]
+    result = {
+        "metric": ("time-mix WKV section (fused producers + WKV-7 + "
+                   "consumer) fwd+bwd tokens/sec at H=32,N=64,T=4096 bf16"),
+        "value": B * T / (ms_per_step / 1e3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if eb == 2 else "f32",
+        "data": "synthetic (normal activations, device RNG)",
+        "config": {
+            "workload": (f"config {args.config}: time-mix WKV section "
+                         f"fwd+bwd B={B} T={T} H={H} N={N} batch-major "
+                         f"[B,T,C] activations, fp32 state"),
+            "B": B, "T": T, "H": H, "N": N, "layout": "bthn",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dominant,
+            "achieved": ach,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": ach / HBM_PEAK_GBS,
+            "traffic": measured_traffic(dominant, args.config, 0, "bthn"),
+            "algorithmic_bytes": moved[dominant],
+            "avg_ms": stage_ms[dominant],
+        },
+        "stages_ms": stage_ms,
+        "fused_kernels": kernels,
+    }
+    result["cpu_baseline"] = (timemix_cpu_baseline(cfg, args.cpu_seconds)
+                              if args.cpu_seconds > 0 else None)
+    print(json.dumps(result), flush=True)
+
 
 def main():
     args = parse_args()
@@ -245,6 +442,8 @@ def main():
         sys.exit(1)
     wkv_hip.load_library()
     cfg = dict(CONFIGS[args.config])
+    if args.path == "timemix":
+        return bench_timemix(args, cfg)
     T, B, H, N, dtype = cfg["T"], cfg["B"], cfg["H"], cfg["N"], cfg["dtype"]
     dev = torch.device("cuda:0")
     inp = make_inputs(T, B, H, N, dtype=dtype, seed=cfg["seed"],

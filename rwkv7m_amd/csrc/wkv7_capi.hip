@@ -8,11 +8,13 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <initializer_list>
 #include <string>
 
+#include "../../include/rwkv7m_timemix.h"
 #include "../../include/rwkv7m_wkv.h"
 #include "wkv7_launch.h"
 
@@ -341,6 +343,75 @@ int forward_aux_impl(const char* fn, int dtype, int64_t T, int64_t B,
                         batch_major);
 }
 
+
+// ---------------------------------------------------------------------------
+// Fused time-mix producers and consumer (include/rwkv7m_timemix.h)
+// ---------------------------------------------------------------------------
+
+struct TmDims {
+    int64_t rows, C, N;
+};
+
+int tm_check(const char* fn, int dtype, int64_t rows, int64_t H, int64_t N,
+             TmDims* d) {
+    const std::string f(fn);
+    if (dtype != RWKV7M_DTYPE_F32 && dtype != RWKV7M_DTYPE_BF16)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    f + ": activations must be bfloat16 or float32 (dtype=" +
+                        std::to_string(dtype) + ")");
+    if (rows < 0 || H < 0 || N < 0)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT, f + ": negative dimension");
+    if (N != 8 && N != 16 && N != 32 && N != 64 && N != 128)
+        return fail(RWKV7M_ERR_UNSUPPORTED,
+                    f + ": head size N=" + std::to_string(N) +
+                        " is not supported (8, 16, 32, 64, 128)");
+    if (H > 0x7fffffff / N)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT, f + ": sizes too large");
+    d->rows = rows;
+    d->N = N;
+    d->C = H * N;
+    if (d->C > 0 && rows > (int64_t(1) << 46) / d->C)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT, f + ": sizes too large");
+    return RWKV7M_OK;
+}
+
+struct Named {
+    const char* name;
+    const void* p;
+};
+
+// Each pointer is required (non-NULL) and 16-byte aligned.
+int tm_need(const char* fn, std::initializer_list<Named> ptrs) {
+    for (const Named& x : ptrs) {
+        if (x.p == nullptr)
+            return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                        std::string(fn) + ": " + x.name + " is NULL");
+        if (!aligned16(x.p))
+            return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                        std::string(fn) + ": " + x.name +
+                            " is not 16-byte aligned");
+    }
+    return RWKV7M_OK;
+}
+
+int tm_eps(const char* fn, double eps) {
+    if (!(eps >= 0.0) || !std::isfinite(eps))
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": eps must be finite and >= 0");
+    return RWKV7M_OK;
+}
+
+int tm_workspace(const char* fn, const TmDims& d, const float* ws,
+                 int64_t ws_floats) {
+    const int64_t need_floats = rwkv7m::timemix_workspace_floats(d.rows, d.C);
+    if (ws_floats < need_floats)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": workspace holds " +
+                        std::to_string(ws_floats) + " floats, needs " +
+                        std::to_string(need_floats));
+    return tm_need(fn, {{"workspace", ws}});
+}
+
 }  // namespace
 
 extern "C" {
@@ -455,6 +526,126 @@ int rwkv7m_wkv7_decode_inplace(int dtype, int64_t B, int64_t H, int64_t N,
     return forward_impl("rwkv7m_wkv7_decode_inplace", dtype, 1, B, H, N, r,
                         w, k, v, neg_kk, kka, state, y, state, nullptr, 0,
                         static_cast<hipStream_t>(stream), false);
+}
+
+int64_t rwkv7m_timemix_workspace_floats(int64_t rows, int64_t H, int64_t N) {
+    TmDims d;
+    const std::string saved = g_last_error;
+    const int rc = tm_check("rwkv7m_timemix_workspace_floats",
+                            RWKV7M_DTYPE_F32, rows, H, N, &d);
+    g_last_error = saved;
+    if (rc != RWKV7M_OK) return -1;
+    return rwkv7m::timemix_workspace_floats(rows, d.C);
+}
+
+int rwkv7m_timemix_wkv_inputs(int dtype, int64_t rows, int64_t H, int64_t N,
+                              const void* w_raw, const void* k, const void* a,
+                              const float* k_k, const float* k_a, void* w,
+                              void* k_out, void* neg_kk, void* kka,
+                              void* stream) {
+    const char* fn = "rwkv7m_timemix_wkv_inputs";
+    g_last_error.clear();
+    TmDims d;
+    RWKV7M_TRY(tm_check(fn, dtype, rows, H, N, &d));
+    if (d.rows == 0 || d.C == 0) return RWKV7M_OK;
+    RWKV7M_TRY(tm_need(fn, {{"w_raw", w_raw}, {"k", k}, {"a", a},
+                            {"k_k", k_k}, {"k_a", k_a}, {"w", w},
+                            {"k_out", k_out}, {"neg_kk", neg_kk},
+                            {"kka", kka}}));
+    rwkv7m::TmInputsArgs A{d.rows, d.C, w_raw, k, a, k_k, k_a,
+                           w, k_out, neg_kk, kka};
+    return hip_status("time-mix producers launch",
+                      rwkv7m::launch_timemix_inputs(
+                          dtype == RWKV7M_DTYPE_BF16, int(d.N), A,
+                          static_cast<hipStream_t>(stream)));
+}
+
+int rwkv7m_timemix_wkv_inputs_backward(
+    int dtype, int64_t rows, int64_t H, int64_t N, const void* w_raw,
+    const void* k, const void* a, const float* k_k, const float* k_a,
+    const void* dw, const void* dk_out, const void* dk_out2,
+    const void* dneg_kk, const void* dkka, void* dw_raw, void* dk, void* da,
+    float* dk_k, float* dk_a, float* workspace, int64_t workspace_floats,
+    void* stream) {
+    const char* fn = "rwkv7m_timemix_wkv_inputs_backward";
+    g_last_error.clear();
+    TmDims d;
+    RWKV7M_TRY(tm_check(fn, dtype, rows, H, N, &d));
+    if (d.C == 0) return RWKV7M_OK;
+    RWKV7M_TRY(tm_need(fn, {{"k_k", k_k}, {"k_a", k_a}, {"dk_k", dk_k},
+                            {"dk_a", dk_a}}));
+    RWKV7M_TRY(tm_workspace(fn, d, workspace, workspace_floats));
+    if (d.rows > 0) {
+        RWKV7M_TRY(tm_need(fn, {{"w_raw", w_raw}, {"k", k}, {"a", a},
+                                {"dw", dw}, {"dk_out", dk_out},
+                                {"dneg_kk", dneg_kk}, {"dkka", dkka},
+                                {"dw_raw", dw_raw}, {"dk", dk}, {"da", da}}));
+        if (dk_out2) RWKV7M_TRY(tm_need(fn, {{"dk_out2", dk_out2}}));
+    }
+    rwkv7m::TmInputsBwdArgs A{d.rows, d.C,  w_raw,  k,      a,       k_k,
+                              k_a,    dw,   dk_out, dk_out2, dneg_kk, dkka,
+                              dw_raw, dk,   da,     dk_k,    dk_a,
+                              workspace};
+    return hip_status("time-mix producers backward launch",
+                      rwkv7m::launch_timemix_inputs_backward(
+                          dtype == RWKV7M_DTYPE_BF16, int(d.N), A,
+                          static_cast<hipStream_t>(stream)));
+}
+
+int rwkv7m_timemix_wkv_output(int dtype, int64_t rows, int64_t H, int64_t N,
+                              const void* y, const void* r, const void* k,
+                              const void* v, const void* g, const float* r_k,
+                              const float* ln_scale, const float* ln_bias,
+                              double eps, void* out, void* stream) {
+    const char* fn = "rwkv7m_timemix_wkv_output";
+    g_last_error.clear();
+    TmDims d;
+    RWKV7M_TRY(tm_check(fn, dtype, rows, H, N, &d));
+    RWKV7M_TRY(tm_eps(fn, eps));
+    if (d.rows == 0 || d.C == 0) return RWKV7M_OK;
+    RWKV7M_TRY(tm_need(fn, {{"y", y}, {"r", r}, {"k", k}, {"v", v},
+                            {"g", g}, {"r_k", r_k}, {"ln_scale", ln_scale},
+                            {"ln_bias", ln_bias}, {"out", out}}));
+    rwkv7m::TmOutputArgs A{d.rows, d.C, float(eps), y, r, k, v, g,
+                           r_k, ln_scale, ln_bias, out};
+    return hip_status("time-mix consumer launch",
+                      rwkv7m::launch_timemix_output(
+                          dtype == RWKV7M_DTYPE_BF16, int(d.N), A,
+                          static_cast<hipStream_t>(stream)));
+}
+
+int rwkv7m_timemix_wkv_output_backward(
+    int dtype, int64_t rows, int64_t H, int64_t N, const void* y,
+    const void* r, const void* k, const void* v, const void* g,
+    const float* r_k, const float* ln_scale, const float* ln_bias, double eps,
+    const void* dout, void* dy, void* dr, void* dk, void* dv, void* dg,
+    float* dr_k, float* dln_scale, float* dln_bias, float* workspace,
+    int64_t workspace_floats, void* stream) {
+    const char* fn = "rwkv7m_timemix_wkv_output_backward";
+    g_last_error.clear();
+    TmDims d;
+    RWKV7M_TRY(tm_check(fn, dtype, rows, H, N, &d));
+    RWKV7M_TRY(tm_eps(fn, eps));
+    if (d.C == 0) return RWKV7M_OK;
+    RWKV7M_TRY(tm_need(fn, {{"r_k", r_k}, {"ln_scale", ln_scale},
+                            {"ln_bias", ln_bias}, {"dr_k", dr_k},
+                            {"dln_scale", dln_scale},
+                            {"dln_bias", dln_bias}}));
+    RWKV7M_TRY(tm_workspace(fn, d, workspace, workspace_floats));
+    if (d.rows > 0)
+        RWKV7M_TRY(tm_need(fn, {{"y", y}, {"r", r}, {"k", k}, {"v", v},
+                                {"g", g}, {"dout", dout}, {"dy", dy},
+                                {"dr", dr}, {"dk", dk}, {"dv", dv},
+                                {"dg", dg}}));
+    rwkv7m::TmOutputBwdArgs A{d.rows, d.C,     float(eps), y,   r,
+                              k,      v,       g,          dout, r_k,
+                              ln_scale, ln_bias, dy,       dr,   dk,
+                              dv,     dg,      dr_k,       dln_scale,
+                              dln_bias, workspace};
+    return hip_status("time-mix consumer backward launch",
+                      rwkv7m::launch_timemix_output_backward(
+                          dtype == RWKV7M_DTYPE_BF16, int(d.N), A,
+                          static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -67,6 +67,55 @@ hipError_t launch_chunk_backward(const ChunkBwdArgs& p, hipStream_t stream);
 
 hipError_t launch_seq_forward(const SeqFwdArgs& p, hipStream_t stream);
 
+// Fused time-mix producers and consumer (wkv7_timemix.hip).  Activations are
+// [rows][C] of the launch dtype; parameters fp32 [C]; N in {8, ..., 128}.
+struct TmInputsArgs {
+    int64_t rows, C;
+    const void *w_raw, *k, *a;
+    const float *k_k, *k_a;
+    void *w, *k_out, *neg_kk, *kka;
+};
+
+struct TmInputsBwdArgs {
+    int64_t rows, C;
+    const void *w_raw, *k, *a;
+    const float *k_k, *k_a;
+    const void *dw, *dk_out, *dk_out2, *dneg_kk, *dkka;  // dk_out2 may be 0
+    void *dw_raw, *dk, *da;
+    float *dk_k, *dk_a;
+    float* workspace;  // timemix_workspace_floats(rows, C) floats
+};
+
+struct TmOutputArgs {
+    int64_t rows, C;
+    float eps;
+    const void *y, *r, *k, *v, *g;
+    const float *r_k, *scale, *bias;
+    void* out;
+};
+
+struct TmOutputBwdArgs {
+    int64_t rows, C;
+    float eps;
+    const void *y, *r, *k, *v, *g, *dout;
+    const float *r_k, *scale, *bias;
+    void *dy, *dr, *dk, *dv, *dg;
+    float *dr_k, *dscale, *dbias;
+    float* workspace;
+};
+
+int64_t timemix_workspace_floats(int64_t rows, int64_t C);
+hipError_t launch_timemix_inputs(bool bf16, int N, const TmInputsArgs& A,
+                                 hipStream_t stream);
+hipError_t launch_timemix_inputs_backward(bool bf16, int N,
+                                          const TmInputsBwdArgs& A,
+                                          hipStream_t stream);
+hipError_t launch_timemix_output(bool bf16, int N, const TmOutputArgs& A,
+                                 hipStream_t stream);
+hipError_t launch_timemix_output_backward(bool bf16, int N,
+                                          const TmOutputBwdArgs& A,
+                                          hipStream_t stream);
+
 // One token (T = 1) for N = 64 without checkpoints; s_t may alias s0.
 hipError_t launch_decode(const SeqFwdArgs& p, hipStream_t stream);
 hipError_t launch_seq_backward(const SeqBwdArgs& p, hipStream_t stream);

@@ -45,7 +45,7 @@ LIB_PATH = os.path.join(_PKG_DIR, "librwkv7m_wkv.so")
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 
-# Every symbol declared in include/rwkv7m_wkv.h.
+# Every symbol declared in include/rwkv7m_wkv.h and include/rwkv7m_timemix.h.
 EXPORTED_SYMBOLS = (
     "rwkv7m_abi_version",
     "rwkv7m_last_error",
@@ -59,6 +59,11 @@ EXPORTED_SYMBOLS = (
     "rwkv7m_wkv7_forward_with_aux_bthn",
     "rwkv7m_wkv7_backward_bthn",
     "rwkv7m_wkv7_decode_inplace",
+    "rwkv7m_timemix_workspace_floats",
+    "rwkv7m_timemix_wkv_inputs",
+    "rwkv7m_timemix_wkv_inputs_backward",
+    "rwkv7m_timemix_wkv_output",
+    "rwkv7m_timemix_wkv_output_backward",
 )
 
 LAYOUTS = ("tbhn", "bthn")
@@ -105,6 +110,21 @@ def load_library(path: str | None = None):
             bwd.argtypes = [i32] + [i64] * 4 + [vp] * 10 + [i64] + [vp] * 8
         lib.rwkv7m_wkv7_decode_inplace.restype = i32
         lib.rwkv7m_wkv7_decode_inplace.argtypes = [i32] + [i64] * 3 + [vp] * 9
+        f64 = ctypes.c_double
+        dims = [i32, i64, i64, i64]
+        lib.rwkv7m_timemix_workspace_floats.restype = i64
+        lib.rwkv7m_timemix_workspace_floats.argtypes = [i64] * 3
+        lib.rwkv7m_timemix_wkv_inputs.restype = i32
+        lib.rwkv7m_timemix_wkv_inputs.argtypes = dims + [vp] * 10
+        lib.rwkv7m_timemix_wkv_inputs_backward.restype = i32
+        lib.rwkv7m_timemix_wkv_inputs_backward.argtypes = (
+            dims + [vp] * 16 + [i64, vp])
+        lib.rwkv7m_timemix_wkv_output.restype = i32
+        lib.rwkv7m_timemix_wkv_output.argtypes = dims + [vp] * 8 + [f64,
+                                                                    vp, vp]
+        lib.rwkv7m_timemix_wkv_output_backward.restype = i32
+        lib.rwkv7m_timemix_wkv_output_backward.argtypes = (
+            dims + [vp] * 8 + [f64] + [vp] * 10 + [i64, vp])
         if path is None:
             _lib = lib
         return lib

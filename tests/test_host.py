@@ -305,6 +305,52 @@ def test_library_rejects_bad_requests_before_any_device_call(lib):
     assert b"rwkv7m_wkv7_backward_bthn" in lib.rwkv7m_last_error()
 
 
+def test_timemix_abi_checks_requests_before_any_device_call(lib):
+    # workspace: one partial row of C floats per row group for 3 parameters
+    assert lib.rwkv7m_timemix_workspace_floats(0, 32, 64) == 3 * 2048
+    assert lib.rwkv7m_timemix_workspace_floats(1, 32, 64) == 3 * 2048
+    assert lib.rwkv7m_timemix_workspace_floats(32768, 32, 64) == \
+        3 * 1024 * 2048
+    assert lib.rwkv7m_timemix_workspace_floats(-1, 32, 64) == -1
+    assert lib.rwkv7m_timemix_workspace_floats(8, 2, 4) == -1
+    fake = 1 << 20  # aligned, never dereferenced: every call below fails
+    odd = fake + 8  # not 16-byte aligned
+    p9 = [fake] * 9
+    fn = lib.rwkv7m_timemix_wkv_inputs
+    assert fn(2, 4, 2, 64, *p9, None) == 1
+    assert b"bfloat16 or float32" in lib.rwkv7m_last_error()
+    assert fn(1, 4, 2, 4, *p9, None) == 2
+    assert b"(8, 16, 32, 64, 128)" in lib.rwkv7m_last_error()
+    assert fn(1, -1, 2, 64, *p9, None) == 1
+    assert fn(1, 4, 2, 64, *p9[:3], None, *p9[4:], None) == 1
+    assert b"k_k is NULL" in lib.rwkv7m_last_error()
+    assert fn(1, 4, 2, 64, *p9[:5], odd, *p9[6:], None) == 1
+    assert b"w is not 16-byte aligned" in lib.rwkv7m_last_error()
+    # nothing to do: no rows, or no heads
+    assert fn(1, 0, 2, 64, *([None] * 9), None) == 0
+    assert fn(1, 4, 0, 64, *([None] * 9), None) == 0
+    bwd = lib.rwkv7m_timemix_wkv_inputs_backward
+    ws = lib.rwkv7m_timemix_workspace_floats(4, 2, 64)
+    args16 = [fake] * 16
+    assert bwd(1, 4, 2, 64, *args16, ws - 1, None) == 1
+    assert b"workspace holds" in lib.rwkv7m_last_error()
+    assert bwd(1, 4, 2, 64, *args16[:15], None, ws, None) == 1
+    assert b"workspace is NULL" in lib.rwkv7m_last_error()
+    out = lib.rwkv7m_timemix_wkv_output
+    assert out(1, 4, 2, 64, *([fake] * 8), -1.0, fake, None) == 1
+    assert b"eps" in lib.rwkv7m_last_error()
+    assert out(1, 4, 2, 64, *([fake] * 8), float("nan"), fake, None) == 1
+    assert out(1, 4, 2, 64, *([fake] * 8), 64e-5, None, None) == 1
+    assert b"out is NULL" in lib.rwkv7m_last_error()
+    obwd = lib.rwkv7m_timemix_wkv_output_backward
+    assert obwd(1, 4, 2, 64, *([fake] * 8), 64e-5, *([fake] * 5), None,
+                *([fake] * 3), None, 0, None) == 1
+    assert b"workspace holds 0" in lib.rwkv7m_last_error()
+    assert obwd(1, 4, 2, 64, *([fake] * 8), 64e-5, *([fake] * 5), None,
+                *([fake] * 3), fake, 10 ** 9, None) == 1
+    assert b"dg is NULL" in lib.rwkv7m_last_error()
+
+
 # ---------------------------------------------------------------------------
 # Oracle against the committed golden fixtures
 # ---------------------------------------------------------------------------

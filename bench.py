@@ -228,6 +228,20 @@ def bench_decode(args, cfg, inp, stream):
                               if args.cpu_seconds > 0 else None)
     print(json.dumps(result), flush=True)
 
+def copy_probe(mib, dev):
+    """One plain device copy of ``mib`` MiB (0: none) -- the reference
+    kernel for scaling HBM counters under rocprofv3 --pmc."""
+    if mib <= 0:
+        return
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def timemix_cpu_baseline(cfg, target_s):
     """Time the CPU restatements of the time-mix section on the host cores:
     the numpy producers/consumer oracle (fp32 arrays) around the C WKV
@@ -305,6 +319,7 @@ def bench_timemix(args, cfg):
     T, B, H, N, dtype = cfg["T"], cfg["B"], cfg["H"], cfg["N"], cfg["dtype"]
     C = H * N
     dev = torch.device("cuda:0")
+    copy_probe(args.copy_probe, dev)
     gen = torch.Generator(device=dev).manual_seed(cfg["seed"])
 
     def act(scale=1.0, shift=0.0):
@@ -456,13 +471,7 @@ def main():
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream(dev)
-    if args.copy_probe > 0:
-        n = args.copy_probe * (1 << 20) // 4
-        src = torch.ones(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+    copy_probe(args.copy_probe, dev)
     if T == 1:
         return bench_decode(args, cfg, inp, stream)
     if args.layout == "bthn":

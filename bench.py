@@ -48,10 +48,13 @@ def parse_args():
                    help="vector layout: time-major [T,B,H,N] (the "
                         "reference's WKV contract) or batch-major "
                         "[B,T,H,N] (the _bthn entry points)")
-    p.add_argument("--path", choices=("wkv", "timemix"), default="wkv",
+    p.add_argument("--path", choices=("wkv", "timemix", "screening"),
+                   default="wkv",
                    help="wkv: the WKV-7 call (the headline); timemix: the "
                         "fused time-mix section around it (producers, "
-                        "batch-major WKV, consumer), forward and backward")
+                        "batch-major WKV, consumer), forward and backward; "
+                        "screening: the state-level screening read path of "
+                        "the 0.185B preset at config 1's B and T")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="target CPU-baseline sample duration (0 = skip)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -437,6 +440,175 @@ def bench_timemix(args, cfg):
     print(json.dumps(result), flush=True)
 
 
+def screening_cpu_baseline(cfg_d, P, B, T, target_s):
+    """Time the CPU restatement of the reference's read-only screening scan
+    (numpy float64, one step per token, forward only) on a reduced T."""
+    import numpy as np
+
+    from oracle import screening_oracle as so
+
+    C, ds, M = cfg_d["d_model"], cfg_d["d_slot"], cfg_d["n_slots"]
+    rng = np.random.default_rng(7)
+
+    def run(t):
+        x = rng.normal(size=(B, t, C))
+        h = rng.normal(size=(B, t, C))
+        t0 = time.perf_counter()
+        so.read_forward(x, h, np.zeros((B, M, ds)), np.zeros((B, M)),
+                        np.zeros((B, M)), P, cfg_d)
+        return time.perf_counter() - t0
+
+    dt = run(8)
+    t = int(max(8, min(T, 8 * target_s / max(dt, 1e-6))))
+    reps, dt = 0, 0.0
+    while reps == 0 or dt < 0.8 * target_s:
+        dt += run(t)
+        reps += 1
+    return {
+        "value": reps * B * t / dt,
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"numpy float64 per-step scan of the read-only screening "
+                   f"(the reference's algorithm), forward only, B={B} T={t}, "
+                   f"{reps} run(s), {dt:.1f} s"),
+    }
+
+
+def bench_screening(args):
+    """State-level screening read path (phase read_screening_only) of the
+    0.185B preset (src/rwkv7m/model/presets.py:93-104: d_model 768,
+    d_slot 128, d_k 64, d_v 64, 16 slots in banks 8/4/4) at config 1's
+    B=8, T=512, bf16: one step = StateLevelScreening forward and the
+    backward of all its inputs and parameters from a cotangent of h.  The
+    four HIP kernels are also timed alone with HIP events."""
+    import numpy as np
+    import torch
+
+    from oracle import screening_oracle as so
+    from rwkv7m_amd.kernels import screening_hip
+    from rwkv7m_amd.screening import (ScreeningConfig, StateLevelScreening,
+                                      init_screen_state)
+
+    B, T = 8, 512
+    cfg_d = so.default_config(d_model=768, d_slot=128, d_k=64, d_v=64,
+                              n_slots=16,
+                              bank_ids=(0,) * 8 + (1,) * 4 + (2,) * 4)
+    cfg = ScreeningConfig(**cfg_d)
+    dev = torch.device("cuda:0")
+    mod = StateLevelScreening(cfg, compute_dtype=torch.bfloat16, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(B, T, 768, generator=gen, device=dev).to(torch.bfloat16)
+    h = torch.randn(B, T, 768, generator=gen, device=dev).to(torch.bfloat16)
+    x.requires_grad_(True)
+    h.requires_grad_(True)
+    dh = torch.randn(B, T, 768, generator=gen, device=dev).to(torch.bfloat16)
+    state = init_screen_state(B, cfg, device=dev)
+    state = state._replace(slots=0.1 * torch.randn(
+        B, 16, 128, generator=gen, device=dev))
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        out, new, _ = mod(x, h, state)
+        (out.float() * dh.float()).sum().backward()
+        return out
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # the four kernels alone, on the step's shapes
+    base = torch.randn(B, T, 128, generator=gen, device=dev).to(torch.bfloat16)
+    st = 0.3 * torch.randn(16, 128, generator=gen, device=dev)
+    mu = torch.full((16,), 0.02, device=dev)
+    seq, _, _ = screening_hip.slot_scan(base, st, mu, state.slots)
+    proj = torch.randn(B, T, 16, 128, generator=gen, device=dev).to(
+        torch.bfloat16)
+    q = torch.nn.functional.normalize(
+        torch.randn(B, T, 64, generator=gen, device=dev), dim=-1)
+    tau = torch.tensor(-0.2, device=dev)
+    du = torch.randn(B, T, 64, generator=gen, device=dev).to(torch.bfloat16)
+    dseq = torch.randn_like(seq)
+    calls = {
+        "scan_fwd": (lambda: screening_hip.slot_scan(base, st, mu,
+                                                     state.slots),
+                     B * T * 128 * 2 + B * T * 16 * 128 * 2),
+        "scan_bwd": (lambda: screening_hip.slot_scan_backward(
+            base, st, mu, seq, dseq),
+                     B * T * 128 * 2 + 2 * B * T * 16 * 128 * 2
+                     + B * T * 16 * 128 * 4),
+        "read_fwd": (lambda: screening_hip.read(q, proj, tau, None, cfg, 64),
+                     B * T * 16 * 128 * 2 + B * T * 64 * 4 + B * T * 64 * 2),
+        "read_bwd": (lambda: screening_hip.read_backward(
+            q, proj, tau, None, cfg, 64, du),
+                     2 * B * T * 16 * 128 * 2 + B * T * 64 * (4 + 2 + 4)),
+    }
+    kernels = {}
+    for name, (fn, nbytes) in calls.items():
+        fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(20):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 20
+        kernels[name] = {"ms": ms, "algorithmic_bytes": nbytes,
+                         "GB/s": nbytes / (ms / 1e3) / 1e9}
+    dominant = max(kernels, key=lambda n: kernels[n]["ms"])
+    ach = kernels[dominant]["GB/s"]
+    result = {
+        "metric": ("screening read path fwd+bwd tokens/sec at the 0.185B "
+                   "preset (B=8, T=512, bf16)"),
+        "value": B * T / (ms_per_step / 1e3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (normal activations, random-init parameters)",
+        "config": {
+            "workload": ("StateLevelScreening read_screening_only fwd+bwd, "
+                         "0.185B preset (d_model 768, d_slot 128, d_k 64, "
+                         "d_v 64, 16 slots), B=8 T=512"),
+            "B": B, "T": T,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dominant,
+            "achieved": ach,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": ach / HBM_PEAK_GBS,
+            "traffic": None,
+            "algorithmic_bytes": kernels[dominant]["algorithmic_bytes"],
+            "avg_ms": kernels[dominant]["ms"],
+        },
+        "screen_kernels": kernels,
+    }
+    if args.cpu_seconds > 0:
+        P = {k: np.asarray(getattr(mod, {"ln_scale": "screen_ln_scale",
+                                         "ln_bias": "screen_ln_bias"}.get(
+                                             k, k)).detach().double().cpu())
+             for k in so.PARAM_NAMES}
+        result["cpu_baseline"] = screening_cpu_baseline(
+            cfg_d, P, B, T, args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -459,6 +631,8 @@ def main():
     cfg = dict(CONFIGS[args.config])
     if args.path == "timemix":
         return bench_timemix(args, cfg)
+    if args.path == "screening":
+        return bench_screening(args)
     T, B, H, N, dtype = cfg["T"], cfg["B"], cfg["H"], cfg["N"], cfg["dtype"]
     dev = torch.device("cuda:0")
     inp = make_inputs(T, B, H, N, dtype=dtype, seed=cfg["seed"],

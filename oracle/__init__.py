@@ -16,4 +16,4 @@ from .wkv_oracle import (  # noqa: F401
     np_backward,
     np_forward,
 )
-from . import timemix_oracle  # noqa: F401,E402
+from . import screening_oracle, timemix_oracle  # noqa: F401,E402

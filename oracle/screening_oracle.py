@@ -1,0 +1,224 @@
+"""TEST INFRASTRUCTURE ONLY: float64 numpy oracle of the state-level screening
+read path (phase ``read_screening_only``).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may import this module, and only as the checker or as
+the timed CPU baseline.  No product code path imports it.
+
+Restates ``NNXStateLevelScreening.__call__`` (src/rwkv7m/model/
+nnx_model.py:999-1160) step by step, as its ``jax.lax.scan`` runs it, with
+the helpers of src/rwkv7m/model/screening.py:
+
+* ``unit_norm`` (:21-24), ``bounded_tau`` (:27-28), ``trim_square``
+  (:37-39), ``tanh_norm`` (:48-52), ``update_rate_from_half_life`` (:55-58),
+  ``compute_slot_delta`` (:61-88, ``tanh`` of the split projection);
+* ``_compute_mu`` (nnx_model.py:1002-1013): per-bank rates gathered by
+  ``bank_ids``;
+* the screen LayerNorm (flax LayerNorm, epsilon 1e-6, fp32 statistics,
+  variance E[x^2] - E[x]^2 clamped at 0);
+* the read-only step (:1062-1112 with ``write_enabled`` false): keys and
+  values of the current slots, relevance, the read, the gated residual, then
+  ``slots + mu * (delta - slots)`` and the usage EMA; ages are unchanged;
+* the statistics (:1117-1137), averaged over the steps.
+
+Parameters are a dict of float64 arrays named as the reference's module
+attributes; linear kernels are ``[in, out]`` (flax layout).  Pinning:
+``tests/test_screening_oracle.py``.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+PARAM_NAMES = ("ln_scale", "ln_bias", "q_proj_r", "k_proj_r", "v_proj",
+               "out_proj", "gate_kernel", "gate_bias", "delta_kernel",
+               "delta_bias", "tau_r_raw", "lambda_raw", "slot_embed",
+               "mu_by_bank_raw")
+
+STAT_NAMES = ("rel_read_mean", "rel_read_max", "active_slots_mean",
+              "z_norm_mean", "u_norm_mean", "tau_r", "lambda_screen",
+              "rel_write_mean", "rel_write_effective_mean",
+              "slot_update_norm_mean", "slot_usage_ema_mean", "tau_w")
+
+
+def sigmoid(x):
+    return 0.5 * (1.0 + np.tanh(0.5 * x))
+
+
+def softplus(x):
+    return np.logaddexp(x, 0.0)
+
+
+def unit_norm(x, eps):
+    return x / np.sqrt((x * x).sum(-1, keepdims=True) + eps * eps)
+
+
+def trim_square(sim, tau, eps):
+    x = (sim - tau) / (1.0 - tau + eps)
+    return np.square(np.maximum(x, 0.0))
+
+
+def tanh_norm(z, cap, eps):
+    n = np.sqrt((z * z).sum(-1, keepdims=True) + eps * eps)
+    return cap * np.tanh(n / cap) / n * z
+
+
+def layer_norm(x, scale, bias, eps=1e-6):
+    mean = x.mean(-1, keepdims=True)
+    var = np.maximum((x * x).mean(-1, keepdims=True) - mean * mean, 0.0)
+    return (x - mean) / np.sqrt(var + eps) * scale + bias
+
+
+def compute_mu(cfg, mu_by_bank_raw):
+    """nnx_model.py:1002-1013."""
+    mu_max = np.array([cfg["mu_short_max"], cfg["mu_mid_max"],
+                       cfg["mu_long_max"]])
+    legacy = mu_max * sigmoid(np.asarray(mu_by_bank_raw, np.float64))
+    per_bank = []
+    for i, hl in enumerate((cfg["short_half_life_tokens"],
+                            cfg["mid_half_life_tokens"],
+                            cfg["long_half_life_tokens"])):
+        per_bank.append(legacy[i] if hl is None
+                        else -np.expm1(-np.log(2.0) / hl))
+    return np.stack(per_bank)[np.asarray(cfg["bank_ids"], np.int64)]
+
+
+def read_forward(x, h_base, slots, ages, usage, P, cfg):
+    """One call in phase ``read_screening_only``.
+
+    x, h_base: [B, T, C]; slots [B, M, d_slot]; ages, usage [B, M].
+    Returns (h [B, T, C], (slots_T, ages, usage_T), stats dict).
+    """
+    eps = cfg["eps"]
+    B, T, C = x.shape
+    x_ln = layer_norm(x, P["ln_scale"], P["ln_bias"])
+    q = unit_norm(x_ln @ P["q_proj_r"], eps)
+    tau = 2.0 * sigmoid(P["tau_r_raw"]) - 1.0
+    lam = softplus(P["lambda_raw"])
+    mu = compute_mu(cfg, P["mu_by_bank_raw"])
+    gate = sigmoid(x_ln @ P["gate_kernel"] + P["gate_bias"])
+    dk = P["delta_kernel"]
+    x_term = x_ln @ dk[:C]
+    h_term = h_base @ dk[C:2 * C]
+    slot_term = P["slot_embed"] @ dk[2 * C:]
+    age_w = (sigmoid((cfg["age_ref"] - ages) / (cfg["age_sigma"] + eps))
+             if cfg["use_age_mask"] else None)
+    hs = np.empty_like(h_base)
+    acc = {n: 0.0 for n in STAT_NAMES}
+    for t in range(T):
+        k_r = unit_norm(slots @ P["k_proj_r"], eps)
+        values = slots @ P["v_proj"]
+        if cfg["use_value_unit_norm"]:
+            values = unit_norm(values, eps)
+        sim = np.einsum("bk,bmk->bm", q[:, t], k_r)
+        if cfg["use_leaky_warmup"]:
+            hard = trim_square(sim, tau, 1e-6)
+            soft = sigmoid(cfg["leaky_gamma"] * (sim - tau))
+            rel = (1.0 - cfg["leaky_alpha"]) * hard + cfg["leaky_alpha"] * soft
+        else:
+            rel = trim_square(sim, tau, eps)
+        if age_w is not None:
+            rel = rel * age_w
+        z = np.einsum("bm,bmv->bv", rel, values)
+        u = tanh_norm(z, cfg["tanh_norm_cap"], eps)
+        read = u @ P["out_proj"]
+        hs[:, t] = h_base[:, t] + lam * gate[:, t] * read
+        delta = np.tanh(x_term[:, t, None, :] + h_term[:, t, None, :]
+                        + slot_term[None] + P["delta_bias"])
+        new_slots = slots + mu[None, :, None] * (delta - slots)
+        upd = new_slots - slots
+        usage = cfg["usage_ema_decay"] * usage + (
+            1.0 - cfg["usage_ema_decay"]) * rel
+        acc["rel_read_mean"] += rel.mean()
+        acc["rel_read_max"] += rel.max()
+        acc["active_slots_mean"] += (rel > 1e-3).sum(-1).mean()
+        acc["z_norm_mean"] += np.linalg.norm(z, axis=-1).mean()
+        acc["u_norm_mean"] += np.linalg.norm(u, axis=-1).mean()
+        acc["tau_r"] += tau
+        acc["lambda_screen"] += lam
+        acc["slot_update_norm_mean"] += np.linalg.norm(upd, axis=-1).mean()
+        acc["slot_usage_ema_mean"] += usage.mean()
+        slots = new_slots
+    stats = {n: float(v) / T for n, v in acc.items()}
+    return hs, (slots, ages, usage), stats
+
+
+def read_forward_torch(x, h_base, slots, ages, usage, P, cfg):
+    """The same step-by-step scan with torch float64 ops, for autograd (the
+    gradient oracle): arguments are float64 torch tensors, P a dict of
+    them.  Returns (h, slots_T, usage_T)."""
+    import torch
+
+    eps = cfg["eps"]
+    B, T, C = x.shape
+
+    def un(v):
+        return v / torch.sqrt((v * v).sum(-1, keepdim=True) + eps * eps)
+
+    def trim(sim, tau, e):
+        return torch.clamp((sim - tau) / (1.0 - tau + e), min=0.0) ** 2
+
+    mean = x.mean(-1, keepdim=True)
+    var = torch.clamp((x * x).mean(-1, keepdim=True) - mean * mean, min=0.0)
+    x_ln = (x - mean) / torch.sqrt(var + 1e-6) * P["ln_scale"] + P["ln_bias"]
+    q = un(x_ln @ P["q_proj_r"])
+    tau = 2.0 * torch.sigmoid(P["tau_r_raw"]) - 1.0
+    lam = torch.nn.functional.softplus(P["lambda_raw"])
+    mu_max = torch.tensor([cfg["mu_short_max"], cfg["mu_mid_max"],
+                           cfg["mu_long_max"]], dtype=x.dtype)
+    legacy = mu_max * torch.sigmoid(P["mu_by_bank_raw"])
+    banks = []
+    for i, hl in enumerate((cfg["short_half_life_tokens"],
+                            cfg["mid_half_life_tokens"],
+                            cfg["long_half_life_tokens"])):
+        banks.append(legacy[i] if hl is None else torch.tensor(
+            -np.expm1(-np.log(2.0) / hl), dtype=x.dtype))
+    mu = torch.stack(banks)[torch.tensor(cfg["bank_ids"])]
+    gate = torch.sigmoid(x_ln @ P["gate_kernel"] + P["gate_bias"])
+    dk = P["delta_kernel"]
+    x_term = x_ln @ dk[:C]
+    h_term = h_base @ dk[C:2 * C]
+    slot_term = P["slot_embed"] @ dk[2 * C:]
+    age_w = (torch.sigmoid((cfg["age_ref"] - ages) / (cfg["age_sigma"] + eps))
+             if cfg["use_age_mask"] else None)
+    hs = []
+    for t in range(T):
+        k_r = un(slots @ P["k_proj_r"])
+        values = slots @ P["v_proj"]
+        if cfg["use_value_unit_norm"]:
+            values = un(values)
+        sim = torch.einsum("bk,bmk->bm", q[:, t], k_r)
+        if cfg["use_leaky_warmup"]:
+            rel = ((1.0 - cfg["leaky_alpha"]) * trim(sim, tau, 1e-6)
+                   + cfg["leaky_alpha"]
+                   * torch.sigmoid(cfg["leaky_gamma"] * (sim - tau)))
+        else:
+            rel = trim(sim, tau, eps)
+        if age_w is not None:
+            rel = rel * age_w
+        z = torch.einsum("bm,bmv->bv", rel, values)
+        n = torch.sqrt((z * z).sum(-1, keepdim=True) + eps * eps)
+        cap = cfg["tanh_norm_cap"]
+        u = cap * torch.tanh(n / cap) / n * z
+        hs.append(h_base[:, t] + lam * gate[:, t] * (u @ P["out_proj"]))
+        delta = torch.tanh(x_term[:, t, None, :] + h_term[:, t, None, :]
+                           + slot_term[None] + P["delta_bias"])
+        slots = slots + mu[None, :, None] * (delta - slots)
+        usage = cfg["usage_ema_decay"] * usage + (
+            1.0 - cfg["usage_ema_decay"]) * rel
+    return torch.stack(hs, 1), slots, usage
+
+
+def default_config(**overrides):
+    """The reference's ScreeningConfig defaults (screening.py:92-121) as a
+    dict, with overrides."""
+    cfg = dict(d_model=512, d_slot=256, d_k=64, d_v=128, n_slots=16,
+               bank_ids=(), tau_init=0.0, tanh_norm_cap=1.0,
+               lambda_screen_init=0.01, eps=1e-6, use_value_unit_norm=True,
+               use_age_mask=False, use_leaky_warmup=False, leaky_alpha=0.0,
+               leaky_gamma=8.0, mu_short_max=0.05, mu_mid_max=0.02,
+               mu_long_max=0.005, short_half_life_tokens=None,
+               mid_half_life_tokens=None, long_half_life_tokens=None,
+               usage_ema_decay=0.99, age_ref=32.0, age_sigma=8.0)
+    cfg.update(overrides)
+    return cfg

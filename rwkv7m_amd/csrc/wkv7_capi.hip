@@ -14,6 +14,7 @@
 #include <initializer_list>
 #include <string>
 
+#include "../../include/rwkv7m_screening.h"
 #include "../../include/rwkv7m_timemix.h"
 #include "../../include/rwkv7m_wkv.h"
 #include "wkv7_launch.h"
@@ -412,6 +413,85 @@ int tm_workspace(const char* fn, const TmDims& d, const float* ws,
     return tm_need(fn, {{"workspace", ws}});
 }
 
+// ---------------------------------------------------------------------------
+// Screening read path (include/rwkv7m_screening.h)
+// ---------------------------------------------------------------------------
+
+int sc_dims(const char* fn, int dtype, int64_t B, int64_t T, int64_t M,
+            int64_t a, int64_t b) {
+    const std::string f(fn);
+    if (dtype != RWKV7M_DTYPE_F32 && dtype != RWKV7M_DTYPE_BF16)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    f + ": activations must be bfloat16 or float32 (dtype=" +
+                        std::to_string(dtype) + ")");
+    if (B < 0 || T < 0 || M < 0 || a < 0 || b < 0)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT, f + ": negative dimension");
+    const int64_t lim = int64_t(1) << 20;
+    if (B > lim || T > lim || M > lim || a > lim || b > lim ||
+        B * T * (M > 0 ? M : 1) > (int64_t(1) << 31) ||
+        B * T * (M > 0 ? M : 1) * (a + b) > (int64_t(1) << 44))
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT, f + ": sizes too large");
+    return RWKV7M_OK;
+}
+
+int sc_need(const char* fn, std::initializer_list<Named> ptrs) {
+    for (const Named& x : ptrs)
+        if (x.p == nullptr)
+            return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                        std::string(fn) + ": " + x.name + " is NULL");
+    return RWKV7M_OK;
+}
+
+int sc_read_checks(const char* fn, int64_t M, int64_t dk, int64_t dv,
+                   double tau, double trim_eps, double cap, double eps,
+                   double alpha, double gamma) {
+    const std::string f(fn);
+    if (M > 64 || dk > 128 || dv > 512)
+        return fail(RWKV7M_ERR_UNSUPPORTED,
+                    f + ": supported sizes are M <= 64, dk <= 128, dv <= 512");
+    if (!std::isfinite(tau) || !(tau < 1.0) || !(tau > -1.0))
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    f + ": tau must lie in (-1, 1)");
+    if (!(trim_eps >= 0.0) || !(eps >= 0.0) || !std::isfinite(eps) ||
+        !std::isfinite(trim_eps))
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    f + ": eps must be finite and >= 0");
+    if (!(cap > 0.0) || !std::isfinite(cap))
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    f + ": cap must be finite and > 0");
+    if (!std::isfinite(alpha) || !std::isfinite(gamma))
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    f + ": leaky_alpha and leaky_gamma must be finite");
+    return RWKV7M_OK;
+}
+
+rwkv7m::ScreenReadArgs sc_read_args(int64_t B, int64_t T, int64_t M,
+                                    int64_t dk, int64_t dv, const float* q,
+                                    const void* proj, double tau,
+                                    double trim_eps, const float* age_w,
+                                    int value_unit_norm, int leaky,
+                                    double alpha, double gamma, double cap,
+                                    double eps) {
+    rwkv7m::ScreenReadArgs A{};
+    A.B = B;
+    A.T = T;
+    A.M = int(M);
+    A.dk = int(dk);
+    A.dv = int(dv);
+    A.q = q;
+    A.proj = proj;
+    A.tau = float(tau);
+    A.trim_eps = float(trim_eps);
+    A.age_w = age_w;
+    A.value_unit_norm = value_unit_norm != 0;
+    A.leaky = leaky != 0;
+    A.leaky_alpha = float(alpha);
+    A.leaky_gamma = float(gamma);
+    A.cap = float(cap);
+    A.eps = float(eps);
+    return A;
+}
+
 }  // namespace
 
 extern "C" {
@@ -645,6 +725,136 @@ int rwkv7m_timemix_wkv_output_backward(
     return hip_status("time-mix consumer backward launch",
                       rwkv7m::launch_timemix_output_backward(
                           dtype == RWKV7M_DTYPE_BF16, int(d.N), A,
+                          static_cast<hipStream_t>(stream)));
+}
+
+int rwkv7m_screen_slot_scan(int dtype, int64_t B, int64_t T, int64_t M,
+                            int64_t ds, const void* base,
+                            const float* slot_term, const float* mu,
+                            const float* slots0, void* slots_seq,
+                            float* slots_T, float* upd2, void* stream) {
+    const char* fn = "rwkv7m_screen_slot_scan";
+    g_last_error.clear();
+    RWKV7M_TRY(sc_dims(fn, dtype, B, T, M, ds, 0));
+    if (B == 0 || M == 0 || ds == 0) return RWKV7M_OK;
+    RWKV7M_TRY(sc_need(fn, {{"slot_term", slot_term}, {"mu", mu},
+                            {"slots0", slots0}, {"slots_T", slots_T}}));
+    if (T > 0)
+        RWKV7M_TRY(sc_need(fn, {{"base", base}, {"slots_seq", slots_seq},
+                                {"upd2", upd2}}));
+    rwkv7m::ScreenScanArgs A{};
+    A.B = B;
+    A.T = T;
+    A.M = M;
+    A.ds = ds;
+    A.base = base;
+    A.slot_term = slot_term;
+    A.mu = mu;
+    A.slots0 = slots0;
+    A.slots_seq = slots_seq;
+    A.slots_T = slots_T;
+    A.upd2 = upd2;
+    return hip_status("screening slot scan launch",
+                      rwkv7m::launch_screen_scan(
+                          dtype == RWKV7M_DTYPE_BF16, false, A,
+                          static_cast<hipStream_t>(stream)));
+}
+
+int rwkv7m_screen_slot_scan_backward(
+    int dtype, int64_t B, int64_t T, int64_t M, int64_t ds, const void* base,
+    const float* slot_term, const float* mu, const void* slots_seq,
+    const void* d_slots_seq, const float* d_slots_T, float* d_pre,
+    float* d_slots0, float* d_mu_part, void* stream) {
+    const char* fn = "rwkv7m_screen_slot_scan_backward";
+    g_last_error.clear();
+    RWKV7M_TRY(sc_dims(fn, dtype, B, T, M, ds, 0));
+    if (B == 0 || M == 0 || ds == 0) return RWKV7M_OK;
+    RWKV7M_TRY(sc_need(fn, {{"slot_term", slot_term}, {"mu", mu},
+                            {"d_slots0", d_slots0},
+                            {"d_mu_part", d_mu_part}}));
+    if (T > 0)
+        RWKV7M_TRY(sc_need(fn, {{"base", base}, {"slots_seq", slots_seq},
+                                {"d_slots_seq", d_slots_seq},
+                                {"d_pre", d_pre}}));
+    rwkv7m::ScreenScanArgs A{};
+    A.B = B;
+    A.T = T;
+    A.M = M;
+    A.ds = ds;
+    A.base = base;
+    A.slot_term = slot_term;
+    A.mu = mu;
+    A.slots_seq = const_cast<void*>(slots_seq);
+    A.d_slots_seq = d_slots_seq;
+    A.d_slots_T = d_slots_T;
+    A.d_pre = d_pre;
+    A.d_slots0 = d_slots0;
+    A.d_mu_part = d_mu_part;
+    return hip_status("screening slot scan backward launch",
+                      rwkv7m::launch_screen_scan(
+                          dtype == RWKV7M_DTYPE_BF16, true, A,
+                          static_cast<hipStream_t>(stream)));
+}
+
+int rwkv7m_screen_read(int dtype, int64_t B, int64_t T, int64_t M,
+                       int64_t dk, int64_t dv, const float* q,
+                       const void* proj, double tau, double trim_eps,
+                       const float* age_w, int value_unit_norm, int leaky,
+                       double leaky_alpha, double leaky_gamma, double cap,
+                       double eps, void* u, float* rel, float* z_norm,
+                       float* u_norm, void* stream) {
+    const char* fn = "rwkv7m_screen_read";
+    g_last_error.clear();
+    RWKV7M_TRY(sc_dims(fn, dtype, B, T, M, dk, dv));
+    RWKV7M_TRY(sc_read_checks(fn, M, dk, dv, tau, trim_eps, cap, eps,
+                              leaky_alpha, leaky_gamma));
+    if (B == 0 || T == 0) return RWKV7M_OK;
+    RWKV7M_TRY(sc_need(fn, {{"q", q}, {"proj", proj}, {"u", u},
+                            {"rel", rel}, {"z_norm", z_norm},
+                            {"u_norm", u_norm}}));
+    rwkv7m::ScreenReadArgs A =
+        sc_read_args(B, T, M, dk, dv, q, proj, tau, trim_eps, age_w,
+                     value_unit_norm, leaky, leaky_alpha, leaky_gamma, cap,
+                     eps);
+    A.u = u;
+    A.rel = rel;
+    A.z_norm = z_norm;
+    A.u_norm = u_norm;
+    return hip_status("screening read launch",
+                      rwkv7m::launch_screen_read(
+                          dtype == RWKV7M_DTYPE_BF16, false, A,
+                          static_cast<hipStream_t>(stream)));
+}
+
+int rwkv7m_screen_read_backward(
+    int dtype, int64_t B, int64_t T, int64_t M, int64_t dk, int64_t dv,
+    const float* q, const void* proj, double tau, double trim_eps,
+    const float* age_w, int value_unit_norm, int leaky, double leaky_alpha,
+    double leaky_gamma, double cap, double eps, const void* du,
+    const float* d_rel, float* dq, void* d_proj, float* d_tau, float* g_age,
+    void* stream) {
+    const char* fn = "rwkv7m_screen_read_backward";
+    g_last_error.clear();
+    RWKV7M_TRY(sc_dims(fn, dtype, B, T, M, dk, dv));
+    RWKV7M_TRY(sc_read_checks(fn, M, dk, dv, tau, trim_eps, cap, eps,
+                              leaky_alpha, leaky_gamma));
+    if (B == 0 || T == 0) return RWKV7M_OK;
+    RWKV7M_TRY(sc_need(fn, {{"q", q}, {"proj", proj}, {"du", du},
+                            {"dq", dq}, {"d_proj", d_proj}, {"d_tau", d_tau},
+                            {"g_age", g_age}}));
+    rwkv7m::ScreenReadArgs A =
+        sc_read_args(B, T, M, dk, dv, q, proj, tau, trim_eps, age_w,
+                     value_unit_norm, leaky, leaky_alpha, leaky_gamma, cap,
+                     eps);
+    A.du = du;
+    A.d_rel = d_rel;
+    A.dq = dq;
+    A.d_proj = d_proj;
+    A.d_tau = d_tau;
+    A.g_age = g_age;
+    return hip_status("screening read backward launch",
+                      rwkv7m::launch_screen_read(
+                          dtype == RWKV7M_DTYPE_BF16, true, A,
                           static_cast<hipStream_t>(stream)));
 }
 

@@ -104,6 +104,45 @@ struct TmOutputBwdArgs {
     float* workspace;
 };
 
+// State-level screening read path (screen_kernels.hip).  Slot recurrence:
+// base [B][T][ds] and slots_seq / d_slots_seq [B][T][M][ds] of the launch
+// dtype; everything else fp32.
+struct ScreenScanArgs {
+    int64_t B, T, M, ds;
+    const void* base;
+    const float *slot_term, *mu, *slots0;  // [M][ds], [M], [B][M][ds]
+    void* slots_seq;                        // S_t, the slots step t reads
+    float *slots_T, *upd2;                  // [B][M][ds], [B][T][M][ds/64]
+    const void* d_slots_seq;                // backward inputs
+    const float* d_slots_T;                 // may be 0
+    float *d_pre, *d_slots0, *d_mu_part;    // [B][T][M][ds], [B][M][ds] x2
+};
+
+// Per-token read: q fp32 [B][T][dk]; proj [B][T][M][dk + dv] (keys then
+// values, launch dtype); u / du [B][T][dv] (launch dtype).
+struct ScreenReadArgs {
+    int64_t B, T;
+    int M, dk, dv;
+    const float* q;
+    const void* proj;
+    float tau, trim_eps;
+    const float* age_w;  // [B][M] or 0
+    int value_unit_norm, leaky;
+    float leaky_alpha, leaky_gamma, cap, eps;
+    void* u;
+    float *rel, *z_norm, *u_norm;  // [B][T][M], [B][T], [B][T]
+    const void* du;                // backward inputs
+    const float* d_rel;            // [B][T][M] or 0
+    float* dq;
+    void* d_proj;
+    float *d_tau, *g_age;  // [B][T], [B][T][M]
+};
+
+hipError_t launch_screen_scan(bool bf16, bool backward,
+                              const ScreenScanArgs& A, hipStream_t stream);
+hipError_t launch_screen_read(bool bf16, bool backward,
+                              const ScreenReadArgs& A, hipStream_t stream);
+
 int64_t timemix_workspace_floats(int64_t rows, int64_t C);
 hipError_t launch_timemix_inputs(bool bf16, int N, const TmInputsArgs& A,
                                  hipStream_t stream);

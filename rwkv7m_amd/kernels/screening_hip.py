@@ -1,0 +1,120 @@
+"""HIP (gfx950) kernels of the state-level screening read path: ctypes
+binding of the ``rwkv7m_screen_*`` entry points of librwkv7m_wkv.so
+(include/rwkv7m_screening.h).
+
+``slot_scan`` / ``slot_scan_backward``: the slot recurrence of the
+read-only scan (src/rwkv7m/model/nnx_model.py:1087-1102) for every step at
+once.  ``read`` / ``read_backward``: the per-token read
+(nnx_model.py:1063-1086).  Tensors are torch device tensors; there is no
+CPU fallback.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import wkv_hip
+
+
+def _call(fn: str, *args) -> None:
+    lib = wkv_hip.load_library()
+    wkv_hip._check(getattr(lib, fn)(*args), fn)
+
+
+def _c(t):
+    return None if t is None else t.contiguous()
+
+
+def _f32(t):
+    return None if t is None else t.detach().to(torch.float32).contiguous()
+
+
+def slot_scan(base, slot_term, mu, slots0):
+    """base [B, T, ds] (bf16/fp32), slot_term [M, ds], mu [M], slots0
+    [B, M, ds] -> (slots_seq [B, T, M, ds] in base's dtype, slots_T
+    [B, M, ds] fp32, upd2 [B, T, M, ceil(ds/64)] fp32)."""
+    base = _c(base)
+    B, T, ds = base.shape
+    M = slot_term.shape[0]
+    dev = wkv_hip._dev([base, slots0])
+    st, mu_, s0 = _f32(slot_term), _f32(mu), _f32(slots0)
+    seq = torch.empty(B, T, M, ds, dtype=base.dtype, device=dev)
+    s_t = torch.empty(B, M, ds, dtype=torch.float32, device=dev)
+    upd2 = torch.empty(B, T, M, (ds + 63) // 64, dtype=torch.float32,
+                       device=dev)
+    P = wkv_hip._p
+    _call("rwkv7m_screen_slot_scan", wkv_hip._dtype_code(base), B, T, M, ds,
+          P(base), P(st), P(mu_), P(s0), P(seq), P(s_t), P(upd2),
+          wkv_hip._stream(dev))
+    return seq, s_t, upd2
+
+
+def slot_scan_backward(base, slot_term, mu, slots_seq, d_slots_seq,
+                       d_slots_T=None):
+    """-> (d_pre [B, T, M, ds] fp32, d_slots0 [B, M, ds], d_mu_part
+    [B, M, ds]); d base = d_pre.sum(2), d slot_term = d_pre.sum((0, 1)),
+    d mu = d_mu_part.sum((0, 2))."""
+    base, slots_seq = _c(base), _c(slots_seq)
+    d_slots_seq = _c(d_slots_seq).to(base.dtype)
+    B, T, ds = base.shape
+    M = slot_term.shape[0]
+    dev = wkv_hip._dev([base, slots_seq, d_slots_seq])
+    st, mu_ = _f32(slot_term), _f32(mu)
+    dst = _f32(d_slots_T)
+    d_pre = torch.empty(B, T, M, ds, dtype=torch.float32, device=dev)
+    d_s0 = torch.empty(B, M, ds, dtype=torch.float32, device=dev)
+    d_mu = torch.empty(B, M, ds, dtype=torch.float32, device=dev)
+    P = wkv_hip._p
+    _call("rwkv7m_screen_slot_scan_backward", wkv_hip._dtype_code(base), B,
+          T, M, ds, P(base), P(st), P(mu_), P(slots_seq), P(d_slots_seq),
+          P(dst), P(d_pre), P(d_s0), P(d_mu), wkv_hip._stream(dev))
+    return d_pre, d_s0, d_mu
+
+
+def _read_scalars(cfg, tau):
+    leaky = bool(cfg.use_leaky_warmup)
+    trim_eps = 1e-6 if leaky else float(cfg.eps)  # nnx_model.py:1071, :1075
+    return (float(tau), trim_eps, int(bool(cfg.use_value_unit_norm)),
+            int(leaky), float(cfg.leaky_alpha), float(cfg.leaky_gamma),
+            float(cfg.tanh_norm_cap), float(cfg.eps))
+
+
+def read(q, proj, tau, age_w, cfg, dv):
+    """q [B, T, dk] fp32, proj [B, T, M, dk + dv] -> (u [B, T, dv] in
+    proj's dtype, rel [B, T, M], z_norm [B, T], u_norm [B, T])."""
+    q, proj = _f32(q), _c(proj)
+    B, T, M, kv = proj.shape
+    dk = kv - dv
+    dev = wkv_hip._dev([q, proj])
+    aw = _f32(age_w)
+    u = torch.empty(B, T, dv, dtype=proj.dtype, device=dev)
+    rel = torch.empty(B, T, M, dtype=torch.float32, device=dev)
+    zn = torch.empty(B, T, dtype=torch.float32, device=dev)
+    un = torch.empty(B, T, dtype=torch.float32, device=dev)
+    P = wkv_hip._p
+    _call("rwkv7m_screen_read", wkv_hip._dtype_code(proj), B, T, M, dk, dv,
+          P(q), P(proj), *_read_scalars(cfg, tau)[:2], P(aw),
+          *_read_scalars(cfg, tau)[2:], P(u), P(rel), P(zn), P(un),
+          wkv_hip._stream(dev))
+    return u, rel, zn, un
+
+
+def read_backward(q, proj, tau, age_w, cfg, dv, du, d_rel=None):
+    """-> (dq [B, T, dk] fp32, d_proj like proj, d_tau [B, T], g_age
+    [B, T, M]) with d age_w = g_age.sum(1)."""
+    q, proj = _f32(q), _c(proj)
+    du = _c(du).to(proj.dtype)
+    B, T, M, kv = proj.shape
+    dk = kv - dv
+    dev = wkv_hip._dev([q, proj, du])
+    aw, dr = _f32(age_w), _f32(d_rel)
+    dq = torch.empty(B, T, dk, dtype=torch.float32, device=dev)
+    dproj = torch.empty_like(proj)
+    dtau = torch.empty(B, T, dtype=torch.float32, device=dev)
+    g_age = torch.empty(B, T, M, dtype=torch.float32, device=dev)
+    sc = _read_scalars(cfg, tau)
+    P = wkv_hip._p
+    _call("rwkv7m_screen_read_backward", wkv_hip._dtype_code(proj), B, T, M,
+          dk, dv, P(q), P(proj), *sc[:2], P(aw), *sc[2:], P(du), P(dr),
+          P(dq), P(dproj), P(dtau), P(g_age), wkv_hip._stream(dev))
+    return dq, dproj, dtau, g_age

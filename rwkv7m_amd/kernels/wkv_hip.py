@@ -45,7 +45,8 @@ LIB_PATH = os.path.join(_PKG_DIR, "librwkv7m_wkv.so")
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 
-# Every symbol declared in include/rwkv7m_wkv.h and include/rwkv7m_timemix.h.
+# Every symbol declared in include/rwkv7m_wkv.h, include/rwkv7m_timemix.h
+# and include/rwkv7m_screening.h.
 EXPORTED_SYMBOLS = (
     "rwkv7m_abi_version",
     "rwkv7m_last_error",
@@ -64,6 +65,10 @@ EXPORTED_SYMBOLS = (
     "rwkv7m_timemix_wkv_inputs_backward",
     "rwkv7m_timemix_wkv_output",
     "rwkv7m_timemix_wkv_output_backward",
+    "rwkv7m_screen_slot_scan",
+    "rwkv7m_screen_slot_scan_backward",
+    "rwkv7m_screen_read",
+    "rwkv7m_screen_read_backward",
 )
 
 LAYOUTS = ("tbhn", "bthn")
@@ -125,6 +130,17 @@ def load_library(path: str | None = None):
         lib.rwkv7m_timemix_wkv_output_backward.restype = i32
         lib.rwkv7m_timemix_wkv_output_backward.argtypes = (
             dims + [vp] * 8 + [f64] + [vp] * 10 + [i64, vp])
+        sdims = [i32, i64, i64, i64, i64]
+        lib.rwkv7m_screen_slot_scan.restype = i32
+        lib.rwkv7m_screen_slot_scan.argtypes = sdims + [vp] * 8
+        lib.rwkv7m_screen_slot_scan_backward.restype = i32
+        lib.rwkv7m_screen_slot_scan_backward.argtypes = sdims + [vp] * 10
+        rdims = [i32, i64, i64, i64, i64, i64, vp, vp, f64, f64, vp, i32,
+                 i32, f64, f64, f64, f64]
+        lib.rwkv7m_screen_read.restype = i32
+        lib.rwkv7m_screen_read.argtypes = rdims + [vp] * 5
+        lib.rwkv7m_screen_read_backward.restype = i32
+        lib.rwkv7m_screen_read_backward.argtypes = rdims + [vp] * 7
         if path is None:
             _lib = lib
         return lib

@@ -1,0 +1,312 @@
+"""State-level screening read path on MI355X.
+
+A torch module with the parameters and call signature of the reference's
+``NNXStateLevelScreening`` (src/rwkv7m/model/nnx_model.py:885-1160) for the
+phase the training loop runs, ``read_screening_only``
+(train/train_loop.py:82, train/train_step.py:20).
+
+The reference scans the sequence one token at a time, projecting every slot
+to keys and values at every step.  With writes disabled the slot update
+never reads the slots' keys or values, so the call reorganises into
+whole-sequence work:
+
+1. the screen LayerNorm, the query, gate and delta projections of every
+   token (library GEMMs);
+2. the slot recurrence ``S_{t+1} = S_t + mu (tanh(base_t + slot_term) -
+   S_t)`` for all steps (HIP kernel, ``rwkv7m_screen_slot_scan``);
+3. keys and values of every step's slots (one library GEMM);
+4. the per-token read -- unit norms, similarity, trim-square relevance with
+   the age weight, the value mix, ``tanh_norm`` (HIP kernel,
+   ``rwkv7m_screen_read``);
+5. the output projection and the gated residual (GEMM, elementwise).
+
+Steps 2 and 4 have HIP backward kernels; the rest is differentiated by
+torch autograd.  The write phase (``read_write``) is not implemented and
+raises.  Arithmetic follows the reference's dtypes: projections in the
+compute dtype, statistics, norms, the slots and the usage EMA in fp32.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import NamedTuple
+
+import torch
+import torch.nn.functional as F
+
+from .kernels import screening_hip
+
+_PHASE_ALIASES = {"read_only": "read_screening_only"}
+_VALID_PHASES = {"read_screening_only", "read_write"}
+
+
+def normalize_phase(phase: str) -> str:
+    """src/rwkv7m/model/screening.py:11-18."""
+    phase = _PHASE_ALIASES.get(phase, phase)
+    if phase not in _VALID_PHASES:
+        raise ValueError(
+            f"Unknown phase {phase!r}. Expected one of "
+            f"{sorted(_VALID_PHASES)} or compatibility alias 'read_only'.")
+    return phase
+
+
+@dataclass
+class ScreeningConfig:
+    """Fields and defaults of the reference's ScreeningConfig
+    (src/rwkv7m/model/screening.py:91-144)."""
+
+    d_model: int = 512
+    d_slot: int = 256
+    d_k: int = 64
+    d_v: int = 128
+    n_slots: int = 16
+    screened_layers: tuple = ()
+    bank_ids: tuple = ()
+    tau_init: float = 0.0
+    tanh_norm_cap: float = 1.0
+    lambda_screen_init: float = 0.01
+    eps: float = 1e-6
+    use_value_unit_norm: bool = True
+    use_age_mask: bool = False
+    use_bank_bias: bool = False
+    use_write_screening: bool = False
+    write_rel_floor: float = 1e-3
+    use_leaky_warmup: bool = False
+    leaky_alpha: float = 0.0
+    leaky_gamma: float = 8.0
+    mu_short_max: float = 0.05
+    mu_mid_max: float = 0.02
+    mu_long_max: float = 0.005
+    short_half_life_tokens: float | None = None
+    mid_half_life_tokens: float | None = None
+    long_half_life_tokens: float | None = None
+    usage_ema_decay: float = 0.99
+    age_ref: float = 32.0
+    age_sigma: float = 8.0
+
+    def __post_init__(self):
+        self.screened_layers = tuple(self.screened_layers)
+        self.bank_ids = tuple(self.bank_ids)
+        if self.bank_ids and len(self.bank_ids) != self.n_slots:
+            raise ValueError("bank_ids must have length n_slots when provided")
+        if [b for b in self.bank_ids if b not in (0, 1, 2)]:
+            raise ValueError("bank_ids values must be only 0, 1, or 2")
+        if self.write_rel_floor < 0.0:
+            raise ValueError("write_rel_floor must be non-negative")
+        for hl in (self.short_half_life_tokens, self.mid_half_life_tokens,
+                   self.long_half_life_tokens):
+            if hl is not None and hl <= 0.0:
+                raise ValueError("half-life values must be positive")
+
+
+class ScreenState(NamedTuple):
+    """LayerScreenState (src/rwkv7m/model/state.py:13-17)."""
+
+    slots: torch.Tensor      # [B, M, d_slot] fp32
+    ages: torch.Tensor       # [B, M]
+    usage_ema: torch.Tensor  # [B, M]
+
+
+def init_screen_state(batch_size: int, config: ScreeningConfig,
+                      device=None) -> ScreenState:
+    """state.py:24-34 for one layer: zeros."""
+    z = dict(dtype=torch.float32, device=device)
+    return ScreenState(
+        torch.zeros(batch_size, config.n_slots, config.d_slot, **z),
+        torch.zeros(batch_size, config.n_slots, **z),
+        torch.zeros(batch_size, config.n_slots, **z))
+
+
+def _theta_from_tau(tau: float) -> float:
+    p = min(max((tau + 1.0) / 2.0, 1e-4), 1.0 - 1e-4)
+    return math.log(p) - math.log1p(-p)
+
+
+class _SlotScan(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, base, slot_term, mu, slots0):
+        seq, s_t, upd2 = screening_hip.slot_scan(base, slot_term, mu, slots0)
+        ctx.save_for_backward(base, slot_term, mu, seq)
+        ctx.mark_non_differentiable(upd2)
+        return seq, s_t, upd2
+
+    @staticmethod
+    def backward(ctx, d_seq, d_s_t, _d_upd2):
+        base, slot_term, mu, seq = ctx.saved_tensors
+        if d_seq is None:
+            d_seq = torch.zeros_like(seq)
+        d_pre, d_s0, d_mu = screening_hip.slot_scan_backward(
+            base, slot_term, mu, seq, d_seq, d_s_t)
+        return (d_pre.sum(2).to(base.dtype),
+                d_pre.sum((0, 1)).to(slot_term.dtype),
+                d_mu.sum((0, 2)).to(mu.dtype), d_s0)
+
+
+class _ScreenRead(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, proj, tau, age_w, cfg, dv):
+        u, rel, zn, un = screening_hip.read(q, proj, tau, age_w, cfg, dv)
+        ctx.save_for_backward(q, proj, tau, age_w)
+        ctx.cfg, ctx.dv = cfg, dv
+        ctx.mark_non_differentiable(zn, un)
+        return u, rel, zn, un
+
+    @staticmethod
+    def backward(ctx, du, d_rel, _dzn, _dun):
+        q, proj, tau, age_w = ctx.saved_tensors
+        if du is None:
+            du = torch.zeros(*proj.shape[:2], ctx.dv, dtype=proj.dtype,
+                             device=proj.device)
+        dq, dproj, dtau, g_age = screening_hip.read_backward(
+            q, proj, tau, age_w, ctx.cfg, ctx.dv, du, d_rel)
+        d_age = g_age.sum(1) if age_w is not None else None
+        return (dq, dproj, dtau.sum().reshape(tau.shape).to(tau.dtype),
+                d_age, None, None)
+
+
+def _ema_mean_per_step(r_bar: torch.Tensor, u0: torch.Tensor, d: float,
+                       block: int = 64) -> torch.Tensor:
+    """u_t = d u_{t-1} + (1 - d) r_t for t = 0..T-1 (u_{-1} = u0), in
+    blocks of ``block`` steps with a Toeplitz matrix inside each block."""
+    T = r_bar.shape[0]
+    out = torch.empty_like(r_bar)
+    i = torch.arange(block, device=r_bar.device, dtype=r_bar.dtype)
+    expo = (i[:, None] - i[None, :])
+    w = torch.where(expo >= 0, (1.0 - d) * d ** expo.clamp(min=0),
+                    torch.zeros_like(expo))
+    carry = u0
+    for s in range(0, T, block):
+        n = min(block, T - s)
+        blk = w[:n, :n] @ r_bar[s:s + n] + carry * d ** (i[:n] + 1)
+        out[s:s + n] = blk
+        carry = blk[-1]
+    return out
+
+
+class StateLevelScreening(torch.nn.Module):
+    """NNXStateLevelScreening's parameters (nnx_model.py:885-999, linear
+    kernels in the flax ``[in, out]`` layout) and its read-only call."""
+
+    def __init__(self, config: ScreeningConfig, *, compute_dtype=None,
+                 param_dtype=torch.float32, device=None, seed: int = 0):
+        super().__init__()
+        self.config = config
+        self.compute_dtype = compute_dtype
+        C, ds, dk, dv, M = (config.d_model, config.d_slot, config.d_k,
+                            config.d_v, config.n_slots)
+        g = torch.Generator().manual_seed(seed)
+        kw = dict(dtype=param_dtype, device=device)
+
+        def lecun(fan_in, fan_out):  # flax's default linear initialiser
+            w = torch.randn(fan_in, fan_out, generator=g) / math.sqrt(fan_in)
+            return torch.nn.Parameter(w.to(**kw))
+
+        def const(shape, v):
+            return torch.nn.Parameter(torch.full(shape, float(v), **kw))
+
+        self.screen_ln_scale = const((C,), 1.0)
+        self.screen_ln_bias = const((C,), 0.0)
+        self.q_proj_r = lecun(C, dk)
+        self.k_proj_r = lecun(ds, dk)
+        self.v_proj = lecun(ds, dv)
+        self.out_proj = lecun(dv, C)
+        self.gate_kernel = lecun(C, C)
+        self.gate_bias = const((C,), 0.0)
+        self.delta_kernel = lecun(2 * C + ds, ds)
+        self.delta_bias = const((ds,), 0.0)
+        self.tau_r_raw = const((), _theta_from_tau(config.tau_init))
+        self.lambda_raw = const(
+            (), math.log(math.expm1(config.lambda_screen_init)))
+        self.slot_embed = torch.nn.Parameter(
+            (0.02 * torch.randn(M, ds, generator=g)).to(**kw))
+        self.mu_by_bank_raw = const((3,), 0.0)
+
+    def compute_mu(self) -> torch.Tensor:
+        """nnx_model.py:1002-1013."""
+        cfg = self.config
+        if len(cfg.bank_ids) != cfg.n_slots:
+            raise ValueError("bank_ids must have length n_slots")
+        raw = self.mu_by_bank_raw.float()
+        mu_max = torch.tensor([cfg.mu_short_max, cfg.mu_mid_max,
+                               cfg.mu_long_max], device=raw.device)
+        legacy = mu_max * torch.sigmoid(raw)
+        per_bank = []
+        for i, hl in enumerate((cfg.short_half_life_tokens,
+                                cfg.mid_half_life_tokens,
+                                cfg.long_half_life_tokens)):
+            per_bank.append(legacy[i] if hl is None else torch.tensor(
+                -math.expm1(-math.log(2.0) / hl), device=raw.device))
+        ids = torch.tensor(cfg.bank_ids, device=raw.device)
+        return torch.stack(per_bank)[ids]
+
+    def forward(self, x_seq, h_base_seq, state: ScreenState, *,
+                phase: str = "read_screening_only", deterministic=True):
+        """(h_seq [B, T, C], new ScreenState, stats) as
+        NNXStateLevelScreening.__call__ (nnx_model.py:1015-1160)."""
+        del deterministic
+        cfg = self.config
+        phase = normalize_phase(phase)
+        if phase == "read_write" and cfg.use_write_screening:
+            raise NotImplementedError(
+                "the read_write screening phase is not implemented on this "
+                "backend; use phase='read_screening_only'")
+        eps = cfg.eps
+        B, T, C = x_seq.shape
+        cd = self.compute_dtype or x_seq.dtype
+        x_ln = F.layer_norm(x_seq.float(), (C,), self.screen_ln_scale.float(),
+                            self.screen_ln_bias.float(), eps=1e-6).to(cd)
+        q = (x_ln @ self.q_proj_r.to(cd)).float()
+        q = q / torch.sqrt((q * q).sum(-1, keepdim=True) + eps * eps)
+        tau = 2.0 * torch.sigmoid(self.tau_r_raw.float()) - 1.0
+        lam = F.softplus(self.lambda_raw.float())
+        mu = self.compute_mu()
+        gate = torch.sigmoid(
+            (x_ln @ self.gate_kernel.to(cd) + self.gate_bias.to(cd)).float())
+        dker = self.delta_kernel.to(cd)
+        base = (x_ln @ dker[:C] + h_base_seq.to(cd) @ dker[C:2 * C]
+                + self.delta_bias.to(cd))
+        slot_term = (self.slot_embed.to(cd) @ dker[2 * C:]).float()
+        age_w = (torch.sigmoid((cfg.age_ref - state.ages.float())
+                               / (cfg.age_sigma + eps))
+                 if cfg.use_age_mask else None)
+        seq, slots_t, upd2 = _SlotScan.apply(base, slot_term, mu,
+                                             state.slots.float())
+        kv = torch.cat([self.k_proj_r, self.v_proj], dim=1).to(cd)
+        proj = seq @ kv
+        u, rel, zn, un = _ScreenRead.apply(q, proj, tau, age_w, cfg,
+                                           cfg.d_v)
+        read = (u @ self.out_proj.to(cd)).to(h_base_seq.dtype)
+        h = (h_base_seq.float() + lam * gate * read.float()).to(
+            h_base_seq.dtype)
+        d = float(cfg.usage_ema_decay)
+        w = (1.0 - d) * d ** torch.arange(T - 1, -1, -1, device=rel.device,
+                                          dtype=torch.float32)
+        usage_t = (d ** T) * state.usage_ema.float() + torch.einsum(
+            "btm,t->bm", rel, w)
+        new_state = ScreenState(slots_t.to(state.slots.dtype), state.ages,
+                                usage_t.to(state.usage_ema.dtype))
+        with torch.no_grad():
+            r = rel.detach()
+            zero = torch.zeros((), device=r.device)
+            u_bar = _ema_mean_per_step(r.mean((0, 2)).double(),
+                                       state.usage_ema.double().mean(), d)
+            stats = {
+                "rel_read_mean": r.mean(),
+                "rel_read_max": r.amax(dim=(0, 2)).mean(),
+                "active_slots_mean": (r > 1e-3).sum(-1).float().mean(),
+                "z_norm_mean": zn.mean(),
+                "u_norm_mean": un.mean(),
+                "tau_r": tau.detach(),
+                "lambda_screen": lam.detach(),
+                "rel_write_mean": zero,
+                "rel_write_effective_mean": zero,
+                "slot_update_norm_mean": upd2.sum(-1).sqrt().mean(),
+                "slot_usage_ema_mean": u_bar.mean().float(),
+                "tau_w": zero,
+            }
+        return h, new_state, stats
+
+
+__all__ = ["ScreenState", "ScreeningConfig", "StateLevelScreening",
+           "init_screen_state", "normalize_phase"]

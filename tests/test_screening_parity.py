@@ -1,0 +1,187 @@
+"""GPU parity of the screening read path (``rwkv7m_amd.screening``, HIP
+kernels ``rwkv7m_screen_*`` of include/rwkv7m_screening.h) against the
+oracle: the float64 numpy scan for the forward and statistics, float64 torch
+autograd of the same scan for every gradient (oracle/screening_oracle.py,
+restating src/rwkv7m/model/nnx_model.py:999-1160).
+
+Tolerances, normalised max error (max |got - want| / max |want|): 1e-4 for
+fp32 activations and parameters, 2e-2 for bf16 activations (compute dtype
+bf16, as the reference's presets run), per tensor.  Shapes include partial
+64-channel waves (d_slot = 80, d_v = 80), d_k < 64, several slot counts,
+every option of the read (age mask, leaky warm-up, values not normalised,
+half-life rates) and the 0.3B preset's sizes.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import screening_oracle as so
+
+pytestmark = pytest.mark.gpu
+
+OPTIONS = [dict(), dict(use_age_mask=True),
+           dict(use_leaky_warmup=True, leaky_alpha=0.3),
+           dict(use_value_unit_norm=False),
+           dict(short_half_life_tokens=4.0, long_half_life_tokens=50.0)]
+PNAME = {"ln_scale": "screen_ln_scale", "ln_bias": "screen_ln_bias"}
+
+
+def _case(B, T, C, ds, dk, dv, M, seed, **opt):
+    rng = np.random.default_rng(seed)
+    cfg = so.default_config(d_model=C, d_slot=ds, d_k=dk, d_v=dv, n_slots=M,
+                            bank_ids=tuple(int(i) for i in
+                                           rng.integers(0, 3, M)), **opt)
+    P = {"ln_scale": 1.0 + 0.1 * rng.normal(size=C),
+         "ln_bias": 0.1 * rng.normal(size=C),
+         "q_proj_r": rng.normal(size=(C, dk)) / np.sqrt(C),
+         "k_proj_r": rng.normal(size=(ds, dk)) / np.sqrt(ds),
+         "v_proj": rng.normal(size=(ds, dv)) / np.sqrt(ds),
+         "out_proj": rng.normal(size=(dv, C)) / np.sqrt(dv),
+         "gate_kernel": rng.normal(size=(C, C)) / np.sqrt(C),
+         "gate_bias": 0.1 * rng.normal(size=C),
+         "delta_kernel": rng.normal(size=(2 * C + ds, ds)) / np.sqrt(2 * C),
+         "delta_bias": 0.1 * rng.normal(size=ds),
+         "tau_r_raw": np.array(-1.0), "lambda_raw": np.array(0.3),
+         "slot_embed": 0.5 * rng.normal(size=(M, ds)),
+         "mu_by_bank_raw": rng.normal(size=3)}
+    x = rng.normal(size=(B, T, C))
+    h = rng.normal(size=(B, T, C))
+    slots = 0.5 * rng.normal(size=(B, M, ds))
+    ages = rng.uniform(0, 60, size=(B, M))
+    usage = rng.uniform(0, 0.2, size=(B, M))
+    return x, h, slots, ages, usage, P, cfg
+
+
+def _module(P, cfg, dtype):
+    from rwkv7m_amd.screening import ScreeningConfig, StateLevelScreening
+    mod = StateLevelScreening(ScreeningConfig(**cfg), compute_dtype=dtype,
+                              device="cuda")
+    with torch.no_grad():
+        for k, v in P.items():
+            getattr(mod, PNAME.get(k, k)).copy_(torch.tensor(v))
+    return mod
+
+
+def _rnd(a, dtype):
+    """Values as the device holds them (bf16 activations are rounded)."""
+    return torch.tensor(a, dtype=torch.float32).to(dtype).double().numpy()
+
+
+def _err(got, want):
+    return oracle.normalized_max_error(
+        got.detach().double().cpu().numpy(), np.asarray(want, np.float64))
+
+
+def _run(case, dtype, grad=False):
+    from rwkv7m_amd.screening import ScreenState
+    x, h, slots, ages, usage, P, cfg = case
+    mod = _module(P, cfg, dtype)
+    xd = torch.tensor(x, dtype=torch.float32).to(dtype).cuda()
+    hd = torch.tensor(h, dtype=torch.float32).to(dtype).cuda()
+    st = ScreenState(*(torch.tensor(a, dtype=torch.float32).cuda()
+                       for a in (slots, ages, usage)))
+    if grad:
+        xd.requires_grad_(True)
+        hd.requires_grad_(True)
+        st = ScreenState(*(t.requires_grad_(True) for t in st))
+    out, new, stats = mod(xd, hd, st)
+    return mod, xd, hd, st, out, new, stats
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("opt", OPTIONS, ids=str)
+def test_forward_matches_oracle(hip_lib, opt, dtype):
+    case = _case(2, 37, 64, 80, 32, 80, 5, seed=len(str(opt)), **opt)
+    name = f"screening fwd {opt} {dtype}"
+    print("case:", name, flush=True)
+    _, _, _, _, out, new, stats = _run(case, dtype)
+    torch.cuda.synchronize()
+    x, h, slots, ages, usage, P, cfg = case
+    eh, (es, _, eu), est = so.read_forward(_rnd(x, dtype), _rnd(h, dtype),
+                                           slots, ages, usage, P, cfg)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    for n, g, w in (("h", out, eh), ("slots_T", new.slots, es),
+                    ("usage_T", new.usage_ema, eu)):
+        e = _err(g, w)
+        assert e <= tol, f"{name} {n}: {e:.3e} > {tol}"
+    for k in so.STAT_NAMES:
+        g, w = float(stats[k]), est[k]
+        assert abs(g - w) <= tol * max(1.0, abs(w)), f"{name} stat {k}"
+    assert torch.equal(new.ages, torch.tensor(ages, dtype=torch.float32,
+                                              device="cuda"))
+
+
+@pytest.mark.parametrize("opt", OPTIONS, ids=str)
+def test_backward_matches_autograd_oracle(hip_lib, opt):
+    case = _case(2, 23, 64, 80, 32, 80, 5, seed=7 + len(str(opt)), **opt)
+    name = f"screening bwd {opt}"
+    print("case:", name, flush=True)
+    mod, xd, hd, st, out, new, _ = _run(case, torch.float32, grad=True)
+    x, h, slots, ages, usage, P, cfg = case
+    rng = np.random.default_rng(3)
+    cot_h = rng.normal(size=x.shape)
+    cot_s = rng.normal(size=slots.shape)
+    cot_u = rng.normal(size=usage.shape)
+    loss = ((out * torch.tensor(cot_h, dtype=torch.float32,
+                                device="cuda")).sum()
+            + (new.slots * torch.tensor(cot_s, dtype=torch.float32,
+                                        device="cuda")).sum()
+            + (new.usage_ema * torch.tensor(cot_u, dtype=torch.float32,
+                                            device="cuda")).sum())
+    loss.backward()
+    torch.cuda.synchronize()
+    arrays = dict(x=x, h=h, slots=slots, ages=ages, usage=usage, **P)
+    tin = {k: torch.tensor(np.asarray(v, np.float64), requires_grad=True)
+           for k, v in arrays.items()}
+    ht, s_t, u_t = so.read_forward_torch(
+        tin["x"], tin["h"], tin["slots"], tin["ages"], tin["usage"],
+        {k: tin[k] for k in P}, cfg)
+    ref_loss = ((ht * torch.tensor(cot_h)).sum()
+                + (s_t * torch.tensor(cot_s)).sum()
+                + (u_t * torch.tensor(cot_u)).sum())
+    names = list(arrays)
+    want = dict(zip(names, torch.autograd.grad(ref_loss,
+                                               [tin[n] for n in names],
+                                               allow_unused=True)))
+    got = {"x": xd.grad, "h": hd.grad, "slots": st.slots.grad,
+           "ages": st.ages.grad, "usage": st.usage_ema.grad}
+    got.update({k: getattr(mod, PNAME.get(k, k)).grad for k in P})
+    for n in names:
+        w = want[n]
+        if w is None or not np.any(w.numpy()):
+            assert got[n] is None or not torch.any(got[n]), f"{name} d{n}"
+            continue
+        assert got[n] is not None, f"{name} d{n} missing"
+        e = _err(got[n], w.numpy())
+        assert e <= 1e-4, f"{name} d{n}: {e:.3e}"
+
+
+def test_preset_sizes_forward(hip_lib):
+    # 0.3B preset: d_model 1024, d_slot 256, d_k 64, d_v 128, 16 slots
+    case = _case(2, 48, 1024, 256, 64, 128, 16, seed=11)
+    print("case: screening preset 0.3b bf16", flush=True)
+    _, _, _, _, out, new, _ = _run(case, torch.bfloat16)
+    torch.cuda.synchronize()
+    x, h, slots, ages, usage, P, cfg = case
+    eh, (es, _, eu), _ = so.read_forward(_rnd(x, torch.bfloat16),
+                                         _rnd(h, torch.bfloat16), slots,
+                                         ages, usage, P, cfg)
+    for n, g, w in (("h", out, eh), ("slots_T", new.slots, es),
+                    ("usage_T", new.usage_ema, eu)):
+        assert _err(g, w) <= 2e-2, n
+
+
+def test_phases(hip_lib):
+    from rwkv7m_amd.screening import normalize_phase
+    case = _case(1, 4, 64, 64, 32, 64, 3, seed=2, use_write_screening=False)
+    mod, xd, hd, st, out, _, _ = _run(case, torch.float32)
+    out2, _, _ = mod(xd, hd, st, phase="read_only")
+    assert torch.equal(out, out2)
+    assert normalize_phase("read_only") == "read_screening_only"
+    with pytest.raises(ValueError, match="Unknown phase"):
+        mod(xd, hd, st, phase="write_only")
+    mod.config.use_write_screening = True
+    with pytest.raises(NotImplementedError, match="read_write"):
+        mod(xd, hd, st, phase="read_write")

@@ -25,7 +25,10 @@
  * proj [B][T][M][dk + dv] (keys then values) and u [B][T][dv] of `dtype`;
  * rel [B][T][M], z_norm and u_norm [B][T], age_w [B][M] fp32.
  * Limits: M <= 64, dk <= 128, dv <= 512.  Calls only enqueue work on
- * `stream`, never allocate, never synchronise.
+ * `stream`, never allocate, never synchronise.  The slot scan runs in
+ * chunks of 32 steps (each chunk's contribution from a zero start, a serial
+ * pass over the chunk ends, then every chunk from its true start), with a
+ * caller-provided fp32 workspace.
  */
 #ifndef RWKV7M_SCREENING_H
 #define RWKV7M_SCREENING_H
@@ -38,6 +41,12 @@
 extern "C" {
 #endif
 
+/* Floats of fp32 device workspace each slot-scan call needs (-1 for
+ * invalid sizes).  No counterpart in the reference (XLA allocates its scan
+ * buffers itself). */
+int64_t rwkv7m_screen_slot_scan_workspace_floats(int64_t B, int64_t T,
+                                                 int64_t M, int64_t ds);
+
 /* Slots read at each step (S_t, t = 0..T-1, rounded to dtype), the final
  * slots S_T, and upd2[b][t][m][g] = sum over channels 64g..64g+63 of
  * (mu (delta - S_t))^2 (for the slot_update_norm statistic).  Replaces the
@@ -46,7 +55,8 @@ int rwkv7m_screen_slot_scan(int dtype, int64_t B, int64_t T, int64_t M,
                             int64_t ds, const void *base,
                             const float *slot_term, const float *mu,
                             const float *slots0, void *slots_seq,
-                            float *slots_T, float *upd2, void *stream);
+                            float *slots_T, float *upd2, float *workspace,
+                            int64_t workspace_floats, void *stream);
 
 /* Adjoint of rwkv7m_screen_slot_scan: from the cotangents of slots_seq and
  * of slots_T (NULL = zero) to d_pre[b][t][m][d] (the cotangent of the tanh
@@ -56,7 +66,8 @@ int rwkv7m_screen_slot_scan_backward(
     int dtype, int64_t B, int64_t T, int64_t M, int64_t ds, const void *base,
     const float *slot_term, const float *mu, const void *slots_seq,
     const void *d_slots_seq, const float *d_slots_T, float *d_pre,
-    float *d_slots0, float *d_mu_part, void *stream);
+    float *d_slots0, float *d_mu_part, float *workspace,
+    int64_t workspace_floats, void *stream);
 
 /* Per-token read.  leaky = 0: rel = trim_square(sim, tau, trim_eps) * age;
  * leaky = 1: ((1 - alpha) trim_square + alpha sigmoid(gamma (sim - tau)))

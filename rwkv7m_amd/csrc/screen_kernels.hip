@@ -12,13 +12,13 @@
 // library GEMM for keys and values of every (b, t, m)) between the two
 // kernels below.
 //
-// screen_scan_fwd:  one lane per (b, m, d) walks t = 0 .. T-1 and writes
-//   S_t (the slots step t reads, rounded to the compute dtype as the
-//   reference casts them for its projections), the per-step squared update
-//   norm |mu (delta - S)|^2 summed over each 64-channel wave, and S_T.
-//   delta is rounded to the compute dtype, as the reference materialises it.
-// screen_scan_bwd:  the reverse walk: G_t = (1 - mu) G_{t+1} + dS_t,
-//   d pre_t = mu G_{t+1} (1 - tanh^2), d mu += G_{t+1} (delta_t - S_t).
+// slot scan, forward: S_t for every step (the slots step t reads, rounded
+//   to the compute dtype as the reference casts them for its projections),
+//   the per-step squared update norm |mu (delta - S)|^2 summed over each
+//   64-channel group, and S_T.  delta is rounded to the compute dtype, as
+//   the reference materialises it.
+// slot scan, backward: G_t = (1 - mu) G_{t+1} + dS_t, d pre_t = mu G_{t+1}
+//   (1 - tanh^2), d mu += G_{t+1} (delta_t - S_t).
 // screen_read_fwd:  one wave per token: keys and values unit-normalised,
 //   sim = q . k, relevance = trim_square (or the leaky blend) times the age
 //   weight, z = sum_m rel_m v_m, u = tanh_norm(z).
@@ -37,7 +37,8 @@
 namespace rwkv7m {
 namespace {
 
-constexpr int kKJ = 2;  // key channels per lane (d_k <= 128)
+constexpr int kScreenChunk = 32;  // steps per chunk of the slot scan
+constexpr int kKJ = 2;            // key channels per lane (d_k <= 128)
 constexpr int kVJ = 8;  // value channels per lane (d_v <= 512)
 
 __device__ __forceinline__ float wave_sum(float x) {
@@ -68,81 +69,222 @@ __device__ __forceinline__ float sigm(float x) {
 // Slot recurrence
 // ---------------------------------------------------------------------------
 
-// Wave -> (b, m, 64-channel group); lane -> channel.
+// The recurrence is affine with a constant rate per slot, so it runs in
+// chunks of kScreenChunk steps, three launches per direction:
+//   local:  each chunk from a zero start (forward: the chunk's end value;
+//           backward: the cotangent it adds at the chunk's start);
+//   carry:  one lane per (b, m, d) walks the chunks, S_end = a^n S_start +
+//           local (a = 1 - mu, n = the chunk's steps), storing every chunk's
+//           true start (and S_T / d S_0);
+//   emit:   each chunk again from its true start, writing the per-step
+//           outputs.
+// Workspace (fp32): two (forward) or three (backward) arrays of
+// [chunks][B][M][ds].  Every chunk of every (b, m, 64 channels) is one
+// wave, so the grid has T / kScreenChunk times more waves than one walk.
+
+// Wave -> (chunk, b, m, 64-channel group); lane -> channel.
 struct ScanLane {
-    int64_t b;
+    int64_t b, c, bmd;  // bmd: the lane's (b, m, d) index in [B][M][ds]
     int m, dw, d, ndw;
+    int64_t t0, t1;  // the chunk's steps
     bool valid, act;
 };
 
 __device__ __forceinline__ ScanLane scan_lane(const ScreenScanArgs& A) {
     ScanLane s;
-    const int64_t w = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+    int64_t w = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
     const int lane = threadIdx.x & 63;
     s.ndw = int((A.ds + 63) / 64);
     s.dw = int(w % s.ndw);
-    const int64_t bm = w / s.ndw;
-    s.m = int(bm % A.M);
-    s.b = bm / A.M;
-    s.valid = s.b < A.B;
+    w /= s.ndw;
+    s.m = int(w % A.M);
+    w /= A.M;
+    s.b = w % A.B;
+    s.c = w / A.B;
+    const int64_t nc = (A.T + kScreenChunk - 1) / kScreenChunk;
+    s.valid = s.c < nc;
     s.d = s.dw * 64 + lane;
     s.act = s.valid && s.d < A.ds;
+    s.bmd = (s.b * A.M + s.m) * A.ds + s.d;
+    s.t0 = s.c * kScreenChunk;
+    s.t1 = s.t0 + kScreenChunk < A.T ? s.t0 + kScreenChunk : A.T;
     return s;
 }
 
+__device__ __forceinline__ int64_t n_bmd(const ScreenScanArgs& A) {
+    return A.B * A.M * A.ds;
+}
+
+__device__ __forceinline__ int64_t n_chunks(const ScreenScanArgs& A) {
+    return (A.T + kScreenChunk - 1) / kScreenChunk;
+}
+
+// forward, local: the chunk's end value from a zero start
 template <typename E>
-__global__ __launch_bounds__(256) void screen_scan_fwd_kernel(
+__global__ __launch_bounds__(256) void scan_fwd_local_kernel(
+    ScreenScanArgs A) {
+    const ScanLane s = scan_lane(A);
+    if (!s.act) return;
+    const E* bp = static_cast<const E*>(A.base) + s.b * A.T * A.ds + s.d;
+    const float st = A.slot_term[int64_t(s.m) * A.ds + s.d];
+    const float mu = A.mu[s.m];
+    float bv[kScreenChunk];
+#pragma unroll
+    for (int u = 0; u < kScreenChunk; ++u)
+        bv[u] = s.t0 + u < s.t1 ? ld1(bp + (s.t0 + u) * A.ds) : 0.f;
+    float S = 0.f;
+#pragma unroll
+    for (int u = 0; u < kScreenChunk; ++u)
+        if (s.t0 + u < s.t1) S += mu * (rnd(tanhf(bv[u] + st), bp) - S);
+    A.workspace[s.c * n_bmd(A) + s.bmd] = S;
+}
+
+// forward, carry: every chunk's start; S_T
+__global__ __launch_bounds__(256) void scan_fwd_carry_kernel(
+    ScreenScanArgs A) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t n = n_bmd(A);
+    if (i >= n) return;
+    const float a = 1.f - A.mu[int((i / A.ds) % A.M)];
+    const int64_t nc = n_chunks(A);
+    const float* loc = A.workspace;
+    float* start = A.workspace + nc * n;
+    float S = A.slots0[i];
+    for (int64_t c = 0; c < nc; ++c) {
+        start[c * n + i] = S;
+        const int64_t len = (c + 1) * kScreenChunk < A.T
+                                ? kScreenChunk
+                                : A.T - c * kScreenChunk;
+        S = powf(a, float(len)) * S + loc[c * n + i];
+    }
+    A.slots_T[i] = S;
+}
+
+// forward, emit: S_t for every step of the chunk and the update norms
+template <typename E>
+__global__ __launch_bounds__(256) void scan_fwd_emit_kernel(
     ScreenScanArgs A) {
     const ScanLane s = scan_lane(A);
     if (!s.valid) return;
-    const E* base = static_cast<const E*>(A.base);
-    E* seq = static_cast<E*>(A.slots_seq);
-    const int64_t M = A.M, ds = A.ds, T = A.T;
-    const int64_t sbm = (s.b * M + s.m) * ds + s.d;
-    float S = s.act ? A.slots0[sbm] : 0.f;
+    const int64_t M = A.M, ds = A.ds, T = A.T, n = n_bmd(A);
+    const E* bp = static_cast<const E*>(A.base) + s.b * T * ds + s.d;
+    E* op = static_cast<E*>(A.slots_seq) + (s.b * T * M + s.m) * ds + s.d;
+    float* up = A.upd2 + (s.b * T * M + s.m) * s.ndw + s.dw;
     const float st = s.act ? A.slot_term[int64_t(s.m) * ds + s.d] : 0.f;
     const float mu = A.mu[s.m];
-    const E* bp = base + s.b * T * ds + s.d;
-    E* op = seq + (s.b * T * M + s.m) * ds + s.d;
-    float* up = A.upd2 + (s.b * T * M + s.m) * s.ndw + s.dw;
-    for (int64_t t = 0; t < T; ++t) {
-        const float pre = (s.act ? ld1(bp + t * ds) : 0.f) + st;
-        const float delta = rnd(tanhf(pre), bp);
-        if (s.act) st1(op + t * M * ds, S);
-        const float u = mu * (delta - S);
-        const float u2 = wave_sum(s.act ? u * u : 0.f);
-        if ((threadIdx.x & 63) == 0) up[t * M * s.ndw] = u2;
-        S += u;
+    float bv[kScreenChunk], u2[kScreenChunk];
+#pragma unroll
+    for (int u = 0; u < kScreenChunk; ++u)
+        bv[u] = s.act && s.t0 + u < s.t1 ? ld1(bp + (s.t0 + u) * ds) : 0.f;
+    float S = s.act ? A.workspace[(n_chunks(A) + s.c) * n + s.bmd] : 0.f;
+#pragma unroll
+    for (int u = 0; u < kScreenChunk; ++u) {
+        const int64_t t = s.t0 + u;
+        const float delta = rnd(tanhf(bv[u] + st), bp);
+        if (s.act && t < s.t1) st1(op + t * M * ds, S);
+        const float du = mu * (delta - S);
+        u2[u] = s.act ? du * du : 0.f;
+        S += du;
     }
-    if (s.act) A.slots_T[sbm] = S;
+#pragma unroll
+    for (int u = 0; u < kScreenChunk; ++u) u2[u] = wave_sum(u2[u]);
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int u = 0; u < kScreenChunk; ++u)
+            if (s.t0 + u < s.t1) up[(s.t0 + u) * M * s.ndw] = u2[u];
+    }
 }
 
+// backward, local: the cotangent a chunk adds at its start, from zero at
+// its end: sum over its steps of a^(t - t0) dS_t
 template <typename E>
-__global__ __launch_bounds__(256) void screen_scan_bwd_kernel(
+__global__ __launch_bounds__(256) void scan_bwd_local_kernel(
     ScreenScanArgs A) {
     const ScanLane s = scan_lane(A);
-    if (!s.valid || !s.act) return;
-    const E* base = static_cast<const E*>(A.base);
-    const E* seq = static_cast<const E*>(A.slots_seq);
-    const E* dseq = static_cast<const E*>(A.d_slots_seq);
+    if (!s.act) return;
     const int64_t M = A.M, ds = A.ds, T = A.T;
-    const int64_t sbm = (s.b * M + s.m) * ds + s.d;
-    float G = A.d_slots_T ? A.d_slots_T[sbm] : 0.f;
+    const E* dp =
+        static_cast<const E*>(A.d_slots_seq) + (s.b * T * M + s.m) * ds + s.d;
+    const float a = 1.f - A.mu[s.m];
+    float dv[kScreenChunk];
+#pragma unroll
+    for (int u = 0; u < kScreenChunk; ++u)
+        dv[u] = s.t0 + u < s.t1 ? ld1(dp + (s.t0 + u) * M * ds) : 0.f;
+    float G = 0.f;
+#pragma unroll
+    for (int u = kScreenChunk - 1; u >= 0; --u) G = a * G + dv[u];
+    A.workspace[s.c * n_bmd(A) + s.bmd] = G;
+}
+
+// backward, carry: the cotangent of S at every chunk's end; d S_0
+__global__ __launch_bounds__(256) void scan_bwd_carry_kernel(
+    ScreenScanArgs A) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t n = n_bmd(A);
+    if (i >= n) return;
+    const float a = 1.f - A.mu[int((i / A.ds) % A.M)];
+    const int64_t nc = n_chunks(A);
+    const float* loc = A.workspace;
+    float* end = A.workspace + nc * n;
+    float G = A.d_slots_T ? A.d_slots_T[i] : 0.f;
+    for (int64_t c = nc - 1; c >= 0; --c) {
+        end[c * n + i] = G;
+        const int64_t len = (c + 1) * kScreenChunk < A.T
+                                ? kScreenChunk
+                                : A.T - c * kScreenChunk;
+        G = powf(a, float(len)) * G + loc[c * n + i];
+    }
+    A.d_slots0[i] = G;
+}
+
+// backward, emit: d pre_t and the chunk's part of d mu
+template <typename E>
+__global__ __launch_bounds__(256) void scan_bwd_emit_kernel(
+    ScreenScanArgs A) {
+    const ScanLane s = scan_lane(A);
+    if (!s.act) return;
+    const int64_t M = A.M, ds = A.ds, T = A.T, n = n_bmd(A);
+    const E* bp = static_cast<const E*>(A.base) + s.b * T * ds + s.d;
+    const int64_t o0 = (s.b * T * M + s.m) * ds + s.d;
+    const E* sp = static_cast<const E*>(A.slots_seq) + o0;
+    const E* dp = static_cast<const E*>(A.d_slots_seq) + o0;
+    float* pp = A.d_pre + o0;
     const float st = A.slot_term[int64_t(s.m) * ds + s.d];
     const float mu = A.mu[s.m];
-    const E* bp = base + s.b * T * ds + s.d;
-    const int64_t o0 = (s.b * T * M + s.m) * ds + s.d;
-    float dmu = 0.f;
-    for (int64_t t = T - 1; t >= 0; --t) {
-        const int64_t o = o0 + t * M * ds;
-        const float th = tanhf(ld1(bp + t * ds) + st);
-        const float delta = rnd(th, bp);
-        dmu += G * (delta - ld1(seq + o));
-        A.d_pre[o] = mu * G * (1.f - th * th);
-        G = G * (1.f - mu) + ld1(dseq + o);
+    float bv[kScreenChunk], sv[kScreenChunk], dv[kScreenChunk];
+#pragma unroll
+    for (int u = 0; u < kScreenChunk; ++u) {
+        const bool in = s.t0 + u < s.t1;
+        const int64_t o = (s.t0 + u) * M * ds;
+        bv[u] = in ? ld1(bp + (s.t0 + u) * ds) : 0.f;
+        sv[u] = in ? ld1(sp + o) : 0.f;
+        dv[u] = in ? ld1(dp + o) : 0.f;
     }
-    A.d_slots0[sbm] = G;
-    A.d_mu_part[sbm] = dmu;
+    float G = A.workspace[(n_chunks(A) + s.c) * n + s.bmd];
+    float dmu = 0.f;
+#pragma unroll
+    for (int u = kScreenChunk - 1; u >= 0; --u) {
+        if (s.t0 + u >= s.t1) continue;
+        const float th = tanhf(bv[u] + st);
+        const float delta = rnd(th, bp);
+        dmu += G * (delta - sv[u]);
+        pp[(s.t0 + u) * M * ds] = mu * G * (1.f - th * th);
+        G = (1.f - mu) * G + dv[u];
+    }
+    A.workspace[(2 * n_chunks(A) + s.c) * n + s.bmd] = dmu;
+}
+
+// backward: d mu per (b, m, d), the chunks added in chunk order
+__global__ __launch_bounds__(256) void scan_bwd_dmu_kernel(
+    ScreenScanArgs A) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t n = n_bmd(A);
+    if (i >= n) return;
+    const int64_t nc = n_chunks(A);
+    const float* part = A.workspace + 2 * nc * n;
+    float s = 0.f;
+    for (int64_t c = 0; c < nc; ++c) s += part[c * n + i];
+    A.d_mu_part[i] = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -409,26 +551,37 @@ unsigned blocks_for_waves(int64_t waves) {
 
 }  // namespace
 
+int64_t screen_scan_workspace_floats(int64_t B, int64_t T, int64_t M,
+                                     int64_t ds) {
+    const int64_t nc = (T + kScreenChunk - 1) / kScreenChunk;
+    return 3 * (nc > 0 ? nc : 1) * B * M * ds;
+}
+
 hipError_t launch_screen_scan(bool bf16, bool backward,
                               const ScreenScanArgs& A, hipStream_t stream) {
-    const int64_t waves = A.B * A.M * ((A.ds + 63) / 64);
-    if (waves == 0) return hipSuccess;
-    const dim3 grid(blocks_for_waves(waves)), block(256);
+    const int64_t n = A.B * A.M * A.ds;
+    if (n == 0) return hipSuccess;
+    const int64_t nc = (A.T + kScreenChunk - 1) / kScreenChunk;
+    const dim3 block(256), grid_n(unsigned((n + 255) / 256));
+    const dim3 grid_c(blocks_for_waves(nc * A.B * A.M * ((A.ds + 63) / 64)));
+#define RWKV7M_SC(K)                                                      \
+    do {                                                                  \
+        if (bf16)                                                         \
+            hipLaunchKernelGGL(K<bf16_t>, grid_c, block, 0, stream, A);   \
+        else                                                              \
+            hipLaunchKernelGGL(K<float>, grid_c, block, 0, stream, A);    \
+    } while (0)
     if (!backward) {
-        if (bf16)
-            hipLaunchKernelGGL(screen_scan_fwd_kernel<bf16_t>, grid, block, 0,
-                               stream, A);
-        else
-            hipLaunchKernelGGL(screen_scan_fwd_kernel<float>, grid, block, 0,
-                               stream, A);
+        if (nc > 0) RWKV7M_SC(scan_fwd_local_kernel);
+        hipLaunchKernelGGL(scan_fwd_carry_kernel, grid_n, block, 0, stream, A);
+        if (nc > 0) RWKV7M_SC(scan_fwd_emit_kernel);
     } else {
-        if (bf16)
-            hipLaunchKernelGGL(screen_scan_bwd_kernel<bf16_t>, grid, block, 0,
-                               stream, A);
-        else
-            hipLaunchKernelGGL(screen_scan_bwd_kernel<float>, grid, block, 0,
-                               stream, A);
+        if (nc > 0) RWKV7M_SC(scan_bwd_local_kernel);
+        hipLaunchKernelGGL(scan_bwd_carry_kernel, grid_n, block, 0, stream, A);
+        if (nc > 0) RWKV7M_SC(scan_bwd_emit_kernel);
+        hipLaunchKernelGGL(scan_bwd_dmu_kernel, grid_n, block, 0, stream, A);
     }
+#undef RWKV7M_SC
     return hipGetLastError();
 }
 

@@ -442,6 +442,18 @@ int sc_need(const char* fn, std::initializer_list<Named> ptrs) {
     return RWKV7M_OK;
 }
 
+int sc_workspace(const char* fn, int64_t B, int64_t T, int64_t M,
+                 int64_t ds, int64_t have) {
+    const int64_t need_floats =
+        rwkv7m::screen_scan_workspace_floats(B, T, M, ds);
+    if (have < need_floats)
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": workspace holds " +
+                        std::to_string(have) + " floats, needs " +
+                        std::to_string(need_floats));
+    return RWKV7M_OK;
+}
+
 int sc_read_checks(const char* fn, int64_t M, int64_t dk, int64_t dv,
                    double tau, double trim_eps, double cap, double eps,
                    double alpha, double gamma) {
@@ -728,17 +740,30 @@ int rwkv7m_timemix_wkv_output_backward(
                           static_cast<hipStream_t>(stream)));
 }
 
+int64_t rwkv7m_screen_slot_scan_workspace_floats(int64_t B, int64_t T,
+                                                 int64_t M, int64_t ds) {
+    const std::string saved = g_last_error;
+    const int rc = sc_dims("rwkv7m_screen_slot_scan_workspace_floats",
+                           RWKV7M_DTYPE_F32, B, T, M, ds, 0);
+    g_last_error = saved;
+    if (rc != RWKV7M_OK) return -1;
+    return rwkv7m::screen_scan_workspace_floats(B, T, M, ds);
+}
+
 int rwkv7m_screen_slot_scan(int dtype, int64_t B, int64_t T, int64_t M,
                             int64_t ds, const void* base,
                             const float* slot_term, const float* mu,
                             const float* slots0, void* slots_seq,
-                            float* slots_T, float* upd2, void* stream) {
+                            float* slots_T, float* upd2, float* workspace,
+                            int64_t workspace_floats, void* stream) {
     const char* fn = "rwkv7m_screen_slot_scan";
     g_last_error.clear();
     RWKV7M_TRY(sc_dims(fn, dtype, B, T, M, ds, 0));
     if (B == 0 || M == 0 || ds == 0) return RWKV7M_OK;
     RWKV7M_TRY(sc_need(fn, {{"slot_term", slot_term}, {"mu", mu},
-                            {"slots0", slots0}, {"slots_T", slots_T}}));
+                            {"slots0", slots0}, {"slots_T", slots_T},
+                            {"workspace", workspace}}));
+    RWKV7M_TRY(sc_workspace(fn, B, T, M, ds, workspace_floats));
     if (T > 0)
         RWKV7M_TRY(sc_need(fn, {{"base", base}, {"slots_seq", slots_seq},
                                 {"upd2", upd2}}));
@@ -754,6 +779,7 @@ int rwkv7m_screen_slot_scan(int dtype, int64_t B, int64_t T, int64_t M,
     A.slots_seq = slots_seq;
     A.slots_T = slots_T;
     A.upd2 = upd2;
+    A.workspace = workspace;
     return hip_status("screening slot scan launch",
                       rwkv7m::launch_screen_scan(
                           dtype == RWKV7M_DTYPE_BF16, false, A,
@@ -764,14 +790,17 @@ int rwkv7m_screen_slot_scan_backward(
     int dtype, int64_t B, int64_t T, int64_t M, int64_t ds, const void* base,
     const float* slot_term, const float* mu, const void* slots_seq,
     const void* d_slots_seq, const float* d_slots_T, float* d_pre,
-    float* d_slots0, float* d_mu_part, void* stream) {
+    float* d_slots0, float* d_mu_part, float* workspace,
+    int64_t workspace_floats, void* stream) {
     const char* fn = "rwkv7m_screen_slot_scan_backward";
     g_last_error.clear();
     RWKV7M_TRY(sc_dims(fn, dtype, B, T, M, ds, 0));
     if (B == 0 || M == 0 || ds == 0) return RWKV7M_OK;
     RWKV7M_TRY(sc_need(fn, {{"slot_term", slot_term}, {"mu", mu},
                             {"d_slots0", d_slots0},
-                            {"d_mu_part", d_mu_part}}));
+                            {"d_mu_part", d_mu_part},
+                            {"workspace", workspace}}));
+    RWKV7M_TRY(sc_workspace(fn, B, T, M, ds, workspace_floats));
     if (T > 0)
         RWKV7M_TRY(sc_need(fn, {{"base", base}, {"slots_seq", slots_seq},
                                 {"d_slots_seq", d_slots_seq},
@@ -790,6 +819,7 @@ int rwkv7m_screen_slot_scan_backward(
     A.d_pre = d_pre;
     A.d_slots0 = d_slots0;
     A.d_mu_part = d_mu_part;
+    A.workspace = workspace;
     return hip_status("screening slot scan backward launch",
                       rwkv7m::launch_screen_scan(
                           dtype == RWKV7M_DTYPE_BF16, true, A,

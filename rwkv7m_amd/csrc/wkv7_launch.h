@@ -116,7 +116,11 @@ struct ScreenScanArgs {
     const void* d_slots_seq;                // backward inputs
     const float* d_slots_T;                 // may be 0
     float *d_pre, *d_slots0, *d_mu_part;    // [B][T][M][ds], [B][M][ds] x2
+    float* workspace;  // screen_scan_workspace_floats(B, T, M, ds) floats
 };
+
+int64_t screen_scan_workspace_floats(int64_t B, int64_t T, int64_t M,
+                                     int64_t ds);
 
 // Per-token read: q fp32 [B][T][dk]; proj [B][T][M][dk + dv] (keys then
 // values, launch dtype); u / du [B][T][dv] (launch dtype).

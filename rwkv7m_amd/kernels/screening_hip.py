@@ -29,6 +29,14 @@ def _f32(t):
     return None if t is None else t.detach().to(torch.float32).contiguous()
 
 
+def _workspace(B, T, M, ds, dev):
+    n = wkv_hip.load_library().rwkv7m_screen_slot_scan_workspace_floats(
+        B, T, M, ds)
+    if n < 0:
+        raise ValueError(f"invalid slot-scan sizes B={B} T={T} M={M} ds={ds}")
+    return torch.empty(max(n, 1), dtype=torch.float32, device=dev), n
+
+
 def slot_scan(base, slot_term, mu, slots0):
     """base [B, T, ds] (bf16/fp32), slot_term [M, ds], mu [M], slots0
     [B, M, ds] -> (slots_seq [B, T, M, ds] in base's dtype, slots_T
@@ -42,9 +50,10 @@ def slot_scan(base, slot_term, mu, slots0):
     s_t = torch.empty(B, M, ds, dtype=torch.float32, device=dev)
     upd2 = torch.empty(B, T, M, (ds + 63) // 64, dtype=torch.float32,
                        device=dev)
+    ws, nws = _workspace(B, T, M, ds, dev)
     P = wkv_hip._p
     _call("rwkv7m_screen_slot_scan", wkv_hip._dtype_code(base), B, T, M, ds,
-          P(base), P(st), P(mu_), P(s0), P(seq), P(s_t), P(upd2),
+          P(base), P(st), P(mu_), P(s0), P(seq), P(s_t), P(upd2), P(ws), nws,
           wkv_hip._stream(dev))
     return seq, s_t, upd2
 
@@ -64,10 +73,12 @@ def slot_scan_backward(base, slot_term, mu, slots_seq, d_slots_seq,
     d_pre = torch.empty(B, T, M, ds, dtype=torch.float32, device=dev)
     d_s0 = torch.empty(B, M, ds, dtype=torch.float32, device=dev)
     d_mu = torch.empty(B, M, ds, dtype=torch.float32, device=dev)
+    ws, nws = _workspace(B, T, M, ds, dev)
     P = wkv_hip._p
     _call("rwkv7m_screen_slot_scan_backward", wkv_hip._dtype_code(base), B,
           T, M, ds, P(base), P(st), P(mu_), P(slots_seq), P(d_slots_seq),
-          P(dst), P(d_pre), P(d_s0), P(d_mu), wkv_hip._stream(dev))
+          P(dst), P(d_pre), P(d_s0), P(d_mu), P(ws), nws,
+          wkv_hip._stream(dev))
     return d_pre, d_s0, d_mu
 
 

@@ -65,6 +65,7 @@ EXPORTED_SYMBOLS = (
     "rwkv7m_timemix_wkv_inputs_backward",
     "rwkv7m_timemix_wkv_output",
     "rwkv7m_timemix_wkv_output_backward",
+    "rwkv7m_screen_slot_scan_workspace_floats",
     "rwkv7m_screen_slot_scan",
     "rwkv7m_screen_slot_scan_backward",
     "rwkv7m_screen_read",
@@ -131,10 +132,13 @@ def load_library(path: str | None = None):
         lib.rwkv7m_timemix_wkv_output_backward.argtypes = (
             dims + [vp] * 8 + [f64] + [vp] * 10 + [i64, vp])
         sdims = [i32, i64, i64, i64, i64]
+        lib.rwkv7m_screen_slot_scan_workspace_floats.restype = i64
+        lib.rwkv7m_screen_slot_scan_workspace_floats.argtypes = [i64] * 4
         lib.rwkv7m_screen_slot_scan.restype = i32
-        lib.rwkv7m_screen_slot_scan.argtypes = sdims + [vp] * 8
+        lib.rwkv7m_screen_slot_scan.argtypes = sdims + [vp] * 8 + [i64, vp]
         lib.rwkv7m_screen_slot_scan_backward.restype = i32
-        lib.rwkv7m_screen_slot_scan_backward.argtypes = sdims + [vp] * 10
+        lib.rwkv7m_screen_slot_scan_backward.argtypes = (
+            sdims + [vp] * 10 + [i64, vp])
         rdims = [i32, i64, i64, i64, i64, i64, vp, vp, f64, f64, vp, i32,
                  i32, f64, f64, f64, f64]
         lib.rwkv7m_screen_read.restype = i32

@@ -165,23 +165,15 @@ class _ScreenRead(torch.autograd.Function):
                 d_age, None, None)
 
 
-def _ema_mean_per_step(r_bar: torch.Tensor, u0: torch.Tensor, d: float,
-                       block: int = 64) -> torch.Tensor:
-    """u_t = d u_{t-1} + (1 - d) r_t for t = 0..T-1 (u_{-1} = u0), in
-    blocks of ``block`` steps with a Toeplitz matrix inside each block."""
+def _ema_time_mean(r_bar: torch.Tensor, u0: torch.Tensor,
+                   d: float) -> torch.Tensor:
+    """Mean over t = 0..T-1 of u_t = d u_{t-1} + (1 - d) r_t (u_{-1} = u0),
+    in closed form: (u0 d (1 - d^T) / (1 - d) + sum_t r_t (1 - d^(T-t))) / T
+    (u0 T in place of the first term when d = 1)."""
     T = r_bar.shape[0]
-    out = torch.empty_like(r_bar)
-    i = torch.arange(block, device=r_bar.device, dtype=r_bar.dtype)
-    expo = (i[:, None] - i[None, :])
-    w = torch.where(expo >= 0, (1.0 - d) * d ** expo.clamp(min=0),
-                    torch.zeros_like(expo))
-    carry = u0
-    for s in range(0, T, block):
-        n = min(block, T - s)
-        blk = w[:n, :n] @ r_bar[s:s + n] + carry * d ** (i[:n] + 1)
-        out[s:s + n] = blk
-        carry = blk[-1]
-    return out
+    t = torch.arange(T, device=r_bar.device, dtype=r_bar.dtype)
+    head = u0 * (T if d == 1.0 else d * (1.0 - d ** T) / (1.0 - d))
+    return (head + (r_bar * (1.0 - d ** (T - t))).sum()) / T
 
 
 class StateLevelScreening(torch.nn.Module):
@@ -289,8 +281,8 @@ class StateLevelScreening(torch.nn.Module):
         with torch.no_grad():
             r = rel.detach()
             zero = torch.zeros((), device=r.device)
-            u_bar = _ema_mean_per_step(r.mean((0, 2)).double(),
-                                       state.usage_ema.double().mean(), d)
+            u_mean = _ema_time_mean(r.mean((0, 2)).double(),
+                                    state.usage_ema.double().mean(), d)
             stats = {
                 "rel_read_mean": r.mean(),
                 "rel_read_max": r.amax(dim=(0, 2)).mean(),
@@ -302,7 +294,7 @@ class StateLevelScreening(torch.nn.Module):
                 "rel_write_mean": zero,
                 "rel_write_effective_mean": zero,
                 "slot_update_norm_mean": upd2.sum(-1).sqrt().mean(),
-                "slot_usage_ema_mean": u_bar.mean().float(),
+                "slot_usage_ema_mean": u_mean.float(),
                 "tau_w": zero,
             }
         return h, new_state, stats

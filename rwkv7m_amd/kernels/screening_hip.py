@@ -102,10 +102,10 @@ def read(q, proj, tau, age_w, cfg, dv):
     rel = torch.empty(B, T, M, dtype=torch.float32, device=dev)
     zn = torch.empty(B, T, dtype=torch.float32, device=dev)
     un = torch.empty(B, T, dtype=torch.float32, device=dev)
+    sc = _read_scalars(cfg, tau)
     P = wkv_hip._p
     _call("rwkv7m_screen_read", wkv_hip._dtype_code(proj), B, T, M, dk, dv,
-          P(q), P(proj), *_read_scalars(cfg, tau)[:2], P(aw),
-          *_read_scalars(cfg, tau)[2:], P(u), P(rel), P(zn), P(un),
+          P(q), P(proj), *sc[:2], P(aw), *sc[2:], P(u), P(rel), P(zn), P(un),
           wkv_hip._stream(dev))
     return u, rel, zn, un
 

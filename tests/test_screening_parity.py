@@ -185,3 +185,31 @@ def test_phases(hip_lib):
     mod.config.use_write_screening = True
     with pytest.raises(NotImplementedError, match="read_write"):
         mod(xd, hd, st, phase="read_write")
+
+
+@pytest.mark.parametrize("pieces", [(1,) * 6, (33, 1, 37), (70, 1)])
+def test_streaming_with_carried_state_equals_one_call(hip_lib, pieces):
+    # the reference's generate loop feeds tokens in pieces with the screen
+    # state carried (infer/generate.py:62-99): h and the final state of the
+    # pieces must equal those of one call over the whole sequence (fp32; the
+    # chunked scan composes the steps in another order, so to rounding)
+    from rwkv7m_amd.screening import ScreenState
+    T = sum(pieces)
+    case = _case(2, T, 64, 80, 32, 80, 5, seed=21, use_age_mask=True)
+    print("case: screening streaming", pieces, flush=True)
+    x, h, slots, ages, usage, P, cfg = case
+    mod, xd, hd, st, out, new, _ = _run(case, torch.float32)
+    state = st
+    outs = []
+    t0 = 0
+    for n in pieces:
+        o, state, _ = mod(xd[:, t0:t0 + n], hd[:, t0:t0 + n], state)
+        outs.append(o)
+        t0 += n
+    torch.cuda.synchronize()
+    assert isinstance(state, ScreenState)
+    for name, a, b in (("h", torch.cat(outs, 1), out),
+                       ("slots", state.slots, new.slots),
+                       ("usage", state.usage_ema, new.usage_ema)):
+        e = _err(a, b.detach().double().cpu().numpy())
+        assert e <= 1e-5, f"streaming {pieces} {name}: {e:.3e}"

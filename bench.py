@@ -480,8 +480,10 @@ def bench_screening(args):
     0.185B preset (src/rwkv7m/model/presets.py:93-104: d_model 768,
     d_slot 128, d_k 64, d_v 64, 16 slots in banks 8/4/4) at config 1's
     B=8, T=512, bf16: one step = StateLevelScreening forward and the
-    backward of all its inputs and parameters from a cotangent of h.  The
-    four HIP kernels are also timed alone with HIP events."""
+    backward of all its inputs and parameters from a cotangent of h, captured
+    in a HIP graph and replayed (``eager_ms_per_step``: the same step
+    launched op by op).  The four HIP kernels are also timed alone with HIP
+    events."""
     import numpy as np
     import torch
 
@@ -519,6 +521,30 @@ def bench_screening(args):
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # the same step captured once in a HIP graph and replayed: the step is
+    # launch-bound (about 200 small launches for 4096 tokens)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            mod.zero_grad(set_to_none=True)
+            x.grad = h.grad = None
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    mod.zero_grad(set_to_none=True)
+    x.grad = h.grad = None
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
 
@@ -596,6 +622,7 @@ def bench_screening(args):
             "avg_ms": kernels[dominant]["ms"],
         },
         "screen_kernels": kernels,
+        "eager_ms_per_step": eager_ms,
     }
     if args.cpu_seconds > 0:
         P = {k: np.asarray(getattr(mod, {"ln_scale": "screen_ln_scale",

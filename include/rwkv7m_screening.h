@@ -69,13 +69,16 @@ int rwkv7m_screen_slot_scan_backward(
     float *d_slots0, float *d_mu_part, float *workspace,
     int64_t workspace_floats, void *stream);
 
-/* Per-token read.  leaky = 0: rel = trim_square(sim, tau, trim_eps) * age;
+/* Per-token read.  tau is one fp32 on the device, in (-1, 1) (the
+ * reference's bounded_tau), read by the kernel so that a caller can capture
+ * the call in a HIP graph.  leaky = 0: rel = trim_square(sim, tau,
+ * trim_eps) * age;
  * leaky = 1: ((1 - alpha) trim_square + alpha sigmoid(gamma (sim - tau)))
  * * age.  age_w may be NULL (no age mask).  Replaces nnx_model.py:1063-1086
  * for every step at once. */
 int rwkv7m_screen_read(int dtype, int64_t B, int64_t T, int64_t M,
                        int64_t dk, int64_t dv, const float *q,
-                       const void *proj, double tau, double trim_eps,
+                       const void *proj, const float *tau, double trim_eps,
                        const float *age_w, int value_unit_norm, int leaky,
                        double leaky_alpha, double leaky_gamma, double cap,
                        double eps, void *u, float *rel, float *z_norm,
@@ -86,7 +89,7 @@ int rwkv7m_screen_read(int dtype, int64_t B, int64_t T, int64_t M,
  * g_age[b][t][m] = d rel * rel / age (summed over t it is d age_w). */
 int rwkv7m_screen_read_backward(
     int dtype, int64_t B, int64_t T, int64_t M, int64_t dk, int64_t dv,
-    const float *q, const void *proj, double tau, double trim_eps,
+    const float *q, const void *proj, const float *tau, double trim_eps,
     const float *age_w, int value_unit_norm, int leaky, double leaky_alpha,
     double leaky_gamma, double cap, double eps, const void *du,
     const float *d_rel, float *dq, void *d_proj, float *d_tau, float *g_age,

@@ -323,8 +323,8 @@ struct ReadMath {
 
 __device__ __forceinline__ ReadMath read_math(const ScreenReadArgs& A) {
     ReadMath r;
-    r.tau = A.tau;
-    r.den = 1.f - A.tau + A.trim_eps;
+    r.tau = *A.tau;
+    r.den = 1.f - r.tau + A.trim_eps;
     r.alpha = A.leaky_alpha;
     r.gamma = A.leaky_gamma;
     r.cap = A.cap;

@@ -455,15 +455,12 @@ int sc_workspace(const char* fn, int64_t B, int64_t T, int64_t M,
 }
 
 int sc_read_checks(const char* fn, int64_t M, int64_t dk, int64_t dv,
-                   double tau, double trim_eps, double cap, double eps,
-                   double alpha, double gamma) {
+                   double trim_eps, double cap, double eps, double alpha,
+                   double gamma) {
     const std::string f(fn);
     if (M > 64 || dk > 128 || dv > 512)
         return fail(RWKV7M_ERR_UNSUPPORTED,
                     f + ": supported sizes are M <= 64, dk <= 128, dv <= 512");
-    if (!std::isfinite(tau) || !(tau < 1.0) || !(tau > -1.0))
-        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
-                    f + ": tau must lie in (-1, 1)");
     if (!(trim_eps >= 0.0) || !(eps >= 0.0) || !std::isfinite(eps) ||
         !std::isfinite(trim_eps))
         return fail(RWKV7M_ERR_INVALID_ARGUMENT,
@@ -479,7 +476,7 @@ int sc_read_checks(const char* fn, int64_t M, int64_t dk, int64_t dv,
 
 rwkv7m::ScreenReadArgs sc_read_args(int64_t B, int64_t T, int64_t M,
                                     int64_t dk, int64_t dv, const float* q,
-                                    const void* proj, double tau,
+                                    const void* proj, const float* tau,
                                     double trim_eps, const float* age_w,
                                     int value_unit_norm, int leaky,
                                     double alpha, double gamma, double cap,
@@ -492,7 +489,7 @@ rwkv7m::ScreenReadArgs sc_read_args(int64_t B, int64_t T, int64_t M,
     A.dv = int(dv);
     A.q = q;
     A.proj = proj;
-    A.tau = float(tau);
+    A.tau = tau;
     A.trim_eps = float(trim_eps);
     A.age_w = age_w;
     A.value_unit_norm = value_unit_norm != 0;
@@ -828,7 +825,7 @@ int rwkv7m_screen_slot_scan_backward(
 
 int rwkv7m_screen_read(int dtype, int64_t B, int64_t T, int64_t M,
                        int64_t dk, int64_t dv, const float* q,
-                       const void* proj, double tau, double trim_eps,
+                       const void* proj, const float* tau, double trim_eps,
                        const float* age_w, int value_unit_norm, int leaky,
                        double leaky_alpha, double leaky_gamma, double cap,
                        double eps, void* u, float* rel, float* z_norm,
@@ -836,10 +833,10 @@ int rwkv7m_screen_read(int dtype, int64_t B, int64_t T, int64_t M,
     const char* fn = "rwkv7m_screen_read";
     g_last_error.clear();
     RWKV7M_TRY(sc_dims(fn, dtype, B, T, M, dk, dv));
-    RWKV7M_TRY(sc_read_checks(fn, M, dk, dv, tau, trim_eps, cap, eps,
-                              leaky_alpha, leaky_gamma));
+    RWKV7M_TRY(sc_read_checks(fn, M, dk, dv, trim_eps, cap, eps, leaky_alpha,
+                              leaky_gamma));
     if (B == 0 || T == 0) return RWKV7M_OK;
-    RWKV7M_TRY(sc_need(fn, {{"q", q}, {"proj", proj}, {"u", u},
+    RWKV7M_TRY(sc_need(fn, {{"q", q}, {"proj", proj}, {"tau", tau}, {"u", u},
                             {"rel", rel}, {"z_norm", z_norm},
                             {"u_norm", u_norm}}));
     rwkv7m::ScreenReadArgs A =
@@ -858,7 +855,7 @@ int rwkv7m_screen_read(int dtype, int64_t B, int64_t T, int64_t M,
 
 int rwkv7m_screen_read_backward(
     int dtype, int64_t B, int64_t T, int64_t M, int64_t dk, int64_t dv,
-    const float* q, const void* proj, double tau, double trim_eps,
+    const float* q, const void* proj, const float* tau, double trim_eps,
     const float* age_w, int value_unit_norm, int leaky, double leaky_alpha,
     double leaky_gamma, double cap, double eps, const void* du,
     const float* d_rel, float* dq, void* d_proj, float* d_tau, float* g_age,
@@ -866,10 +863,10 @@ int rwkv7m_screen_read_backward(
     const char* fn = "rwkv7m_screen_read_backward";
     g_last_error.clear();
     RWKV7M_TRY(sc_dims(fn, dtype, B, T, M, dk, dv));
-    RWKV7M_TRY(sc_read_checks(fn, M, dk, dv, tau, trim_eps, cap, eps,
-                              leaky_alpha, leaky_gamma));
+    RWKV7M_TRY(sc_read_checks(fn, M, dk, dv, trim_eps, cap, eps, leaky_alpha,
+                              leaky_gamma));
     if (B == 0 || T == 0) return RWKV7M_OK;
-    RWKV7M_TRY(sc_need(fn, {{"q", q}, {"proj", proj}, {"du", du},
+    RWKV7M_TRY(sc_need(fn, {{"q", q}, {"proj", proj}, {"tau", tau}, {"du", du},
                             {"dq", dq}, {"d_proj", d_proj}, {"d_tau", d_tau},
                             {"g_age", g_age}}));
     rwkv7m::ScreenReadArgs A =

@@ -129,7 +129,8 @@ struct ScreenReadArgs {
     int M, dk, dv;
     const float* q;
     const void* proj;
-    float tau, trim_eps;
+    const float* tau;  // one fp32 on the device
+    float trim_eps;
     const float* age_w;  // [B][M] or 0
     int value_unit_norm, leaky;
     float leaky_alpha, leaky_gamma, cap, eps;

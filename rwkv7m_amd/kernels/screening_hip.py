@@ -83,15 +83,20 @@ def slot_scan_backward(base, slot_term, mu, slots_seq, d_slots_seq,
 
 
 def _read_scalars(cfg, tau):
+    """(tau on the device, trim_eps, value_unit_norm, leaky, alpha, gamma,
+    cap, eps).  tau stays a device tensor: no host synchronisation, so the
+    call can be captured in a HIP graph."""
     leaky = bool(cfg.use_leaky_warmup)
     trim_eps = 1e-6 if leaky else float(cfg.eps)  # nnx_model.py:1071, :1075
-    return (float(tau), trim_eps, int(bool(cfg.use_value_unit_norm)),
+    tau_d = tau.detach().to(torch.float32).reshape(1).contiguous()
+    return (tau_d, trim_eps, int(bool(cfg.use_value_unit_norm)),
             int(leaky), float(cfg.leaky_alpha), float(cfg.leaky_gamma),
             float(cfg.tanh_norm_cap), float(cfg.eps))
 
 
 def read(q, proj, tau, age_w, cfg, dv):
-    """q [B, T, dk] fp32, proj [B, T, M, dk + dv] -> (u [B, T, dv] in
+    """q [B, T, dk] fp32, proj [B, T, M, dk + dv], tau a device scalar
+    tensor -> (u [B, T, dv] in
     proj's dtype, rel [B, T, M], z_norm [B, T], u_norm [B, T])."""
     q, proj = _f32(q), _c(proj)
     B, T, M, kv = proj.shape
@@ -105,8 +110,8 @@ def read(q, proj, tau, age_w, cfg, dv):
     sc = _read_scalars(cfg, tau)
     P = wkv_hip._p
     _call("rwkv7m_screen_read", wkv_hip._dtype_code(proj), B, T, M, dk, dv,
-          P(q), P(proj), *sc[:2], P(aw), *sc[2:], P(u), P(rel), P(zn), P(un),
-          wkv_hip._stream(dev))
+          P(q), P(proj), P(sc[0]), sc[1], P(aw), *sc[2:], P(u), P(rel), P(zn),
+          P(un), wkv_hip._stream(dev))
     return u, rel, zn, un
 
 
@@ -126,6 +131,6 @@ def read_backward(q, proj, tau, age_w, cfg, dv, du, d_rel=None):
     sc = _read_scalars(cfg, tau)
     P = wkv_hip._p
     _call("rwkv7m_screen_read_backward", wkv_hip._dtype_code(proj), B, T, M,
-          dk, dv, P(q), P(proj), *sc[:2], P(aw), *sc[2:], P(du), P(dr),
-          P(dq), P(dproj), P(dtau), P(g_age), wkv_hip._stream(dev))
+          dk, dv, P(q), P(proj), P(sc[0]), sc[1], P(aw), *sc[2:], P(du),
+          P(dr), P(dq), P(dproj), P(dtau), P(g_age), wkv_hip._stream(dev))
     return dq, dproj, dtau, g_age

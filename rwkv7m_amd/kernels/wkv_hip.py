@@ -139,7 +139,7 @@ def load_library(path: str | None = None):
         lib.rwkv7m_screen_slot_scan_backward.restype = i32
         lib.rwkv7m_screen_slot_scan_backward.argtypes = (
             sdims + [vp] * 10 + [i64, vp])
-        rdims = [i32, i64, i64, i64, i64, i64, vp, vp, f64, f64, vp, i32,
+        rdims = [i32, i64, i64, i64, i64, i64, vp, vp, vp, f64, vp, i32,
                  i32, f64, f64, f64, f64]
         lib.rwkv7m_screen_read.restype = i32
         lib.rwkv7m_screen_read.argtypes = rdims + [vp] * 5

@@ -165,6 +165,28 @@ class _ScreenRead(torch.autograd.Function):
                 d_age, None, None)
 
 
+class _SlotProjection(torch.autograd.Function):
+    """keys and values of every step's slots: seq [B, T, M, ds] @ kv
+    [ds, dk + dv].  The weight gradient is a reduction over B*T*M rows; it
+    runs as one batched product per batch row, summed in fp32, instead of a
+    single long-K GEMM."""
+
+    @staticmethod
+    def forward(ctx, seq, kv):
+        ctx.save_for_backward(seq, kv)
+        return seq @ kv
+
+    @staticmethod
+    def backward(ctx, g):
+        seq, kv = ctx.saved_tensors
+        g = g.contiguous()
+        d_seq = g @ kv.t().contiguous()
+        B, ds = seq.shape[0], seq.shape[-1]
+        part = torch.bmm(seq.reshape(B, -1, ds).transpose(1, 2).contiguous(),
+                         g.reshape(B, -1, g.shape[-1]))
+        return d_seq, part.float().sum(0).to(kv.dtype)
+
+
 def _ema_time_mean(r_bar: torch.Tensor, u0: torch.Tensor,
                    d: float) -> torch.Tensor:
     """Mean over t = 0..T-1 of u_t = d u_{t-1} + (1 - d) r_t (u_{-1} = u0),
@@ -213,24 +235,31 @@ class StateLevelScreening(torch.nn.Module):
         self.slot_embed = torch.nn.Parameter(
             (0.02 * torch.randn(M, ds, generator=g)).to(**kw))
         self.mu_by_bank_raw = const((3,), 0.0)
+        fixed = [None if hl is None else -math.expm1(-math.log(2.0) / hl)
+                 for hl in (config.short_half_life_tokens,
+                            config.mid_half_life_tokens,
+                            config.long_half_life_tokens)]
+        self.register_buffer("_mu_max", torch.tensor(
+            [config.mu_short_max, config.mu_mid_max, config.mu_long_max],
+            dtype=torch.float32, device=device), persistent=False)
+        self.register_buffer("_mu_fixed", torch.tensor(
+            [0.0 if f is None else f for f in fixed], dtype=torch.float32,
+            device=device), persistent=False)
+        self.register_buffer("_mu_fixed_mask", torch.tensor(
+            [f is not None for f in fixed], device=device), persistent=False)
+        self.register_buffer("_bank_ids", torch.tensor(
+            config.bank_ids, dtype=torch.long, device=device),
+            persistent=False)
 
     def compute_mu(self) -> torch.Tensor:
-        """nnx_model.py:1002-1013."""
-        cfg = self.config
-        if len(cfg.bank_ids) != cfg.n_slots:
+        """nnx_model.py:1002-1013: per-bank rates (mu_max * sigmoid(raw), or
+        the half-life rate where one is set) gathered by bank_ids.  Built
+        from device buffers only, so the call can be captured in a graph."""
+        if self._bank_ids.numel() != self.config.n_slots:
             raise ValueError("bank_ids must have length n_slots")
-        raw = self.mu_by_bank_raw.float()
-        mu_max = torch.tensor([cfg.mu_short_max, cfg.mu_mid_max,
-                               cfg.mu_long_max], device=raw.device)
-        legacy = mu_max * torch.sigmoid(raw)
-        per_bank = []
-        for i, hl in enumerate((cfg.short_half_life_tokens,
-                                cfg.mid_half_life_tokens,
-                                cfg.long_half_life_tokens)):
-            per_bank.append(legacy[i] if hl is None else torch.tensor(
-                -math.expm1(-math.log(2.0) / hl), device=raw.device))
-        ids = torch.tensor(cfg.bank_ids, device=raw.device)
-        return torch.stack(per_bank)[ids]
+        legacy = self._mu_max * torch.sigmoid(self.mu_by_bank_raw.float())
+        per_bank = torch.where(self._mu_fixed_mask, self._mu_fixed, legacy)
+        return per_bank[self._bank_ids]
 
     def forward(self, x_seq, h_base_seq, state: ScreenState, *,
                 phase: str = "read_screening_only", deterministic=True):
@@ -265,7 +294,7 @@ class StateLevelScreening(torch.nn.Module):
         seq, slots_t, upd2 = _SlotScan.apply(base, slot_term, mu,
                                              state.slots.float())
         kv = torch.cat([self.k_proj_r, self.v_proj], dim=1).to(cd)
-        proj = seq @ kv
+        proj = _SlotProjection.apply(seq, kv)
         u, rel, zn, un = _ScreenRead.apply(q, proj, tau, age_w, cfg,
                                            cfg.d_v)
         read = (u @ self.out_proj.to(cd)).to(h_base_seq.dtype)

@@ -213,3 +213,62 @@ def test_streaming_with_carried_state_equals_one_call(hip_lib, pieces):
                        ("usage", state.usage_ema, new.usage_ema)):
         e = _err(a, b.detach().double().cpu().numpy())
         assert e <= 1e-5, f"streaming {pieces} {name}: {e:.3e}"
+
+
+def test_graph_capture_replays_match_eager(hip_lib):
+    # forward + backward captured in one HIP graph (the launch-bound step's
+    # deployment form) and replayed three times, with unrelated eager work
+    # between replays; every replay must reproduce the eager outputs and
+    # gradients
+    from rwkv7m_amd.screening import ScreenState
+    case = _case(2, 40, 64, 80, 32, 80, 5, seed=31, use_age_mask=True)
+    print("case: screening graph replay", flush=True)
+    x, h, slots, ages, usage, P, cfg = case
+    mod = _module(P, cfg, torch.float32)
+    xd = torch.tensor(x, dtype=torch.float32, device="cuda",
+                      requires_grad=True)
+    hd = torch.tensor(h, dtype=torch.float32, device="cuda",
+                      requires_grad=True)
+    st = ScreenState(*(torch.tensor(a, dtype=torch.float32, device="cuda")
+                       for a in (slots, ages, usage)))
+    dh = torch.randn(xd.shape, device="cuda")
+    params = list(mod.parameters())
+
+    def clear():
+        mod.zero_grad(set_to_none=True)
+        xd.grad = None
+        hd.grad = None
+
+    def step():
+        out, new, stats = mod(xd, hd, st)
+        (out * dh).sum().backward()
+        return [out, new.slots, new.usage_ema, stats["rel_read_mean"],
+                stats["slot_usage_ema_mean"]]
+
+    clear()
+    ref = [t.detach().clone() for t in step()]
+    ref_g = [p.grad.clone() for p in params] + [xd.grad.clone(),
+                                                hd.grad.clone()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            clear()
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    clear()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    grads = [p.grad for p in params] + [xd.grad, hd.grad]
+    for i in range(3):
+        noise = torch.randn(4096, device="cuda")
+        (noise * noise).sum().item()
+        graph.replay()
+        torch.cuda.synchronize()
+        for k, (a, b) in enumerate(zip(outs, ref)):
+            torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6,
+                                       msg=f"replay {i} output {k}")
+        for k, (a, b) in enumerate(zip(grads, ref_g)):
+            torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6,
+                                       msg=f"replay {i} gradient {k}")

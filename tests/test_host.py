@@ -377,3 +377,37 @@ def test_oracle_reproduces_golden_fixture(path):
         for name, g in zip(GRAD_NAMES, grads):
             np.testing.assert_allclose(g, data[name], rtol=1e-5, atol=1e-6,
                                        err_msg=name)
+
+
+def test_screening_abi_checks_requests_before_any_device_call(lib):
+    # workspace: three [chunks][B][M][ds] fp32 arrays, 32 steps per chunk
+    assert lib.rwkv7m_screen_slot_scan_workspace_floats(8, 512, 16, 128) == \
+        3 * 16 * 8 * 16 * 128
+    assert lib.rwkv7m_screen_slot_scan_workspace_floats(2, 0, 4, 64) == \
+        3 * 2 * 4 * 64
+    assert lib.rwkv7m_screen_slot_scan_workspace_floats(-1, 8, 4, 64) == -1
+    fake = 1 << 20
+    scan = lib.rwkv7m_screen_slot_scan
+    assert scan(3, 2, 8, 4, 64, *([fake] * 8), 10 ** 6, None) == 1
+    assert b"bfloat16 or float32" in lib.rwkv7m_last_error()
+    assert scan(1, 2, 8, 4, 64, *([fake] * 8), 10, None) == 1
+    assert b"workspace holds 10" in lib.rwkv7m_last_error()
+    assert scan(1, 2, 8, 4, 64, fake, None, *([fake] * 6), 10 ** 6,
+                None) == 1
+    assert b"slot_term is NULL" in lib.rwkv7m_last_error()
+    assert scan(1, 0, 8, 4, 64, *([None] * 8), 0, None) == 0  # no batch
+    read = lib.rwkv7m_screen_read
+    args = [fake, fake, fake, 1e-6, None, 1, 0, 0.0, 8.0, 1.0, 1e-6]
+    assert read(1, 2, 8, 65, 64, 64, *args, *([fake] * 4), None) == 2
+    assert b"M <= 64" in lib.rwkv7m_last_error()
+    assert read(1, 2, 8, 16, 64, 600, *args, *([fake] * 4), None) == 2
+    bad_cap = args[:9] + [0.0] + args[10:]
+    assert read(1, 2, 8, 16, 64, 64, *bad_cap, *([fake] * 4), None) == 1
+    assert b"cap" in lib.rwkv7m_last_error()
+    no_tau = args[:2] + [None] + args[3:]
+    assert read(1, 2, 8, 16, 64, 64, *no_tau, *([fake] * 4), None) == 1
+    assert b"tau is NULL" in lib.rwkv7m_last_error()
+    bwd = lib.rwkv7m_screen_read_backward
+    assert bwd(1, 2, 8, 16, 64, 64, *args, fake, None, None,
+               *([fake] * 3), None) == 1
+    assert b"dq is NULL" in lib.rwkv7m_last_error()

@@ -74,15 +74,17 @@ int rwkv7m_screen_slot_scan_backward(
  * the call in a HIP graph.  leaky = 0: rel = trim_square(sim, tau,
  * trim_eps) * age;
  * leaky = 1: ((1 - alpha) trim_square + alpha sigmoid(gamma (sim - tau)))
- * * age.  age_w may be NULL (no age mask).  Replaces nnx_model.py:1063-1086
+ * * age.  age_w may be NULL (no age mask); it is [B][M], or [B][T][M] with
+ * age_per_step = 1 (the write phase's ages change at every step).  Replaces nnx_model.py:1063-1086
  * for every step at once. */
 int rwkv7m_screen_read(int dtype, int64_t B, int64_t T, int64_t M,
                        int64_t dk, int64_t dv, const float *q,
                        const void *proj, const float *tau, double trim_eps,
-                       const float *age_w, int value_unit_norm, int leaky,
-                       double leaky_alpha, double leaky_gamma, double cap,
-                       double eps, void *u, float *rel, float *z_norm,
-                       float *u_norm, void *stream);
+                       const float *age_w, int age_per_step,
+                       int value_unit_norm, int leaky, double leaky_alpha,
+                       double leaky_gamma, double cap, double eps, void *u,
+                       float *rel, float *z_norm, float *u_norm,
+                       void *stream);
 
 /* Adjoint of rwkv7m_screen_read: from du (and d_rel, the cotangent of rel,
  * may be NULL) to dq, d_proj, d_tau[b][t] (summed it is d tau) and
@@ -90,10 +92,47 @@ int rwkv7m_screen_read(int dtype, int64_t B, int64_t T, int64_t M,
 int rwkv7m_screen_read_backward(
     int dtype, int64_t B, int64_t T, int64_t M, int64_t dk, int64_t dv,
     const float *q, const void *proj, const float *tau, double trim_eps,
-    const float *age_w, int value_unit_norm, int leaky, double leaky_alpha,
-    double leaky_gamma, double cap, double eps, const void *du,
-    const float *d_rel, float *dq, void *d_proj, float *d_tau, float *g_age,
-    void *stream);
+    const float *age_w, int age_per_step, int value_unit_norm, int leaky,
+    double leaky_alpha, double leaky_gamma, double cap, double eps,
+    const void *du, const float *d_rel, float *dq, void *d_proj,
+    float *d_tau, float *g_age, void *stream);
+
+/* Write phase (read_write, nnx_model.py:1040-1047 and :1103-1115): the slot
+ * recurrence whose update strength is mu * max(rel_w, floor), rel_w the
+ * trim-square relevance of the write query q_w [B][T][dk] (fp32, unit
+ * norm) against the write keys unit_norm(round(S_t + slot_embed) kw)
+ * (kw [ds][dk] fp32), with ages reset where rel_w > 1e-3.  One workgroup
+ * per (b, m) walks the steps.  Outputs: slots_seq (S_t rounded to dtype,
+ * for the read), slots32 (S_t fp32, for the backward), ages_seq [B][T][M]
+ * (the ages step t reads), rel_w [B][T][M], upd2 as the read-only scan,
+ * slots_T, ages_T.  Limits: ds <= 1024, dk <= 128. */
+int rwkv7m_screen_write(int dtype, int64_t B, int64_t T, int64_t M,
+                        int64_t ds, int64_t dk, const void *base,
+                        const float *slot_term, const float *slot_embed,
+                        const float *kw, const float *q_w, const float *tau_w,
+                        const float *mu, double floor, double eps,
+                        const float *slots0, const float *ages0,
+                        void *slots_seq, float *slots32, float *ages_seq,
+                        float *rel_w, float *upd2, float *slots_T,
+                        float *ages_T, void *stream);
+
+/* Adjoint of rwkv7m_screen_write.  Cotangents in: d_slots_seq (dtype),
+ * d_slots_T, d_rel_w, d_ages_seq, d_ages_T (fp32; each may be NULL = 0).
+ * Out: d_pre [B][T][M][ds] (as the read-only scan), d_slots0, d_ages0,
+ * d_embed_part [B][M][ds] (summed over b: d slot_embed through the write
+ * keys), d_mu_bm [B][M] (summed over b: d mu), d_kraw [B][T][M][dk] (the
+ * cotangent of the write keys before normalisation: d kw is the sum over
+ * (b, t, m) of round(S_t + slot_embed)^T d_kraw), dq_w [B][T][M][dk]
+ * (summed over m: d q_w) and d_tau_w [B][T][M] (summed: d tau_w). */
+int rwkv7m_screen_write_backward(
+    int dtype, int64_t B, int64_t T, int64_t M, int64_t ds, int64_t dk,
+    const void *base, const float *slot_term, const float *slot_embed,
+    const float *kw, const float *q_w, const float *tau_w, const float *mu,
+    double floor, double eps, const float *slots32, const void *d_slots_seq,
+    const float *d_slots_T, const float *d_rel_w, const float *d_ages_seq,
+    const float *d_ages_T, float *d_pre, float *d_slots0, float *d_ages0,
+    float *d_embed_part, float *d_mu_bm, float *d_kraw, float *dq_w,
+    float *d_tau_w, void *stream);
 
 #ifdef __cplusplus
 }

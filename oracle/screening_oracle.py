@@ -19,6 +19,10 @@ the helpers of src/rwkv7m/model/screening.py:
 * the read-only step (:1062-1112 with ``write_enabled`` false): keys and
   values of the current slots, relevance, the read, the gated residual, then
   ``slots + mu * (delta - slots)`` and the usage EMA; ages are unchanged;
+* the read/write step (``phase="read_write"``, :1040-1047 and :1103-1115):
+  write keys of ``slots + slot_embed``, write relevance against the write
+  query, the update scaled by ``mu * max(rel_w, write_rel_floor)``, ages
+  reset where ``rel_w > 1e-3``, usage fed by ``max(rel, rel_w)``;
 * the statistics (:1117-1137), averaged over the steps.
 
 Parameters are a dict of float64 arrays named as the reference's module
@@ -83,13 +87,17 @@ def compute_mu(cfg, mu_by_bank_raw):
     return np.stack(per_bank)[np.asarray(cfg["bank_ids"], np.int64)]
 
 
-def read_forward(x, h_base, slots, ages, usage, P, cfg):
-    """One call in phase ``read_screening_only``.
+def read_forward(x, h_base, slots, ages, usage, P, cfg,
+                 phase="read_screening_only"):
+    """One call in ``phase`` (``read_screening_only`` or ``read_write``; the
+    write path needs ``cfg["use_write_screening"]`` and the parameters
+    ``q_proj_w``, ``k_proj_w``, ``tau_w_raw``).
 
     x, h_base: [B, T, C]; slots [B, M, d_slot]; ages, usage [B, M].
-    Returns (h [B, T, C], (slots_T, ages, usage_T), stats dict).
+    Returns (h [B, T, C], (slots_T, ages_T, usage_T), stats dict).
     """
     eps = cfg["eps"]
+    write = phase == "read_write" and cfg.get("use_write_screening", False)
     B, T, C = x.shape
     x_ln = layer_norm(x, P["ln_scale"], P["ln_bias"])
     q = unit_norm(x_ln @ P["q_proj_r"], eps)
@@ -101,11 +109,15 @@ def read_forward(x, h_base, slots, ages, usage, P, cfg):
     x_term = x_ln @ dk[:C]
     h_term = h_base @ dk[C:2 * C]
     slot_term = P["slot_embed"] @ dk[2 * C:]
-    age_w = (sigmoid((cfg["age_ref"] - ages) / (cfg["age_sigma"] + eps))
-             if cfg["use_age_mask"] else None)
+    if write:  # nnx_model.py:1040-1047
+        q_w = unit_norm(np.concatenate([x_ln, h_base], -1) @ P["q_proj_w"],
+                        eps)
+        tau_w = 2.0 * sigmoid(P["tau_w_raw"]) - 1.0
     hs = np.empty_like(h_base)
     acc = {n: 0.0 for n in STAT_NAMES}
     for t in range(T):
+        age_w = (sigmoid((cfg["age_ref"] - ages) / (cfg["age_sigma"] + eps))
+                 if cfg["use_age_mask"] else None)
         k_r = unit_norm(slots @ P["k_proj_r"], eps)
         values = slots @ P["v_proj"]
         if cfg["use_value_unit_norm"]:
@@ -125,10 +137,25 @@ def read_forward(x, h_base, slots, ages, usage, P, cfg):
         hs[:, t] = h_base[:, t] + lam * gate[:, t] * read
         delta = np.tanh(x_term[:, t, None, :] + h_term[:, t, None, :]
                         + slot_term[None] + P["delta_bias"])
-        new_slots = slots + mu[None, :, None] * (delta - slots)
+        if write:  # nnx_model.py:1103-1115
+            k_w = unit_norm((slots + P["slot_embed"][None]) @ P["k_proj_w"],
+                            eps)
+            rel_w = trim_square(np.einsum("bk,bmk->bm", q_w[:, t], k_w),
+                                tau_w, eps)
+            strength = mu[None, :] * np.maximum(rel_w, cfg["write_rel_floor"])
+            new_slots = slots + strength[:, :, None] * (delta - slots)
+            ages = np.where(rel_w > 1e-3, 0.0, ages + 1.0)
+            activity = np.maximum(rel, rel_w)
+            acc["rel_write_mean"] += rel_w.mean()
+            acc["rel_write_effective_mean"] += np.maximum(
+                rel_w, cfg["write_rel_floor"]).mean()
+            acc["tau_w"] += tau_w
+        else:
+            new_slots = slots + mu[None, :, None] * (delta - slots)
+            activity = rel
         upd = new_slots - slots
         usage = cfg["usage_ema_decay"] * usage + (
-            1.0 - cfg["usage_ema_decay"]) * rel
+            1.0 - cfg["usage_ema_decay"]) * activity
         acc["rel_read_mean"] += rel.mean()
         acc["rel_read_max"] += rel.max()
         acc["active_slots_mean"] += (rel > 1e-3).sum(-1).mean()
@@ -143,13 +170,15 @@ def read_forward(x, h_base, slots, ages, usage, P, cfg):
     return hs, (slots, ages, usage), stats
 
 
-def read_forward_torch(x, h_base, slots, ages, usage, P, cfg):
+def read_forward_torch(x, h_base, slots, ages, usage, P, cfg,
+                       phase="read_screening_only"):
     """The same step-by-step scan with torch float64 ops, for autograd (the
     gradient oracle): arguments are float64 torch tensors, P a dict of
     them.  Returns (h, slots_T, usage_T)."""
     import torch
 
     eps = cfg["eps"]
+    write = phase == "read_write" and cfg.get("use_write_screening", False)
     B, T, C = x.shape
 
     def un(v):
@@ -179,10 +208,14 @@ def read_forward_torch(x, h_base, slots, ages, usage, P, cfg):
     x_term = x_ln @ dk[:C]
     h_term = h_base @ dk[C:2 * C]
     slot_term = P["slot_embed"] @ dk[2 * C:]
-    age_w = (torch.sigmoid((cfg["age_ref"] - ages) / (cfg["age_sigma"] + eps))
-             if cfg["use_age_mask"] else None)
+    if write:
+        q_w = un(torch.cat([x_ln, h_base], -1) @ P["q_proj_w"])
+        tau_w = 2.0 * torch.sigmoid(P["tau_w_raw"]) - 1.0
     hs = []
     for t in range(T):
+        age_w = (torch.sigmoid((cfg["age_ref"] - ages)
+                               / (cfg["age_sigma"] + eps))
+                 if cfg["use_age_mask"] else None)
         k_r = un(slots @ P["k_proj_r"])
         values = slots @ P["v_proj"]
         if cfg["use_value_unit_norm"]:
@@ -203,9 +236,21 @@ def read_forward_torch(x, h_base, slots, ages, usage, P, cfg):
         hs.append(h_base[:, t] + lam * gate[:, t] * (u @ P["out_proj"]))
         delta = torch.tanh(x_term[:, t, None, :] + h_term[:, t, None, :]
                            + slot_term[None] + P["delta_bias"])
-        slots = slots + mu[None, :, None] * (delta - slots)
+        if write:
+            k_w = un((slots + P["slot_embed"][None]) @ P["k_proj_w"])
+            rel_w = trim(torch.einsum("bk,bmk->bm", q_w[:, t], k_w), tau_w,
+                         eps)
+            strength = mu[None, :] * torch.clamp(
+                rel_w, min=cfg["write_rel_floor"])
+            slots = slots + strength[:, :, None] * (delta - slots)
+            ages = torch.where(rel_w > 1e-3, torch.zeros_like(ages),
+                               ages + 1.0)
+            activity = torch.maximum(rel, rel_w)
+        else:
+            slots = slots + mu[None, :, None] * (delta - slots)
+            activity = rel
         usage = cfg["usage_ema_decay"] * usage + (
-            1.0 - cfg["usage_ema_decay"]) * rel
+            1.0 - cfg["usage_ema_decay"]) * activity
     return torch.stack(hs, 1), slots, usage
 
 
@@ -219,6 +264,7 @@ def default_config(**overrides):
                leaky_gamma=8.0, mu_short_max=0.05, mu_mid_max=0.02,
                mu_long_max=0.005, short_half_life_tokens=None,
                mid_half_life_tokens=None, long_half_life_tokens=None,
-               usage_ema_decay=0.99, age_ref=32.0, age_sigma=8.0)
+               usage_ema_decay=0.99, age_ref=32.0, age_sigma=8.0,
+               use_write_screening=False, write_rel_floor=1e-3)
     cfg.update(overrides)
     return cfg

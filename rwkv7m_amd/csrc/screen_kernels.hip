@@ -347,7 +347,7 @@ __global__ __launch_bounds__(256) void screen_read_fwd_kernel(
     if (!read_token(A, &tok)) return;
     const int lane = threadIdx.x & 63;
     const int dk = A.dk, dv = A.dv, M = A.M;
-    const int64_t b = tok / A.T;
+    const int64_t b = tok / A.T, t_tok = tok % A.T;
     const E* proj = static_cast<const E*>(A.proj) + tok * M * (dk + dv);
     const ReadMath rm = read_math(A);
     float q[kKJ];
@@ -375,7 +375,8 @@ __global__ __launch_bounds__(256) void screen_read_fwd_kernel(
         const float sim = dot / sqrtf(nk + rm.eps * rm.eps);
         float dsim;
         float rel = rm.rel0(sim, &dsim);
-        if (A.age_w) rel *= A.age_w[b * M + m];
+        if (A.age_w)
+            rel *= A.age_w[b * A.age_bstride + t_tok * A.age_tstride + m];
         const E* vp = kp + dk;
         float v[kVJ], nv = 0.f;
 #pragma unroll
@@ -417,7 +418,7 @@ __global__ __launch_bounds__(256) void screen_read_bwd_kernel(
     if (!read_token(A, &tok)) return;
     const int lane = threadIdx.x & 63;
     const int dk = A.dk, dv = A.dv, M = A.M;
-    const int64_t b = tok / A.T;
+    const int64_t b = tok / A.T, t_tok = tok % A.T;
     const E* proj = static_cast<const E*>(A.proj) + tok * M * (dk + dv);
     E* dproj = static_cast<E*>(A.d_proj) + tok * M * (dk + dv);
     const ReadMath rm = read_math(A);
@@ -448,7 +449,9 @@ __global__ __launch_bounds__(256) void screen_read_bwd_kernel(
         const float sim = wave_sum(dot) / nk;
         float dsim;
         const float r0 = rm.rel0(sim, &dsim);
-        const float aw = A.age_w ? A.age_w[b * M + m] : 1.f;
+        const float aw =
+            A.age_w ? A.age_w[b * A.age_bstride + t_tok * A.age_tstride + m]
+                    : 1.f;
         const float rel = r0 * aw;
         const E* vp = kp + dk;
         float v[kVJ], nv = 0.f;
@@ -545,6 +548,300 @@ __global__ __launch_bounds__(256) void screen_read_bwd_kernel(
     if (lane == 0) A.d_tau[tok] = dtau;
 }
 
+// ---------------------------------------------------------------------------
+// Write phase (read_write): the slot recurrence with write screening
+// ---------------------------------------------------------------------------
+//
+// With writes enabled the update's strength depends on the current slots
+// (nnx_model.py:1103-1115):
+//   k_w = unit_norm(round(S_t + slot_embed) W_kw)   (write keys)
+//   rel_w = trim_square(q_w . k_w, tau_w)
+//   S_{t+1} = S_t + mu max(rel_w, floor) (delta_t - S_t)
+//   ages_{t+1} = rel_w > 1e-3 ? 0 : ages_t + 1
+// so each (b, slot) walks the steps in order: one 256-thread workgroup per
+// (b, m), channels c = tid + 256 i in registers, the write key's GEMV over
+// the slot's channels through LDS (four channel quarters per output column,
+// added in order), three barriers per step.  The backward replays each step
+// from the stored fp32 S_t in reverse.
+
+constexpr int kWThreads = 256;
+constexpr int kWMaxCh = 4;  // channels per thread (d_slot <= 1024)
+
+constexpr int kWLdsWeights = 24576;  // fp32 weights staged in LDS up to 96 KB
+
+struct WriteSmem {
+    float sk[kWThreads * kWMaxCh];  // the step's write-key input / d input
+    float red[4][128];              // GEMV partials per channel quarter
+    float dk[128];                  // d k_raw (backward)
+    float scal[8];
+};
+
+// k_raw[j] = sum_c sk[c] W[c][j]: thread (part, j) sums its channel quarter;
+// wave 0 adds the quarters.  Returns k_raw for j = lane, lane + 64 in wave 0
+// (other waves: unspecified).
+// The write-key weights [ds][dk]: staged in dynamic LDS when they fit.
+__device__ __forceinline__ const float* write_weights(const ScreenWriteArgs& A,
+                                                      float* lds) {
+    const int n = int(A.ds) * A.dk;
+    if (n > kWLdsWeights) return A.kw;
+    for (int i = threadIdx.x; i < n; i += kWThreads) lds[i] = A.kw[i];
+    __syncthreads();
+    return lds;
+}
+
+template <typename E>
+__device__ __forceinline__ void write_gemv(const ScreenWriteArgs& A,
+                                           const float* W, WriteSmem& sm,
+                                           float (&k)[2]) {
+    const int tid = threadIdx.x, lane = tid & 63, part = tid >> 6;
+    const int ds = int(A.ds), dk = A.dk;
+    const int q0 = (ds * part) / 4, q1 = (ds * (part + 1)) / 4;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int j = lane + 64 * h;
+        float s = 0.f;
+        if (j < dk)
+            for (int c = q0; c < q1; ++c) s += sm.sk[c] * W[c * dk + j];
+        sm.red[part][lane + 64 * h] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int j = lane + 64 * h;
+        k[h] = (sm.red[0][j] + sm.red[1][j]) + (sm.red[2][j] + sm.red[3][j]);
+        k[h] = j < dk ? rnd(k[h], static_cast<const E*>(nullptr)) : 0.f;
+    }
+}
+
+template <typename E>
+__global__ __launch_bounds__(kWThreads) void screen_write_fwd_kernel(
+    ScreenWriteArgs A) {
+    __shared__ WriteSmem sm;
+    extern __shared__ float wlds[];
+    const float* W = write_weights(A, wlds);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int64_t b = blockIdx.x / A.M;
+    const int m = int(blockIdx.x % A.M);
+    const int64_t T = A.T, M = A.M, ds = A.ds;
+    const int ndw = int((ds + 63) / 64);
+    const E* base = static_cast<const E*>(A.base) + b * T * ds;
+    E* seq = static_cast<E*>(A.slots_seq);
+    const float mu = A.mu[m], tau = *A.tau_w;
+    const float den = 1.f - tau + A.eps;
+    float S[kWMaxCh], e[kWMaxCh], st[kWMaxCh];
+#pragma unroll
+    for (int i = 0; i < kWMaxCh; ++i) {
+        const int c = tid + kWThreads * i;
+        const bool in = c < ds;
+        S[i] = in ? A.slots0[(b * M + m) * ds + c] : 0.f;
+        e[i] = in ? A.slot_embed[m * ds + c] : 0.f;
+        st[i] = in ? A.slot_term[m * ds + c] : 0.f;
+    }
+    float age = A.ages0[b * M + m];  // kept by every thread
+    for (int64_t t = 0; t < T; ++t) {
+        // this step's loads first: they arrive while the key is formed
+        float bv[kWMaxCh], qv[2];
+#pragma unroll
+        for (int i = 0; i < kWMaxCh; ++i) {
+            const int c = tid + kWThreads * i;
+            bv[i] = c < ds ? ld1(base + t * ds + c) : 0.f;
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int j = lane + 64 * h;
+            qv[h] = wv == 0 && j < A.dk ? A.q_w[(b * T + t) * A.dk + j] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < kWMaxCh; ++i) {
+            const int c = tid + kWThreads * i;
+            if (c < ds) sm.sk[c] = rnd(S[i] + e[i], base);
+        }
+        __syncthreads();
+        float k[2];
+        write_gemv<E>(A, W, sm, k);
+        if (wv == 0) {
+            float kk = 0.f, dot = 0.f;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                kk += k[h] * k[h];
+                dot += k[h] * qv[h];
+            }
+            kk = wave_sum(kk);
+            dot = wave_sum(dot);
+            const float sim = dot / sqrtf(kk + A.eps * A.eps);
+            const float x = fmaxf((sim - tau) / den, 0.f);
+            if (lane == 0) {
+                const float rw = x * x;
+                sm.scal[0] = rw;
+                A.rel_w[(b * T + t) * M + m] = rw;
+            }
+        }
+        __syncthreads();
+        const float rw = sm.scal[0];
+        if (tid == 0) A.ages_seq[(b * T + t) * M + m] = age;
+        age = rw > 1e-3f ? 0.f : age + 1.f;
+        const float strength = mu * fmaxf(rw, A.floor);
+        const int64_t o = ((b * T + t) * M + m) * ds;
+#pragma unroll
+        for (int i = 0; i < kWMaxCh; ++i) {
+            const int c = tid + kWThreads * i;
+            const bool in = c < ds;
+            const float delta = in ? rnd(tanhf(bv[i] + st[i]), base) : 0.f;
+            if (in) {
+                st1(seq + o + c, S[i]);
+                A.slots32[o + c] = S[i];
+            }
+            const float u = in ? strength * (delta - S[i]) : 0.f;
+            const float u2 = wave_sum(u * u);
+            const int g = (tid >> 6) + 4 * i;
+            if (lane == 0 && g < ndw)
+                A.upd2[((b * T + t) * M + m) * ndw + g] = u2;
+            S[i] += u;
+        }
+        // sm.sk and sm.scal are rewritten only after the next step's first
+        // barrier, which every thread reaches after these reads
+    }
+#pragma unroll
+    for (int i = 0; i < kWMaxCh; ++i) {
+        const int c = tid + kWThreads * i;
+        if (c < ds) A.slots_T[(b * M + m) * ds + c] = S[i];
+    }
+    if (tid == 0) A.ages_T[b * M + m] = age;
+}
+
+template <typename E>
+__global__ __launch_bounds__(kWThreads) void screen_write_bwd_kernel(
+    ScreenWriteArgs A) {
+    __shared__ WriteSmem sm;
+    extern __shared__ float wlds[];
+    const float* W = write_weights(A, wlds);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int64_t b = blockIdx.x / A.M;
+    const int m = int(blockIdx.x % A.M);
+    const int64_t T = A.T, M = A.M, ds = A.ds;
+    const int dk = A.dk;
+    const E* base = static_cast<const E*>(A.base) + b * T * ds;
+    const E* dseq = static_cast<const E*>(A.d_slots_seq);
+    (void)0;
+    const float mu = A.mu[m], tau = *A.tau_w;
+    const float den = 1.f - tau + A.eps;
+    float G[kWMaxCh], e[kWMaxCh], st[kWMaxCh], de[kWMaxCh];
+#pragma unroll
+    for (int i = 0; i < kWMaxCh; ++i) {
+        const int c = tid + kWThreads * i;
+        const bool in = c < ds;
+        G[i] = in && A.d_slots_T ? A.d_slots_T[(b * M + m) * ds + c] : 0.f;
+        e[i] = in ? A.slot_embed[m * ds + c] : 0.f;
+        st[i] = in ? A.slot_term[m * ds + c] : 0.f;
+        de[i] = 0.f;
+    }
+    float dage = A.d_ages_T ? A.d_ages_T[b * M + m] : 0.f;
+    float dmu = 0.f;
+    for (int64_t t = T - 1; t >= 0; --t) {
+        const int64_t o = ((b * T + t) * M + m) * ds;
+        float S[kWMaxCh], bv[kWMaxCh], dsv[kWMaxCh], th[kWMaxCh];
+#pragma unroll
+        for (int i = 0; i < kWMaxCh; ++i) {
+            const int c = tid + kWThreads * i;
+            const bool in = c < ds;
+            S[i] = in ? A.slots32[o + c] : 0.f;
+            bv[i] = in ? ld1(base + t * ds + c) : 0.f;
+            dsv[i] = in ? ld1(dseq + o + c) : 0.f;
+        }
+        float part = 0.f;  // this thread's part of sum_c G (delta - S)
+#pragma unroll
+        for (int i = 0; i < kWMaxCh; ++i) {
+            const int c = tid + kWThreads * i;
+            const bool in = c < ds;
+            th[i] = in ? tanhf(bv[i] + st[i]) : 0.f;
+            part += in ? G[i] * (rnd(th[i], base) - S[i]) : 0.f;
+            if (in) sm.sk[c] = rnd(S[i] + e[i], base);
+        }
+        part = wave_sum(part);
+        if (lane == 0) sm.scal[4 + wv] = part;
+        __syncthreads();
+        float k[2];
+        write_gemv<E>(A, W, sm, k);
+        if (wv == 0) {
+            const int64_t bt = b * T + t;
+            const float* q = A.q_w + bt * dk;
+            float qv[2];
+            float kk = 0.f, dot = 0.f;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int j = lane + 64 * h;
+                qv[h] = j < dk ? q[j] : 0.f;
+                kk += k[h] * k[h];
+                dot += k[h] * qv[h];
+            }
+            const float kn = sqrtf(wave_sum(kk) + A.eps * A.eps);
+            const float sim = wave_sum(dot) / kn;
+            const float x = (sim - tau) / den;
+            const float r = fmaxf(x, 0.f);
+            const float rw = r * r;
+            const float dstr = (sm.scal[4] + sm.scal[5]) +
+                               (sm.scal[6] + sm.scal[7]);
+            const bool above = rw > A.floor;
+            dmu += dstr * fmaxf(rw, A.floor);
+            const float drw = (A.d_rel_w ? A.d_rel_w[bt * M + m] : 0.f) +
+                              (above ? dstr * mu : 0.f);
+            const float dsim = drw * 2.f * r / den;
+            // d k_hat = dsim q; d k_raw = (d k_hat - k_hat (k_hat . d k_hat)) / kn
+            float kh[2], kd = 0.f;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                kh[h] = k[h] / kn;
+                kd += kh[h] * qv[h];
+            }
+            kd = wave_sum(kd) * dsim;
+            float* dq = A.dq_w + (bt * M + m) * dk;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int j = lane + 64 * h;
+                const float dkr = (dsim * qv[h] - kh[h] * kd) / kn;
+                if (j < dk) {
+                    dq[j] = dsim * kh[h];
+                    A.d_kraw[(bt * M + m) * dk + j] = dkr;
+                    sm.dk[j] = dkr;
+                }
+            }
+            if (lane == 0) {
+                A.d_tau_w[bt * M + m] = drw * 2.f * r * (x - 1.f) / den;
+                sm.scal[0] = mu * fmaxf(rw, A.floor);  // strength
+                sm.scal[1] = rw;
+            }
+        }
+        __syncthreads();
+        const float strength = sm.scal[0], rw = sm.scal[1];
+        // ages: step t read ages_t; ages_{t+1} = rw > 1e-3 ? 0 : ages_t + 1
+        dage = (A.d_ages_seq ? A.d_ages_seq[(b * T + t) * M + m] : 0.f) +
+               (rw > 1e-3f ? 0.f : dage);
+#pragma unroll
+        for (int i = 0; i < kWMaxCh; ++i) {
+            const int c = tid + kWThreads * i;
+            if (c >= ds) continue;
+            float dsk = 0.f;
+            for (int j = 0; j < dk; ++j) dsk += W[c * dk + j] * sm.dk[j];
+            de[i] += dsk;
+            A.d_pre[o + c] = strength * G[i] * (1.f - th[i] * th[i]);
+            G[i] = G[i] * (1.f - strength) + dsk + dsv[i];
+        }
+        __syncthreads();  // sm.dk and sm.scal are rewritten next step
+    }
+#pragma unroll
+    for (int i = 0; i < kWMaxCh; ++i) {
+        const int c = tid + kWThreads * i;
+        if (c < ds) {
+            A.d_slots0[(b * M + m) * ds + c] = G[i];
+            A.d_embed_part[(b * M + m) * ds + c] = de[i];
+        }
+    }
+    if (tid == 0) {
+        A.d_ages0[b * M + m] = dage;
+        A.d_mu_bm[b * M + m] = dmu;
+    }
+}
+
 unsigned blocks_for_waves(int64_t waves) {
     return unsigned((waves + 3) / 4);  // 4 waves of 64 per 256-thread block
 }
@@ -582,6 +879,31 @@ hipError_t launch_screen_scan(bool bf16, bool backward,
         hipLaunchKernelGGL(scan_bwd_dmu_kernel, grid_n, block, 0, stream, A);
     }
 #undef RWKV7M_SC
+    return hipGetLastError();
+}
+
+hipError_t launch_screen_write(bool bf16, bool backward,
+                               const ScreenWriteArgs& A, hipStream_t stream) {
+    const int64_t nwg = A.B * A.M;
+    if (nwg == 0) return hipSuccess;
+    const int64_t nw = A.ds * A.dk;
+    const size_t lds = nw <= kWLdsWeights ? size_t(nw) * sizeof(float) : 0;
+    const dim3 grid{unsigned(nwg)}, block{unsigned(kWThreads)};
+    if (!backward) {
+        if (bf16)
+            hipLaunchKernelGGL(screen_write_fwd_kernel<bf16_t>, grid, block,
+                               lds, stream, A);
+        else
+            hipLaunchKernelGGL(screen_write_fwd_kernel<float>, grid, block,
+                               lds, stream, A);
+    } else {
+        if (bf16)
+            hipLaunchKernelGGL(screen_write_bwd_kernel<bf16_t>, grid, block,
+                               lds, stream, A);
+        else
+            hipLaunchKernelGGL(screen_write_bwd_kernel<float>, grid, block,
+                               lds, stream, A);
+    }
     return hipGetLastError();
 }
 

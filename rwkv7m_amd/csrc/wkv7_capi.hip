@@ -478,7 +478,8 @@ rwkv7m::ScreenReadArgs sc_read_args(int64_t B, int64_t T, int64_t M,
                                     int64_t dk, int64_t dv, const float* q,
                                     const void* proj, const float* tau,
                                     double trim_eps, const float* age_w,
-                                    int value_unit_norm, int leaky,
+                                    int age_per_step, int value_unit_norm,
+                                    int leaky,
                                     double alpha, double gamma, double cap,
                                     double eps) {
     rwkv7m::ScreenReadArgs A{};
@@ -492,11 +493,53 @@ rwkv7m::ScreenReadArgs sc_read_args(int64_t B, int64_t T, int64_t M,
     A.tau = tau;
     A.trim_eps = float(trim_eps);
     A.age_w = age_w;
+    A.age_bstride = age_per_step ? T * M : M;
+    A.age_tstride = age_per_step ? M : 0;
     A.value_unit_norm = value_unit_norm != 0;
     A.leaky = leaky != 0;
     A.leaky_alpha = float(alpha);
     A.leaky_gamma = float(gamma);
     A.cap = float(cap);
+    A.eps = float(eps);
+    return A;
+}
+
+int sc_write_checks(const char* fn, int dtype, int64_t B, int64_t T,
+                    int64_t M, int64_t ds, int64_t dk, double floor,
+                    double eps) {
+    RWKV7M_TRY(sc_dims(fn, dtype, B, T, M, ds, dk));
+    if (ds > 1024 || dk > 128)
+        return fail(RWKV7M_ERR_UNSUPPORTED,
+                    std::string(fn) +
+                        ": supported sizes are ds <= 1024, dk <= 128");
+    if (!(floor >= 0.0) || !std::isfinite(floor) || !(eps >= 0.0) ||
+        !std::isfinite(eps))
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": floor and eps must be finite, >= 0");
+    return RWKV7M_OK;
+}
+
+rwkv7m::ScreenWriteArgs sc_write_args(int64_t B, int64_t T, int64_t M,
+                                      int64_t ds, int64_t dk,
+                                      const void* base, const float* st,
+                                      const float* se, const float* kw,
+                                      const float* q_w, const float* tau_w,
+                                      const float* mu, double floor,
+                                      double eps) {
+    rwkv7m::ScreenWriteArgs A{};
+    A.B = B;
+    A.T = T;
+    A.M = M;
+    A.ds = ds;
+    A.dk = int(dk);
+    A.base = base;
+    A.slot_term = st;
+    A.slot_embed = se;
+    A.kw = kw;
+    A.q_w = q_w;
+    A.tau_w = tau_w;
+    A.mu = mu;
+    A.floor = float(floor);
     A.eps = float(eps);
     return A;
 }
@@ -826,10 +869,11 @@ int rwkv7m_screen_slot_scan_backward(
 int rwkv7m_screen_read(int dtype, int64_t B, int64_t T, int64_t M,
                        int64_t dk, int64_t dv, const float* q,
                        const void* proj, const float* tau, double trim_eps,
-                       const float* age_w, int value_unit_norm, int leaky,
-                       double leaky_alpha, double leaky_gamma, double cap,
-                       double eps, void* u, float* rel, float* z_norm,
-                       float* u_norm, void* stream) {
+                       const float* age_w, int age_per_step,
+                       int value_unit_norm, int leaky, double leaky_alpha,
+                       double leaky_gamma, double cap, double eps, void* u,
+                       float* rel, float* z_norm, float* u_norm,
+                       void* stream) {
     const char* fn = "rwkv7m_screen_read";
     g_last_error.clear();
     RWKV7M_TRY(sc_dims(fn, dtype, B, T, M, dk, dv));
@@ -841,8 +885,8 @@ int rwkv7m_screen_read(int dtype, int64_t B, int64_t T, int64_t M,
                             {"u_norm", u_norm}}));
     rwkv7m::ScreenReadArgs A =
         sc_read_args(B, T, M, dk, dv, q, proj, tau, trim_eps, age_w,
-                     value_unit_norm, leaky, leaky_alpha, leaky_gamma, cap,
-                     eps);
+                     age_per_step, value_unit_norm, leaky, leaky_alpha,
+                     leaky_gamma, cap, eps);
     A.u = u;
     A.rel = rel;
     A.z_norm = z_norm;
@@ -856,10 +900,10 @@ int rwkv7m_screen_read(int dtype, int64_t B, int64_t T, int64_t M,
 int rwkv7m_screen_read_backward(
     int dtype, int64_t B, int64_t T, int64_t M, int64_t dk, int64_t dv,
     const float* q, const void* proj, const float* tau, double trim_eps,
-    const float* age_w, int value_unit_norm, int leaky, double leaky_alpha,
-    double leaky_gamma, double cap, double eps, const void* du,
-    const float* d_rel, float* dq, void* d_proj, float* d_tau, float* g_age,
-    void* stream) {
+    const float* age_w, int age_per_step, int value_unit_norm, int leaky,
+    double leaky_alpha, double leaky_gamma, double cap, double eps,
+    const void* du, const float* d_rel, float* dq, void* d_proj,
+    float* d_tau, float* g_age, void* stream) {
     const char* fn = "rwkv7m_screen_read_backward";
     g_last_error.clear();
     RWKV7M_TRY(sc_dims(fn, dtype, B, T, M, dk, dv));
@@ -871,8 +915,8 @@ int rwkv7m_screen_read_backward(
                             {"g_age", g_age}}));
     rwkv7m::ScreenReadArgs A =
         sc_read_args(B, T, M, dk, dv, q, proj, tau, trim_eps, age_w,
-                     value_unit_norm, leaky, leaky_alpha, leaky_gamma, cap,
-                     eps);
+                     age_per_step, value_unit_norm, leaky, leaky_alpha,
+                     leaky_gamma, cap, eps);
     A.du = du;
     A.d_rel = d_rel;
     A.dq = dq;
@@ -881,6 +925,95 @@ int rwkv7m_screen_read_backward(
     A.g_age = g_age;
     return hip_status("screening read backward launch",
                       rwkv7m::launch_screen_read(
+                          dtype == RWKV7M_DTYPE_BF16, true, A,
+                          static_cast<hipStream_t>(stream)));
+}
+
+int rwkv7m_screen_write(int dtype, int64_t B, int64_t T, int64_t M,
+                        int64_t ds, int64_t dk, const void* base,
+                        const float* slot_term, const float* slot_embed,
+                        const float* kw, const float* q_w, const float* tau_w,
+                        const float* mu, double floor, double eps,
+                        const float* slots0, const float* ages0,
+                        void* slots_seq, float* slots32, float* ages_seq,
+                        float* rel_w, float* upd2, float* slots_T,
+                        float* ages_T, void* stream) {
+    const char* fn = "rwkv7m_screen_write";
+    g_last_error.clear();
+    RWKV7M_TRY(sc_write_checks(fn, dtype, B, T, M, ds, dk, floor, eps));
+    if (B == 0 || M == 0 || ds == 0) return RWKV7M_OK;
+    RWKV7M_TRY(sc_need(fn, {{"slot_term", slot_term},
+                            {"slot_embed", slot_embed}, {"kw", kw},
+                            {"tau_w", tau_w}, {"mu", mu}, {"slots0", slots0},
+                            {"ages0", ages0}, {"slots_T", slots_T},
+                            {"ages_T", ages_T}}));
+    if (T > 0)
+        RWKV7M_TRY(sc_need(fn, {{"base", base}, {"q_w", q_w},
+                                {"slots_seq", slots_seq},
+                                {"slots32", slots32}, {"ages_seq", ages_seq},
+                                {"rel_w", rel_w}, {"upd2", upd2}}));
+    rwkv7m::ScreenWriteArgs A = sc_write_args(
+        B, T, M, ds, dk, base, slot_term, slot_embed, kw, q_w, tau_w, mu,
+        floor, eps);
+    A.slots0 = slots0;
+    A.ages0 = ages0;
+    A.slots_seq = slots_seq;
+    A.slots32 = slots32;
+    A.ages_seq = ages_seq;
+    A.rel_w = rel_w;
+    A.upd2 = upd2;
+    A.slots_T = slots_T;
+    A.ages_T = ages_T;
+    return hip_status("screening write launch",
+                      rwkv7m::launch_screen_write(
+                          dtype == RWKV7M_DTYPE_BF16, false, A,
+                          static_cast<hipStream_t>(stream)));
+}
+
+int rwkv7m_screen_write_backward(
+    int dtype, int64_t B, int64_t T, int64_t M, int64_t ds, int64_t dk,
+    const void* base, const float* slot_term, const float* slot_embed,
+    const float* kw, const float* q_w, const float* tau_w, const float* mu,
+    double floor, double eps, const float* slots32, const void* d_slots_seq,
+    const float* d_slots_T, const float* d_rel_w, const float* d_ages_seq,
+    const float* d_ages_T, float* d_pre, float* d_slots0, float* d_ages0,
+    float* d_embed_part, float* d_mu_bm, float* d_kraw, float* dq_w,
+    float* d_tau_w, void* stream) {
+    const char* fn = "rwkv7m_screen_write_backward";
+    g_last_error.clear();
+    RWKV7M_TRY(sc_write_checks(fn, dtype, B, T, M, ds, dk, floor, eps));
+    if (B == 0 || M == 0 || ds == 0) return RWKV7M_OK;
+    RWKV7M_TRY(sc_need(fn, {{"slot_term", slot_term},
+                            {"slot_embed", slot_embed}, {"kw", kw},
+                            {"tau_w", tau_w}, {"mu", mu},
+                            {"d_slots0", d_slots0}, {"d_ages0", d_ages0},
+                            {"d_embed_part", d_embed_part},
+                            {"d_mu_bm", d_mu_bm}}));
+    if (T > 0)
+        RWKV7M_TRY(sc_need(fn, {{"base", base}, {"q_w", q_w},
+                                {"slots32", slots32},
+                                {"d_slots_seq", d_slots_seq},
+                                {"d_pre", d_pre}, {"d_kraw", d_kraw},
+                                {"dq_w", dq_w}, {"d_tau_w", d_tau_w}}));
+    rwkv7m::ScreenWriteArgs A = sc_write_args(
+        B, T, M, ds, dk, base, slot_term, slot_embed, kw, q_w, tau_w, mu,
+        floor, eps);
+    A.slots32 = const_cast<float*>(slots32);
+    A.d_slots_seq = d_slots_seq;
+    A.d_slots_T = d_slots_T;
+    A.d_rel_w = d_rel_w;
+    A.d_ages_seq = d_ages_seq;
+    A.d_ages_T = d_ages_T;
+    A.d_pre = d_pre;
+    A.d_slots0 = d_slots0;
+    A.d_ages0 = d_ages0;
+    A.d_embed_part = d_embed_part;
+    A.d_mu_bm = d_mu_bm;
+    A.d_kraw = d_kraw;
+    A.dq_w = dq_w;
+    A.d_tau_w = d_tau_w;
+    return hip_status("screening write backward launch",
+                      rwkv7m::launch_screen_write(
                           dtype == RWKV7M_DTYPE_BF16, true, A,
                           static_cast<hipStream_t>(stream)));
 }

@@ -131,7 +131,8 @@ struct ScreenReadArgs {
     const void* proj;
     const float* tau;  // one fp32 on the device
     float trim_eps;
-    const float* age_w;  // [B][M] or 0
+    const float* age_w;  // [B][M] or [B][T][M] (see the strides) or 0
+    int64_t age_bstride, age_tstride;  // M, 0 or T * M, M
     int value_unit_norm, leaky;
     float leaky_alpha, leaky_gamma, cap, eps;
     void* u;
@@ -142,6 +143,27 @@ struct ScreenReadArgs {
     void* d_proj;
     float *d_tau, *g_age;  // [B][T], [B][T][M]
 };
+
+// Write phase (read_write): one workgroup per (b, m) walks the steps.
+struct ScreenWriteArgs {
+    int64_t B, T, M, ds;
+    int dk;
+    const void* base;                           // [B][T][ds]
+    const float *slot_term, *slot_embed, *kw;  // [M][ds] x2, [ds][dk]
+    const float *q_w, *tau_w, *mu;             // [B][T][dk], 1, [M]
+    float floor, eps;
+    const float *slots0, *ages0;               // [B][M][ds], [B][M]
+    void* slots_seq;                           // S_t rounded, [B][T][M][ds]
+    float *slots32, *ages_seq, *rel_w, *upd2;  // S_t fp32, [B][T][M] x2, ..
+    float *slots_T, *ages_T;
+    const void* d_slots_seq;                   // backward inputs
+    const float *d_slots_T, *d_rel_w, *d_ages_seq, *d_ages_T;  // may be 0
+    float *d_pre, *d_slots0, *d_ages0, *d_embed_part, *d_mu_bm;
+    float *d_kraw, *dq_w, *d_tau_w;            // [B][T][M][dk] x2, [B][T][M]
+};
+
+hipError_t launch_screen_write(bool bf16, bool backward,
+                               const ScreenWriteArgs& A, hipStream_t stream);
 
 hipError_t launch_screen_scan(bool bf16, bool backward,
                               const ScreenScanArgs& A, hipStream_t stream);

@@ -4,7 +4,8 @@ binding of the ``rwkv7m_screen_*`` entry points of librwkv7m_wkv.so
 
 ``slot_scan`` / ``slot_scan_backward``: the slot recurrence of the
 read-only scan (src/rwkv7m/model/nnx_model.py:1087-1102) for every step at
-once.  ``read`` / ``read_backward``: the per-token read
+once.  ``write`` / ``write_backward``: the read/write phase's recurrence
+(:1040-1047, :1103-1115).  ``read`` / ``read_backward``: the per-token read
 (nnx_model.py:1063-1086).  Tensors are torch device tensors; there is no
 CPU fallback.
 """
@@ -108,10 +109,11 @@ def read(q, proj, tau, age_w, cfg, dv):
     zn = torch.empty(B, T, dtype=torch.float32, device=dev)
     un = torch.empty(B, T, dtype=torch.float32, device=dev)
     sc = _read_scalars(cfg, tau)
+    per_step = int(aw is not None and aw.dim() == 3)
     P = wkv_hip._p
     _call("rwkv7m_screen_read", wkv_hip._dtype_code(proj), B, T, M, dk, dv,
-          P(q), P(proj), P(sc[0]), sc[1], P(aw), *sc[2:], P(u), P(rel), P(zn),
-          P(un), wkv_hip._stream(dev))
+          P(q), P(proj), P(sc[0]), sc[1], P(aw), per_step, *sc[2:], P(u),
+          P(rel), P(zn), P(un), wkv_hip._stream(dev))
     return u, rel, zn, un
 
 
@@ -129,8 +131,72 @@ def read_backward(q, proj, tau, age_w, cfg, dv, du, d_rel=None):
     dtau = torch.empty(B, T, dtype=torch.float32, device=dev)
     g_age = torch.empty(B, T, M, dtype=torch.float32, device=dev)
     sc = _read_scalars(cfg, tau)
+    per_step = int(aw is not None and aw.dim() == 3)
     P = wkv_hip._p
     _call("rwkv7m_screen_read_backward", wkv_hip._dtype_code(proj), B, T, M,
-          dk, dv, P(q), P(proj), P(sc[0]), sc[1], P(aw), *sc[2:], P(du),
-          P(dr), P(dq), P(dproj), P(dtau), P(g_age), wkv_hip._stream(dev))
+          dk, dv, P(q), P(proj), P(sc[0]), sc[1], P(aw), per_step, *sc[2:],
+          P(du), P(dr), P(dq), P(dproj), P(dtau), P(g_age),
+          wkv_hip._stream(dev))
     return dq, dproj, dtau, g_age
+
+
+def _write_common(base, slot_term, slot_embed, kw, q_w, tau_w, mu):
+    return (_c(base), _f32(slot_term), _f32(slot_embed), _f32(kw), _f32(q_w),
+            tau_w.detach().to(torch.float32).reshape(1).contiguous(),
+            _f32(mu))
+
+
+def write(base, slot_term, slot_embed, kw, q_w, tau_w, mu, floor, eps,
+          slots0, ages0):
+    """The write-phase slot recurrence (read_write).  -> (slots_seq
+    [B, T, M, ds] in base's dtype, slots32 fp32, ages_seq [B, T, M], rel_w
+    [B, T, M], upd2 [B, T, M, ceil(ds/64)], slots_T [B, M, ds], ages_T
+    [B, M])."""
+    base, st, se, kw_, qw, tw, mu_ = _write_common(base, slot_term,
+                                                   slot_embed, kw, q_w, tau_w,
+                                                   mu)
+    B, T, ds = base.shape
+    M, dk = st.shape[0], kw_.shape[1]
+    dev = wkv_hip._dev([base, slots0])
+    f = dict(dtype=torch.float32, device=dev)
+    seq = torch.empty(B, T, M, ds, dtype=base.dtype, device=dev)
+    s32 = torch.empty(B, T, M, ds, **f)
+    ages_seq = torch.empty(B, T, M, **f)
+    rel_w = torch.empty(B, T, M, **f)
+    upd2 = torch.empty(B, T, M, (ds + 63) // 64, **f)
+    s_t = torch.empty(B, M, ds, **f)
+    a_t = torch.empty(B, M, **f)
+    P = wkv_hip._p
+    _call("rwkv7m_screen_write", wkv_hip._dtype_code(base), B, T, M, ds, dk,
+          P(base), P(st), P(se), P(kw_), P(qw), P(tw), P(mu_), float(floor),
+          float(eps), P(_f32(slots0)), P(_f32(ages0)), P(seq), P(s32),
+          P(ages_seq), P(rel_w), P(upd2), P(s_t), P(a_t),
+          wkv_hip._stream(dev))
+    return seq, s32, ages_seq, rel_w, upd2, s_t, a_t
+
+
+def write_backward(base, slot_term, slot_embed, kw, q_w, tau_w, mu, floor,
+                   eps, slots32, d_slots_seq, d_slots_T=None, d_rel_w=None,
+                   d_ages_seq=None, d_ages_T=None):
+    """-> (d_pre [B, T, M, ds], d_slots0, d_ages0, d_embed_part [B, M, ds],
+    d_mu_bm [B, M], d_kraw [B, T, M, dk], dq_w [B, T, M, dk], d_tau_w
+    [B, T, M])."""
+    base, st, se, kw_, qw, tw, mu_ = _write_common(base, slot_term,
+                                                   slot_embed, kw, q_w, tau_w,
+                                                   mu)
+    B, T, ds = base.shape
+    M, dk = st.shape[0], kw_.shape[1]
+    dev = wkv_hip._dev([base, slots32])
+    f = dict(dtype=torch.float32, device=dev)
+    d_seq = _c(d_slots_seq).to(base.dtype)
+    outs = [torch.empty(B, T, M, ds, **f), torch.empty(B, M, ds, **f),
+            torch.empty(B, M, **f), torch.empty(B, M, ds, **f),
+            torch.empty(B, M, **f), torch.empty(B, T, M, dk, **f),
+            torch.empty(B, T, M, dk, **f), torch.empty(B, T, M, **f)]
+    P = wkv_hip._p
+    _call("rwkv7m_screen_write_backward", wkv_hip._dtype_code(base), B, T, M,
+          ds, dk, P(base), P(st), P(se), P(kw_), P(qw), P(tw), P(mu_),
+          float(floor), float(eps), P(_f32(slots32)), P(d_seq),
+          P(_f32(d_slots_T)), P(_f32(d_rel_w)), P(_f32(d_ages_seq)),
+          P(_f32(d_ages_T)), *map(P, outs), wkv_hip._stream(dev))
+    return tuple(outs)

@@ -70,6 +70,8 @@ EXPORTED_SYMBOLS = (
     "rwkv7m_screen_slot_scan_backward",
     "rwkv7m_screen_read",
     "rwkv7m_screen_read_backward",
+    "rwkv7m_screen_write",
+    "rwkv7m_screen_write_backward",
 )
 
 LAYOUTS = ("tbhn", "bthn")
@@ -140,11 +142,16 @@ def load_library(path: str | None = None):
         lib.rwkv7m_screen_slot_scan_backward.argtypes = (
             sdims + [vp] * 10 + [i64, vp])
         rdims = [i32, i64, i64, i64, i64, i64, vp, vp, vp, f64, vp, i32,
-                 i32, f64, f64, f64, f64]
+                 i32, i32, f64, f64, f64, f64]
         lib.rwkv7m_screen_read.restype = i32
         lib.rwkv7m_screen_read.argtypes = rdims + [vp] * 5
         lib.rwkv7m_screen_read_backward.restype = i32
         lib.rwkv7m_screen_read_backward.argtypes = rdims + [vp] * 7
+        wdims = [i32] + [i64] * 5 + [vp] * 7 + [f64, f64]
+        lib.rwkv7m_screen_write.restype = i32
+        lib.rwkv7m_screen_write.argtypes = wdims + [vp] * 10
+        lib.rwkv7m_screen_write_backward.restype = i32
+        lib.rwkv7m_screen_write_backward.argtypes = wdims + [vp] * 15
         if path is None:
             _lib = lib
         return lib

@@ -21,8 +21,11 @@ whole-sequence work:
 5. the output projection and the gated residual (GEMM, elementwise).
 
 Steps 2 and 4 have HIP backward kernels; the rest is differentiated by
-torch autograd.  The write phase (``read_write``) is not implemented and
-raises.  Arithmetic follows the reference's dtypes: projections in the
+torch autograd.  The read/write phase (``read_write`` with
+``use_write_screening``) replaces step 2 with the write recurrence (HIP
+kernels ``rwkv7m_screen_write`` and its backward), whose update strength
+depends on the slots' own write keys, and feeds the read per-step ages.
+Arithmetic follows the reference's dtypes: projections in the
 compute dtype, statistics, norms, the slots and the usage EMA in fp32.
 """
 
@@ -160,7 +163,9 @@ class _ScreenRead(torch.autograd.Function):
                              device=proj.device)
         dq, dproj, dtau, g_age = screening_hip.read_backward(
             q, proj, tau, age_w, ctx.cfg, ctx.dv, du, d_rel)
-        d_age = g_age.sum(1) if age_w is not None else None
+        d_age = None
+        if age_w is not None:  # [B, M] (summed over steps) or [B, T, M]
+            d_age = g_age.sum(1) if age_w.dim() == 2 else g_age
         return (dq, dproj, dtau.sum().reshape(tau.shape).to(tau.dtype),
                 d_age, None, None)
 
@@ -185,6 +190,44 @@ class _SlotProjection(torch.autograd.Function):
         part = torch.bmm(seq.reshape(B, -1, ds).transpose(1, 2).contiguous(),
                          g.reshape(B, -1, g.shape[-1]))
         return d_seq, part.float().sum(0).to(kv.dtype)
+
+
+class _WriteScan(torch.autograd.Function):
+    """The read/write phase's slot recurrence (HIP kernels
+    rwkv7m_screen_write / _backward)."""
+
+    @staticmethod
+    def forward(ctx, base, slot_term, slot_embed, kw, q_w, tau_w, mu,
+                slots0, ages0, floor, eps):
+        seq, s32, ages_seq, rel_w, upd2, s_t, a_t = screening_hip.write(
+            base, slot_term, slot_embed, kw, q_w, tau_w, mu, floor, eps,
+            slots0, ages0)
+        ctx.save_for_backward(base, slot_term, slot_embed, kw, q_w, tau_w,
+                              mu, s32)
+        ctx.floor, ctx.eps = floor, eps
+        ctx.mark_non_differentiable(upd2)
+        return seq, ages_seq, rel_w, upd2, s_t, a_t
+
+    @staticmethod
+    def backward(ctx, d_seq, d_ages_seq, d_rel_w, _d_upd2, d_s_t, d_a_t):
+        base, slot_term, slot_embed, kw, q_w, tau_w, mu, s32 = \
+            ctx.saved_tensors
+        if d_seq is None:
+            d_seq = torch.zeros(s32.shape, dtype=base.dtype,
+                                device=base.device)
+        (d_pre, d_s0, d_a0, d_emb, d_mu, d_kraw, dq_w,
+         d_tau) = screening_hip.write_backward(
+            base, slot_term, slot_embed, kw, q_w, tau_w, mu, ctx.floor,
+            ctx.eps, s32, d_seq, d_s_t, d_rel_w, d_ages_seq, d_a_t)
+        B, T, M, ds = s32.shape
+        skey = (s32 + slot_embed.float()[None, None]).to(base.dtype).float()
+        d_kw = torch.bmm(skey.reshape(B, -1, ds).transpose(1, 2).contiguous(),
+                         d_kraw.reshape(B, -1, kw.shape[1])).sum(0)
+        return (d_pre.sum(2).to(base.dtype),
+                d_pre.sum((0, 1)).to(slot_term.dtype),
+                d_emb.sum(0).to(slot_embed.dtype), d_kw.to(kw.dtype),
+                dq_w.sum(2), d_tau.sum().reshape(tau_w.shape).to(tau_w.dtype),
+                d_mu.sum(0).to(mu.dtype), d_s0, d_a0, None, None)
 
 
 def _ema_time_mean(r_bar: torch.Tensor, u0: torch.Tensor,
@@ -235,6 +278,10 @@ class StateLevelScreening(torch.nn.Module):
         self.slot_embed = torch.nn.Parameter(
             (0.02 * torch.randn(M, ds, generator=g)).to(**kw))
         self.mu_by_bank_raw = const((3,), 0.0)
+        if config.use_write_screening:  # nnx_model.py:977-1000
+            self.q_proj_w = lecun(2 * C, dk)
+            self.k_proj_w = lecun(ds, dk)
+            self.tau_w_raw = const((), _theta_from_tau(config.tau_init))
         fixed = [None if hl is None else -math.expm1(-math.log(2.0) / hl)
                  for hl in (config.short_half_life_tokens,
                             config.mid_half_life_tokens,
@@ -268,10 +315,11 @@ class StateLevelScreening(torch.nn.Module):
         del deterministic
         cfg = self.config
         phase = normalize_phase(phase)
-        if phase == "read_write" and cfg.use_write_screening:
-            raise NotImplementedError(
-                "the read_write screening phase is not implemented on this "
-                "backend; use phase='read_screening_only'")
+        write = phase == "read_write" and cfg.use_write_screening
+        if write and not hasattr(self, "k_proj_w"):
+            raise ValueError("the read_write phase needs the write "
+                             "parameters: build the module with "
+                             "use_write_screening=True")
         eps = cfg.eps
         B, T, C = x_seq.shape
         cd = self.compute_dtype or x_seq.dtype
@@ -288,11 +336,27 @@ class StateLevelScreening(torch.nn.Module):
         base = (x_ln @ dker[:C] + h_base_seq.to(cd) @ dker[C:2 * C]
                 + self.delta_bias.to(cd))
         slot_term = (self.slot_embed.to(cd) @ dker[2 * C:]).float()
-        age_w = (torch.sigmoid((cfg.age_ref - state.ages.float())
+        if write:
+            # nnx_model.py:1040-1047: the write query and threshold
+            q_w = torch.cat([x_ln, h_base_seq.float().to(cd)], -1) @ \
+                self.q_proj_w.to(cd)
+            q_w = q_w.float()
+            q_w = q_w / torch.sqrt((q_w * q_w).sum(-1, keepdim=True)
+                                   + eps * eps)
+            tau_w = 2.0 * torch.sigmoid(self.tau_w_raw.float()) - 1.0
+            kw = self.k_proj_w.to(cd)
+            seq, ages_seq, rel_w, upd2, slots_t, ages_t = _WriteScan.apply(
+                base, slot_term, self.slot_embed.float(), kw, q_w, tau_w, mu,
+                state.slots.float(), state.ages.float(),
+                float(cfg.write_rel_floor), float(eps))
+            ages_for_read = ages_seq
+        else:
+            seq, slots_t, upd2 = _SlotScan.apply(base, slot_term, mu,
+                                                 state.slots.float())
+            rel_w, ages_t, ages_for_read = None, state.ages, state.ages
+        age_w = (torch.sigmoid((cfg.age_ref - ages_for_read.float())
                                / (cfg.age_sigma + eps))
                  if cfg.use_age_mask else None)
-        seq, slots_t, upd2 = _SlotScan.apply(base, slot_term, mu,
-                                             state.slots.float())
         kv = torch.cat([self.k_proj_r, self.v_proj], dim=1).to(cd)
         proj = _SlotProjection.apply(seq, kv)
         u, rel, zn, un = _ScreenRead.apply(q, proj, tau, age_w, cfg,
@@ -301,16 +365,19 @@ class StateLevelScreening(torch.nn.Module):
         h = (h_base_seq.float() + lam * gate * read.float()).to(
             h_base_seq.dtype)
         d = float(cfg.usage_ema_decay)
+        activity = rel if rel_w is None else torch.maximum(rel, rel_w)
         w = (1.0 - d) * d ** torch.arange(T - 1, -1, -1, device=rel.device,
                                           dtype=torch.float32)
         usage_t = (d ** T) * state.usage_ema.float() + torch.einsum(
-            "btm,t->bm", rel, w)
-        new_state = ScreenState(slots_t.to(state.slots.dtype), state.ages,
+            "btm,t->bm", activity, w)
+        new_state = ScreenState(slots_t.to(state.slots.dtype),
+                                ages_t.to(state.ages.dtype),
                                 usage_t.to(state.usage_ema.dtype))
         with torch.no_grad():
             r = rel.detach()
             zero = torch.zeros((), device=r.device)
-            u_mean = _ema_time_mean(r.mean((0, 2)).double(),
+            act = activity.detach()
+            u_mean = _ema_time_mean(act.mean((0, 2)).double(),
                                     state.usage_ema.double().mean(), d)
             stats = {
                 "rel_read_mean": r.mean(),
@@ -320,11 +387,13 @@ class StateLevelScreening(torch.nn.Module):
                 "u_norm_mean": un.mean(),
                 "tau_r": tau.detach(),
                 "lambda_screen": lam.detach(),
-                "rel_write_mean": zero,
-                "rel_write_effective_mean": zero,
+                "rel_write_mean": zero if rel_w is None else rel_w.mean(),
+                "rel_write_effective_mean": (
+                    zero if rel_w is None else torch.clamp(
+                        rel_w, min=cfg.write_rel_floor).mean()),
                 "slot_update_norm_mean": upd2.sum(-1).sqrt().mean(),
                 "slot_usage_ema_mean": u_mean.float(),
-                "tau_w": zero,
+                "tau_w": zero if rel_w is None else tau_w.detach(),
             }
         return h, new_state, stats
 

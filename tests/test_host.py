@@ -397,11 +397,11 @@ def test_screening_abi_checks_requests_before_any_device_call(lib):
     assert b"slot_term is NULL" in lib.rwkv7m_last_error()
     assert scan(1, 0, 8, 4, 64, *([None] * 8), 0, None) == 0  # no batch
     read = lib.rwkv7m_screen_read
-    args = [fake, fake, fake, 1e-6, None, 1, 0, 0.0, 8.0, 1.0, 1e-6]
+    args = [fake, fake, fake, 1e-6, None, 0, 1, 0, 0.0, 8.0, 1.0, 1e-6]
     assert read(1, 2, 8, 65, 64, 64, *args, *([fake] * 4), None) == 2
     assert b"M <= 64" in lib.rwkv7m_last_error()
     assert read(1, 2, 8, 16, 64, 600, *args, *([fake] * 4), None) == 2
-    bad_cap = args[:9] + [0.0] + args[10:]
+    bad_cap = args[:10] + [0.0] + args[11:]
     assert read(1, 2, 8, 16, 64, 64, *bad_cap, *([fake] * 4), None) == 1
     assert b"cap" in lib.rwkv7m_last_error()
     no_tau = args[:2] + [None] + args[3:]

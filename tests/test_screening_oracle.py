@@ -34,6 +34,10 @@ OPTIONS = [dict(), dict(use_age_mask=True), dict(use_leaky_warmup=True,
 
 
 def _case(B=2, T=5, C=8, ds=6, dk=4, dv=5, M=3, seed=0, **opt):
+    rng = np.random.default_rng(seed + 1000)
+    wparams = {"q_proj_w": rng.normal(size=(2 * C, dk)) / np.sqrt(2 * C),
+               "k_proj_w": rng.normal(size=(ds, dk)) / np.sqrt(ds),
+               "tau_w_raw": np.array(-0.8)}
     rng = np.random.default_rng(seed)
     cfg = so.default_config(d_model=C, d_slot=ds, d_k=dk, d_v=dv, n_slots=M,
                             bank_ids=tuple(int(i) for i in
@@ -51,6 +55,8 @@ def _case(B=2, T=5, C=8, ds=6, dk=4, dv=5, M=3, seed=0, **opt):
          "tau_r_raw": np.array(-0.4), "lambda_raw": np.array(0.3),
          "slot_embed": 0.5 * rng.normal(size=(M, ds)),
          "mu_by_bank_raw": rng.normal(size=3)}
+    if opt.get("use_write_screening"):
+        P.update(wparams)
     x = rng.normal(size=(B, T, C))
     h = rng.normal(size=(B, T, C))
     slots = 0.5 * rng.normal(size=(B, M, ds))
@@ -204,3 +210,87 @@ def test_pins_catch_planted_mistakes(monkeypatch):
         {k: _t(v) for k, v in P.items()}, cfg)
     assert np.max(np.abs(s_bad - s_t.numpy())) > 1e-3
     assert np.max(np.abs(h_bad - h_t.numpy())) > 1e-6
+
+
+WRITE = dict(use_write_screening=True, write_rel_floor=0.05)
+
+
+@pytest.mark.parametrize("opt", [dict(), dict(use_age_mask=True)], ids=str)
+def test_write_phase_restatements_agree(opt):
+    x, h, slots, ages, usage, P, cfg = _case(seed=11, T=7, **WRITE, **opt)
+    hn, (sn, an, un), stats = so.read_forward(x, h, slots, ages, usage, P,
+                                              cfg, phase="read_write")
+    ht, st, ut = so.read_forward_torch(
+        _t(x), _t(h), _t(slots), _t(ages), _t(usage),
+        {k: _t(v) for k, v in P.items()}, cfg, phase="read_write")
+    np.testing.assert_allclose(hn, ht.numpy(), rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(sn, st.numpy(), rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(un, ut.numpy(), rtol=1e-12, atol=1e-13)
+    # the write phase changes the slots, ages and statistics
+    _, (s_ro, a_ro, _), st_ro = so.read_forward(x, h, slots, ages, usage, P,
+                                                cfg)
+    assert np.max(np.abs(sn - s_ro)) > 1e-6
+    assert np.array_equal(a_ro, ages) and not np.array_equal(an, ages)
+    assert stats["rel_write_effective_mean"] >= 0.05 - 1e-12
+    assert st_ro["rel_write_mean"] == 0.0 and stats["tau_w"] != 0.0
+
+
+def test_write_phase_ages_and_floor():
+    # ages count steps without a write and reset where rel_w > 1e-3; with a
+    # query orthogonal to every write key nothing is written and the
+    # strength is the floor: slots move by mu * floor per step
+    x, h, slots, ages, usage, P, cfg = _case(seed=12, T=3, **WRITE)
+    P0 = dict(P, q_proj_w=np.zeros_like(P["q_proj_w"]),
+              tau_w_raw=np.array(0.0))
+    _, (s_t, a_t, _), st = so.read_forward(x, h, slots, ages, usage, P0,
+                                           cfg, phase="read_write")
+    np.testing.assert_allclose(a_t, ages + 3.0)
+    assert st["rel_write_mean"] == 0.0
+    cfg_ro = dict(cfg, mu_short_max=cfg["mu_short_max"] * 0.05,
+                  mu_mid_max=cfg["mu_mid_max"] * 0.05,
+                  mu_long_max=cfg["mu_long_max"] * 0.05)
+    _, (s_ro, _, _), _ = so.read_forward(x, h, slots, ages, usage, P0,
+                                         cfg_ro)
+    np.testing.assert_allclose(s_t, s_ro, rtol=1e-12, atol=1e-14)
+
+
+def test_write_phase_autograd_matches_finite_differences():
+    x, h, slots, ages, usage, P, cfg = _case(B=1, T=3, C=4, ds=3, dk=3,
+                                             dv=3, M=2, seed=13,
+                                             use_age_mask=True, **WRITE)
+    rng = np.random.default_rng(130)
+    cot_h = rng.normal(size=x.shape)
+    cot_s = rng.normal(size=slots.shape)
+    cot_u = rng.normal(size=usage.shape)
+    names = ["x", "h", "slots", "usage"] + sorted(P)
+    arrays = dict(x=x, h=h, slots=slots, usage=usage, **P)
+    tin = {k: _t(v, True) for k, v in arrays.items()}
+    ht, st, ut = so.read_forward_torch(
+        tin["x"], tin["h"], tin["slots"], _t(ages), tin["usage"],
+        {k: tin[k] for k in P}, cfg, phase="read_write")
+    loss = ((ht * _t(cot_h)).sum() + (st * _t(cot_s)).sum()
+            + (ut * _t(cot_u)).sum())
+    grads = dict(zip(names, torch.autograd.grad(loss, [tin[n]
+                                                       for n in names])))
+
+    def objective(a):
+        hh, (ss, _, uu), _ = so.read_forward(
+            a["x"], a["h"], a["slots"], ages, a["usage"],
+            {k: a[k] for k in P}, cfg, phase="read_write")
+        return (hh * cot_h).sum() + (ss * cot_s).sum() + (uu * cot_u).sum()
+
+    eps = 1e-6
+    for n in names:
+        flat = np.array(arrays[n], np.float64).reshape(-1)
+        g = grads[n].numpy().reshape(-1)
+        for i in range(flat.size):
+            a = {k: np.array(v, np.float64) for k, v in arrays.items()}
+            f = a[n].reshape(-1)
+            f[i] = flat[i] + eps
+            a[n] = f.reshape(np.shape(arrays[n]))
+            fp = objective(a)
+            f[i] = flat[i] - eps
+            fm = objective(a)
+            fd = (fp - fm) / (2 * eps)
+            assert abs(fd - g[i]) < 1e-6 * max(1.0, abs(fd)), (n, i, fd,
+                                                                g[i])

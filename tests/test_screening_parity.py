@@ -29,6 +29,10 @@ PNAME = {"ln_scale": "screen_ln_scale", "ln_bias": "screen_ln_bias"}
 
 
 def _case(B, T, C, ds, dk, dv, M, seed, **opt):
+    rng = np.random.default_rng(seed + 1000)
+    wparams = {"q_proj_w": rng.normal(size=(2 * C, dk)) / np.sqrt(2 * C),
+               "k_proj_w": rng.normal(size=(ds, dk)) / np.sqrt(ds),
+               "tau_w_raw": np.array(-1.2)}
     rng = np.random.default_rng(seed)
     cfg = so.default_config(d_model=C, d_slot=ds, d_k=dk, d_v=dv, n_slots=M,
                             bank_ids=tuple(int(i) for i in
@@ -46,6 +50,8 @@ def _case(B, T, C, ds, dk, dv, M, seed, **opt):
          "tau_r_raw": np.array(-1.0), "lambda_raw": np.array(0.3),
          "slot_embed": 0.5 * rng.normal(size=(M, ds)),
          "mu_by_bank_raw": rng.normal(size=3)}
+    if opt.get("use_write_screening"):
+        P.update(wparams)
     x = rng.normal(size=(B, T, C))
     h = rng.normal(size=(B, T, C))
     slots = 0.5 * rng.normal(size=(B, M, ds))
@@ -74,7 +80,7 @@ def _err(got, want):
         got.detach().double().cpu().numpy(), np.asarray(want, np.float64))
 
 
-def _run(case, dtype, grad=False):
+def _run(case, dtype, grad=False, phase="read_screening_only"):
     from rwkv7m_amd.screening import ScreenState
     x, h, slots, ages, usage, P, cfg = case
     mod = _module(P, cfg, dtype)
@@ -86,7 +92,7 @@ def _run(case, dtype, grad=False):
         xd.requires_grad_(True)
         hd.requires_grad_(True)
         st = ScreenState(*(t.requires_grad_(True) for t in st))
-    out, new, stats = mod(xd, hd, st)
+    out, new, stats = mod(xd, hd, st, phase=phase)
     return mod, xd, hd, st, out, new, stats
 
 
@@ -175,16 +181,21 @@ def test_preset_sizes_forward(hip_lib):
 
 def test_phases(hip_lib):
     from rwkv7m_amd.screening import normalize_phase
-    case = _case(1, 4, 64, 64, 32, 64, 3, seed=2, use_write_screening=False)
+    case = _case(1, 4, 64, 64, 32, 64, 3, seed=2)
     mod, xd, hd, st, out, _, _ = _run(case, torch.float32)
     out2, _, _ = mod(xd, hd, st, phase="read_only")
     assert torch.equal(out, out2)
     assert normalize_phase("read_only") == "read_screening_only"
     with pytest.raises(ValueError, match="Unknown phase"):
         mod(xd, hd, st, phase="write_only")
+    # read_write without write screening is the read-only call
+    out3, _, _ = mod(xd, hd, st, phase="read_write")
+    assert torch.equal(out, out3)
+    # write screening switched on after construction: no write parameters
     mod.config.use_write_screening = True
-    with pytest.raises(NotImplementedError, match="read_write"):
+    with pytest.raises(ValueError, match="write parameters"):
         mod(xd, hd, st, phase="read_write")
+
 
 
 @pytest.mark.parametrize("pieces", [(1,) * 6, (33, 1, 37), (70, 1)])
@@ -272,3 +283,76 @@ def test_graph_capture_replays_match_eager(hip_lib):
         for k, (a, b) in enumerate(zip(grads, ref_g)):
             torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6,
                                        msg=f"replay {i} gradient {k}")
+
+
+WRITE = dict(use_write_screening=True, write_rel_floor=0.05)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("opt", [dict(), dict(use_age_mask=True)], ids=str)
+def test_write_phase_forward_matches_oracle(hip_lib, opt, dtype):
+    case = _case(2, 29, 64, 80, 32, 80, 5, seed=51, **WRITE, **opt)
+    name = f"screening read_write fwd {opt} {dtype}"
+    print("case:", name, flush=True)
+    _, _, _, _, out, new, stats = _run(case, dtype, phase="read_write")
+    torch.cuda.synchronize()
+    x, h, slots, ages, usage, P, cfg = case
+    eh, (es, ea, eu), est = so.read_forward(_rnd(x, dtype), _rnd(h, dtype),
+                                            slots, ages, usage, P, cfg,
+                                            phase="read_write")
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    for n, g, w in (("h", out, eh), ("slots_T", new.slots, es),
+                    ("usage_T", new.usage_ema, eu)):
+        e = _err(g, w)
+        assert e <= tol, f"{name} {n}: {e:.3e} > {tol}"
+    if dtype == torch.float32:
+        assert torch.equal(new.ages.cpu(), torch.tensor(ea,
+                                                        dtype=torch.float32))
+    assert est["rel_write_mean"] > 0.0
+    for k in so.STAT_NAMES:
+        g, w = float(stats[k]), est[k]
+        assert abs(g - w) <= tol * max(1.0, abs(w)), f"{name} stat {k}"
+
+
+@pytest.mark.parametrize("opt", [dict(), dict(use_age_mask=True)], ids=str)
+def test_write_phase_backward_matches_autograd_oracle(hip_lib, opt):
+    case = _case(2, 17, 64, 80, 32, 80, 5, seed=61, **WRITE, **opt)
+    name = f"screening read_write bwd {opt}"
+    print("case:", name, flush=True)
+    mod, xd, hd, st, out, new, _ = _run(case, torch.float32, grad=True,
+                                        phase="read_write")
+    x, h, slots, ages, usage, P, cfg = case
+    rng = np.random.default_rng(9)
+    cot_h = rng.normal(size=x.shape)
+    cot_s = rng.normal(size=slots.shape)
+    cot_u = rng.normal(size=usage.shape)
+    dev = dict(dtype=torch.float32, device="cuda")
+    loss = ((out * torch.tensor(cot_h, **dev)).sum()
+            + (new.slots * torch.tensor(cot_s, **dev)).sum()
+            + (new.usage_ema * torch.tensor(cot_u, **dev)).sum())
+    loss.backward()
+    torch.cuda.synchronize()
+    arrays = dict(x=x, h=h, slots=slots, ages=ages, usage=usage, **P)
+    tin = {k: torch.tensor(np.asarray(v, np.float64), requires_grad=True)
+           for k, v in arrays.items()}
+    ht, s_t, u_t = so.read_forward_torch(
+        tin["x"], tin["h"], tin["slots"], tin["ages"], tin["usage"],
+        {k: tin[k] for k in P}, cfg, phase="read_write")
+    ref_loss = ((ht * torch.tensor(cot_h)).sum()
+                + (s_t * torch.tensor(cot_s)).sum()
+                + (u_t * torch.tensor(cot_u)).sum())
+    names = list(arrays)
+    want = dict(zip(names, torch.autograd.grad(ref_loss,
+                                               [tin[n] for n in names],
+                                               allow_unused=True)))
+    got = {"x": xd.grad, "h": hd.grad, "slots": st.slots.grad,
+           "ages": st.ages.grad, "usage": st.usage_ema.grad}
+    got.update({k: getattr(mod, PNAME.get(k, k)).grad for k in P})
+    for n in names:
+        w = want[n]
+        if w is None or not np.any(w.numpy()):
+            assert got[n] is None or not torch.any(got[n]), f"{name} d{n}"
+            continue
+        assert got[n] is not None, f"{name} d{n} missing"
+        e = _err(got[n], w.numpy())
+        assert e <= 1e-4, f"{name} d{n}: {e:.3e}"

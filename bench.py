@@ -55,6 +55,9 @@ def parse_args():
                         "batch-major WKV, consumer), forward and backward; "
                         "screening: the state-level screening read path of "
                         "the 0.185B preset at config 1's B and T")
+    p.add_argument("--screen-phase", default="read_screening_only",
+                   choices=("read_screening_only", "read_write"),
+                   help="screening phase for --path screening")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="target CPU-baseline sample duration (0 = skip)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -440,7 +443,8 @@ def bench_timemix(args, cfg):
     print(json.dumps(result), flush=True)
 
 
-def screening_cpu_baseline(cfg_d, P, B, T, target_s):
+def screening_cpu_baseline(cfg_d, P, B, T, target_s,
+                           phase="read_screening_only"):
     """Time the CPU restatement of the reference's read-only screening scan
     (numpy float64, one step per token, forward only) on a reduced T."""
     import numpy as np
@@ -455,7 +459,7 @@ def screening_cpu_baseline(cfg_d, P, B, T, target_s):
         h = rng.normal(size=(B, t, C))
         t0 = time.perf_counter()
         so.read_forward(x, h, np.zeros((B, M, ds)), np.zeros((B, M)),
-                        np.zeros((B, M)), P, cfg_d)
+                        np.zeros((B, M)), P, cfg_d, phase=phase)
         return time.perf_counter() - t0
 
     dt = run(8)
@@ -469,7 +473,7 @@ def screening_cpu_baseline(cfg_d, P, B, T, target_s):
         "unit": "tokens/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"numpy float64 per-step scan of the read-only screening "
+        "sample": (f"numpy float64 per-step scan of the {phase} screening "
                    f"(the reference's algorithm), forward only, B={B} T={t}, "
                    f"{reps} run(s), {dt:.1f} s"),
     }
@@ -482,8 +486,9 @@ def bench_screening(args):
     B=8, T=512, bf16: one step = StateLevelScreening forward and the
     backward of all its inputs and parameters from a cotangent of h, captured
     in a HIP graph and replayed (``eager_ms_per_step``: the same step
-    launched op by op).  The four HIP kernels are also timed alone with HIP
-    events."""
+    launched op by op).  The HIP kernels (the slot scan, or in phase
+    read_write the write recurrence, and the read) are also timed alone with
+    HIP events."""
     import numpy as np
     import torch
 
@@ -495,7 +500,9 @@ def bench_screening(args):
     B, T = 8, 512
     cfg_d = so.default_config(d_model=768, d_slot=128, d_k=64, d_v=64,
                               n_slots=16,
-                              bank_ids=(0,) * 8 + (1,) * 4 + (2,) * 4)
+                              bank_ids=(0,) * 8 + (1,) * 4 + (2,) * 4,
+                              use_write_screening=True)
+    phase = args.screen_phase
     cfg = ScreeningConfig(**cfg_d)
     dev = torch.device("cuda:0")
     mod = StateLevelScreening(cfg, compute_dtype=torch.bfloat16, device=dev)
@@ -511,7 +518,7 @@ def bench_screening(args):
     stream = torch.cuda.current_stream(dev)
 
     def step():
-        out, new, _ = mod(x, h, state)
+        out, new, _ = mod(x, h, state, phase=phase)
         (out.float() * dh.float()).sum().backward()
         return out
 
@@ -548,7 +555,7 @@ def bench_screening(args):
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
 
-    # the four kernels alone, on the step's shapes
+    # the kernels alone, on the step's shapes
     base = torch.randn(B, T, 128, generator=gen, device=dev).to(torch.bfloat16)
     st = 0.3 * torch.randn(16, 128, generator=gen, device=dev)
     mu = torch.full((16,), 0.02, device=dev)
@@ -574,6 +581,26 @@ def bench_screening(args):
             q, proj, tau, None, cfg, 64, du),
                      2 * B * T * 16 * 128 * 2 + B * T * 64 * (4 + 2 + 4)),
     }
+    if phase == "read_write":
+        # the write-phase recurrence replaces the slot scan
+        se = 0.1 * torch.randn(16, 128, generator=gen, device=dev)
+        kw = torch.randn(128, 64, generator=gen, device=dev) / 128 ** 0.5
+        tau_w = torch.tensor(0.1, device=dev)
+        ages0 = torch.zeros(B, 16, device=dev)
+        wargs = (base, st, se, kw, q, tau_w, mu, 0.05, 1e-6)
+        wout = screening_hip.write(*wargs, state.slots, ages0)
+        wseq, ws32 = wout[0], wout[1]
+        dwseq = torch.randn_like(wseq)
+        btm = B * T * 16
+        del calls["scan_fwd"], calls["scan_bwd"]
+        calls["write_fwd"] = (
+            lambda: screening_hip.write(*wargs, state.slots, ages0),
+            B * T * 128 * 2 + B * T * 64 * 4 + btm * 128 * (2 + 4)
+            + btm * 16)
+        calls["write_bwd"] = (
+            lambda: screening_hip.write_backward(*wargs, ws32, dwseq),
+            B * T * 128 * 2 + B * T * 64 * 4 + btm * 128 * (4 + 2 + 4)
+            + btm * 64 * 8 + btm * 4)
     kernels = {}
     for name, (fn, nbytes) in calls.items():
         fn()
@@ -591,7 +618,7 @@ def bench_screening(args):
     dominant = max(kernels, key=lambda n: kernels[n]["ms"])
     ach = kernels[dominant]["GB/s"]
     result = {
-        "metric": ("screening read path fwd+bwd tokens/sec at the 0.185B "
+        "metric": (f"screening {phase} fwd+bwd tokens/sec at the 0.185B "
                    "preset (B=8, T=512, bf16)"),
         "value": B * T / (ms_per_step / 1e3),
         "unit": "tokens/s",
@@ -605,10 +632,10 @@ def bench_screening(args):
         "dtype": "bf16",
         "data": "synthetic (normal activations, random-init parameters)",
         "config": {
-            "workload": ("StateLevelScreening read_screening_only fwd+bwd, "
+            "workload": (f"StateLevelScreening {phase} fwd+bwd, "
                          "0.185B preset (d_model 768, d_slot 128, d_k 64, "
                          "d_v 64, 16 slots), B=8 T=512"),
-            "B": B, "T": T,
+            "B": B, "T": T, "phase": phase,
         },
         "roofline": {
             "bound": "hbm",
@@ -629,8 +656,11 @@ def bench_screening(args):
                                          "ln_bias": "screen_ln_bias"}.get(
                                              k, k)).detach().double().cpu())
              for k in so.PARAM_NAMES}
+        if phase == "read_write":
+            for k in ("q_proj_w", "k_proj_w", "tau_w_raw"):
+                P[k] = np.asarray(getattr(mod, k).detach().double().cpu())
         result["cpu_baseline"] = screening_cpu_baseline(
-            cfg_d, P, B, T, args.cpu_seconds)
+            cfg_d, P, B, T, args.cpu_seconds, phase)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

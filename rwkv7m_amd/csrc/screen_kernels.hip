@@ -41,12 +41,31 @@ constexpr int kScreenChunk = 32;  // steps per chunk of the slot scan
 constexpr int kKJ = 2;            // key channels per lane (d_k <= 128)
 constexpr int kVJ = 8;  // value channels per lane (d_v <= 512)
 
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m);
-    return x;
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(
+        0, __float_as_int(x), CTRL, 0xf, 0xf, false));
 }
 
+__device__ __forceinline__ float lane_value(float x, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+// Sum over the 64 lanes of a wave (every lane active), the same bits in every
+// lane: DPP butterflies inside each 16-lane row (quad_perm [1,0,3,2],
+// [2,3,0,1], row_half_mirror, row_mirror), then the four row sums read from
+// lanes 0, 16, 32 and 48 and added pairwise.
+__device__ __forceinline__ float wave_sum(float x) {
+    x += dpp<0xB1>(x);
+    x += dpp<0x4E>(x);
+    x += dpp<0x141>(x);
+    x += dpp<0x140>(x);
+    return (lane_value(x, 0) + lane_value(x, 16)) +
+           (lane_value(x, 32) + lane_value(x, 48));
+}
+
+__device__ __forceinline__ float cvt(float x) { return x; }
+__device__ __forceinline__ float cvt(bf16_t x) { return bf16_to_f32(x); }
 __device__ __forceinline__ float ld1(const float* p) { return *p; }
 __device__ __forceinline__ float ld1(const bf16_t* p) {
     return bf16_to_f32(*p);
@@ -567,28 +586,81 @@ __global__ __launch_bounds__(256) void screen_read_bwd_kernel(
 constexpr int kWThreads = 256;
 constexpr int kWMaxCh = 4;  // channels per thread (d_slot <= 1024)
 
-constexpr int kWLdsWeights = 24576;  // fp32 weights staged in LDS up to 96 KB
+constexpr int kWLdsWeights = 16384;  // fp32 weights staged in LDS up to 64 KB
+// Per-step inputs are staged through LDS a chunk of steps at a time: up to
+// kWStage floats per staged array, kWStage / kWThreads per thread.
+constexpr int kWStage = 4096;
+constexpr int kWPer = kWStage / kWThreads;
+constexpr int kWMaxSteps = 32;
 
-struct WriteSmem {
-    float sk[kWThreads * kWMaxCh];  // the step's write-key input / d input
+struct alignas(16) WriteSmem {
+    float sk[kWThreads * kWMaxCh];  // the step's write-key input
     float red[4][128];              // GEMV partials per channel quarter
     float dk[128];                  // d k_raw (backward)
     float scal[8];
+    float q[kWStage];               // the chunk's write queries [u][dk]
+    float x0[kWStage];              // forward: delta; backward: tanh
+    float x1[kWStage];              // backward: S_t (fp32)
+    float x2[kWStage];              // backward: d slots_seq
+    float drel[kWMaxSteps], dage[kWMaxSteps];
 };
 
-// k_raw[j] = sum_c sk[c] W[c][j]: thread (part, j) sums its channel quarter;
-// wave 0 adds the quarters.  Returns k_raw for j = lane, lane + 64 in wave 0
-// (other waves: unspecified).
-// The write-key weights [ds][dk]: staged in dynamic LDS when they fit.
-__device__ __forceinline__ const float* write_weights(const ScreenWriteArgs& A,
-                                                      float* lds) {
-    const int n = int(A.ds) * A.dk;
-    if (n > kWLdsWeights) return A.kw;
-    for (int i = threadIdx.x; i < n; i += kWThreads) lds[i] = A.kw[i];
-    __syncthreads();
-    return lds;
+// Steps per staged chunk.
+__device__ __forceinline__ int write_chunk(int ds) {
+    const int n = kWStage / ds;
+    return n < kWMaxSteps ? n : kWMaxSteps;
 }
 
+// The write-key weights [ds][dk], staged in dynamic LDS (kLds) or read from
+// global memory.  The choice is a template parameter so that the GEMV reads
+// through LDS (or global) loads, not flat loads, which wait for the stores
+// and loads still in flight as well.
+template <bool kLds>
+__device__ __forceinline__ const float* write_weights(const ScreenWriteArgs& A,
+                                                      float* lds) {
+    if constexpr (!kLds) {
+        return A.kw;
+    } else {
+        const int n = int(A.ds) * A.dk;
+        for (int i = threadIdx.x; i < n; i += kWThreads) lds[i] = A.kw[i];
+        __syncthreads();
+        return lds;
+    }
+}
+
+// Stages rows [n][width] that are `stride` elements apart in global memory
+// (src points at the chunk's first row) into dst[n * width] as fp32, through
+// kWPer loads per thread from clamped in-bounds addresses with no branch, so
+// the loads are all in flight together.  add (a per-column fp32 row, or
+// nullptr) is added to each value, and f maps the sum to what is stored.
+template <typename E, typename F>
+__device__ __forceinline__ void stage_rows(float* dst, const E* src,
+                                           int64_t stride, int n, int width,
+                                           const float* add, F f) {
+    const int tot = n * width;
+    float v[kWPer], a[kWPer];
+#pragma unroll
+    for (int r = 0; r < kWPer; ++r) {
+        const int idx = threadIdx.x + kWThreads * r;
+        const int ic = idx < tot ? idx : tot - 1;
+        const int u = ic / width;
+        const int col = ic - u * width;
+        v[r] = ld1(src + u * stride + col);
+        a[r] = add ? add[col] : 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < kWPer; ++r) {
+        const int idx = threadIdx.x + kWThreads * r;
+        if (idx < tot) dst[idx] = f(v[r] + a[r]);
+    }
+}
+
+// k_raw[j] = sum_c sk[c] W[c][j]: thread (part, j) sums its channel quarter
+// (eight running sums, so that eight pairs of LDS reads are in flight
+// together, added pairwise); wave 0 adds the quarters in order.
+// Returns k_raw, rounded to the element type, for j = lane, lane + 64 in
+// wave 0 (0 for j >= dk; other waves: unspecified).  The forward and the
+// backward call this same code, so both see the same bits.
 template <typename E>
 __device__ __forceinline__ void write_gemv(const ScreenWriteArgs& A,
                                            const float* W, WriteSmem& sm,
@@ -598,108 +670,158 @@ __device__ __forceinline__ void write_gemv(const ScreenWriteArgs& A,
     const int q0 = (ds * part) / 4, q1 = (ds * (part + 1)) / 4;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
+        if (64 * h >= dk) break;
         const int j = lane + 64 * h;
-        float s = 0.f;
-        if (j < dk)
-            for (int c = q0; c < q1; ++c) s += sm.sk[c] * W[c * dk + j];
-        sm.red[part][lane + 64 * h] = s;
+        const int jc = j < dk ? j : dk - 1;
+        float a[8] = {};
+        int c = q0;
+        for (; c + 8 <= q1; c += 8) {
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                a[r] += sm.sk[c + r] * W[(c + r) * dk + jc];
+        }
+        for (; c < q1; ++c) a[0] += sm.sk[c] * W[c * dk + jc];
+        sm.red[part][j] = ((a[0] + a[1]) + (a[2] + a[3])) +
+                          ((a[4] + a[5]) + (a[6] + a[7]));
     }
     __syncthreads();
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int j = lane + 64 * h;
-        k[h] = (sm.red[0][j] + sm.red[1][j]) + (sm.red[2][j] + sm.red[3][j]);
-        k[h] = j < dk ? rnd(k[h], static_cast<const E*>(nullptr)) : 0.f;
+        k[h] = 0.f;
+        if (j < dk) {
+            const float v = (sm.red[0][j] + sm.red[1][j]) +
+                            (sm.red[2][j] + sm.red[3][j]);
+            k[h] = rnd(v, static_cast<const E*>(nullptr));
+        }
     }
 }
 
-template <typename E>
+// d s_key[c] = sum_j W[c][j] dk[j] for this thread's channel c.  Lanes hold
+// different channels, so each lane starts its sum at its own column block
+// (lane mod 16 blocks of four) and the LDS reads of W rows spread over the
+// banks; with dk a multiple of 4 the rows are read 16 bytes at a time.
+__device__ __forceinline__ float write_gemv_t(const float* W,
+                                              const float* dkv, int c, int dk,
+                                              int lane) {
+    float a[4] = {};
+    if ((dk & 3) == 0) {
+        const int n4 = dk >> 2;
+        const int r4 = (lane & 15) % n4;
+        const float4* w4 = reinterpret_cast<const float4*>(W + c * dk);
+        const float4* d4 = reinterpret_cast<const float4*>(dkv);
+#pragma unroll 4
+        for (int j = 0; j < n4; ++j) {
+            int x = r4 + j;
+            x = x >= n4 ? x - n4 : x;
+            const float4 w = w4[x], d = d4[x];
+            a[0] += w.x * d.x;
+            a[1] += w.y * d.y;
+            a[2] += w.z * d.z;
+            a[3] += w.w * d.w;
+        }
+    } else {
+        const int r0 = lane % dk;
+        for (int j = 0; j < dk; ++j) {
+            int x = r0 + j;
+            x = x >= dk ? x - dk : x;
+            a[j & 3] += W[c * dk + x] * dkv[x];
+        }
+    }
+    return (a[0] + a[1]) + (a[2] + a[3]);
+}
+
+template <typename E, bool kLds>
 __global__ __launch_bounds__(kWThreads) void screen_write_fwd_kernel(
     ScreenWriteArgs A) {
     __shared__ WriteSmem sm;
-    extern __shared__ float wlds[];
-    const float* W = write_weights(A, wlds);
+    extern __shared__ __align__(16) float wlds[];
+    const float* W = write_weights<kLds>(A, wlds);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int64_t b = blockIdx.x / A.M;
     const int m = int(blockIdx.x % A.M);
-    const int64_t T = A.T, M = A.M, ds = A.ds;
-    const int ndw = int((ds + 63) / 64);
+    const int64_t T = A.T, M = A.M;
+    const int ds = int(A.ds), dk = A.dk;
+    const int ndw = (ds + 63) / 64;
     const E* base = static_cast<const E*>(A.base) + b * T * ds;
+    const float* qw = A.q_w + b * T * dk;
+    const float* st_m = A.slot_term + m * ds;
     E* seq = static_cast<E*>(A.slots_seq);
     const float mu = A.mu[m], tau = *A.tau_w;
     const float den = 1.f - tau + A.eps;
-    float S[kWMaxCh], e[kWMaxCh], st[kWMaxCh];
+    float S[kWMaxCh], e[kWMaxCh];
 #pragma unroll
     for (int i = 0; i < kWMaxCh; ++i) {
         const int c = tid + kWThreads * i;
         const bool in = c < ds;
         S[i] = in ? A.slots0[(b * M + m) * ds + c] : 0.f;
         e[i] = in ? A.slot_embed[m * ds + c] : 0.f;
-        st[i] = in ? A.slot_term[m * ds + c] : 0.f;
     }
     float age = A.ages0[b * M + m];  // kept by every thread
-    for (int64_t t = 0; t < T; ++t) {
-        // this step's loads first: they arrive while the key is formed
-        float bv[kWMaxCh], qv[2];
-#pragma unroll
-        for (int i = 0; i < kWMaxCh; ++i) {
-            const int c = tid + kWThreads * i;
-            bv[i] = c < ds ? ld1(base + t * ds + c) : 0.f;
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int j = lane + 64 * h;
-            qv[h] = wv == 0 && j < A.dk ? A.q_w[(b * T + t) * A.dk + j] : 0.f;
-        }
-#pragma unroll
-        for (int i = 0; i < kWMaxCh; ++i) {
-            const int c = tid + kWThreads * i;
-            if (c < ds) sm.sk[c] = rnd(S[i] + e[i], base);
-        }
+    const int chunk = write_chunk(ds);
+    for (int64_t t0 = 0; t0 < T; t0 += chunk) {
+        const int n = int(T - t0 < chunk ? T - t0 : chunk);
+        // delta_t = round(tanh(base_t + slot_term)) for the chunk's steps
+        stage_rows(sm.x0, base + t0 * ds, ds, n, ds, st_m,
+                   [&](float x) { return rnd(tanhf(x), base); });
+        stage_rows(sm.q, qw + t0 * dk, dk, n, dk, nullptr,
+                   [](float x) { return x; });
         __syncthreads();
-        float k[2];
-        write_gemv<E>(A, W, sm, k);
-        if (wv == 0) {
-            float kk = 0.f, dot = 0.f;
+        for (int u = 0; u < n; ++u) {
+            const int64_t t = t0 + u;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                kk += k[h] * k[h];
-                dot += k[h] * qv[h];
+            for (int i = 0; i < kWMaxCh; ++i) {
+                const int c = tid + kWThreads * i;
+                if (c < ds) sm.sk[c] = rnd(S[i] + e[i], base);
             }
-            kk = wave_sum(kk);
-            dot = wave_sum(dot);
-            const float sim = dot / sqrtf(kk + A.eps * A.eps);
-            const float x = fmaxf((sim - tau) / den, 0.f);
-            if (lane == 0) {
-                const float rw = x * x;
-                sm.scal[0] = rw;
-                A.rel_w[(b * T + t) * M + m] = rw;
-            }
-        }
-        __syncthreads();
-        const float rw = sm.scal[0];
-        if (tid == 0) A.ages_seq[(b * T + t) * M + m] = age;
-        age = rw > 1e-3f ? 0.f : age + 1.f;
-        const float strength = mu * fmaxf(rw, A.floor);
-        const int64_t o = ((b * T + t) * M + m) * ds;
+            __syncthreads();
+            float k[2];
+            write_gemv<E>(A, W, sm, k);
+            if (wv == 0) {
+                float kk = 0.f, dot = 0.f;
 #pragma unroll
-        for (int i = 0; i < kWMaxCh; ++i) {
-            const int c = tid + kWThreads * i;
-            const bool in = c < ds;
-            const float delta = in ? rnd(tanhf(bv[i] + st[i]), base) : 0.f;
-            if (in) {
-                st1(seq + o + c, S[i]);
-                A.slots32[o + c] = S[i];
+                for (int h = 0; h < 2; ++h) {
+                    const int j = lane + 64 * h;
+                    kk += k[h] * k[h];
+                    dot += j < dk ? k[h] * sm.q[u * dk + j] : 0.f;
+                }
+                kk = wave_sum(kk);
+                dot = wave_sum(dot);
+                const float sim = dot / sqrtf(kk + A.eps * A.eps);
+                const float x = fmaxf((sim - tau) / den, 0.f);
+                if (lane == 0) {
+                    const float rw = x * x;
+                    sm.scal[0] = rw;
+                    A.rel_w[(b * T + t) * M + m] = rw;
+                }
             }
-            const float u = in ? strength * (delta - S[i]) : 0.f;
-            const float u2 = wave_sum(u * u);
-            const int g = (tid >> 6) + 4 * i;
-            if (lane == 0 && g < ndw)
-                A.upd2[((b * T + t) * M + m) * ndw + g] = u2;
-            S[i] += u;
+            __syncthreads();
+            const float rw = sm.scal[0];
+            if (tid == 0) A.ages_seq[(b * T + t) * M + m] = age;
+            age = rw > 1e-3f ? 0.f : age + 1.f;
+            const float strength = mu * fmaxf(rw, A.floor);
+            const int64_t o = ((b * T + t) * M + m) * ds;
+#pragma unroll
+            for (int i = 0; i < kWMaxCh; ++i) {
+                if (kWThreads * i >= ds) break;
+                const int c = tid + kWThreads * i;
+                const bool in = c < ds;
+                if (in) {
+                    st1(seq + o + c, S[i]);
+                    A.slots32[o + c] = S[i];
+                }
+                const float u_ =
+                    in ? strength * (sm.x0[u * ds + c] - S[i]) : 0.f;
+                const float u2 = wave_sum(u_ * u_);
+                const int g = (tid >> 6) + 4 * i;
+                if (lane == 0 && g < ndw)
+                    A.upd2[((b * T + t) * M + m) * ndw + g] = u2;
+                S[i] += u_;
+            }
+            // sm.sk and sm.scal are rewritten only after the next step's
+            // first barrier, which every thread reaches after these reads
         }
-        // sm.sk and sm.scal are rewritten only after the next step's first
-        // barrier, which every thread reaches after these reads
+        __syncthreads();  // the staged chunk is read up to here
     }
 #pragma unroll
     for (int i = 0; i < kWMaxCh; ++i) {
@@ -709,124 +831,134 @@ __global__ __launch_bounds__(kWThreads) void screen_write_fwd_kernel(
     if (tid == 0) A.ages_T[b * M + m] = age;
 }
 
-template <typename E>
+template <typename E, bool kLds>
 __global__ __launch_bounds__(kWThreads) void screen_write_bwd_kernel(
     ScreenWriteArgs A) {
     __shared__ WriteSmem sm;
-    extern __shared__ float wlds[];
-    const float* W = write_weights(A, wlds);
+    extern __shared__ __align__(16) float wlds[];
+    const float* W = write_weights<kLds>(A, wlds);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int64_t b = blockIdx.x / A.M;
     const int m = int(blockIdx.x % A.M);
-    const int64_t T = A.T, M = A.M, ds = A.ds;
-    const int dk = A.dk;
+    const int64_t T = A.T, M = A.M;
+    const int ds = int(A.ds), dk = A.dk;
     const E* base = static_cast<const E*>(A.base) + b * T * ds;
     const E* dseq = static_cast<const E*>(A.d_slots_seq);
-    (void)0;
+    const float* st_m = A.slot_term + m * ds;
     const float mu = A.mu[m], tau = *A.tau_w;
     const float den = 1.f - tau + A.eps;
-    float G[kWMaxCh], e[kWMaxCh], st[kWMaxCh], de[kWMaxCh];
+    float G[kWMaxCh], e[kWMaxCh], de[kWMaxCh];
 #pragma unroll
     for (int i = 0; i < kWMaxCh; ++i) {
         const int c = tid + kWThreads * i;
         const bool in = c < ds;
         G[i] = in && A.d_slots_T ? A.d_slots_T[(b * M + m) * ds + c] : 0.f;
         e[i] = in ? A.slot_embed[m * ds + c] : 0.f;
-        st[i] = in ? A.slot_term[m * ds + c] : 0.f;
         de[i] = 0.f;
     }
     float dage = A.d_ages_T ? A.d_ages_T[b * M + m] : 0.f;
     float dmu = 0.f;
-    for (int64_t t = T - 1; t >= 0; --t) {
-        const int64_t o = ((b * T + t) * M + m) * ds;
-        float S[kWMaxCh], bv[kWMaxCh], dsv[kWMaxCh], th[kWMaxCh];
-#pragma unroll
-        for (int i = 0; i < kWMaxCh; ++i) {
-            const int c = tid + kWThreads * i;
-            const bool in = c < ds;
-            S[i] = in ? A.slots32[o + c] : 0.f;
-            bv[i] = in ? ld1(base + t * ds + c) : 0.f;
-            dsv[i] = in ? ld1(dseq + o + c) : 0.f;
+    const int chunk = write_chunk(ds);
+    const int64_t nchunks = (T + chunk - 1) / chunk;
+    for (int64_t ci = nchunks - 1; ci >= 0; --ci) {
+        const int64_t t0 = ci * chunk;
+        const int n = int(T - t0 < chunk ? T - t0 : chunk);
+        const int64_t row0 = (b * T + t0) * M + m;  // (b, t0, m)
+        const auto id = [](float x) { return x; };
+        stage_rows(sm.x0, base + t0 * ds, ds, n, ds, st_m,
+                   [](float x) { return tanhf(x); });
+        stage_rows(sm.x1, A.slots32 + row0 * ds, M * ds, n, ds, nullptr, id);
+        stage_rows(sm.x2, dseq + row0 * ds, M * ds, n, ds, nullptr, id);
+        stage_rows(sm.q, A.q_w + (b * T + t0) * dk, dk, n, dk, nullptr, id);
+        if (tid < n) {
+            sm.drel[tid] = A.d_rel_w ? A.d_rel_w[row0 + tid * M] : 0.f;
+            sm.dage[tid] = A.d_ages_seq ? A.d_ages_seq[row0 + tid * M] : 0.f;
         }
-        float part = 0.f;  // this thread's part of sum_c G (delta - S)
-#pragma unroll
-        for (int i = 0; i < kWMaxCh; ++i) {
-            const int c = tid + kWThreads * i;
-            const bool in = c < ds;
-            th[i] = in ? tanhf(bv[i] + st[i]) : 0.f;
-            part += in ? G[i] * (rnd(th[i], base) - S[i]) : 0.f;
-            if (in) sm.sk[c] = rnd(S[i] + e[i], base);
-        }
-        part = wave_sum(part);
-        if (lane == 0) sm.scal[4 + wv] = part;
         __syncthreads();
-        float k[2];
-        write_gemv<E>(A, W, sm, k);
-        if (wv == 0) {
-            const int64_t bt = b * T + t;
-            const float* q = A.q_w + bt * dk;
-            float qv[2];
-            float kk = 0.f, dot = 0.f;
+        for (int u = n - 1; u >= 0; --u) {
+            const int64_t bt = b * T + t0 + u;
+            const int64_t o = (bt * M + m) * ds;
+            float th[kWMaxCh] = {};
+            float part = 0.f;  // this thread's part of sum_c G (delta - S)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int j = lane + 64 * h;
-                qv[h] = j < dk ? q[j] : 0.f;
-                kk += k[h] * k[h];
-                dot += k[h] * qv[h];
-            }
-            const float kn = sqrtf(wave_sum(kk) + A.eps * A.eps);
-            const float sim = wave_sum(dot) / kn;
-            const float x = (sim - tau) / den;
-            const float r = fmaxf(x, 0.f);
-            const float rw = r * r;
-            const float dstr = (sm.scal[4] + sm.scal[5]) +
-                               (sm.scal[6] + sm.scal[7]);
-            const bool above = rw > A.floor;
-            dmu += dstr * fmaxf(rw, A.floor);
-            const float drw = (A.d_rel_w ? A.d_rel_w[bt * M + m] : 0.f) +
-                              (above ? dstr * mu : 0.f);
-            const float dsim = drw * 2.f * r / den;
-            // d k_hat = dsim q; d k_raw = (d k_hat - k_hat (k_hat . d k_hat)) / kn
-            float kh[2], kd = 0.f;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                kh[h] = k[h] / kn;
-                kd += kh[h] * qv[h];
-            }
-            kd = wave_sum(kd) * dsim;
-            float* dq = A.dq_w + (bt * M + m) * dk;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int j = lane + 64 * h;
-                const float dkr = (dsim * qv[h] - kh[h] * kd) / kn;
-                if (j < dk) {
-                    dq[j] = dsim * kh[h];
-                    A.d_kraw[(bt * M + m) * dk + j] = dkr;
-                    sm.dk[j] = dkr;
+            for (int i = 0; i < kWMaxCh; ++i) {
+                if (kWThreads * i >= ds) break;
+                const int c = tid + kWThreads * i;
+                if (c < ds) {
+                    const float S = sm.x1[u * ds + c];
+                    th[i] = sm.x0[u * ds + c];
+                    part += G[i] * (rnd(th[i], base) - S);
+                    sm.sk[c] = rnd(S + e[i], base);
                 }
             }
-            if (lane == 0) {
-                A.d_tau_w[bt * M + m] = drw * 2.f * r * (x - 1.f) / den;
-                sm.scal[0] = mu * fmaxf(rw, A.floor);  // strength
-                sm.scal[1] = rw;
-            }
-        }
-        __syncthreads();
-        const float strength = sm.scal[0], rw = sm.scal[1];
-        // ages: step t read ages_t; ages_{t+1} = rw > 1e-3 ? 0 : ages_t + 1
-        dage = (A.d_ages_seq ? A.d_ages_seq[(b * T + t) * M + m] : 0.f) +
-               (rw > 1e-3f ? 0.f : dage);
+            part = wave_sum(part);
+            if (lane == 0) sm.scal[4 + wv] = part;
+            __syncthreads();
+            float k[2];
+            write_gemv<E>(A, W, sm, k);
+            if (wv == 0) {
+                float qv[2];
+                float kk = 0.f, dot = 0.f;
 #pragma unroll
-        for (int i = 0; i < kWMaxCh; ++i) {
-            const int c = tid + kWThreads * i;
-            if (c >= ds) continue;
-            float dsk = 0.f;
-            for (int j = 0; j < dk; ++j) dsk += W[c * dk + j] * sm.dk[j];
-            de[i] += dsk;
-            A.d_pre[o + c] = strength * G[i] * (1.f - th[i] * th[i]);
-            G[i] = G[i] * (1.f - strength) + dsk + dsv[i];
+                for (int h = 0; h < 2; ++h) {
+                    const int j = lane + 64 * h;
+                    qv[h] = j < dk ? sm.q[u * dk + j] : 0.f;
+                    kk += k[h] * k[h];
+                    dot += k[h] * qv[h];
+                }
+                const float kn = sqrtf(wave_sum(kk) + A.eps * A.eps);
+                const float sim = wave_sum(dot) / kn;
+                const float x = (sim - tau) / den;
+                const float r = fmaxf(x, 0.f);
+                const float rw = r * r;
+                const float dstr = (sm.scal[4] + sm.scal[5]) +
+                                   (sm.scal[6] + sm.scal[7]);
+                const bool above = rw > A.floor;
+                dmu += dstr * fmaxf(rw, A.floor);
+                const float drw = sm.drel[u] + (above ? dstr * mu : 0.f);
+                const float dsim = drw * 2.f * r / den;
+                // d k_hat = dsim q;
+                // d k_raw = (d k_hat - k_hat (k_hat . d k_hat)) / kn
+                float kh[2], kd = 0.f;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    kh[h] = k[h] / kn;
+                    kd += kh[h] * qv[h];
+                }
+                kd = wave_sum(kd) * dsim;
+                float* dq = A.dq_w + (bt * M + m) * dk;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int j = lane + 64 * h;
+                    const float dkr = (dsim * qv[h] - kh[h] * kd) / kn;
+                    if (j < dk) {
+                        dq[j] = dsim * kh[h];
+                        A.d_kraw[(bt * M + m) * dk + j] = dkr;
+                        sm.dk[j] = dkr;
+                    }
+                }
+                if (lane == 0) {
+                    A.d_tau_w[bt * M + m] = drw * 2.f * r * (x - 1.f) / den;
+                    sm.scal[0] = mu * fmaxf(rw, A.floor);  // strength
+                    sm.scal[1] = rw;
+                }
+            }
+            __syncthreads();
+            const float strength = sm.scal[0], rw = sm.scal[1];
+            // ages: step t read ages_t; ages_{t+1} = rw > 1e-3 ? 0 : ages_t + 1
+            dage = sm.dage[u] + (rw > 1e-3f ? 0.f : dage);
+#pragma unroll
+            for (int i = 0; i < kWMaxCh; ++i) {
+                if (kWThreads * i >= ds) break;
+                const int c = tid + kWThreads * i;
+                if (c >= ds) continue;
+                const float dsk = write_gemv_t(W, sm.dk, c, dk, lane);
+                de[i] += dsk;
+                A.d_pre[o + c] = strength * G[i] * (1.f - th[i] * th[i]);
+                G[i] = G[i] * (1.f - strength) + dsk + sm.x2[u * ds + c];
+            }
+            __syncthreads();  // sm.dk and sm.scal are rewritten next step
         }
-        __syncthreads();  // sm.dk and sm.scal are rewritten next step
     }
 #pragma unroll
     for (int i = 0; i < kWMaxCh; ++i) {
@@ -840,6 +972,18 @@ __global__ __launch_bounds__(kWThreads) void screen_write_bwd_kernel(
         A.d_ages0[b * M + m] = dage;
         A.d_mu_bm[b * M + m] = dmu;
     }
+}
+
+template <typename E, bool kLds>
+void launch_write(bool backward, const ScreenWriteArgs& A, size_t lds,
+                  hipStream_t stream) {
+    const dim3 grid{unsigned(A.B * A.M)}, block{unsigned(kWThreads)};
+    if (backward)
+        hipLaunchKernelGGL((screen_write_bwd_kernel<E, kLds>), grid, block,
+                           lds, stream, A);
+    else
+        hipLaunchKernelGGL((screen_write_fwd_kernel<E, kLds>), grid, block,
+                           lds, stream, A);
 }
 
 unsigned blocks_for_waves(int64_t waves) {
@@ -884,25 +1028,16 @@ hipError_t launch_screen_scan(bool bf16, bool backward,
 
 hipError_t launch_screen_write(bool bf16, bool backward,
                                const ScreenWriteArgs& A, hipStream_t stream) {
-    const int64_t nwg = A.B * A.M;
-    if (nwg == 0) return hipSuccess;
+    if (A.B * A.M == 0) return hipSuccess;
     const int64_t nw = A.ds * A.dk;
-    const size_t lds = nw <= kWLdsWeights ? size_t(nw) * sizeof(float) : 0;
-    const dim3 grid{unsigned(nwg)}, block{unsigned(kWThreads)};
-    if (!backward) {
-        if (bf16)
-            hipLaunchKernelGGL(screen_write_fwd_kernel<bf16_t>, grid, block,
-                               lds, stream, A);
-        else
-            hipLaunchKernelGGL(screen_write_fwd_kernel<float>, grid, block,
-                               lds, stream, A);
+    const bool in_lds = nw <= kWLdsWeights;
+    const size_t lds = in_lds ? size_t(nw) * sizeof(float) : 0;
+    if (bf16) {
+        if (in_lds) launch_write<bf16_t, true>(backward, A, lds, stream);
+        else launch_write<bf16_t, false>(backward, A, lds, stream);
     } else {
-        if (bf16)
-            hipLaunchKernelGGL(screen_write_bwd_kernel<bf16_t>, grid, block,
-                               lds, stream, A);
-        else
-            hipLaunchKernelGGL(screen_write_bwd_kernel<float>, grid, block,
-                               lds, stream, A);
+        if (in_lds) launch_write<float, true>(backward, A, lds, stream);
+        else launch_write<float, false>(backward, A, lds, stream);
     }
     return hipGetLastError();
 }

@@ -292,7 +292,10 @@ WRITE = dict(use_write_screening=True, write_rel_floor=0.05)
 @pytest.mark.parametrize("opt", [dict(), dict(use_age_mask=True)], ids=str)
 def test_write_phase_forward_matches_oracle(hip_lib, opt, dtype):
     case = _case(2, 29, 64, 80, 32, 80, 5, seed=51, **WRITE, **opt)
-    name = f"screening read_write fwd {opt} {dtype}"
+    _check_write_forward(case, dtype, f"screening read_write fwd {opt} {dtype}")
+
+
+def _check_write_forward(case, dtype, name):
     print("case:", name, flush=True)
     _, _, _, _, out, new, stats = _run(case, dtype, phase="read_write")
     torch.cuda.synchronize()
@@ -317,7 +320,26 @@ def test_write_phase_forward_matches_oracle(hip_lib, opt, dtype):
 @pytest.mark.parametrize("opt", [dict(), dict(use_age_mask=True)], ids=str)
 def test_write_phase_backward_matches_autograd_oracle(hip_lib, opt):
     case = _case(2, 17, 64, 80, 32, 80, 5, seed=61, **WRITE, **opt)
-    name = f"screening read_write bwd {opt}"
+    _check_write_backward(case, f"screening read_write bwd {opt}")
+
+
+# The write kernels stage min(32, 4096 // d_slot) steps at a time: these
+# shapes cross several chunk boundaries (d_slot 128: chunks of 32, the last
+# partial; d_slot 300: chunks of 13, two channels per thread, and d_k not a
+# multiple of 4).
+WRITE_CHUNKED = [(1, 70, 64, 128, 64, 64, 3), (1, 30, 48, 300, 30, 40, 2)]
+
+
+@pytest.mark.parametrize("shape", WRITE_CHUNKED, ids=str)
+def test_write_phase_chunked(hip_lib, shape):
+    case = _case(*shape, seed=71, **WRITE, use_age_mask=True)
+    for dtype in (torch.float32, torch.bfloat16):
+        _check_write_forward(case, dtype,
+                             f"screening read_write fwd {shape} {dtype}")
+    _check_write_backward(case, f"screening read_write bwd {shape}")
+
+
+def _check_write_backward(case, name):
     print("case:", name, flush=True)
     mod, xd, hd, st, out, new, _ = _run(case, torch.float32, grad=True,
                                         phase="read_write")

@@ -1,7 +1,7 @@
 /*
- * rwkv7m_screening.h -- C ABI of the state-level screening read path (phase
- * read_screening_only) in librwkv7m_wkv.so; status codes, dtype codes and
- * rwkv7m_last_error() are those of rwkv7m_wkv.h.
+ * rwkv7m_screening.h -- C ABI of the state-level screening module (phases
+ * read_screening_only and read_write) in librwkv7m_wkv.so; status codes,
+ * dtype codes and rwkv7m_last_error() are those of rwkv7m_wkv.h.
  *
  * The reference runs NNXStateLevelScreening.__call__
  * (src/rwkv7m/model/nnx_model.py:999-1160) as one jax.lax.scan step per

@@ -577,38 +577,43 @@ __global__ __launch_bounds__(256) void screen_read_bwd_kernel(
 //   rel_w = trim_square(q_w . k_w, tau_w)
 //   S_{t+1} = S_t + mu max(rel_w, floor) (delta_t - S_t)
 //   ages_{t+1} = rel_w > 1e-3 ? 0 : ages_t + 1
-// so each (b, slot) walks the steps in order: one 256-thread workgroup per
-// (b, m), channels c = tid + 256 i in registers, the write key's GEMV over
-// the slot's channels through LDS (four channel quarters per output column,
-// added in order), three barriers per step.  The backward replays each step
-// from the stored fp32 S_t in reverse.
-
-constexpr int kWThreads = 256;
-constexpr int kWMaxCh = 4;  // channels per thread (d_slot <= 1024)
-
+// so each (b, slot) walks the steps in order.  Two waves per (b, slot):
+// wave 0 runs the steps, with the slot's channels c = lane + 64 i in
+// registers and the write key's GEMV through LDS; wave 1 stages the next
+// chunk of per-step inputs into the other half of a double buffer, and the
+// two meet at one barrier per chunk.  Inside a step only wave 0 touches the
+// step's LDS, and one wave's LDS operations complete in order, so a step
+// needs no barrier.  The backward replays each step from the stored fp32
+// S_t in reverse.
+constexpr int kWThreads = 128;
+constexpr int kWMaxCh = 16;  // channels per lane (d_slot <= 1024)
 constexpr int kWLdsWeights = 16384;  // fp32 weights staged in LDS up to 64 KB
-// Per-step inputs are staged through LDS a chunk of steps at a time: up to
-// kWStage floats per staged array, kWStage / kWThreads per thread.
-constexpr int kWStage = 4096;
-constexpr int kWPer = kWStage / kWThreads;
+constexpr int kWStage = 2048;        // floats per staged array and buffer
+constexpr int kWBatch = 16;          // loads in flight per lane when staging
 constexpr int kWMaxSteps = 32;
 
 struct alignas(16) WriteSmem {
-    float sk[kWThreads * kWMaxCh];  // the step's write-key input
-    float red[4][128];              // GEMV partials per channel quarter
-    float dk[128];                  // d k_raw (backward)
-    float scal[8];
-    float q[kWStage];               // the chunk's write queries [u][dk]
-    float x0[kWStage];              // forward: delta; backward: tanh
-    float x1[kWStage];              // backward: S_t (fp32)
-    float x2[kWStage];              // backward: d slots_seq
-    float drel[kWMaxSteps], dage[kWMaxSteps];
+    float sk[1024];              // the step's write-key input
+    float dk[128];               // d k_raw (backward)
+    float q[2][kWStage];         // write queries [u][dk]
+    float x0[2][kWStage];        // forward: delta; backward: tanh
+    float x1[2][kWStage];        // backward: S_t (fp32)
+    float x2[2][kWStage];        // backward: d slots_seq
+    float drel[2][kWMaxSteps], dage[2][kWMaxSteps];
 };
 
 // Steps per staged chunk.
-__device__ __forceinline__ int write_chunk(int ds) {
-    const int n = kWStage / ds;
+__device__ __forceinline__ int write_chunk(int ds, int dk) {
+    int n = kWStage / (ds > dk ? ds : dk);
     return n < kWMaxSteps ? n : kWMaxSteps;
+}
+
+// Orders the chain wave's LDS accesses across lanes: a code-motion barrier
+// (the hardware keeps one wave's LDS operations in order).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // The write-key weights [ds][dk], staged in dynamic LDS (kLds) or read from
@@ -628,76 +633,107 @@ __device__ __forceinline__ const float* write_weights(const ScreenWriteArgs& A,
     }
 }
 
-// Stages rows [n][width] that are `stride` elements apart in global memory
-// (src points at the chunk's first row) into dst[n * width] as fp32, through
-// kWPer loads per thread from clamped in-bounds addresses with no branch, so
-// the loads are all in flight together.  add (a per-column fp32 row, or
-// nullptr) is added to each value, and f maps the sum to what is stored.
+// One wave stages rows [n][width] that are `stride` elements apart in global
+// memory (src points at the chunk's first row) into dst[n * width] as fp32:
+// batches of kWBatch loads per lane from clamped in-bounds addresses with no
+// branch, so that a batch's loads are in flight together.  add (a
+// per-column fp32 row, or nullptr) is added to each value, and f maps the
+// sum to what is stored.
 template <typename E, typename F>
 __device__ __forceinline__ void stage_rows(float* dst, const E* src,
                                            int64_t stride, int n, int width,
-                                           const float* add, F f) {
+                                           const float* add, F f, int lane) {
     const int tot = n * width;
-    float v[kWPer], a[kWPer];
+    for (int b0 = 0; b0 < tot; b0 += 64 * kWBatch) {
+        float v[kWBatch], a[kWBatch];
 #pragma unroll
-    for (int r = 0; r < kWPer; ++r) {
-        const int idx = threadIdx.x + kWThreads * r;
-        const int ic = idx < tot ? idx : tot - 1;
-        const int u = ic / width;
-        const int col = ic - u * width;
-        v[r] = ld1(src + u * stride + col);
-        a[r] = add ? add[col] : 0.f;
-    }
+        for (int r = 0; r < kWBatch; ++r) {
+            const int idx = b0 + lane + 64 * r;
+            const int ic = idx < tot ? idx : tot - 1;
+            const int u = ic / width;
+            const int col = ic - u * width;
+            v[r] = ld1(src + u * stride + col);
+            a[r] = add ? add[col] : 0.f;
+        }
 #pragma unroll
-    for (int r = 0; r < kWPer; ++r) {
-        const int idx = threadIdx.x + kWThreads * r;
-        if (idx < tot) dst[idx] = f(v[r] + a[r]);
+        for (int r = 0; r < kWBatch; ++r) {
+            const int idx = b0 + lane + 64 * r;
+            if (idx < tot) dst[idx] = f(v[r] + a[r]);
+        }
     }
 }
 
-// k_raw[j] = sum_c sk[c] W[c][j]: thread (part, j) sums its channel quarter
-// (eight running sums, so that eight pairs of LDS reads are in flight
-// together, added pairwise); wave 0 adds the quarters in order.
-// Returns k_raw, rounded to the element type, for j = lane, lane + 64 in
-// wave 0 (0 for j >= dk; other waves: unspecified).  The forward and the
-// backward call this same code, so both see the same bits.
+// k_raw[j] = sum_c sk[c] W[c][j] for j = lane, lane + 64 (eight running
+// sums over c mod 8, added pairwise), rounded to the element type; 0 for
+// j >= dk.  The forward and the backward call this same code, so both see
+// the same key bits.
 template <typename E>
-__device__ __forceinline__ void write_gemv(const ScreenWriteArgs& A,
-                                           const float* W, WriteSmem& sm,
+__device__ __forceinline__ void write_gemv(const float* W, const float* sk,
+                                           int ds, int dk, int lane,
                                            float (&k)[2]) {
-    const int tid = threadIdx.x, lane = tid & 63, part = tid >> 6;
-    const int ds = int(A.ds), dk = A.dk;
-    const int q0 = (ds * part) / 4, q1 = (ds * (part + 1)) / 4;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        if (64 * h >= dk) break;
+        k[h] = 0.f;
+        if (64 * h >= dk) continue;
         const int j = lane + 64 * h;
         const int jc = j < dk ? j : dk - 1;
         float a[8] = {};
-        int c = q0;
-        for (; c + 8 <= q1; c += 8) {
+        int c = 0;
+        for (; c + 8 <= ds; c += 8) {
+            float w[8], x[8];
 #pragma unroll
-            for (int r = 0; r < 8; ++r)
-                a[r] += sm.sk[c + r] * W[(c + r) * dk + jc];
-        }
-        for (; c < q1; ++c) a[0] += sm.sk[c] * W[c * dk + jc];
-        sm.red[part][j] = ((a[0] + a[1]) + (a[2] + a[3])) +
-                          ((a[4] + a[5]) + (a[6] + a[7]));
-    }
-    __syncthreads();
+            for (int r = 0; r < 8; ++r) w[r] = W[(c + r) * dk + jc];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int j = lane + 64 * h;
-        k[h] = 0.f;
-        if (j < dk) {
-            const float v = (sm.red[0][j] + sm.red[1][j]) +
-                            (sm.red[2][j] + sm.red[3][j]);
-            k[h] = rnd(v, static_cast<const E*>(nullptr));
+            for (int r = 0; r < 8; ++r) x[r] = sk[c + r];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) a[r] += x[r] * w[r];
         }
+        for (; c < ds; ++c) a[0] += sk[c] * W[c * dk + jc];
+        const float v = ((a[0] + a[1]) + (a[2] + a[3])) +
+                        ((a[4] + a[5]) + (a[6] + a[7]));
+        k[h] = j < dk ? rnd(v, static_cast<const E*>(nullptr)) : 0.f;
     }
 }
 
-// d s_key[c] = sum_j W[c][j] dk[j] for this thread's channel c.  Lanes hold
+// The same GEMV with the lane's weight column W[0..127][lane] in registers
+// (d_slot <= 128, dk <= 64; rows past d_slot hold zeros, and so does sk).
+constexpr int kWRegC = 128;
+
+template <typename E>
+__device__ __forceinline__ void write_gemv_reg(const float (&wr)[kWRegC],
+                                               const float* sk, int dk,
+                                               int lane, float (&k)[2]) {
+    float a[8] = {};
+#pragma unroll
+    for (int c = 0; c < kWRegC; c += 8) {
+        float x[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) x[r] = sk[c + r];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) a[r] += x[r] * wr[c + r];
+    }
+    const float v = ((a[0] + a[1]) + (a[2] + a[3])) +
+                    ((a[4] + a[5]) + (a[6] + a[7]));
+    k[0] = lane < dk ? rnd(v, static_cast<const E*>(nullptr)) : 0.f;
+    k[1] = 0.f;
+}
+
+// Loads the lane's weight column for write_gemv_reg and clears sk (its
+// channels past d_slot are read as zeros).
+template <bool kReg>
+__device__ __forceinline__ void write_reg_init(const float* W, int ds, int dk,
+                                               int lane, float* wr,
+                                               float* sk) {
+    if constexpr (kReg) {
+        const int jc = lane < dk ? lane : dk - 1;
+#pragma unroll
+        for (int c = 0; c < kWRegC; ++c)
+            wr[c] = c < ds ? W[c * dk + jc] : 0.f;
+    }
+    for (int i = threadIdx.x; i < 1024; i += kWThreads) sk[i] = 0.f;
+}
+
+// d s_key[c] = sum_j W[c][j] dk[j] for this lane's channel c.  Lanes hold
 // different channels, so each lane starts its sum at its own column block
 // (lane mod 16 blocks of four) and the LDS reads of W rows spread over the
 // banks; with dk a multiple of 4 the rows are read 16 bytes at a time.
@@ -710,8 +746,25 @@ __device__ __forceinline__ float write_gemv_t(const float* W,
         const int r4 = (lane & 15) % n4;
         const float4* w4 = reinterpret_cast<const float4*>(W + c * dk);
         const float4* d4 = reinterpret_cast<const float4*>(dkv);
-#pragma unroll 4
-        for (int j = 0; j < n4; ++j) {
+        int j = 0;
+        for (; j + 4 <= n4; j += 4) {
+            float4 w[4], d[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                int x = r4 + j + r;
+                x = x >= n4 ? x - n4 : x;
+                w[r] = w4[x];
+                d[r] = d4[x];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                a[0] += w[r].x * d[r].x;
+                a[1] += w[r].y * d[r].y;
+                a[2] += w[r].z * d[r].z;
+                a[3] += w[r].w * d[r].w;
+            }
+        }
+        for (; j < n4; ++j) {
             int x = r4 + j;
             x = x >= n4 ? x - n4 : x;
             const float4 w = w4[x], d = d4[x];
@@ -731,113 +784,147 @@ __device__ __forceinline__ float write_gemv_t(const float* W,
     return (a[0] + a[1]) + (a[2] + a[3]);
 }
 
-template <typename E, bool kLds>
-__global__ __launch_bounds__(kWThreads) void screen_write_fwd_kernel(
+template <typename E, bool kLds, bool kReg>
+__global__ __launch_bounds__(kWThreads)
+__attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_fwd_kernel(
     ScreenWriteArgs A) {
     __shared__ WriteSmem sm;
     extern __shared__ __align__(16) float wlds[];
     const float* W = write_weights<kLds>(A, wlds);
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const bool chain = tid < 64;  // wave 0: the steps; wave 1: staging
+    float wr[kReg ? kWRegC : 1];
+    write_reg_init<kReg>(W, int(A.ds), A.dk, lane, wr, sm.sk);
     const int64_t b = blockIdx.x / A.M;
     const int m = int(blockIdx.x % A.M);
     const int64_t T = A.T, M = A.M;
     const int ds = int(A.ds), dk = A.dk;
-    const int ndw = (ds + 63) / 64;
     const E* base = static_cast<const E*>(A.base) + b * T * ds;
     const float* qw = A.q_w + b * T * dk;
     const float* st_m = A.slot_term + m * ds;
     E* seq = static_cast<E*>(A.slots_seq);
     const float mu = A.mu[m], tau = *A.tau_w;
     const float den = 1.f - tau + A.eps;
+    const int chunk = write_chunk(ds, dk);
+    const int64_t nchunks = (T + chunk - 1) / chunk;
+    auto stage = [&](int64_t ci) {
+        const int64_t t0 = ci * chunk;
+        const int n = int(T - t0 < chunk ? T - t0 : chunk);
+        const int buf = int(ci & 1);
+        // delta_t = round(tanh(base_t + slot_term))
+        stage_rows(sm.x0[buf], base + t0 * ds, ds, n, ds, st_m,
+                   [&](float x) { return rnd(tanhf(x), base); }, lane);
+        stage_rows(sm.q[buf], qw + t0 * dk, dk, n, dk, nullptr,
+                   [](float x) { return x; }, lane);
+    };
     float S[kWMaxCh], e[kWMaxCh];
 #pragma unroll
     for (int i = 0; i < kWMaxCh; ++i) {
-        const int c = tid + kWThreads * i;
-        const bool in = c < ds;
+        const int c = lane + 64 * i;
+        const bool in = chain && c < ds;
         S[i] = in ? A.slots0[(b * M + m) * ds + c] : 0.f;
         e[i] = in ? A.slot_embed[m * ds + c] : 0.f;
     }
-    float age = A.ages0[b * M + m];  // kept by every thread
-    const int chunk = write_chunk(ds);
-    for (int64_t t0 = 0; t0 < T; t0 += chunk) {
-        const int n = int(T - t0 < chunk ? T - t0 : chunk);
-        // delta_t = round(tanh(base_t + slot_term)) for the chunk's steps
-        stage_rows(sm.x0, base + t0 * ds, ds, n, ds, st_m,
-                   [&](float x) { return rnd(tanhf(x), base); });
-        stage_rows(sm.q, qw + t0 * dk, dk, n, dk, nullptr,
-                   [](float x) { return x; });
-        __syncthreads();
-        for (int u = 0; u < n; ++u) {
-            const int64_t t = t0 + u;
+    float age = A.ages0[b * M + m];
+    if (!chain && nchunks > 0) stage(0);
+    __syncthreads();
+    for (int64_t ci = 0; ci < nchunks; ++ci) {
+        if (!chain) {
+            if (ci + 1 < nchunks) stage(ci + 1);
+        } else {
+            const int buf = int(ci & 1);
+            const int64_t t0 = ci * chunk;
+            const int n = int(T - t0 < chunk ? T - t0 : chunk);
+            const float* dl = sm.x0[buf];
+            const float* qs = sm.q[buf];
+            for (int u = 0; u < n; ++u) {
+                const int64_t t = t0 + u;
 #pragma unroll
-            for (int i = 0; i < kWMaxCh; ++i) {
-                const int c = tid + kWThreads * i;
-                if (c < ds) sm.sk[c] = rnd(S[i] + e[i], base);
-            }
-            __syncthreads();
-            float k[2];
-            write_gemv<E>(A, W, sm, k);
-            if (wv == 0) {
+                for (int i = 0; i < kWMaxCh; ++i) {
+                    if (64 * i >= ds) break;
+                    const int c = lane + 64 * i;
+                    if (c < ds) sm.sk[c] = rnd(S[i] + e[i], base);
+                }
+                wave_sync();
+                float k[2];
+                if constexpr (kReg)
+                    write_gemv_reg<E>(wr, sm.sk, dk, lane, k);
+                else
+                    write_gemv<E>(W, sm.sk, ds, dk, lane, k);
                 float kk = 0.f, dot = 0.f;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int j = lane + 64 * h;
                     kk += k[h] * k[h];
-                    dot += j < dk ? k[h] * sm.q[u * dk + j] : 0.f;
+                    dot += j < dk ? k[h] * qs[u * dk + j] : 0.f;
                 }
                 kk = wave_sum(kk);
                 dot = wave_sum(dot);
                 const float sim = dot / sqrtf(kk + A.eps * A.eps);
                 const float x = fmaxf((sim - tau) / den, 0.f);
+                const float rw = x * x;
+                const int64_t row = (b * T + t) * M + m;
                 if (lane == 0) {
-                    const float rw = x * x;
-                    sm.scal[0] = rw;
-                    A.rel_w[(b * T + t) * M + m] = rw;
+                    A.rel_w[row] = rw;
+                    A.ages_seq[row] = age;
                 }
-            }
-            __syncthreads();
-            const float rw = sm.scal[0];
-            if (tid == 0) A.ages_seq[(b * T + t) * M + m] = age;
-            age = rw > 1e-3f ? 0.f : age + 1.f;
-            const float strength = mu * fmaxf(rw, A.floor);
-            const int64_t o = ((b * T + t) * M + m) * ds;
+                age = rw > 1e-3f ? 0.f : age + 1.f;
+                const float strength = mu * fmaxf(rw, A.floor);
 #pragma unroll
-            for (int i = 0; i < kWMaxCh; ++i) {
-                if (kWThreads * i >= ds) break;
-                const int c = tid + kWThreads * i;
-                const bool in = c < ds;
-                if (in) {
-                    st1(seq + o + c, S[i]);
-                    A.slots32[o + c] = S[i];
+                for (int i = 0; i < kWMaxCh; ++i) {
+                    if (64 * i >= ds) break;
+                    const int c = lane + 64 * i;
+                    const bool in = c < ds;
+                    if (in) {
+                        st1(seq + row * ds + c, S[i]);
+                        A.slots32[row * ds + c] = S[i];
+                    }
+                    const float u_ =
+                        in ? strength * (dl[u * ds + c] - S[i]) : 0.f;
+                    const float u2 = wave_sum(u_ * u_);
+                    if (lane == 0) A.upd2[row * ((ds + 63) / 64) + i] = u2;
+                    S[i] += u_;
                 }
-                const float u_ =
-                    in ? strength * (sm.x0[u * ds + c] - S[i]) : 0.f;
-                const float u2 = wave_sum(u_ * u_);
-                const int g = (tid >> 6) + 4 * i;
-                if (lane == 0 && g < ndw)
-                    A.upd2[((b * T + t) * M + m) * ndw + g] = u2;
-                S[i] += u_;
+                wave_sync();  // this step's GEMV reads come before the next
+                              // step's writes of sk
             }
-            // sm.sk and sm.scal are rewritten only after the next step's
-            // first barrier, which every thread reaches after these reads
         }
-        __syncthreads();  // the staged chunk is read up to here
+        __syncthreads();  // chunk ci is read, chunk ci + 1 is staged
     }
+    if (chain) {
 #pragma unroll
-    for (int i = 0; i < kWMaxCh; ++i) {
-        const int c = tid + kWThreads * i;
-        if (c < ds) A.slots_T[(b * M + m) * ds + c] = S[i];
+        for (int i = 0; i < kWMaxCh; ++i) {
+            const int c = lane + 64 * i;
+            if (c < ds) A.slots_T[(b * M + m) * ds + c] = S[i];
+        }
+        if (lane == 0) A.ages_T[b * M + m] = age;
     }
-    if (tid == 0) A.ages_T[b * M + m] = age;
 }
 
-template <typename E, bool kLds>
-__global__ __launch_bounds__(kWThreads) void screen_write_bwd_kernel(
+template <typename E, bool kLds, bool kReg>
+__global__ __launch_bounds__(kWThreads)
+__attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
     ScreenWriteArgs A) {
     __shared__ WriteSmem sm;
     extern __shared__ __align__(16) float wlds[];
     const float* W = write_weights<kLds>(A, wlds);
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const bool chain = tid < 64;  // wave 0: the steps; wave 1: staging
+    float wr[kReg ? kWRegC : 1];
+    write_reg_init<kReg>(W, int(A.ds), A.dk, lane, wr, sm.sk);
+    // with kReg also the rows W[lane + 64 i][0..63] of the lane's channels,
+    // for the transposed GEMV (sm.dk past dk reads as zero)
+    float wt[kReg ? 2 : 1][kReg ? 64 : 1];
+    if constexpr (kReg) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = lane + 64 * i;
+#pragma unroll
+            for (int j = 0; j < 64; ++j)
+                wt[i][j] = c < int(A.ds) && j < A.dk ? W[c * A.dk + j] : 0.f;
+        }
+    }
+    for (int j = threadIdx.x; j < 128; j += kWThreads) sm.dk[j] = 0.f;
     const int64_t b = blockIdx.x / A.M;
     const int m = int(blockIdx.x % A.M);
     const int64_t T = A.T, M = A.M;
@@ -847,62 +934,77 @@ __global__ __launch_bounds__(kWThreads) void screen_write_bwd_kernel(
     const float* st_m = A.slot_term + m * ds;
     const float mu = A.mu[m], tau = *A.tau_w;
     const float den = 1.f - tau + A.eps;
+    const int chunk = write_chunk(ds, dk);
+    const int64_t nchunks = (T + chunk - 1) / chunk;
+    auto stage = [&](int64_t ci) {
+        const int64_t t0 = ci * chunk;
+        const int n = int(T - t0 < chunk ? T - t0 : chunk);
+        const int buf = int(ci & 1);
+        const int64_t row0 = (b * T + t0) * M + m;  // (b, t0, m)
+        const auto id = [](float x) { return x; };
+        stage_rows(sm.x0[buf], base + t0 * ds, ds, n, ds, st_m,
+                   [](float x) { return tanhf(x); }, lane);
+        stage_rows(sm.x1[buf], A.slots32 + row0 * ds, M * ds, n, ds, nullptr,
+                   id, lane);
+        stage_rows(sm.x2[buf], dseq + row0 * ds, M * ds, n, ds, nullptr, id,
+                   lane);
+        stage_rows(sm.q[buf], A.q_w + (b * T + t0) * dk, dk, n, dk, nullptr,
+                   id, lane);
+        if (lane < n) {
+            sm.drel[buf][lane] = A.d_rel_w ? A.d_rel_w[row0 + lane * M] : 0.f;
+            sm.dage[buf][lane] =
+                A.d_ages_seq ? A.d_ages_seq[row0 + lane * M] : 0.f;
+        }
+    };
     float G[kWMaxCh], e[kWMaxCh], de[kWMaxCh];
 #pragma unroll
     for (int i = 0; i < kWMaxCh; ++i) {
-        const int c = tid + kWThreads * i;
-        const bool in = c < ds;
+        const int c = lane + 64 * i;
+        const bool in = chain && c < ds;
         G[i] = in && A.d_slots_T ? A.d_slots_T[(b * M + m) * ds + c] : 0.f;
         e[i] = in ? A.slot_embed[m * ds + c] : 0.f;
         de[i] = 0.f;
     }
     float dage = A.d_ages_T ? A.d_ages_T[b * M + m] : 0.f;
     float dmu = 0.f;
-    const int chunk = write_chunk(ds);
-    const int64_t nchunks = (T + chunk - 1) / chunk;
+    if (!chain && nchunks > 0) stage(nchunks - 1);
+    __syncthreads();
     for (int64_t ci = nchunks - 1; ci >= 0; --ci) {
-        const int64_t t0 = ci * chunk;
-        const int n = int(T - t0 < chunk ? T - t0 : chunk);
-        const int64_t row0 = (b * T + t0) * M + m;  // (b, t0, m)
-        const auto id = [](float x) { return x; };
-        stage_rows(sm.x0, base + t0 * ds, ds, n, ds, st_m,
-                   [](float x) { return tanhf(x); });
-        stage_rows(sm.x1, A.slots32 + row0 * ds, M * ds, n, ds, nullptr, id);
-        stage_rows(sm.x2, dseq + row0 * ds, M * ds, n, ds, nullptr, id);
-        stage_rows(sm.q, A.q_w + (b * T + t0) * dk, dk, n, dk, nullptr, id);
-        if (tid < n) {
-            sm.drel[tid] = A.d_rel_w ? A.d_rel_w[row0 + tid * M] : 0.f;
-            sm.dage[tid] = A.d_ages_seq ? A.d_ages_seq[row0 + tid * M] : 0.f;
-        }
-        __syncthreads();
-        for (int u = n - 1; u >= 0; --u) {
-            const int64_t bt = b * T + t0 + u;
-            const int64_t o = (bt * M + m) * ds;
-            float th[kWMaxCh] = {};
-            float part = 0.f;  // this thread's part of sum_c G (delta - S)
+        if (!chain) {
+            if (ci > 0) stage(ci - 1);
+        } else {
+            const int buf = int(ci & 1);
+            const int64_t t0 = ci * chunk;
+            const int n = int(T - t0 < chunk ? T - t0 : chunk);
+            for (int u = n - 1; u >= 0; --u) {
+                const int64_t bt = b * T + t0 + u;
+                const int64_t row = bt * M + m;
+                float th[kWMaxCh] = {};
+                float part = 0.f;  // sum_c G (delta - S), this lane's part
 #pragma unroll
-            for (int i = 0; i < kWMaxCh; ++i) {
-                if (kWThreads * i >= ds) break;
-                const int c = tid + kWThreads * i;
-                if (c < ds) {
-                    const float S = sm.x1[u * ds + c];
-                    th[i] = sm.x0[u * ds + c];
-                    part += G[i] * (rnd(th[i], base) - S);
-                    sm.sk[c] = rnd(S + e[i], base);
+                for (int i = 0; i < kWMaxCh; ++i) {
+                    if (64 * i >= ds) break;
+                    const int c = lane + 64 * i;
+                    if (c < ds) {
+                        const float S = sm.x1[buf][u * ds + c];
+                        th[i] = sm.x0[buf][u * ds + c];
+                        part += G[i] * (rnd(th[i], base) - S);
+                        sm.sk[c] = rnd(S + e[i], base);
+                    }
                 }
-            }
-            part = wave_sum(part);
-            if (lane == 0) sm.scal[4 + wv] = part;
-            __syncthreads();
-            float k[2];
-            write_gemv<E>(A, W, sm, k);
-            if (wv == 0) {
+                const float dstr = wave_sum(part);
+                wave_sync();
+                float k[2];
+                if constexpr (kReg)
+                    write_gemv_reg<E>(wr, sm.sk, dk, lane, k);
+                else
+                    write_gemv<E>(W, sm.sk, ds, dk, lane, k);
                 float qv[2];
                 float kk = 0.f, dot = 0.f;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int j = lane + 64 * h;
-                    qv[h] = j < dk ? sm.q[u * dk + j] : 0.f;
+                    qv[h] = j < dk ? sm.q[buf][u * dk + j] : 0.f;
                     kk += k[h] * k[h];
                     dot += k[h] * qv[h];
                 }
@@ -911,11 +1013,9 @@ __global__ __launch_bounds__(kWThreads) void screen_write_bwd_kernel(
                 const float x = (sim - tau) / den;
                 const float r = fmaxf(x, 0.f);
                 const float rw = r * r;
-                const float dstr = (sm.scal[4] + sm.scal[5]) +
-                                   (sm.scal[6] + sm.scal[7]);
                 const bool above = rw > A.floor;
                 dmu += dstr * fmaxf(rw, A.floor);
-                const float drw = sm.drel[u] + (above ? dstr * mu : 0.f);
+                const float drw = sm.drel[buf][u] + (above ? dstr * mu : 0.f);
                 const float dsim = drw * 2.f * r / den;
                 // d k_hat = dsim q;
                 // d k_raw = (d k_hat - k_hat (k_hat . d k_hat)) / kn
@@ -926,64 +1026,111 @@ __global__ __launch_bounds__(kWThreads) void screen_write_bwd_kernel(
                     kd += kh[h] * qv[h];
                 }
                 kd = wave_sum(kd) * dsim;
-                float* dq = A.dq_w + (bt * M + m) * dk;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int j = lane + 64 * h;
                     const float dkr = (dsim * qv[h] - kh[h] * kd) / kn;
                     if (j < dk) {
-                        dq[j] = dsim * kh[h];
-                        A.d_kraw[(bt * M + m) * dk + j] = dkr;
+                        A.dq_w[row * dk + j] = dsim * kh[h];
+                        A.d_kraw[row * dk + j] = dkr;
                         sm.dk[j] = dkr;
                     }
                 }
-                if (lane == 0) {
-                    A.d_tau_w[bt * M + m] = drw * 2.f * r * (x - 1.f) / den;
-                    sm.scal[0] = mu * fmaxf(rw, A.floor);  // strength
-                    sm.scal[1] = rw;
+                if (lane == 0)
+                    A.d_tau_w[row] = drw * 2.f * r * (x - 1.f) / den;
+                const float strength = mu * fmaxf(rw, A.floor);
+                // ages: step t read ages_t; ages_{t+1} = rw > 1e-3 ? 0 :
+                // ages_t + 1
+                dage = sm.dage[buf][u] + (rw > 1e-3f ? 0.f : dage);
+                wave_sync();
+                float dskr[2] = {};
+                if constexpr (kReg) {
+                    // d s_key for both channels of the lane, dk read as
+                    // broadcasts 16 bytes at a time
+                    float a0[4] = {}, a1[4] = {};
+#pragma unroll
+                    for (int j = 0; j < 64; j += 4) {
+                        const float4 d =
+                            *reinterpret_cast<const float4*>(sm.dk + j);
+                        a0[0] += wt[0][j] * d.x;
+                        a0[1] += wt[0][j + 1] * d.y;
+                        a0[2] += wt[0][j + 2] * d.z;
+                        a0[3] += wt[0][j + 3] * d.w;
+                        a1[0] += wt[1][j] * d.x;
+                        a1[1] += wt[1][j + 1] * d.y;
+                        a1[2] += wt[1][j + 2] * d.z;
+                        a1[3] += wt[1][j + 3] * d.w;
+                    }
+                    dskr[0] = (a0[0] + a0[1]) + (a0[2] + a0[3]);
+                    dskr[1] = (a1[0] + a1[1]) + (a1[2] + a1[3]);
                 }
-            }
-            __syncthreads();
-            const float strength = sm.scal[0], rw = sm.scal[1];
-            // ages: step t read ages_t; ages_{t+1} = rw > 1e-3 ? 0 : ages_t + 1
-            dage = sm.dage[u] + (rw > 1e-3f ? 0.f : dage);
 #pragma unroll
-            for (int i = 0; i < kWMaxCh; ++i) {
-                if (kWThreads * i >= ds) break;
-                const int c = tid + kWThreads * i;
-                if (c >= ds) continue;
-                const float dsk = write_gemv_t(W, sm.dk, c, dk, lane);
-                de[i] += dsk;
-                A.d_pre[o + c] = strength * G[i] * (1.f - th[i] * th[i]);
-                G[i] = G[i] * (1.f - strength) + dsk + sm.x2[u * ds + c];
+                for (int i = 0; i < kWMaxCh; ++i) {
+                    if (64 * i >= ds) break;
+                    const int c = lane + 64 * i;
+                    if (c >= ds) continue;
+                    float dsk;
+                    if constexpr (kReg)
+                        dsk = dskr[i < 2 ? i : 0];
+                    else
+                        dsk = write_gemv_t(W, sm.dk, c, dk, lane);
+                    de[i] += dsk;
+                    A.d_pre[row * ds + c] =
+                        strength * G[i] * (1.f - th[i] * th[i]);
+                    G[i] = G[i] * (1.f - strength) + dsk +
+                           sm.x2[buf][u * ds + c];
+                }
+                wave_sync();  // this step's reads of sk and dk come before
+                              // the next step's writes
             }
-            __syncthreads();  // sm.dk and sm.scal are rewritten next step
         }
+        __syncthreads();  // chunk ci is read, chunk ci - 1 is staged
     }
+    if (chain) {
 #pragma unroll
-    for (int i = 0; i < kWMaxCh; ++i) {
-        const int c = tid + kWThreads * i;
-        if (c < ds) {
-            A.d_slots0[(b * M + m) * ds + c] = G[i];
-            A.d_embed_part[(b * M + m) * ds + c] = de[i];
+        for (int i = 0; i < kWMaxCh; ++i) {
+            const int c = lane + 64 * i;
+            if (c < ds) {
+                A.d_slots0[(b * M + m) * ds + c] = G[i];
+                A.d_embed_part[(b * M + m) * ds + c] = de[i];
+            }
         }
-    }
-    if (tid == 0) {
-        A.d_ages0[b * M + m] = dage;
-        A.d_mu_bm[b * M + m] = dmu;
+        if (lane == 0) {
+            A.d_ages0[b * M + m] = dage;
+            A.d_mu_bm[b * M + m] = dmu;
+        }
     }
 }
 
-template <typename E, bool kLds>
+template <typename E, bool kLds, bool kReg>
 void launch_write(bool backward, const ScreenWriteArgs& A, size_t lds,
                   hipStream_t stream) {
     const dim3 grid{unsigned(A.B * A.M)}, block{unsigned(kWThreads)};
     if (backward)
-        hipLaunchKernelGGL((screen_write_bwd_kernel<E, kLds>), grid, block,
-                           lds, stream, A);
+        hipLaunchKernelGGL((screen_write_bwd_kernel<E, kLds, kReg>), grid,
+                           block, lds, stream, A);
     else
-        hipLaunchKernelGGL((screen_write_fwd_kernel<E, kLds>), grid, block,
-                           lds, stream, A);
+        hipLaunchKernelGGL((screen_write_fwd_kernel<E, kLds, kReg>), grid,
+                           block, lds, stream, A);
+}
+
+// Weights in registers for d_slot <= 128 and dk <= 64 (the forward then
+// reads them once from global memory; the backward's transposed GEMV still
+// reads rows from LDS), else through LDS when they fit, else from global.
+template <typename E>
+void launch_write_e(bool backward, const ScreenWriteArgs& A,
+                    hipStream_t stream) {
+    const int64_t nw = A.ds * A.dk;
+    const bool reg = A.ds <= kWRegC && A.dk <= 64;
+    const bool in_lds = nw <= kWLdsWeights && (backward || !reg);
+    const size_t lds = in_lds ? size_t(nw) * sizeof(float) : 0;
+    if (reg) {
+        if (in_lds) launch_write<E, true, true>(backward, A, lds, stream);
+        else launch_write<E, false, true>(backward, A, lds, stream);
+    } else {
+        if (in_lds) launch_write<E, true, false>(backward, A, lds, stream);
+        else launch_write<E, false, false>(backward, A, lds, stream);
+    }
 }
 
 unsigned blocks_for_waves(int64_t waves) {
@@ -1029,16 +1176,10 @@ hipError_t launch_screen_scan(bool bf16, bool backward,
 hipError_t launch_screen_write(bool bf16, bool backward,
                                const ScreenWriteArgs& A, hipStream_t stream) {
     if (A.B * A.M == 0) return hipSuccess;
-    const int64_t nw = A.ds * A.dk;
-    const bool in_lds = nw <= kWLdsWeights;
-    const size_t lds = in_lds ? size_t(nw) * sizeof(float) : 0;
-    if (bf16) {
-        if (in_lds) launch_write<bf16_t, true>(backward, A, lds, stream);
-        else launch_write<bf16_t, false>(backward, A, lds, stream);
-    } else {
-        if (in_lds) launch_write<float, true>(backward, A, lds, stream);
-        else launch_write<float, false>(backward, A, lds, stream);
-    }
+    if (bf16)
+        launch_write_e<bf16_t>(backward, A, stream);
+    else
+        launch_write_e<float>(backward, A, stream);
     return hipGetLastError();
 }
 

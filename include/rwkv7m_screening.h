@@ -105,7 +105,7 @@ int rwkv7m_screen_read_backward(
  * per (b, m) walks the steps.  Outputs: slots_seq (S_t rounded to dtype,
  * for the read), slots32 (S_t fp32, for the backward), ages_seq [B][T][M]
  * (the ages step t reads), rel_w [B][T][M], upd2 as the read-only scan,
- * slots_T, ages_T.  Limits: ds <= 1024, dk <= 128. */
+ * slots_T, ages_T.  Limits: ds <= 1024, 1 <= dk <= 128. */
 int rwkv7m_screen_write(int dtype, int64_t B, int64_t T, int64_t M,
                         int64_t ds, int64_t dk, const void *base,
                         const float *slot_term, const float *slot_embed,

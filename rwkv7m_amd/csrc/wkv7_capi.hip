@@ -508,10 +508,10 @@ int sc_write_checks(const char* fn, int dtype, int64_t B, int64_t T,
                     int64_t M, int64_t ds, int64_t dk, double floor,
                     double eps) {
     RWKV7M_TRY(sc_dims(fn, dtype, B, T, M, ds, dk));
-    if (ds > 1024 || dk > 128)
+    if (ds > 1024 || dk > 128 || dk < 1)
         return fail(RWKV7M_ERR_UNSUPPORTED,
                     std::string(fn) +
-                        ": supported sizes are ds <= 1024, dk <= 128");
+                        ": supported sizes are ds <= 1024, 1 <= dk <= 128");
     if (!(floor >= 0.0) || !std::isfinite(floor) || !(eps >= 0.0) ||
         !std::isfinite(eps))
         return fail(RWKV7M_ERR_INVALID_ARGUMENT,

@@ -411,3 +411,39 @@ def test_screening_abi_checks_requests_before_any_device_call(lib):
     assert bwd(1, 2, 8, 16, 64, 64, *args, fake, None, None,
                *([fake] * 3), None) == 1
     assert b"dq is NULL" in lib.rwkv7m_last_error()
+
+
+def test_screening_write_abi_checks_requests_before_any_device_call(lib):
+    fake = 1 << 20
+    write = lib.rwkv7m_screen_write
+    ins = [fake] * 7  # base, slot_term, slot_embed, kw, q_w, tau_w, mu
+    outs = [fake] * 9  # slots0, ages0, slots_seq, .., slots_T, ages_T
+    for ds, dk, msg in ((2048, 64, b"ds <= 1024"), (128, 200, b"dk <= 128"),
+                        (128, 0, b"1 <= dk")):
+        assert write(1, 2, 8, 4, ds, dk, *ins, 0.05, 1e-6, *outs,
+                     None) == 2, (ds, dk)
+        assert msg in lib.rwkv7m_last_error()
+    assert write(1, 2, 8, 4, 128, 64, *ins, -0.1, 1e-6, *outs, None) == 1
+    assert b"floor and eps" in lib.rwkv7m_last_error()
+    assert write(3, 2, 8, 4, 128, 64, *ins, 0.05, 1e-6, *outs, None) == 1
+    assert b"bfloat16 or float32" in lib.rwkv7m_last_error()
+    no_kw = ins[:3] + [None] + ins[4:]
+    assert write(1, 2, 8, 4, 128, 64, *no_kw, 0.05, 1e-6, *outs,
+                 None) == 1
+    assert b"kw is NULL" in lib.rwkv7m_last_error()
+    no_q = ins[:4] + [None] + ins[5:]
+    assert write(1, 2, 8, 4, 128, 64, *no_q, 0.05, 1e-6, *outs, None) == 1
+    assert b"q_w is NULL" in lib.rwkv7m_last_error()
+    # no batch rows or no slots: nothing to do, no pointer read
+    assert write(1, 0, 8, 4, 128, 64, *([None] * 7), 0.05, 1e-6,
+                 *([None] * 9), None) == 0
+    bwd = lib.rwkv7m_screen_write_backward
+    bouts = [fake] * 8  # d_pre, d_slots0, .., d_tau_w
+    cots = [fake, fake, None, None, None]  # slots32, d_slots_seq, optional
+    assert bwd(1, 2, 8, 4, 128, 0, *ins, 0.05, 1e-6, *cots, None, *bouts,
+               None) == 2
+    assert b"1 <= dk" in lib.rwkv7m_last_error()
+    no_dpre = [None] + bouts[1:]
+    assert bwd(1, 2, 8, 4, 128, 64, *ins, 0.05, 1e-6, *cots, None,
+               *no_dpre, None) == 1
+    assert b"d_pre is NULL" in lib.rwkv7m_last_error()

@@ -226,14 +226,17 @@ def test_streaming_with_carried_state_equals_one_call(hip_lib, pieces):
         assert e <= 1e-5, f"streaming {pieces} {name}: {e:.3e}"
 
 
-def test_graph_capture_replays_match_eager(hip_lib):
+@pytest.mark.parametrize("phase", ["read_screening_only", "read_write"])
+def test_graph_capture_replays_match_eager(hip_lib, phase):
     # forward + backward captured in one HIP graph (the launch-bound step's
     # deployment form) and replayed three times, with unrelated eager work
     # between replays; every replay must reproduce the eager outputs and
     # gradients
     from rwkv7m_amd.screening import ScreenState
-    case = _case(2, 40, 64, 80, 32, 80, 5, seed=31, use_age_mask=True)
-    print("case: screening graph replay", flush=True)
+    wopt = WRITE if phase == "read_write" else {}
+    case = _case(2, 40, 64, 80, 32, 80, 5, seed=31, use_age_mask=True,
+                 **wopt)
+    print(f"case: screening graph replay {phase}", flush=True)
     x, h, slots, ages, usage, P, cfg = case
     mod = _module(P, cfg, torch.float32)
     xd = torch.tensor(x, dtype=torch.float32, device="cuda",
@@ -251,7 +254,7 @@ def test_graph_capture_replays_match_eager(hip_lib):
         hd.grad = None
 
     def step():
-        out, new, stats = mod(xd, hd, st)
+        out, new, stats = mod(xd, hd, st, phase=phase)
         (out * dh).sum().backward()
         return [out, new.slots, new.usage_ema, stats["rel_read_mean"],
                 stats["slot_usage_ema_mean"]]

@@ -839,11 +839,23 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_fwd_kernel(
             const float* qs = sm.q[buf];
             for (int u = 0; u < n; ++u) {
                 const int64_t t = t0 + u;
+                // the step's staged inputs, read before the fence so that
+                // their latency overlaps the GEMV
+                float qv[2], dlt[kWMaxCh];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int j = lane + 64 * h;
+                    qv[h] = j < dk ? qs[u * dk + j] : 0.f;
+                }
 #pragma unroll
                 for (int i = 0; i < kWMaxCh; ++i) {
+                    dlt[i] = 0.f;
                     if (64 * i >= ds) break;
                     const int c = lane + 64 * i;
-                    if (c < ds) sm.sk[c] = rnd(S[i] + e[i], base);
+                    if (c < ds) {
+                        dlt[i] = dl[u * ds + c];
+                        sm.sk[c] = rnd(S[i] + e[i], base);
+                    }
                 }
                 wave_sync();
                 float k[2];
@@ -856,7 +868,7 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_fwd_kernel(
                 for (int h = 0; h < 2; ++h) {
                     const int j = lane + 64 * h;
                     kk += k[h] * k[h];
-                    dot += j < dk ? k[h] * qs[u * dk + j] : 0.f;
+                    dot += j < dk ? k[h] * qv[h] : 0.f;
                 }
                 kk = wave_sum(kk);
                 dot = wave_sum(dot);
@@ -879,8 +891,7 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_fwd_kernel(
                         st1(seq + row * ds + c, S[i]);
                         A.slots32[row * ds + c] = S[i];
                     }
-                    const float u_ =
-                        in ? strength * (dl[u * ds + c] - S[i]) : 0.f;
+                    const float u_ = in ? strength * (dlt[i] - S[i]) : 0.f;
                     const float u2 = wave_sum(u_ * u_);
                     if (lane == 0) A.upd2[row * ((ds + 63) / 64) + i] = u2;
                     S[i] += u_;
@@ -979,7 +990,17 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
             for (int u = n - 1; u >= 0; --u) {
                 const int64_t bt = b * T + t0 + u;
                 const int64_t row = bt * M + m;
-                float th[kWMaxCh] = {};
+                float th[kWMaxCh] = {}, dsv[kWMaxCh] = {};
+                float qv[2];
+                // the step's staged inputs, read before the fence so that
+                // their latency overlaps the GEMV
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int j = lane + 64 * h;
+                    qv[h] = j < dk ? sm.q[buf][u * dk + j] : 0.f;
+                }
+                const float drel_u = sm.drel[buf][u];
+                const float dage_u = sm.dage[buf][u];
                 float part = 0.f;  // sum_c G (delta - S), this lane's part
 #pragma unroll
                 for (int i = 0; i < kWMaxCh; ++i) {
@@ -988,6 +1009,7 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
                     if (c < ds) {
                         const float S = sm.x1[buf][u * ds + c];
                         th[i] = sm.x0[buf][u * ds + c];
+                        dsv[i] = sm.x2[buf][u * ds + c];
                         part += G[i] * (rnd(th[i], base) - S);
                         sm.sk[c] = rnd(S + e[i], base);
                     }
@@ -999,12 +1021,9 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
                     write_gemv_reg<E>(wr, sm.sk, dk, lane, k);
                 else
                     write_gemv<E>(W, sm.sk, ds, dk, lane, k);
-                float qv[2];
                 float kk = 0.f, dot = 0.f;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    const int j = lane + 64 * h;
-                    qv[h] = j < dk ? sm.q[buf][u * dk + j] : 0.f;
                     kk += k[h] * k[h];
                     dot += k[h] * qv[h];
                 }
@@ -1015,7 +1034,7 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
                 const float rw = r * r;
                 const bool above = rw > A.floor;
                 dmu += dstr * fmaxf(rw, A.floor);
-                const float drw = sm.drel[buf][u] + (above ? dstr * mu : 0.f);
+                const float drw = drel_u + (above ? dstr * mu : 0.f);
                 const float dsim = drw * 2.f * r / den;
                 // d k_hat = dsim q;
                 // d k_raw = (d k_hat - k_hat (k_hat . d k_hat)) / kn
@@ -1041,7 +1060,7 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
                 const float strength = mu * fmaxf(rw, A.floor);
                 // ages: step t read ages_t; ages_{t+1} = rw > 1e-3 ? 0 :
                 // ages_t + 1
-                dage = sm.dage[buf][u] + (rw > 1e-3f ? 0.f : dage);
+                dage = dage_u + (rw > 1e-3f ? 0.f : dage);
                 wave_sync();
                 float dskr[2] = {};
                 if constexpr (kReg) {
@@ -1077,8 +1096,7 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
                     de[i] += dsk;
                     A.d_pre[row * ds + c] =
                         strength * G[i] * (1.f - th[i] * th[i]);
-                    G[i] = G[i] * (1.f - strength) + dsk +
-                           sm.x2[buf][u * ds + c];
+                    G[i] = G[i] * (1.f - strength) + dsk + dsv[i];
                 }
                 wave_sync();  // this step's reads of sk and dk come before
                               // the next step's writes

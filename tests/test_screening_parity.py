@@ -326,11 +326,14 @@ def test_write_phase_backward_matches_autograd_oracle(hip_lib, opt):
     _check_write_backward(case, f"screening read_write bwd {opt}")
 
 
-# The write kernels stage min(32, 4096 // d_slot) steps at a time: these
-# shapes cross several chunk boundaries (d_slot 128: chunks of 32, the last
-# partial; d_slot 300: chunks of 13, two channels per thread, and d_k not a
-# multiple of 4).
-WRITE_CHUNKED = [(1, 70, 64, 128, 64, 64, 3), (1, 30, 48, 300, 30, 40, 2)]
+# The write kernels stage min(32, 2048 // max(d_slot, d_k)) steps at a
+# time: these shapes cross several chunk boundaries.  d_slot 128, d_k 64:
+# chunks of 16, weights in registers.  d_slot 300, d_k 30: chunks of 6,
+# five channels per lane, weights in LDS, d_k not a multiple of 4.
+# d_slot 260, d_k 72: chunks of 7, weights read from global memory, two key
+# columns per lane.
+WRITE_CHUNKED = [(1, 70, 64, 128, 64, 64, 3), (1, 30, 48, 300, 30, 40, 2),
+                 (1, 20, 48, 260, 72, 40, 2)]
 
 
 @pytest.mark.parametrize("shape", WRITE_CHUNKED, ids=str)

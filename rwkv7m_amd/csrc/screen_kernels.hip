@@ -793,6 +793,9 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_fwd_kernel(
     const float* W = write_weights<kLds>(A, wlds);
     const int tid = threadIdx.x, lane = tid & 63;
     const bool chain = tid < 64;  // wave 0: the steps; wave 1: staging
+    // channels per lane: at most 2 with the weights in registers
+    // (d_slot <= 128)
+    constexpr int NCH = kReg ? 2 : kWMaxCh;
     float wr[kReg ? kWRegC : 1];
     write_reg_init<kReg>(W, int(A.ds), A.dk, lane, wr, sm.sk);
     const int64_t b = blockIdx.x / A.M;
@@ -817,9 +820,9 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_fwd_kernel(
         stage_rows(sm.q[buf], qw + t0 * dk, dk, n, dk, nullptr,
                    [](float x) { return x; }, lane);
     };
-    float S[kWMaxCh], e[kWMaxCh];
+    float S[NCH], e[NCH];
 #pragma unroll
-    for (int i = 0; i < kWMaxCh; ++i) {
+    for (int i = 0; i < NCH; ++i) {
         const int c = lane + 64 * i;
         const bool in = chain && c < ds;
         S[i] = in ? A.slots0[(b * M + m) * ds + c] : 0.f;
@@ -841,14 +844,14 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_fwd_kernel(
                 const int64_t t = t0 + u;
                 // the step's staged inputs, read before the fence so that
                 // their latency overlaps the GEMV
-                float qv[2], dlt[kWMaxCh];
+                float qv[2], dlt[NCH];
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int j = lane + 64 * h;
                     qv[h] = j < dk ? qs[u * dk + j] : 0.f;
                 }
 #pragma unroll
-                for (int i = 0; i < kWMaxCh; ++i) {
+                for (int i = 0; i < NCH; ++i) {
                     dlt[i] = 0.f;
                     if (64 * i >= ds) break;
                     const int c = lane + 64 * i;
@@ -883,7 +886,7 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_fwd_kernel(
                 age = rw > 1e-3f ? 0.f : age + 1.f;
                 const float strength = mu * fmaxf(rw, A.floor);
 #pragma unroll
-                for (int i = 0; i < kWMaxCh; ++i) {
+                for (int i = 0; i < NCH; ++i) {
                     if (64 * i >= ds) break;
                     const int c = lane + 64 * i;
                     const bool in = c < ds;
@@ -904,7 +907,7 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_fwd_kernel(
     }
     if (chain) {
 #pragma unroll
-        for (int i = 0; i < kWMaxCh; ++i) {
+        for (int i = 0; i < NCH; ++i) {
             const int c = lane + 64 * i;
             if (c < ds) A.slots_T[(b * M + m) * ds + c] = S[i];
         }
@@ -921,6 +924,9 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
     const float* W = write_weights<kLds>(A, wlds);
     const int tid = threadIdx.x, lane = tid & 63;
     const bool chain = tid < 64;  // wave 0: the steps; wave 1: staging
+    // channels per lane: at most 2 with the weights in registers
+    // (d_slot <= 128)
+    constexpr int NCH = kReg ? 2 : kWMaxCh;
     float wr[kReg ? kWRegC : 1];
     write_reg_init<kReg>(W, int(A.ds), A.dk, lane, wr, sm.sk);
     // with kReg also the rows W[lane + 64 i][0..63] of the lane's channels,
@@ -967,9 +973,9 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
                 A.d_ages_seq ? A.d_ages_seq[row0 + lane * M] : 0.f;
         }
     };
-    float G[kWMaxCh], e[kWMaxCh], de[kWMaxCh];
+    float G[NCH], e[NCH], de[NCH];
 #pragma unroll
-    for (int i = 0; i < kWMaxCh; ++i) {
+    for (int i = 0; i < NCH; ++i) {
         const int c = lane + 64 * i;
         const bool in = chain && c < ds;
         G[i] = in && A.d_slots_T ? A.d_slots_T[(b * M + m) * ds + c] : 0.f;
@@ -990,7 +996,7 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
             for (int u = n - 1; u >= 0; --u) {
                 const int64_t bt = b * T + t0 + u;
                 const int64_t row = bt * M + m;
-                float th[kWMaxCh] = {}, dsv[kWMaxCh] = {};
+                float th[NCH] = {}, dsv[NCH] = {};
                 float qv[2];
                 // the step's staged inputs, read before the fence so that
                 // their latency overlaps the GEMV
@@ -1003,7 +1009,7 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
                 const float dage_u = sm.dage[buf][u];
                 float part = 0.f;  // sum_c G (delta - S), this lane's part
 #pragma unroll
-                for (int i = 0; i < kWMaxCh; ++i) {
+                for (int i = 0; i < NCH; ++i) {
                     if (64 * i >= ds) break;
                     const int c = lane + 64 * i;
                     if (c < ds) {
@@ -1084,7 +1090,7 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
                     dskr[1] = (a1[0] + a1[1]) + (a1[2] + a1[3]);
                 }
 #pragma unroll
-                for (int i = 0; i < kWMaxCh; ++i) {
+                for (int i = 0; i < NCH; ++i) {
                     if (64 * i >= ds) break;
                     const int c = lane + 64 * i;
                     if (c >= ds) continue;
@@ -1106,7 +1112,7 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
     }
     if (chain) {
 #pragma unroll
-        for (int i = 0; i < kWMaxCh; ++i) {
+        for (int i = 0; i < NCH; ++i) {
             const int c = lane + 64 * i;
             if (c < ds) {
                 A.d_slots0[(b * M + m) * ds + c] = G[i];

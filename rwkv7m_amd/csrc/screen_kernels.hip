@@ -947,8 +947,18 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
     const int64_t T = A.T, M = A.M;
     const int ds = int(A.ds), dk = A.dk;
     const E* base = static_cast<const E*>(A.base) + b * T * ds;
-    const E* dseq = static_cast<const E*>(A.d_slots_seq);
     const float* st_m = A.slot_term + m * ds;
+    // per-(b, slot) bases: row (b, t, m) of a [B][T][M][x] array is
+    // t * M * x past them
+    const int64_t bm0 = b * T * M + m;
+    const float* s32_bm = A.slots32 + bm0 * ds;
+    const E* dseq_bm = static_cast<const E*>(A.d_slots_seq) + bm0 * ds;
+    const float* qw_b = A.q_w + b * T * dk;
+    float* dpre_bm = A.d_pre + bm0 * ds;
+    float* dqw_bm = A.dq_w + bm0 * dk;
+    float* dkraw_bm = A.d_kraw + bm0 * dk;
+    float* dtau_bm = A.d_tau_w + bm0;
+    const int64_t Mds = M * ds, Mdk = M * dk;
     const float mu = A.mu[m], tau = *A.tau_w;
     const float den = 1.f - tau + A.eps;
     const int chunk = write_chunk(ds, dk);
@@ -957,16 +967,15 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
         const int64_t t0 = ci * chunk;
         const int n = int(T - t0 < chunk ? T - t0 : chunk);
         const int buf = int(ci & 1);
-        const int64_t row0 = (b * T + t0) * M + m;  // (b, t0, m)
+        const int64_t row0 = bm0 + t0 * M;  // (b, t0, m)
         const auto id = [](float x) { return x; };
         stage_rows(sm.x0[buf], base + t0 * ds, ds, n, ds, st_m,
                    [](float x) { return tanhf(x); }, lane);
-        stage_rows(sm.x1[buf], A.slots32 + row0 * ds, M * ds, n, ds, nullptr,
-                   id, lane);
-        stage_rows(sm.x2[buf], dseq + row0 * ds, M * ds, n, ds, nullptr, id,
+        stage_rows(sm.x1[buf], s32_bm + t0 * Mds, Mds, n, ds, nullptr, id,
                    lane);
-        stage_rows(sm.q[buf], A.q_w + (b * T + t0) * dk, dk, n, dk, nullptr,
-                   id, lane);
+        stage_rows(sm.x2[buf], dseq_bm + t0 * Mds, Mds, n, ds, nullptr, id,
+                   lane);
+        stage_rows(sm.q[buf], qw_b + t0 * dk, dk, n, dk, nullptr, id, lane);
         if (lane < n) {
             sm.drel[buf][lane] = A.d_rel_w ? A.d_rel_w[row0 + lane * M] : 0.f;
             sm.dage[buf][lane] =
@@ -994,8 +1003,7 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
             const int64_t t0 = ci * chunk;
             const int n = int(T - t0 < chunk ? T - t0 : chunk);
             for (int u = n - 1; u >= 0; --u) {
-                const int64_t bt = b * T + t0 + u;
-                const int64_t row = bt * M + m;
+                const int64_t tt = t0 + u;
                 float th[NCH] = {}, dsv[NCH] = {};
                 float qv[2];
                 // the step's staged inputs, read before the fence so that
@@ -1056,13 +1064,13 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
                     const int j = lane + 64 * h;
                     const float dkr = (dsim * qv[h] - kh[h] * kd) / kn;
                     if (j < dk) {
-                        A.dq_w[row * dk + j] = dsim * kh[h];
-                        A.d_kraw[row * dk + j] = dkr;
+                        dqw_bm[tt * Mdk + j] = dsim * kh[h];
+                        dkraw_bm[tt * Mdk + j] = dkr;
                         sm.dk[j] = dkr;
                     }
                 }
                 if (lane == 0)
-                    A.d_tau_w[row] = drw * 2.f * r * (x - 1.f) / den;
+                    dtau_bm[tt * M] = drw * 2.f * r * (x - 1.f) / den;
                 const float strength = mu * fmaxf(rw, A.floor);
                 // ages: step t read ages_t; ages_{t+1} = rw > 1e-3 ? 0 :
                 // ages_t + 1
@@ -1100,7 +1108,7 @@ __attribute__((amdgpu_waves_per_eu(1, 1))) void screen_write_bwd_kernel(
                     else
                         dsk = write_gemv_t(W, sm.dk, c, dk, lane);
                     de[i] += dsk;
-                    A.d_pre[row * ds + c] =
+                    dpre_bm[tt * Mds + c] =
                         strength * G[i] * (1.f - th[i] * th[i]);
                     G[i] = G[i] * (1.f - strength) + dsk + dsv[i];
                 }

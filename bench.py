@@ -7,13 +7,16 @@ callables the reference's FFI registry binds (src/rwkv7m/kernels/
 wkv_ffi.py:21-34).  Inputs (vectors, S0, dy, dS_T) are synthetic, with the
 model's input distributions, and resident in HBM before timing starts.
 
-The method mirrors the reference's WKV microbenchmark
-(scripts/benchmark_wkv_accelerator.py:88-97): W untimed warmup steps, then
-K steps between two device synchronisations.  Tokens/s = B*T / seconds per
-step.  Kernel durations come from HIP events recorded on the stream the
-kernels run on.  ``cpu_baseline`` times the CPU restatement of the reference
-scan (oracle/, fp32, OpenMP over (b, h)) on a bounded sample of the same
-workload on the host cores.
+Two timings.  The headline: W untimed warmup steps, then K steps back to
+back between two device synchronisations; tokens/s = B*T / seconds per
+step, with kernel durations from HIP events recorded on the stream the
+kernels run on.  Beside it, ``reference_method`` repeats the reference's WKV
+microbenchmark (scripts/benchmark_wkv_accelerator.py:88-97, :162-185):
+each call host-synchronised, median / p95 / min over ``--ref-iters``
+iterations, for the forward alone and for forward+backward.
+``cpu_baseline`` times the CPU restatement of the reference scan (oracle/,
+fp32, OpenMP over (b, h)) on a bounded sample of the same workload on the
+host cores.
 
 Prints ONE JSON line.
 """
@@ -60,6 +63,9 @@ def parse_args():
                    help="screening phase for --path screening")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="target CPU-baseline sample duration (0 = skip)")
+    p.add_argument("--ref-iters", type=int, default=100,
+                   help="iterations of the reference's per-call "
+                        "synchronised timing (0 = skip)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="before warmup, run one plain device copy of this "
                         "many MiB (the reference kernel for scaling HBM "
@@ -93,6 +99,41 @@ def measured_traffic(kernel, config, chunk, layout="tbhn"):
     return None
 
 
+def cpu_threads():
+    """(threads used, CPUs in this process's affinity set).  The threads are
+    the affinity set, capped at 16: the GPU boxes give one GPU a 16-CPU
+    share whatever the affinity mask shows."""
+    cpus = len(os.sched_getaffinity(0))
+    return min(cpus, 16), cpus
+
+
+def timing_summary(samples_ms):
+    """The reference's per-call summary (benchmark_wkv_accelerator.py:
+    72-85): median, mean, min, p95 and max in milliseconds."""
+    import statistics
+    xs = sorted(samples_ms)
+    p95 = xs[min(len(xs) - 1, int(round(0.95 * (len(xs) - 1))))]
+    return {"median_ms": statistics.median(xs),
+            "mean_ms": statistics.fmean(xs), "min_ms": xs[0],
+            "p95_ms": p95, "max_ms": xs[-1], "iterations": len(xs)}
+
+
+def per_call_timing(fn, iters, warmup=3):
+    """Host-synchronised wall time of each of ``iters`` calls of fn (the
+    reference's _measure, benchmark_wkv_accelerator.py:88-97)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(iters):
+        t0 = time.perf_counter_ns()
+        fn()
+        torch.cuda.synchronize()
+        samples.append((time.perf_counter_ns() - t0) / 1e6)
+    return timing_summary(samples)
+
+
 def cpu_baseline(cfg, target_s):
     """Time the CPU restatement (oracle, fp32, OpenMP over (b, h)) on the
     config's (B, H, N): a reduced T chosen to take about ``target_s``, or
@@ -102,7 +143,7 @@ def cpu_baseline(cfg, target_s):
     import oracle
     from rwkv7m_amd.synthetic import make_inputs
 
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    threads, cpus = cpu_threads()
     B, H, N = cfg["B"], cfg["H"], cfg["N"]
 
     def run(T):
@@ -129,10 +170,12 @@ def cpu_baseline(cfg, target_s):
         "value": reps * B * T / dt,
         "unit": "tokens/s",
         "cores": threads,
+        "affinity_cpus": cpus,
         "kind": "port",
         "sample": (f"fp32 C restatement of the reference scan fwd+bwd, "
                    f"B={B} T={T} H={H} N={N}, {reps} run(s), {dt:.1f} s "
-                   f"on {threads} threads"),
+                   f"on {threads} threads ({cpus} CPUs in the affinity "
+                   f"set)"),
     }
 
 
@@ -142,7 +185,7 @@ def decode_cpu_baseline(cfg, target_s):
     import oracle
     from rwkv7m_amd.synthetic import make_inputs
 
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    threads, cpus = cpu_threads()
     B, H, N = cfg["B"], cfg["H"], cfg["N"]
     inp = make_inputs(1, B, H, N, dtype=cfg["dtype"], seed=7,
                       state_std=cfg.get("state_std", 0.0))
@@ -158,10 +201,11 @@ def decode_cpu_baseline(cfg, target_s):
         "value": reps * B / dt,
         "unit": "tokens/s",
         "cores": threads,
+        "affinity_cpus": cpus,
         "kind": "port",
         "sample": (f"fp32 C restatement of one reference step, B={B} H={H} "
                    f"N={N}, {reps} step(s), {dt:.1f} s on {threads} "
-                   f"threads"),
+                   f"threads ({cpus} CPUs in the affinity set)"),
     }
 
 
@@ -258,7 +302,7 @@ def timemix_cpu_baseline(cfg, target_s):
     import oracle
     from oracle import timemix_oracle as tmo
 
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    threads, cpus = cpu_threads()
     B, H, N = cfg["B"], cfg["H"], cfg["N"]
     C = H * N
     rng = np.random.default_rng(7)
@@ -303,6 +347,7 @@ def timemix_cpu_baseline(cfg, target_s):
         "value": reps * B * T / dt,
         "unit": "tokens/s",
         "cores": threads,
+        "affinity_cpus": cpus,
         "kind": "port",
         "sample": (f"numpy time-mix producers/consumer (fp32) around the "
                    f"fp32 C WKV restatement, fwd+bwd, B={B} T={T} H={H} "
@@ -790,6 +835,21 @@ def main():
         "kernels_ms": {"forward": fwd_ms, "backward": bwd_ms},
         "step_roofline_frac": step_gbs / HBM_PEAK_GBS,
     }
+    if args.ref_iters > 0:
+        # the reference's method: every call host-synchronised, median over
+        # the iterations, forward alone and forward+backward
+        def fwd_only():
+            wkv_hip.forward(*vecs, s0, layout=args.layout)
+
+        fwd_t = per_call_timing(fwd_only, args.ref_iters)
+        step_t = per_call_timing(step, args.ref_iters)
+        result["reference_method"] = {
+            "forward": fwd_t,
+            "forward_backward": step_t,
+            "fwd_bwd_tokens_per_s_median": tokens / (step_t["median_ms"] /
+                                                     1e3),
+            "fwd_tokens_per_s_median": tokens / (fwd_t["median_ms"] / 1e3),
+        }
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
     else:

@@ -55,7 +55,8 @@ typedef enum rwkv7m_status {
     RWKV7M_OK = 0,
     RWKV7M_ERR_INVALID_ARGUMENT = 1, /* bad shape, dtype, pointer or size */
     RWKV7M_ERR_UNSUPPORTED = 2,      /* valid request this build cannot run */
-    RWKV7M_ERR_HIP = 3               /* a HIP runtime call or launch failed */
+    RWKV7M_ERR_HIP = 3,              /* a HIP runtime call or launch failed */
+    RWKV7M_ERR_DEVICE = 4            /* a kernel's bounded wait gave up */
 } rwkv7m_status;
 
 /* Version of this ABI; bumped on any incompatible change. */
@@ -63,6 +64,41 @@ int rwkv7m_abi_version(void);
 
 /* Message describing the last failed call on this thread ("" if none). */
 const char *rwkv7m_last_error(void);
+
+/*
+ * Device status of the kernels' bounded waits.  The MFMA kernels hand data
+ * between their waves through LDS and wait for each hand-over a bounded
+ * number of times, so every wave always exits.  A wait that gives up does
+ * not pass silently: the workgroup overwrites every output of its
+ * (batch, head) -- y, S_T, checkpoints, gradients -- with NaN and raises a
+ * per-device failure counter.  This call synchronises `stream`, then reads
+ * and clears the current device's counter: RWKV7M_OK if no wait gave up
+ * since the last call, RWKV7M_ERR_DEVICE (with the count in
+ * rwkv7m_last_error()) otherwise.  No counterpart in the reference (its
+ * Pallas kernels have no inter-wave hand-over); for callers that check a
+ * run's health, and for the failure-path tests.
+ */
+int rwkv7m_device_status(void *stream);
+
+/*
+ * Poll budget of every bounded wait in later launches; 0 restores the
+ * default (2^20 polls, about 70 ms at the lowest clock, orders of magnitude
+ * above any real hand-over).  A hook for tests of the failure path: a budget
+ * of 1 makes the waits give up without any kernel hanging or faulting.  Not
+ * thread-safe against launches on other threads.  No counterpart in the
+ * reference.
+ */
+void rwkv7m_debug_set_wait_limit(int64_t polls);
+
+/*
+ * Name of the kernel path the last successful WKV-7 call on this thread
+ * launched: "wave_forward" (MFMA chunked forward), "decode" (single-token
+ * kernel), "seq_forward", "chunk_backward" (MFMA chunked backward),
+ * "seq_backward", or "" (nothing launched).  A diagnostic for tests that
+ * must prove which kernel served a request; no counterpart in the
+ * reference.
+ */
+const char *rwkv7m_wkv7_last_path(void);
 
 /* Number of aux checkpoints for T tokens at interval ci: ceil(T/ci) + 1. */
 int64_t rwkv7m_wkv7_checkpoint_count(int64_t T, int64_t checkpoint_interval);

@@ -64,8 +64,6 @@ __device__ __forceinline__ float wave_sum(float x) {
            (lane_value(x, 32) + lane_value(x, 48));
 }
 
-__device__ __forceinline__ float cvt(float x) { return x; }
-__device__ __forceinline__ float cvt(bf16_t x) { return bf16_to_f32(x); }
 __device__ __forceinline__ float ld1(const float* p) { return *p; }
 __device__ __forceinline__ float ld1(const bf16_t* p) {
     return bf16_to_f32(*p);

@@ -22,6 +22,8 @@
 namespace {
 
 thread_local std::string g_last_error;
+// The kernel the last successful WKV-7 call on this thread launched.
+thread_local const char* g_last_path = "";
 
 int fail(int code, const std::string& msg) {
     g_last_error = msg;
@@ -169,6 +171,7 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
                  const void* v, const void* a, const void* b,
                  const float* s0, void* y, float* s_t, void* ckpt,
                  int64_t ci, hipStream_t stream, bool batch_major) {
+    g_last_path = "";
     Dims d;
     RWKV7M_TRY(check_dims(fn, dtype, T, B, H, N, &d));
     const bool vecs = d.vec_elems > 0, st = d.state_elems > 0;
@@ -203,6 +206,9 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
         c.y = y;
         c.s_t = s_t;
         c.ckpt = ckpt;
+        RWKV7M_TRY(hip_status("device wait configuration",
+                              rwkv7m::wait_config(&c.wait)));
+        g_last_path = "wave_forward";
         return hip_status("chunked forward launch",
                           rwkv7m::launch_wave_forward(c, stream));
     }
@@ -226,8 +232,11 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     p.ckpt_bf16 = ckpt_bf16(dtype, N, ci);
     p.ci = ci;
     if (T == 1 && !ckpt && N == 64 &&
-        all_aligned16({r, w, k, v, a, b, y, s0, s_t}))
+        all_aligned16({r, w, k, v, a, b, y, s0, s_t})) {
+        g_last_path = "decode";
         return hip_status("decode launch", rwkv7m::launch_decode(p, stream));
+    }
+    g_last_path = "seq_forward";
     return hip_status("sequential forward launch",
                       rwkv7m::launch_seq_forward(p, stream));
 }
@@ -242,6 +251,7 @@ int backward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
                          void* dk, void* dv, void* dneg_kk, void* dkka,
                          float* ds0, hipStream_t s, bool batch_major) {
     (void)initial_state;  // checkpoints[0] holds it
+    g_last_path = "";
     Dims d;
     RWKV7M_TRY(check_dims(fn, dtype, T, B, H, N, &d));
     if (checkpoint_interval < 0)
@@ -293,6 +303,7 @@ int backward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
         c.da = dneg_kk;
         c.db = dkka;
         c.ds0 = ds0;
+        g_last_path = "chunk_backward";
         return hip_status("chunked backward launch",
                           rwkv7m::launch_chunk_backward(c, s));
     }
@@ -321,6 +332,7 @@ int backward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     p.da = dneg_kk;
     p.db = dkka;
     p.ds0 = ds0;
+    g_last_path = "seq_backward";
     return hip_status("sequential backward launch",
                       rwkv7m::launch_seq_backward(p, s));
 }
@@ -551,6 +563,27 @@ extern "C" {
 int rwkv7m_abi_version(void) { return 1; }
 
 const char* rwkv7m_last_error(void) { return g_last_error.c_str(); }
+
+const char* rwkv7m_wkv7_last_path(void) { return g_last_path; }
+
+int rwkv7m_device_status(void* stream) {
+    g_last_error.clear();
+    unsigned int n = 0;
+    RWKV7M_TRY(hip_status("rwkv7m_device_status",
+                          rwkv7m::take_wait_failures(
+                              static_cast<hipStream_t>(stream), &n)));
+    if (n != 0)
+        return fail(RWKV7M_ERR_DEVICE,
+                    "rwkv7m_device_status: " + std::to_string(n) +
+                        " bounded wait(s) inside the kernels gave up; the "
+                        "outputs of the affected (batch, head) pairs were "
+                        "set to NaN");
+    return RWKV7M_OK;
+}
+
+void rwkv7m_debug_set_wait_limit(int64_t polls) {
+    rwkv7m::set_wait_limit(polls);
+}
 
 int64_t rwkv7m_wkv7_checkpoint_count(int64_t T, int64_t checkpoint_interval) {
     if (T < 0 || checkpoint_interval <= 0) return -1;

@@ -9,6 +9,21 @@
 
 namespace rwkv7m {
 
+// Bounded waits (wkv7_status.hip): the poll budget of one hand-over and this
+// device's failure counter.
+constexpr int kDefaultWaitPolls = 1 << 20;
+struct WaitCfg {
+    int limit;                // polls per wait before it gives up
+    unsigned int* failures;   // device address of the failure counter
+};
+// The current device's configuration (looks the counter up once per device).
+hipError_t wait_config(WaitCfg* out);
+// Poll budget for later launches (0: the default); a hook for tests of the
+// failure path.
+void set_wait_limit(int64_t polls);
+// Synchronises the stream, then reads and clears the current device's count.
+hipError_t take_wait_failures(hipStream_t stream, unsigned int* count);
+
 struct SeqFwdArgs {
     bool bf16;
     int64_t T, B, H, N;
@@ -45,6 +60,7 @@ struct ChunkFwdArgs {
     void* y;
     float* s_t;
     void* ckpt;  // nullptr: no checkpoints; else bf16, one per chunk (every L)
+    WaitCfg wait;
 };
 
 // The forward runs in 16-token chunks (wkv7_wave_fwd.hip); L in {16, 32, 64}

@@ -62,10 +62,11 @@ constexpr int NPROD = 8;     // producer waves
 constexpr int NSLOT = 3;     // hand-over ring
 constexpr int WTHREADS = 64 * (NCHAIN + NPROD);
 constexpr int XPITCH = WN + 8;  // bf16 transpose buffer row pitch
-// Bound on the polls of one hand-over (each poll sleeps ~64 cycles).  A wave
-// waits for at most a few other chunks; the bound is orders of magnitude
-// above that and only guarantees that every wave exits.
-constexpr int kPollLimit = 1 << 20;
+// Every hand-over wait is bounded (WaitCfg::limit polls of ~64 cycles; a
+// wave waits for at most a few other chunks, and the default bound is orders
+// of magnitude above that), so every wave exits.  A wait that gives up marks
+// the workgroup failed: its outputs are then overwritten with NaN and the
+// device's failure counter is raised (wkv7_status.hip).
 
 typedef short i16x8_t __attribute__((ext_vector_type(8)));
 
@@ -101,6 +102,7 @@ struct WaveFwdSmem {
     float eL[NPROD][WN];    // per producer: 2^{g_L} per column
     int ready[NSLOT];       // chunk held by the slot (-1: none yet)
     int done[NSLOT];        // chains finished with the slot, over all uses
+    int failed;             // a bounded wait of this workgroup gave up
 };
 
 __device__ __forceinline__ bf16x8_t pk8(const i16x4_t& lo, const i16x4_t& hi) {
@@ -158,14 +160,31 @@ __device__ __forceinline__ void lds_store(int* p, int x) {
     __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Poll an LDS word until pred(value) holds (bounded).
+// Poll an LDS word until pred(value) holds, at most `limit` times; false if
+// it never did.
 template <typename Pred>
-__device__ __forceinline__ void poll(int* p, Pred pred) {
-    for (int it = 0; it < kPollLimit; ++it) {
-        if (pred(__builtin_amdgcn_readfirstlane(lds_load(p)))) break;
+__device__ __forceinline__ bool poll(int* p, int limit, Pred pred) {
+    bool ok = false;
+    for (int it = 0; it < limit; ++it) {
+        if (pred(__builtin_amdgcn_readfirstlane(lds_load(p)))) {
+            ok = true;
+            break;
+        }
         __builtin_amdgcn_s_sleep(1);
     }
     asm volatile("" ::: "memory");
+    return ok;
+}
+
+// A wait gave up: mark the workgroup failed (LDS) and count it on the device
+// (a per-lane global atomic from lane 0).
+__device__ __forceinline__ void wait_failed(int* failed, unsigned int* counter,
+                                         int lane) {
+    if (lane == 0) {
+        lds_store(failed, 1);
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 struct FwdArgs {
@@ -177,6 +196,7 @@ struct FwdArgs {
     float* s_t;
     bf16_t* ckpt;  // nullptr, or bf16 checkpoints every cstride chunks
     int cstride;   // checkpoint interval / 16
+    WaitCfg wait;
 };
 
 // ---------------------------------------------------------------------------
@@ -427,7 +447,9 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
         // ---- hand the chunk to the chains ---------------------------------
         const int s = int(c % NSLOT);
         const int uses = int(c / NSLOT);  // earlier uses of this slot
-        poll(vdone + s, [&](int d) { return d >= NCHAIN * uses; });
+        if (!poll(vdone + s, A.wait.limit,
+                  [&](int d) { return d >= NCHAIN * uses; }))
+            wait_failed(&sm.failed, A.wait.failures, lane);
         Slot& sl = sm.slot[s];
 #pragma unroll
         for (int jpb = 0; jpb < 4; ++jpb) {
@@ -503,7 +525,9 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
         const bf16x8_t Sb0 = pk8(sb[0], sb[1]), Sb1 = pk8(sb[2], sb[3]);
 
         const int s = int(c % NSLOT);
-        poll(vready + s, [&](int x) { return x == int(c); });
+        if (!poll(vready + s, A.wait.limit,
+                  [&](int x) { return x == int(c); }))
+            wait_failed(&sm.failed, A.wait.failures, lane);
         const Slot& sl = sm.slot[s];
         bf16x8_t M[4][2], Q[2];
         i16x4_t B[4], K[4];
@@ -622,6 +646,27 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
     }
 }
 
+// A workgroup whose hand-over failed overwrites every output of its
+// (batch, head) -- y, S_T and the checkpoints -- with NaN, so that a lost
+// hand-over can never pass as a result.
+__device__ __forceinline__ void poison(const FwdArgs& A, int tid) {
+    const int64_t bh = blockIdx.x;
+    const int64_t hoff = A.lay.head(bh, WN);
+    const int64_t NN = WN * WN;
+    const bf16_t nan16 = 0x7fc0;
+    for (int64_t e = tid; e < A.T * WN; e += WTHREADS)
+        A.y[(e / WN) * A.lay.ts + hoff + e % WN] = nan16;
+    for (int e = tid; e < WN * WN; e += WTHREADS)
+        A.s_t[bh * NN + e] = __builtin_nanf("");
+    if (A.ckpt) {
+        const int64_t nch = (A.T + WL - 1) / WL;
+        const int64_t nck = (nch + A.cstride - 1) / A.cstride + 1;
+        for (int64_t c = 0; c < nck; ++c)
+            for (int e = tid; e < WN * WN; e += WTHREADS)
+                A.ckpt[c * A.BH * NN + bh * NN + e] = nan16;
+    }
+}
+
 __global__ void __launch_bounds__(WTHREADS)
 wkv7_wave_fwd_kernel(FwdArgs A) {
     __shared__ WaveFwdSmem sm;
@@ -633,11 +678,15 @@ wkv7_wave_fwd_kernel(FwdArgs A) {
         sm.ready[tid] = -1;
         sm.done[tid] = 0;
     }
+    if (tid == 0) sm.failed = 0;
     __syncthreads();
     if (wv < NCHAIN)
         chain(A, sm, wv, lane);
     else
         produce(A, sm, wv - NCHAIN, lane);
+    // every wait is bounded, so every wave arrives here
+    __syncthreads();
+    if (lds_load(&sm.failed) != 0) poison(A, tid);
 }
 
 }  // namespace
@@ -661,6 +710,7 @@ hipError_t launch_wave_forward(const ChunkFwdArgs& p, hipStream_t stream) {
     A.s_t = p.s_t;
     A.ckpt = static_cast<bf16_t*>(p.ckpt);
     A.cstride = p.L / WL;
+    A.wait = p.wait;
     if (A.BH <= 0) return hipSuccess;
     hipLaunchKernelGGL(wkv7_wave_fwd_kernel, dim3(unsigned(A.BH)),
                        dim3(WTHREADS), 0, stream, A);

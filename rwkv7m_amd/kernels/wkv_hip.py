@@ -50,6 +50,9 @@ DTYPE_BF16 = 1
 EXPORTED_SYMBOLS = (
     "rwkv7m_abi_version",
     "rwkv7m_last_error",
+    "rwkv7m_device_status",
+    "rwkv7m_debug_set_wait_limit",
+    "rwkv7m_wkv7_last_path",
     "rwkv7m_wkv7_checkpoint_count",
     "rwkv7m_wkv7_default_checkpoint_interval",
     "rwkv7m_wkv7_checkpoint_dtype",
@@ -100,6 +103,12 @@ def load_library(path: str | None = None):
         lib.rwkv7m_abi_version.argtypes = []
         lib.rwkv7m_last_error.restype = ctypes.c_char_p
         lib.rwkv7m_last_error.argtypes = []
+        lib.rwkv7m_device_status.restype = i32
+        lib.rwkv7m_device_status.argtypes = [vp]
+        lib.rwkv7m_debug_set_wait_limit.restype = None
+        lib.rwkv7m_debug_set_wait_limit.argtypes = [i64]
+        lib.rwkv7m_wkv7_last_path.restype = ctypes.c_char_p
+        lib.rwkv7m_wkv7_last_path.argtypes = []
         lib.rwkv7m_wkv7_checkpoint_count.restype = i64
         lib.rwkv7m_wkv7_checkpoint_count.argtypes = [i64, i64]
         lib.rwkv7m_wkv7_default_checkpoint_interval.restype = i64
@@ -208,6 +217,30 @@ def _layout(layout: str, r: torch.Tensor):
         B, T, H, N = r.shape
         return "_bthn", T, B, H, N
     raise ValueError(f"layout must be one of {LAYOUTS}, got {layout!r}")
+
+
+def last_path() -> str:
+    """Kernel path of the last successful WKV-7 call on this thread
+    ("wave_forward", "decode", "seq_forward", "chunk_backward",
+    "seq_backward" or "")."""
+    return load_library().rwkv7m_wkv7_last_path().decode()
+
+
+def device_status(device=None) -> None:
+    """Synchronise the device's current stream and raise ``RuntimeError`` if
+    any bounded wait inside the kernels gave up since the last check (the
+    affected outputs are NaN); clears the device's failure count."""
+    dev = torch.device(device) if device is not None else \
+        torch.device("cuda", torch.cuda.current_device())
+    with torch.cuda.device(dev):
+        rc = load_library().rwkv7m_device_status(_stream(dev))
+    _check(rc, "rwkv7m_device_status")
+
+
+def set_wait_limit(polls: int) -> None:
+    """Poll budget of the kernels' bounded waits for later launches (0: the
+    library default).  For tests of the failure path."""
+    load_library().rwkv7m_debug_set_wait_limit(int(polls))
 
 
 def default_checkpoint_interval(dtype: torch.dtype, head_size: int) -> int:
@@ -340,7 +373,7 @@ def register_hip_backend(*, replace: bool = False) -> WKVFFIBackend:
 __all__ = [
     "EXPORTED_SYMBOLS", "LAYOUTS", "LIB_PATH", "backward", "checkpoint_count",
     "checkpoint_dtype",
-    "decode_inplace", "default_checkpoint_interval", "forward",
-    "forward_with_aux", "hip_wkv_ffi_backend", "load_library",
-    "register_hip_backend",
+    "decode_inplace", "default_checkpoint_interval", "device_status",
+    "forward", "forward_with_aux", "hip_wkv_ffi_backend", "last_path",
+    "load_library", "register_hip_backend", "set_wait_limit",
 ]

@@ -1,10 +1,12 @@
 """GPU parity of the chunked MFMA kernels (bf16 vectors, N = 64) against the
 float64 CPU oracle.
 
-The chunked path serves bf16 inputs with head size 64 and a checkpoint
-interval (= chunk length) of 16, 32 or 64.  Tolerance:
-max|diff| <= 2e-2 * max|oracle| per tensor.  Cases cover partial final
-chunks, every chunk length, nonzero initial state and state cotangent, and
+The MFMA path serves bf16 inputs with head size 64 and the checkpoint
+intervals in MFMA_INTERVALS; any other interval runs the sequential kernels.
+Every case asserts which kernels served it (rwkv7m_wkv7_last_path), so a
+case is labelled by the path it provably took.  Tolerance (BASELINE north
+star): max|diff| <= 2e-2 * max|oracle| per tensor.  Cases cover partial
+final chunks, every interval, nonzero initial state and state cotangent, and
 decays strong enough to force the in-kernel exact sequential fallback.
 """
 
@@ -21,6 +23,15 @@ NAMES = ("r", "w", "k", "v", "neg_kk", "kka")
 GRAD_NAMES = ("dr", "dw", "dk", "dv", "dneg_kk", "dkka", "ds0")
 TOL = 2e-2
 THREADS = 8
+# checkpoint intervals (= backward chunk lengths) the MFMA kernels serve
+MFMA_INTERVALS = (16, 32)
+
+
+def expected_paths(ci):
+    """(forward, backward) kernel paths of a bf16 N = 64 training call."""
+    if ci in MFMA_INTERVALS:
+        return ("wave_forward", "chunk_backward")
+    return ("seq_forward", "seq_backward")
 
 
 @pytest.fixture(scope="module")
@@ -44,20 +55,29 @@ def _run_case(hip, inp, ci, case, check_grads=True):
     vecs = [dev[n] for n in NAMES]
     (y, s_t), aux = hip.forward_with_aux(*vecs, dev["s0"],
                                          checkpoint_interval=ci)
-    grads = hip.backward(*vecs, dev["s0"], dev["dy"], dev["ds_t"], *aux) \
-        if check_grads else None
+    paths = [hip.last_path()]
+    grads = None
+    if check_grads:
+        grads = hip.backward(*vecs, dev["s0"], dev["dy"], dev["ds_t"], *aux)
+        paths.append(hip.last_path())
     torch.cuda.synchronize()
+    hip.device_status()
+    assert tuple(paths) == expected_paths(ci)[:len(paths)], (case, paths)
     host = [_np(inp[n]) for n in NAMES]
     ey, es, eck = oracle.forward(*host, _np(inp["s0"]),
                                  checkpoint_interval=ci, threads=THREADS)
     assert y.dtype == torch.bfloat16 and s_t.dtype == torch.float32
     _check("y", y, ey, case)
     _check("s_t", s_t, es, case)
-    # bf16 checkpoints: S0 and S_T rounded to nearest even
-    assert aux[0].dtype == torch.bfloat16
+    # checkpoints in the library's dtype for this interval (bf16 on every
+    # MFMA interval): S0 and S_T rounded to nearest even
+    cdt = hip.checkpoint_dtype(torch.bfloat16, 64, ci)
+    assert aux[0].dtype == cdt
+    if ci in MFMA_INTERVALS:
+        assert cdt == torch.bfloat16
     _check("checkpoints", aux[0], eck, case)
-    assert torch.equal(aux[0][0], dev["s0"].to(torch.bfloat16))
-    assert torch.equal(aux[0][-1], s_t.to(torch.bfloat16))
+    assert torch.equal(aux[0][0], dev["s0"].to(cdt))
+    assert torch.equal(aux[0][-1], s_t.to(cdt))
     if check_grads:
         egr = oracle.backward(*host, _np(inp["s0"]), _np(inp["dy"]),
                               _np(inp["ds_t"]), threads=THREADS)
@@ -88,16 +108,17 @@ def test_chunked_strong_decay_uses_exact_fallback(hip, ci):
     _run_case(hip, inp, ci, case)
 
 
-def test_chunked_mixed_fast_and_fallback_chunks(hip):
+@pytest.mark.parametrize("ci", [16, 32])
+def test_chunked_mixed_fast_and_fallback_chunks(hip, ci):
     # decay strong only in tokens 64..127 of head 1: chunks there take the
     # exact fallback, the rest the MFMA path, and the state crosses both
-    case = "mixed decay T192 L64"
+    case = f"mixed decay T192 L{ci}"
     print("case:", case, flush=True)
     inp = make_inputs(192, 2, 2, 64, seed=44, state_std=0.1, dstate_std=0.1)
     w = inp["w"].float()
     w[64:128, :, 1] += 3.0
     inp["w"] = w.to(torch.bfloat16)
-    _run_case(hip, inp, 64, case)
+    _run_case(hip, inp, ci, case)
 
 
 def test_chunked_unit_decay_and_tiny_inputs(hip):
@@ -127,20 +148,31 @@ def test_chunked_plain_forward_and_in_place_state(hip):
     assert torch.equal(y, y2) and torch.equal(state, s_t)
 
 
-def test_config1_forward_backward(hip):
-    case = "config 1: B8 T512 H12 N64 bf16"
+def test_config1_forward_backward_default_path(hip):
+    # config 1 in full on the library's default (MFMA) path
+    case = "config 1: B8 T512 H12 N64 bf16 L32"
     print("case:", case, flush=True)
     inp = config_inputs(1)
-    _run_case(hip, inp, 64, case)
+    _run_case(hip, inp, 32, case)
 
 
-def test_config4_shape_slow_decay_carry_state(hip):
+def test_config1_forward_backward_sequential_kernels(hip):
+    # an interval outside MFMA_INTERVALS runs the sequential kernels
+    case = "config 1: B8 T512 H12 N64 bf16 L128 (sequential kernels)"
+    print("case:", case, flush=True)
+    inp = config_inputs(1)
+    _run_case(hip, inp, 128, case)
+
+
+@pytest.mark.parametrize("ci", [16, 32])
+def test_config4_distributions_slow_decay_carry_state(hip, ci):
     # config 4's distributions (slow decay, S0 and dS_T ~ N(0, 0.1)) on a
-    # reduced (B, H) so the float64 oracle finishes in seconds
-    case = "config 4 distributions B1 T2048 H2 N64"
+    # reduced (B, H) at T = 2048; the full size is in
+    # test_fullsize_parity.py
+    case = f"config 4 distributions B1 T2048 H2 N64 L{ci}"
     print("case:", case, flush=True)
     inp = config_inputs(4, T=2048, B=1, H=2)
-    _run_case(hip, inp, 64, case)
+    _run_case(hip, inp, ci, case)
 
 
 @pytest.mark.parametrize("ci", [16, 32, 64])
@@ -157,7 +189,9 @@ def test_chunked_results_are_deterministic(hip, ci):
     for _ in range(6):
         (y, s_t), aux = hip.forward_with_aux(*vecs, dev["s0"],
                                              checkpoint_interval=ci)
+        fwd_path = hip.last_path()
         grads = hip.backward(*vecs, dev["s0"], dev["dy"], dev["ds_t"], *aux)
+        assert (fwd_path, hip.last_path()) == expected_paths(ci)
         outs = [y, s_t, aux[0], *grads]
         torch.cuda.synchronize()
         if first is None:

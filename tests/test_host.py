@@ -7,6 +7,7 @@ of tests/test_wkv_pallas.py:113-198 with torch in place of JAX.  Nothing here
 launches GPU work.
 """
 
+import ctypes
 import glob
 import os
 import re
@@ -303,6 +304,19 @@ def test_library_rejects_bad_requests_before_any_device_call(lib):
     assert lib.rwkv7m_wkv7_backward_bthn(
         0, 2, 1, 1, 4, *null, -1, *([None] * 8)) == 1
     assert b"rwkv7m_wkv7_backward_bthn" in lib.rwkv7m_last_error()
+
+
+def test_last_path_is_empty_after_a_rejected_call(lib):
+    # the path query names only kernels a successful call launched
+    null = [None] * 10
+    assert lib.rwkv7m_wkv7_forward(0, 2, 1, 1, 4, *null) == 1
+    assert lib.rwkv7m_wkv7_last_path() == b""
+    assert lib.rwkv7m_wkv7_backward(
+        0, 2, 1, 1, 4, *null, 0, *([None] * 8)) == 1
+    assert lib.rwkv7m_wkv7_last_path() == b""
+    # the wait-budget hook takes any value without touching a device
+    lib.rwkv7m_debug_set_wait_limit(1)
+    lib.rwkv7m_debug_set_wait_limit(0)
 
 
 def test_timemix_abi_checks_requests_before_any_device_call(lib):

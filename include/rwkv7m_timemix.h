@@ -97,6 +97,29 @@ int rwkv7m_timemix_wkv_output_backward(
     float *dr_k, float *dln_scale, float *dln_bias, float *workspace,
     int64_t workspace_floats, void *stream);
 
+/*
+ * Backward of the consumer that allocates nothing: rwkv7m_timemix_wkv_
+ * output_backward without the workspace arguments.  No counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The parameter gradients' partial rows go to a scratch array built into
+ * the library, 24 MiB per device, held by each device the library runs on
+ * until the process ends.  Limit: rwkv7m_timemix_workspace_floats(rows, H,
+ * N) <= 3 * 1024 * 2048 floats, which holds for every H * N up to 2^21
+ * channels; larger requests fail with RWKV7M_ERR_INVALID_ARGUMENT.  Every
+ * call on a device shares that device's scratch: calls that overlap on one
+ * device (concurrent streams, other threads) race and must be serialised by
+ * the caller.  Each call writes every scratch entry it reads, so nothing
+ * carries over from an earlier call.  Results are bit-identical to
+ * rwkv7m_timemix_wkv_output_backward.
+ */
+int rwkv7m_timemix_wkv_output_backward_noalloc(
+    int dtype, int64_t rows, int64_t H, int64_t N, const void *y,
+    const void *r, const void *k, const void *v, const void *g,
+    const float *r_k, const float *ln_scale, const float *ln_bias, double eps,
+    const void *dout, void *dy, void *dr, void *dk, void *dv, void *dg,
+    float *dr_k, float *dln_scale, float *dln_bias, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,6 +12,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <initializer_list>
+#include <mutex>
 #include <string>
 
 #include "../../include/rwkv7m_screening.h"
@@ -558,6 +559,97 @@ rwkv7m::ScreenWriteArgs sc_write_args(int64_t B, int64_t T, int64_t M,
 
 }  // namespace
 
+namespace {
+
+// Built-in scratch of the no-allocation consumer backward: the parameter
+// gradients' partial rows (3 parameters x row groups x C floats).  The
+// geometry keeps row groups x column tiles <= 1024 and a column tile is 2048
+// channels, so 3 * 1024 * 2048 floats (24 MiB) serve every C up to
+// 2048 * 1024 channels.  Each device holds its own copy for the life of the
+// process.  Host code never uses this name as an address: the device
+// address comes from hipGetSymbolAddress, looked up once per device with
+// that device current.
+constexpr int64_t kScratchFloats = int64_t(3) * 1024 * 2048;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kScratchDevices];
+
+// The current device's address of `scratch` (looked up on first use).
+int scratch_address(const char* fn, float** out) {
+    int dev = 0;
+    RWKV7M_TRY(hip_status(fn, hipGetDevice(&dev)));
+    if (dev < 0 || dev >= kScratchDevices)
+        return fail(RWKV7M_ERR_UNSUPPORTED,
+                    std::string(fn) + ": device index " + std::to_string(dev) +
+                        " is beyond the " + std::to_string(kScratchDevices) +
+                        " devices the built-in scratch tracks");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return fail(RWKV7M_ERR_HIP,
+                        std::string(fn) +
+                            ": address of the built-in scratch: " +
+                            hipGetErrorString(e));
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return RWKV7M_OK;
+}
+
+// The consumer backward's checks and launch; `workspace` is the caller's
+// (checked against workspace_floats) or, with `builtin`, the device's
+// built-in scratch.
+int output_backward_impl(
+    const char* fn, int dtype, int64_t rows, int64_t H, int64_t N,
+    const void* y, const void* r, const void* k, const void* v, const void* g,
+    const float* r_k, const float* ln_scale, const float* ln_bias, double eps,
+    const void* dout, void* dy, void* dr, void* dk, void* dv, void* dg,
+    float* dr_k, float* dln_scale, float* dln_bias, float* workspace,
+    int64_t workspace_floats, bool builtin, hipStream_t stream) {
+    TmDims d;
+    RWKV7M_TRY(tm_check(fn, dtype, rows, H, N, &d));
+    RWKV7M_TRY(tm_eps(fn, eps));
+    if (d.C == 0) return RWKV7M_OK;
+    RWKV7M_TRY(tm_need(fn, {{"r_k", r_k}, {"ln_scale", ln_scale},
+                            {"ln_bias", ln_bias}, {"dr_k", dr_k},
+                            {"dln_scale", dln_scale},
+                            {"dln_bias", dln_bias}}));
+    if (builtin) {
+        const int64_t need_floats =
+            rwkv7m::timemix_workspace_floats(d.rows, d.C);
+        if (need_floats > kScratchFloats)
+            return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                        std::string(fn) + ": H*N = " + std::to_string(d.C) +
+                            " channels need " + std::to_string(need_floats) +
+                            " floats of scratch; the built-in scratch holds " +
+                            std::to_string(kScratchFloats) +
+                            " (use rwkv7m_timemix_wkv_output_backward with a "
+                            "workspace)");
+    } else {
+        RWKV7M_TRY(tm_workspace(fn, d, workspace, workspace_floats));
+    }
+    if (d.rows > 0)
+        RWKV7M_TRY(tm_need(fn, {{"y", y}, {"r", r}, {"k", k}, {"v", v},
+                                {"g", g}, {"dout", dout}, {"dy", dy},
+                                {"dr", dr}, {"dk", dk}, {"dv", dv},
+                                {"dg", dg}}));
+    if (builtin) RWKV7M_TRY(scratch_address(fn, &workspace));
+    rwkv7m::TmOutputBwdArgs A{d.rows, d.C,     float(eps), y,   r,
+                              k,      v,       g,          dout, r_k,
+                              ln_scale, ln_bias, dy,       dr,   dk,
+                              dv,     dg,      dr_k,       dln_scale,
+                              dln_bias, workspace};
+    return hip_status("time-mix consumer backward launch",
+                      rwkv7m::launch_timemix_output_backward(
+                          dtype == RWKV7M_DTYPE_BF16, int(d.N), A, stream));
+}
+
+}  // namespace
+
 extern "C" {
 
 int rwkv7m_abi_version(void) { return 1; }
@@ -786,31 +878,26 @@ int rwkv7m_timemix_wkv_output_backward(
     const void* dout, void* dy, void* dr, void* dk, void* dv, void* dg,
     float* dr_k, float* dln_scale, float* dln_bias, float* workspace,
     int64_t workspace_floats, void* stream) {
-    const char* fn = "rwkv7m_timemix_wkv_output_backward";
     g_last_error.clear();
-    TmDims d;
-    RWKV7M_TRY(tm_check(fn, dtype, rows, H, N, &d));
-    RWKV7M_TRY(tm_eps(fn, eps));
-    if (d.C == 0) return RWKV7M_OK;
-    RWKV7M_TRY(tm_need(fn, {{"r_k", r_k}, {"ln_scale", ln_scale},
-                            {"ln_bias", ln_bias}, {"dr_k", dr_k},
-                            {"dln_scale", dln_scale},
-                            {"dln_bias", dln_bias}}));
-    RWKV7M_TRY(tm_workspace(fn, d, workspace, workspace_floats));
-    if (d.rows > 0)
-        RWKV7M_TRY(tm_need(fn, {{"y", y}, {"r", r}, {"k", k}, {"v", v},
-                                {"g", g}, {"dout", dout}, {"dy", dy},
-                                {"dr", dr}, {"dk", dk}, {"dv", dv},
-                                {"dg", dg}}));
-    rwkv7m::TmOutputBwdArgs A{d.rows, d.C,     float(eps), y,   r,
-                              k,      v,       g,          dout, r_k,
-                              ln_scale, ln_bias, dy,       dr,   dk,
-                              dv,     dg,      dr_k,       dln_scale,
-                              dln_bias, workspace};
-    return hip_status("time-mix consumer backward launch",
-                      rwkv7m::launch_timemix_output_backward(
-                          dtype == RWKV7M_DTYPE_BF16, int(d.N), A,
-                          static_cast<hipStream_t>(stream)));
+    return output_backward_impl(
+        "rwkv7m_timemix_wkv_output_backward", dtype, rows, H, N, y, r, k, v,
+        g, r_k, ln_scale, ln_bias, eps, dout, dy, dr, dk, dv, dg, dr_k,
+        dln_scale, dln_bias, workspace, workspace_floats, false,
+        static_cast<hipStream_t>(stream));
+}
+
+int rwkv7m_timemix_wkv_output_backward_noalloc(
+    int dtype, int64_t rows, int64_t H, int64_t N, const void* y,
+    const void* r, const void* k, const void* v, const void* g,
+    const float* r_k, const float* ln_scale, const float* ln_bias, double eps,
+    const void* dout, void* dy, void* dr, void* dk, void* dv, void* dg,
+    float* dr_k, float* dln_scale, float* dln_bias, void* stream) {
+    g_last_error.clear();
+    return output_backward_impl(
+        "rwkv7m_timemix_wkv_output_backward_noalloc", dtype, rows, H, N, y, r,
+        k, v, g, r_k, ln_scale, ln_bias, eps, dout, dy, dr, dk, dv, dg, dr_k,
+        dln_scale, dln_bias, nullptr, 0, true,
+        static_cast<hipStream_t>(stream));
 }
 
 int64_t rwkv7m_screen_slot_scan_workspace_floats(int64_t B, int64_t T,

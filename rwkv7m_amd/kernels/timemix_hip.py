@@ -164,3 +164,32 @@ def output_backward(y, r, k, v, g, r_k, ln_scale, ln_bias, dout,
           float(eps), P(dout), *map(P, grads), *map(P, pgrads), P(ws), nws,
           wkv_hip._stream(dev))
     return (*grads, *pgrads)
+
+
+def output_backward_noalloc(y, r, k, v, g, r_k, ln_scale, ln_bias, dout,
+                            head_size: int, eps: float = GROUPNORM_EPS,
+                            out=None):
+    """``output_backward`` through the entry point that allocates nothing
+    on the device: the partial rows go to the library's built-in scratch.
+    ``out`` (optional) holds the eight result tensors to write, so that the
+    call itself allocates nothing either; calls overlapping on one device
+    race on the scratch."""
+    C = r_k.numel()
+    H = _heads(C, head_size)
+    rows = _rows(g, C, (y, r, k, v, dout), ("y", "r", "k", "v", "dout"))
+    dev = wkv_hip._dev([y, r, k, v, g, r_k, ln_scale, ln_bias, dout])
+    y, r, k, v, g, dout = _acts(y, r, k, v, g, dout)
+    prk = _param(r_k, C, "r_k")
+    psc = _param(ln_scale, C, "ln_scale")
+    pbi = _param(ln_bias, C, "ln_bias")
+    if out is None:
+        out = [torch.empty_like(y) for _ in range(4)] + [
+            torch.empty_like(g)] + [
+            torch.empty(C, dtype=torch.float32, device=dev)
+            for _ in range(3)]
+    P = wkv_hip._p
+    _call("rwkv7m_timemix_wkv_output_backward_noalloc",
+          wkv_hip._dtype_code(g), rows, H, head_size, P(y), P(r), P(k), P(v),
+          P(g), P(prk), P(psc), P(pbi), float(eps), P(dout), *map(P, out),
+          wkv_hip._stream(dev))
+    return tuple(out)

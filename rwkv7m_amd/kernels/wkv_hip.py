@@ -68,6 +68,7 @@ EXPORTED_SYMBOLS = (
     "rwkv7m_timemix_wkv_inputs_backward",
     "rwkv7m_timemix_wkv_output",
     "rwkv7m_timemix_wkv_output_backward",
+    "rwkv7m_timemix_wkv_output_backward_noalloc",
     "rwkv7m_screen_slot_scan_workspace_floats",
     "rwkv7m_screen_slot_scan",
     "rwkv7m_screen_slot_scan_backward",
@@ -142,6 +143,9 @@ def load_library(path: str | None = None):
         lib.rwkv7m_timemix_wkv_output_backward.restype = i32
         lib.rwkv7m_timemix_wkv_output_backward.argtypes = (
             dims + [vp] * 8 + [f64] + [vp] * 10 + [i64, vp])
+        lib.rwkv7m_timemix_wkv_output_backward_noalloc.restype = i32
+        lib.rwkv7m_timemix_wkv_output_backward_noalloc.argtypes = (
+            dims + [vp] * 8 + [f64] + [vp] * 9 + [vp])
         sdims = [i32, i64, i64, i64, i64]
         lib.rwkv7m_screen_slot_scan_workspace_floats.restype = i64
         lib.rwkv7m_screen_slot_scan_workspace_floats.argtypes = [i64] * 4

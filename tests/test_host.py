@@ -306,6 +306,17 @@ def test_library_rejects_bad_requests_before_any_device_call(lib):
     assert b"rwkv7m_wkv7_backward_bthn" in lib.rwkv7m_last_error()
 
 
+def test_noalloc_consumer_backward_rejects_sizes_beyond_its_scratch(lib):
+    # 2^22 channels need more partial rows than the built-in scratch holds:
+    # rejected by the size check, before any pointer is used or any device
+    # is touched (the fake addresses below are never dereferenced)
+    fake = [ctypes.c_void_p(0x1000 * (i + 1)) for i in range(17)]
+    rc = lib.rwkv7m_timemix_wkv_output_backward_noalloc(
+        1, 4, 1 << 15, 128, *fake[:8], 64e-5, *fake[8:], None)
+    assert rc == 1
+    assert b"built-in scratch" in lib.rwkv7m_last_error()
+
+
 def test_last_path_is_empty_after_a_rejected_call(lib):
     # the path query names only kernels a successful call launched
     null = [None] * 10

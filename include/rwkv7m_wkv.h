@@ -93,7 +93,8 @@ void rwkv7m_debug_set_wait_limit(int64_t polls);
 /*
  * Name of the kernel path the last successful WKV-7 call on this thread
  * launched: "wave_forward" (MFMA chunked forward), "decode" (single-token
- * kernel), "seq_forward", "chunk_backward" (MFMA chunked backward),
+ * kernel), "seq_forward", "wave_backward" (MFMA chunked backward, with the
+ * exact sequential pass for any head outside the factored form's range),
  * "seq_backward", or "" (nothing launched).  A diagnostic for tests that
  * must prove which kernel served a request; no counterpart in the
  * reference.
@@ -128,7 +129,7 @@ int rwkv7m_wkv7_forward(int dtype, int64_t T, int64_t B, int64_t H, int64_t N,
  * needs.  Replaces WKVFFIBackend.forward_with_aux (wkv_ffi.py:33; called at
  * wkv.py:174) and the reference's fwd+aux kernel (wkv_pallas_gpu.py:66-120,
  * :303-375).  checkpoint_interval = 0 selects the library default; the
- * MFMA path serves bf16, N = 64 and an interval of 16 or 32; other
+ * MFMA path serves bf16, N = 64 and an interval of 16, 32 or 64; other
  * intervals run the sequential kernels.
  * checkpoints: [rwkv7m_wkv7_checkpoint_count(T, ci)][B][H][N][N] of
  * rwkv7m_wkv7_checkpoint_dtype(dtype, N, ci).

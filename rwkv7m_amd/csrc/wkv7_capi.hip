@@ -155,15 +155,17 @@ bool all_aligned16(std::initializer_list<const void*> ptrs) {
     return true;
 }
 
-// The chunked MFMA kernels serve bf16 vectors with N = 64, a chunk length
-// (= checkpoint interval) of 16 or 32, 16-byte aligned buffers, and chunks
-// whose element span L * (token stride) stays below 2^31 (32-bit lane
-// offsets).
-bool use_chunked(int dtype, int64_t N, int64_t ci, int64_t token_stride,
+// The MFMA kernels (16-token chunks) serve bf16 vectors with N = 64, a
+// checkpoint interval of 16, 32 or 64, 16-byte aligned buffers, chunks whose
+// element span 16 * (token stride) stays below 2^31 (32-bit lane offsets)
+// and fewer than 2^31 chunks.
+bool use_chunked(int dtype, int64_t N, int64_t ci, int64_t T,
+                 int64_t token_stride,
                  std::initializer_list<const void*> ptrs) {
     if (dtype != RWKV7M_DTYPE_BF16 || N != 64) return false;
-    if (ci != 16 && ci != 32) return false;
-    if (token_stride * ci >= (int64_t(1) << 31)) return false;
+    if (ci != 16 && ci != 32 && ci != 64) return false;
+    if (token_stride * 64 >= (int64_t(1) << 31)) return false;
+    if (T / 16 >= (int64_t(1) << 31) - 1) return false;
     return all_aligned16(ptrs);
 }
 
@@ -189,8 +191,8 @@ int forward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     if (T == 0 && !ckpt) return copy_or_clear(s_t, s0, d.state_elems, stream);
     const int64_t L = ckpt ? ci : kDefaultChunk;
     const rwkv7m::VecLayout lay = vec_layout(batch_major, T, B, H, N);
-    if (T > 1 &&
-        use_chunked(dtype, N, L, lay.ts, {r, w, k, v, a, b, y, s0, s_t, ckpt})) {
+    if (T > 1 && use_chunked(dtype, N, L, T, lay.ts,
+                             {r, w, k, v, a, b, y, s0, s_t, ckpt})) {
         rwkv7m::ChunkFwdArgs c{};
         c.L = int(L);
         c.T = T;
@@ -279,35 +281,6 @@ int backward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     if (d.state_elems == 0) return RWKV7M_OK;
     if (T == 0) return copy_or_clear(ds0, ds_t, d.state_elems, s);
     const rwkv7m::VecLayout lay = vec_layout(batch_major, T, B, H, N);
-    if (use_chunked(dtype, N, ci, lay.ts,
-                    {r, w, k, v, neg_kk, kka, dy, ds_t, checkpoints, dr, dw,
-                     dk, dv, dneg_kk, dkka, ds0})) {
-        rwkv7m::ChunkBwdArgs c{};
-        c.L = int(ci);
-        c.T = T;
-        c.B = B;
-        c.H = H;
-        c.lay = lay;
-        c.r = r;
-        c.w = w;
-        c.k = k;
-        c.v = v;
-        c.a = neg_kk;
-        c.b = kka;
-        c.dy = dy;
-        c.ds_t = ds_t;
-        c.ckpt = checkpoints;
-        c.dr = dr;
-        c.dw = dw;
-        c.dk = dk;
-        c.dv = dv;
-        c.da = dneg_kk;
-        c.db = dkka;
-        c.ds0 = ds0;
-        g_last_path = "chunk_backward";
-        return hip_status("chunked backward launch",
-                          rwkv7m::launch_chunk_backward(c, s));
-    }
     rwkv7m::SeqBwdArgs p{};
     p.bf16 = dtype == RWKV7M_DTYPE_BF16;
     p.T = T;
@@ -333,6 +306,43 @@ int backward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     p.da = dneg_kk;
     p.db = dkka;
     p.ds0 = ds0;
+    if (use_chunked(dtype, N, ci, T, lay.ts,
+                    {r, w, k, v, neg_kk, kka, dy, ds_t, checkpoints, dr, dw,
+                     dk, dv, dneg_kk, dkka, ds0})) {
+        rwkv7m::WaveBwdArgs c{};
+        c.L = int(ci);
+        c.T = T;
+        c.B = B;
+        c.H = H;
+        c.lay = lay;
+        c.r = r;
+        c.w = w;
+        c.k = k;
+        c.v = v;
+        c.a = neg_kk;
+        c.b = kka;
+        c.dy = dy;
+        c.ds_t = ds_t;
+        c.ckpt = checkpoints;
+        c.dr = dr;
+        c.dw = dw;
+        c.dk = dk;
+        c.dv = dv;
+        c.da = dneg_kk;
+        c.db = dkka;
+        c.ds0 = ds0;
+        RWKV7M_TRY(hip_status("device wait configuration",
+                              rwkv7m::wait_config(&c.wait)));
+        RWKV7M_TRY(hip_status("wave backward launch",
+                              rwkv7m::launch_wave_backward(c, s)));
+        // heads with a chunk outside the factored form's range were left to
+        // the exact sequential pass (marked in dS0); every other head
+        // returns at once
+        p.marked_only = true;
+        g_last_path = "wave_backward";
+        return hip_status("exact pass launch",
+                          rwkv7m::launch_seq_backward(p, s));
+    }
     g_last_path = "seq_backward";
     return hip_status("sequential backward launch",
                       rwkv7m::launch_seq_backward(p, s));

@@ -48,7 +48,14 @@ struct SeqBwdArgs {
     int64_t ci;
     void *dr, *dw, *dk, *dv, *da, *db;
     float* ds0;
+    // only the heads whose ds0[b][h][0][0] holds kExactPassMark (left by the
+    // wave backward to this exact pass); others are untouched
+    bool marked_only;
 };
+
+// Bit pattern (a NaN no arithmetic produces) that the wave backward leaves in
+// dS0[b][h][0][0] of a head it hands to the exact sequential pass.
+constexpr uint32_t kExactPassMark = 0x7fa5a5a5u;
 
 // MFMA forward: bf16 vectors, N = 64; L is the checkpoint interval.
 struct ChunkFwdArgs {
@@ -67,19 +74,23 @@ struct ChunkFwdArgs {
 // is the checkpoint interval (checkpoints every L / 16 chunks).
 hipError_t launch_wave_forward(const ChunkFwdArgs& p, hipStream_t stream);
 
-// Chunked backward: L in {16, 32}; ckpt holds a state every L tokens.
-struct ChunkBwdArgs {
+// Wave-specialised backward (wkv7_wave_bwd.hip): 16-token chunks, bf16
+// checkpoints every L in {16, 32, 64} tokens.  A head with a chunk outside
+// the factored form's range is left with kExactPassMark in dS0[b][h][0][0]
+// for the exact pass (launch_seq_backward with marked_only).
+struct WaveBwdArgs {
     int L;
     int64_t T, B, H;
     VecLayout lay;
     const void *r, *w, *k, *v, *a, *b, *dy;
     const float* ds_t;
-    const void* ckpt;  // bf16, one state every L tokens
+    const void* ckpt;
     void *dr, *dw, *dk, *dv, *da, *db;
     float* ds0;
+    WaitCfg wait;
 };
 
-hipError_t launch_chunk_backward(const ChunkBwdArgs& p, hipStream_t stream);
+hipError_t launch_wave_backward(const WaveBwdArgs& p, hipStream_t stream);
 
 hipError_t launch_seq_forward(const SeqFwdArgs& p, hipStream_t stream);
 

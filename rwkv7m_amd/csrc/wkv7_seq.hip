@@ -142,7 +142,8 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
                     const VT* __restrict__ b, const VT* __restrict__ dy,
                     const float* __restrict__ ds_t,
                     const CT* __restrict__ ckpt, int64_t ci, VT* dr,
-                    VT* dw, VT* dk, VT* dv, VT* da, VT* db, float* ds0) {
+                    VT* dw, VT* dk, VT* dv, VT* da, VT* db, float* ds0,
+                    int marked_only) {
     using Sh = SeqShape<N>;
     constexpr int G = Sh::G, C = Sh::C, SUB = Sh::SUB, TH = Sh::THREADS;
     constexpr int WL = Sh::WAVE_LANES, NW = Sh::NWAVES;
@@ -152,6 +153,11 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
     __shared__ float sh_dv[SUB][N];
 
     const int64_t bh = blockIdx.x;
+    // marked_only: serve only the heads another kernel left to this exact
+    // pass (their dS0 holds kExactPassMark); every other head is complete
+    if (marked_only &&
+        __float_as_uint(ds0[bh * NN]) != kExactPassMark)
+        return;
     const int tid = threadIdx.x;
     const int row = tid / G, col0 = (tid % G) * C;
     const int wave = tid / 64, lane = tid % 64;
@@ -314,7 +320,7 @@ hipError_t launch_bwd_nc(const SeqBwdArgs& p, hipStream_t stream) {
                        static_cast<VT*>(p.dr), static_cast<VT*>(p.dw),
                        static_cast<VT*>(p.dk), static_cast<VT*>(p.dv),
                        static_cast<VT*>(p.da), static_cast<VT*>(p.db),
-                       p.ds0);
+                       p.ds0, p.marked_only ? 1 : 0);
     return hipGetLastError();
 }
 

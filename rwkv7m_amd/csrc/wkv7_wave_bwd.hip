@@ -1,0 +1,924 @@
+// Wave-specialised WKV-7 backward for gfx950: bf16 vectors, fp32 state,
+// N = 64, 16-token chunks, bf16 checkpoints every L = 16 m tokens
+// (m = 1, 2 or 4).
+//
+// Per 16-token chunk with start state S_0 and end-state cotangent D (the
+// chunk's closed form; g = running log2-decay, g_ref its value at token 7,
+// A~ = a 2^{g_{t-1}-g_ref}, R~ = r 2^{g_t-g_ref},
+// B~ = b 2^{g_ref-g_t}, K~ = k 2^{g_ref-g_t}, A^ = A~ 2^{g_ref},
+// B^ = B~ 2^{g_L-g_ref}, K^ = K~ 2^{g_L-g_ref}; Aab = A~ B~^T and
+// Aak = A~ K~^T strictly lower, Arb = R~ B~^T and Ark = R~ K~^T lower with
+// the diagonal; Minv = (I - Aab)^{-1}):
+//
+//   U  = A^ S_0^T + Aak V        X = Minv U   (X_t = S_{t-1} a_t)
+//   dX = B^ D^T + Arb^T dY       dU = Minv^T dX
+//   dV = K^ D^T + Ark^T dY + Aak^T dU
+//   dArb = lower(dY X^T), dArk = lower(dY V^T), dAab = slower(dU X^T),
+//   dAak = slower(dU V^T)
+//   dR~ = (dY S_0) 2^{g_ref} + dArb B~ + dArk K~
+//   dA~ = (dU S_0) 2^{g_ref} + dAab B~ + dAak K~
+//   dB~ = dAab^T A~ + dArb^T R~ + (X D) 2^{g_L-g_ref}
+//   dK~ = dAak^T A~ + dArk^T R~ + (V D) 2^{g_L-g_ref}
+//   D_0 = D 2^{g_L} + bf16(D) B^^T W^ + dY^T Q^      (the cotangent of S_0)
+//
+// with W^ = Minv A^ and Q^ = R~ 2^{g_ref} + Arb W^.  The decay gradient
+// uses the chunk-start identity (S_0 and D_0 fixed; exact for the chunk)
+//
+//   dlog d_t = sum_{t' < t} (b db + k dk - r dr)_{t'} - sum_{t' <= t} (a da)_{t'}
+//              + sum_i D_0[i, :] S_0[i, :]
+//
+// and dw = dlog d * (-e^w).  These are the reference's reverse equations
+// (src/rwkv7m/kernels/wkv_pallas_gpu.py:221-257) summed over a chunk; states
+// come from checkpoints, never from dividing by the decay.  Inside an
+// interval of m chunks, the start state of chunk c + 1 is recomputed from
+// chunk c's: S_L = S_0 2^{g_L} + X^T B^ + V^T K^.
+//
+// One workgroup of 8 waves per (batch, head):
+//   * waves 0..3, the chains: chain ib holds rows 16 ib .. 16 ib + 15 of the
+//     fp32 cotangent D in registers and walks the chunks in reverse.  Per
+//     chunk it writes bf16(D) into the chunk's worker's D buffer, takes the
+//     worker's map (B^, W^, Q^, dY), advances D_0 (2 + 8 MFMAs: D_0 depends
+//     only on rows of D, so the four chains are independent) and adds its
+//     rows' share of sum_i D_0 S_0 for the worker;
+//   * waves 4..7, the workers: worker w takes chunks nch - 1 - w,
+//     nch - 1 - w - 4, ...  It loads the chunk's vectors, forms the factors,
+//     the 16 x 16 matrices and the inverse in registers, publishes the map,
+//     recomputes the next chunk's start state if the interval continues,
+//     then, once D has arrived, forms every gradient in registers and writes
+//     them.  Four chunks are in flight at once; only D is serial.
+// Register layouts are those of wkv7_wave_common.h.  The S and D buffers are
+// bf16 64 x 64 in 16-byte units (sd_off), read as row fragments (plain
+// reads) or column fragments (gfx950 transposing reads).
+//
+// A chunk outside the factored form's range (log-decay span beyond +-40
+// around the reference point) stops the workgroup: it leaves
+// kExactPassMark in dS0[b][h][0][0] and the exact sequential backward
+// recomputes that head.  Every wait is bounded (wkv7_status.hip); a wait
+// that gives up sets every output of the head to NaN and raises the
+// device's failure counter.
+
+#include "wkv7_wave_common.h"
+
+namespace rwkv7m {
+namespace {
+
+using namespace wave;
+
+constexpr int NCHAIN = 4;
+constexpr int NWORK = 4;
+constexpr int BTHREADS = 64 * (NCHAIN + NWORK);
+constexpr int NN = WN * WN;
+
+// Element (i, j) of a 64 x 64 bf16 S/D buffer: 16-byte unit (i, j / 8) at
+// ((i / 8) * 8 + j / 8) * 8 + i % 8, so one global_load_lds of 64 lanes
+// (16 bytes each, at consecutive units) fills rows 8g .. 8g + 7.
+__device__ __forceinline__ int sd_off(int i, int j) {
+    return ((((i >> 3) << 3) + (j >> 3)) * 8 + (i & 7)) * 8 + (j & 7);
+}
+
+__device__ __forceinline__ uint2 sd_read4(const bf16_t* buf, int i, int j) {
+    return *reinterpret_cast<const uint2*>(buf + sd_off(i, j));
+}
+
+__device__ __forceinline__ void sd_write4(bf16_t* buf, int i, int j, uint2 v) {
+    *reinterpret_cast<uint2*>(buf + sd_off(i, j)) = v;
+}
+
+// x32 fragment of rows 16 rb .. 16 rb + 15 over the 32 columns of pair p:
+// lane (q, r) takes row 16 rb + r, columns 32p + 4q .. + 3 (slots 0..3) and
+// 32p + 16 + 4q .. + 3 (slots 4..7).  As an A operand: the rows (m = i,
+// k = j); as a B operand: their transpose (k = j, n = i).
+__device__ __forceinline__ bf16x8_t frag_rows(const bf16_t* buf, int rb,
+                                              int p, int lane) {
+    const int r = lane & 15, q = lane >> 4;
+    const int i = 16 * rb + r, j = 32 * p + 4 * q;
+    return pk8(as_i16x4(sd_read4(buf, i, j)),
+               as_i16x4(sd_read4(buf, i, j + 16)));
+}
+
+// x32 fragment of columns 16 cb .. 16 cb + 15 over the 32 rows of pair p,
+// by two transposing reads: lane (q, r) takes column 16 cb + r at rows
+// 32p + 4q + e (slots 0..3) and 32p + 16 + 4q + e (slots 4..7).  Lane
+// s = a + 4e of each 16-lane group addresses row 32p + 4q + e, columns
+// 16 cb + 4a .. + 3.  As an A operand: the transpose (m = j, k = i); as a B
+// operand: the matrix (k = i, n = j).
+__device__ __forceinline__ bf16x8_t frag_cols(const bf16_t* buf, int cb,
+                                              int p, int lane) {
+    const int s = lane & 15, q = lane >> 4;
+    const int i = 32 * p + 4 * q + (s >> 2), j = 16 * cb + 4 * (s & 3);
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_i16x4_t*)(buf + sd_off(i, j)));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_i16x4_t*)(buf + sd_off(i + 16, j)));
+    return pk8(lo, hi);
+}
+
+// A chunk's hand-over from its worker to the chains, as register images
+// (element [..][lane] is that lane's operand).
+struct BMap {
+    bf16x8_t Bh[2][64];  // B^ (T layout pairs): x32 A operands (m = t, k = j)
+    i16x4_t W[4][64];    // D(W^_jb)
+    i16x4_t Q[4][64];    // D(Q^_jb)
+    i16x4_t dY[4][64];   // D(dY_ib)
+};
+
+struct BwdFlags {
+    int map_ready[NWORK];  // maps the worker has published (count)
+    int map_taken[NWORK];  // chain reads of its maps (NCHAIN per map)
+    int d_cnt[NWORK];      // chain writes into its D buffer (NCHAIN per chunk)
+    int d_done[NWORK];     // chunks whose D buffer the worker has finished
+    int tail_cnt[NWORK];   // chain tail partials (NCHAIN per chunk)
+    int s_ready[NWORK];    // chunk whose start state the S buffer holds
+    int s_free[NWORK];     // chunk whose start state the S buffer takes next
+    int abort;             // a chunk needs the exact pass: every wave stops
+    int failed;            // a bounded wait gave up
+};
+
+// LDS, as separate objects: the vector stage (the only LDS DMA target read
+// after a DMA is issued in the same chunk) is then provably distinct from
+// every other array, and the compiler inserts no vmcnt wait before their
+// reads while a prefetch is in flight.
+// lds_stage[w][v][h][s][u]: 16-byte segment s (columns 8s .. 8s + 7) of
+// token 8h + u of vector v (r, w, k, v, neg_kk, kka, dy)
+__shared__ uint4 lds_stage[NWORK][7][2][8][8];
+__shared__ bf16_t lds_S[NWORK][NN];  // the chunk's start state (sd_off)
+__shared__ bf16_t lds_D[NWORK][NN];  // the cotangent of its end state
+__shared__ BMap lds_map[NWORK];
+__shared__ float lds_tail[NWORK][NCHAIN][WN];  // sum_i D_0 S_0 per chain
+__shared__ float lds_eref[NWORK][WN];          // 2^{g_ref} per column
+__shared__ float lds_eLR[NWORK][WN];           // 2^{g_L - g_ref}
+__shared__ float lds_eL[NWORK][WN];            // 2^{g_L}
+__shared__ BwdFlags lds_flags;
+
+struct BwdArgs {
+    int64_t T, BH;
+    VecLayout lay;
+    const bf16_t *r, *w, *k, *v, *a, *b, *dy;
+    const float* ds_t;
+    const bf16_t* ckpt;
+    int m;  // checkpoint interval / 16
+    bf16_t *dr, *dw, *dk, *dv, *da, *db;
+    float* ds0;
+    WaitCfg wait;
+};
+
+// Wait until pred(*p) holds: 1 when it does, 0 when the workgroup aborted
+// first, -1 when the poll budget ran out (then the workgroup is marked
+// failed and aborted).
+template <typename Pred>
+__device__ __forceinline__ int wait_for(const WaitCfg& wc, int* p, int lane,
+                                        Pred pred) {
+    for (int it = 0; it < wc.limit; ++it) {
+        if (pred(__builtin_amdgcn_readfirstlane(lds_load(p)))) {
+            asm volatile("" ::: "memory");
+            return 1;
+        }
+        if (__builtin_amdgcn_readfirstlane(lds_load(&lds_flags.abort)) != 0)
+            return 0;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    wait_failed(&lds_flags.failed, wc.failures, lane);
+    if (lane == 0) lds_store(&lds_flags.abort, 1);
+    return -1;
+}
+
+// Keeps the scheduler from moving instructions across this point: placed
+// between the unrolled iterations of the worker's block loops, so that one
+// iteration's LDS reads are not all hoisted to the top (each would hold its
+// registers across the whole loop).
+__device__ __forceinline__ void fence_sched() {
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ __forceinline__ f32x4_t unpack_i16(const i16x4_t& x) {
+    return unpack4(__builtin_bit_cast(uint2, x));
+}
+
+// ---------------------------------------------------------------------------
+// Chain ib: rows 16 ib .. 16 ib + 15 of the cotangent through every chunk.
+__device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
+    const int lr = lane & 15, lq = lane >> 4;
+    const int64_t bh = blockIdx.x;
+    const int nch = int((A.T + WL - 1) / WL);
+    const int row = 16 * ib + lr;
+    BwdFlags& fl = lds_flags;
+    __builtin_amdgcn_s_setprio(2);  // the serial path
+    // tiles D(D^T_{j'b, ib}): lane holds D[row][16 j'b + 4 lq + e]
+    f32x4_t Dt[4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+        Dt[jb] = zero4();
+        if (A.ds_t)
+            Dt[jb] = *reinterpret_cast<const f32x4_t*>(
+                A.ds_t + bh * NN + row * WN + 16 * jb + 4 * lq);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+
+    bool done = true;
+    for (int p = 0; p < nch; ++p) {
+        const int c = nch - 1 - p;
+        const int w = p % NWORK, kord = p / NWORK;
+
+        // bf16(D): the step's operand and the worker's D buffer
+        i16x4_t sb[4];
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) sb[jb] = kq(Dt[jb]);
+        if (wait_for(A.wait, &fl.d_done[w], lane,
+                     [&](int x) { return x >= kord; }) <= 0) {
+            done = false;
+            break;
+        }
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+            sd_write4(lds_D[w], row, 16 * jb + 4 * lq,
+                      __builtin_bit_cast(uint2, sb[jb]));
+        lds_drain();
+        if (lane == 0) lds_add(&fl.d_cnt[w], 1);
+
+        // the chunk's map
+        if (wait_for(A.wait, &fl.map_ready[w], lane,
+                     [&](int x) { return x >= kord + 1; }) <= 0) {
+            done = false;
+            break;
+        }
+        const BMap& mp = lds_map[w];
+        const bf16x8_t Bh0 = mp.Bh[0][lane], Bh1 = mp.Bh[1][lane];
+        i16x4_t Wt[4], Qt[4];
+        f32x4_t eL[4];
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            Wt[jb] = mp.W[jb][lane];
+            Qt[jb] = mp.Q[jb][lane];
+            eL[jb] = *reinterpret_cast<const f32x4_t*>(
+                &lds_eL[w][16 * jb + 4 * lq]);
+        }
+        const i16x4_t dYt = mp.dY[ib][lane];
+        lds_drain();
+        if (lane == 0) lds_add(&fl.map_taken[w], 1);
+
+        // Z = B^ bf16(D)^T ([t][i]), then
+        // D_0^T = 2^{g_L} D^T + Q^^T dY + W^^T Z (rows of block ib)
+        f32x4_t z = zero4();
+        mfma(z, Bh0, pk8(sb[0], sb[1]));
+        mfma(z, Bh1, pk8(sb[2], sb[3]));
+        const i16x4_t kz = kq(z);
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            f32x4_t acc;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = Dt[jb][e] * eL[jb][e];
+            mfma16(acc, Qt[jb], dYt);
+            mfma16(acc, Wt[jb], kz);
+            Dt[jb] = acc;
+        }
+
+        // this block's share of sum_i D_0[i][j] S_0[i][j] for the worker
+        if (wait_for(A.wait, &fl.s_ready[w], lane,
+                     [&](int x) { return x == c; }) <= 0) {
+            done = false;
+            break;
+        }
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            const f32x4_t s0 =
+                unpack4(sd_read4(lds_S[w], row, 16 * jb + 4 * lq));
+            f32x4_t t4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                t4[e] = row_sum16(Dt[jb][e] * s0[e]);
+            if (lr == 0)
+                *reinterpret_cast<f32x4_t*>(
+                    &lds_tail[w][ib][16 * jb + 4 * lq]) = t4;
+        }
+        lds_drain();
+        if (lane == 0) lds_add(&fl.tail_cnt[w], 1);
+    }
+    if (done) {
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+            *reinterpret_cast<f32x4_t*>(A.ds0 + bh * NN + row * WN + 16 * jb +
+                                        4 * lq) = Dt[jb];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Worker w: chunks nch - 1 - w, nch - 1 - w - NWORK, ...
+// The vectors of chunk c straight to worker w's stage (global_load_lds
+// writes lane l's 16 bytes at 16 l): lane l of load (vector, h) fetches
+// segment l / 8 of token 8h + l % 8; tokens past the end re-read the last
+// token.
+__device__ __forceinline__ void fetch_vecs(const BwdArgs& A, int w, int c,
+                                           int lane) {
+    const VecPtrs src{A.r, A.w, A.k, A.v, A.a, A.b, A.dy};
+    const int64_t cbase = int64_t(c) * WL * A.lay.ts +
+                          A.lay.head(int64_t(blockIdx.x), WN);
+    const int64_t left = A.T - int64_t(c) * WL;
+    const int n = int(left < WL ? left : WL);
+    const uint32_t TS = uint32_t(A.lay.ts);
+    const int ldu = lane & 7, ldseg = lane >> 3;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int t = 8 * h + ldu;
+        const uint32_t off = uint32_t(t < n ? t : n - 1) * TS + 8 * ldseg;
+#pragma unroll
+        for (int vv = 0; vv < 7; ++vv)
+            __builtin_amdgcn_global_load_lds(
+                (const void __attribute__((address_space(1)))*)(
+                    (src.get(vv) + cbase) + off),
+                (void __attribute__((address_space(3)))*)(
+                    &lds_stage[w][vv][h][0][0]),
+                16, 0, 0);
+    }
+}
+
+// Checkpoint c / m (chunk c starts an interval) straight to worker w's S
+// buffer: load g fills rows 8g .. 8g + 7 (lane l: row 8g + l % 8, segment
+// l / 8).
+__device__ __forceinline__ void fetch_state(const BwdArgs& A, int w, int c,
+                                            int lane) {
+    const bf16_t* base =
+        A.ckpt + (int64_t(c / A.m) * A.BH + int64_t(blockIdx.x)) * NN;
+    const int ldu = lane & 7, ldseg = lane >> 3;
+#pragma unroll
+    for (int g = 0; g < 8; ++g)
+        __builtin_amdgcn_global_load_lds(
+            (const void __attribute__((address_space(1)))*)(
+                base + ((8 * g + ldu) * WN + 8 * ldseg)),
+            (void __attribute__((address_space(3)))*)(&lds_S[w][512 * g]),
+            16, 0, 0);
+}
+
+// The T layout read of vector vv from worker w's stage: token lr, columns
+// 16 kb + 4 lq .. + 3 (segment 2 kb + lq / 2, half lq % 2).
+__device__ __forceinline__ uint2 read_t(int w, int vv, int kb, int lane) {
+    const int lr = lane & 15, lq = lane >> 4;
+    const bf16_t* p = reinterpret_cast<const bf16_t*>(
+        &lds_stage[w][vv][lr >> 3][2 * kb + (lq >> 1)][lr & 7]);
+    return *reinterpret_cast<const uint2*>(p + 4 * (lq & 1));
+}
+
+// The J layout tile D(X_kb) of a T layout tile of X: X_kb I, with the
+// identity as the B operand (exact for bf16 values).
+__device__ __forceinline__ i16x4_t to_j(const i16x4_t& t, const i16x4_t& kI) {
+    f32x4_t x = zero4();
+    mfma16(x, t, kI);
+    return kq(x);
+}
+
+// ---------------------------------------------------------------------------
+// Worker w: chunks nch - 1 - w, nch - 1 - w - NWORK, ...
+__device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
+    const int64_t bh = blockIdx.x;
+    const int64_t hoff = A.lay.head(bh, WN);
+    const int64_t T = A.T;
+    const int nch = int((T + WL - 1) / WL);
+    const uint32_t TS = uint32_t(A.lay.ts);
+    const int m = A.m;
+    // the worker of chunk c + 1 (one position earlier in the reverse order),
+    // whose start state chunk c's end state is
+    const int wfeed = (w + NWORK - 1) % NWORK;
+    BwdFlags& fl = lds_flags;
+    bf16_t* const S = lds_S[w];
+    bf16_t* const D = lds_D[w];
+    BMap& map = lds_map[w];
+
+    if (nch - 1 - w >= 0) {
+        fetch_vecs(A, w, nch - 1 - w, lane0);
+        if ((nch - 1 - w) % m == 0) fetch_state(A, w, nch - 1 - w, lane0);
+    }
+
+    for (int kord = 0, p = w; p < nch; ++kord, p += NWORK) {
+        // lane-derived addresses and masks are formed inside each iteration:
+        // hoisted out of the loop they would each hold a register for the
+        // whole run
+        int lane_it = threadIdx.x;
+        asm volatile("" : "+v"(lane_it));
+        const int lane = lane_it & 63, lr = lane & 15, lq = lane >> 4;
+        // the identity as a B operand (for to_j)
+        i16x4_t kI;
+        {
+            f32x4_t id;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) id[e] = (4 * lq + e == lr) ? 1.f : 0.f;
+            kI = kq(id);
+        }
+        const int c = nch - 1 - p;
+        const int cn = c - NWORK;  // this worker's next chunk
+        const int64_t t0 = int64_t(c) * WL;
+        const int n = int(T - t0 < WL ? T - t0 : WL);
+        const bool valid = lr < n;
+        const bool starts = c % m == 0;  // S_0 is checkpoint c / m
+        const bool feeds = c % m != m - 1 && c + 1 < nch;  // S_0 of c + 1
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): vectors (and S_0)
+        asm volatile("" ::: "memory");
+        if (starts && lane == 0) lds_store(&fl.s_ready[w], c);
+
+        uint2 raw[7][4];
+#pragma unroll
+        for (int vv = 0; vv < 7; ++vv)
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) raw[vv][kb] = read_t(w, vv, kb, lane);
+        lds_drain();
+        // the stage is free: the next chunk's vectors load during this one
+        if (cn >= 0) fetch_vecs(A, w, cn, lane);
+        if (n < WL) {
+#pragma unroll
+            for (int vv = 0; vv < 7; ++vv)
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+                    raw[vv][kb] = valid ? raw[vv][kb] : make_uint2(0, 0);
+        }
+
+        // ---- factors (T layout) ------------------------------------------
+        // lam = log2 d_t, g its running sum over the chunk, g_ref = g at
+        // token 7, g_L = g at token 15 (padding tokens decay by nothing)
+        i16x4_t tA[4], tR[4], tB[4], tK[4], tAh[4], tBh[4], tKh[4];
+        float lo = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const f32x4_t wr = unpack4(raw[1][kb]);
+            const f32x4_t ar = unpack4(raw[4][kb]), br = unpack4(raw[5][kb]);
+            const f32x4_t rr = unpack4(raw[0][kb]), kr = unpack4(raw[2][kb]);
+            f32x4_t sp4, lr4, fA, fR, fB, fK, eh, bh4, kh4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float ew = __builtin_amdgcn_exp2f(
+                    valid ? wr[e] * kLog2e : -__builtin_inff());
+                const float g = scan16(-ew * kLog2e);
+                const float gref = row_bcast<7>(g), gL = row_bcast<15>(g);
+                lo = fminf(lo, fminf(gref, gL - gref));
+                const float dg = g - gref;
+                const float eg = __builtin_amdgcn_exp2f(dg);
+                const float eng = __builtin_amdgcn_exp2f(-dg);
+                // token 0: 2^{-g_ref} (its A~ factor); tokens 1, 2: the
+                // column's 2^{g_ref}, 2^{g_L}
+                const float sp = __builtin_amdgcn_exp2f(
+                    lr == 0 ? -gref : lr == 1 ? gref : gL);
+                const float eprev = row_prev(eg, sp);
+                sp4[e] = sp;
+                const float sLR = pin_lanes(row_bcast<15>(eg));
+                lr4[e] = sLR;
+                fA[e] = ar[e] * eprev;
+                fR[e] = rr[e] * eg;
+                fB[e] = br[e] * eng;
+                fK[e] = kr[e] * eng;
+                eh[e] = fA[e] * pin_lanes(row_bcast<1>(sp));
+                bh4[e] = fB[e] * sLR;
+                kh4[e] = fK[e] * sLR;
+            }
+            tA[kb] = kq(fA);
+            tR[kb] = kq(fR);
+            tB[kb] = kq(fB);
+            tK[kb] = kq(fK);
+            tAh[kb] = kq(eh);
+            tBh[kb] = kq(bh4);
+            tKh[kb] = kq(kh4);
+            if (lr == 1)
+                *reinterpret_cast<f32x4_t*>(&lds_eref[w][16 * kb + 4 * lq]) =
+                    sp4;
+            if (lr == 2)
+                *reinterpret_cast<f32x4_t*>(&lds_eL[w][16 * kb + 4 * lq]) = sp4;
+            if (lr == 0)
+                *reinterpret_cast<f32x4_t*>(&lds_eLR[w][16 * kb + 4 * lq]) =
+                    lr4;
+        }
+        // the factored form needs g_ref >= -H and g_L - g_ref >= -H
+        if (__builtin_amdgcn_ballot_w64(lo < -kHalfRange * kLog2e) != 0) {
+            // hand the head to the exact pass: every wave stops
+            if (lane == 0) {
+                lds_store(&fl.abort, 1);
+                *reinterpret_cast<uint32_t*>(A.ds0 + bh * NN) = kExactPassMark;
+            }
+            break;
+        }
+        // kept for the rest of the chunk: w (the decay gradient), and v, dy
+        // as T layout pairs (products over the value index)
+        uint2 wraw[4];
+        bf16x8_t Vp[2], dYp[2];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) wraw[kb] = raw[1][kb];
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            Vp[kp] = pk8(as_i16x4(raw[3][2 * kp]), as_i16x4(raw[3][2 * kp + 1]));
+            dYp[kp] =
+                pk8(as_i16x4(raw[6][2 * kp]), as_i16x4(raw[6][2 * kp + 1]));
+        }
+
+        // ---- the 16 x 16 matrices (K = 64) ---------------------------------
+        f32x4_t mA = zero4(), mAT = zero4(), mAak = zero4(), mAakT = zero4(),
+                mArb = zero4(), mArbT = zero4(), mArk = zero4();
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            const bf16x8_t a8 = pk8(tA[2 * kp], tA[2 * kp + 1]);
+            const bf16x8_t b8 = pk8(tB[2 * kp], tB[2 * kp + 1]);
+            const bf16x8_t k8 = pk8(tK[2 * kp], tK[2 * kp + 1]);
+            const bf16x8_t r8 = pk8(tR[2 * kp], tR[2 * kp + 1]);
+            mfma(mA, a8, b8);     // Aab[t][s] = A~_t . B~_s
+            mfma(mAT, b8, a8);    // Aab^T
+            mfma(mAak, a8, k8);   // Aak[t][s] = A~_t . K~_s
+            mfma(mAakT, k8, a8);  // Aak^T
+            mfma(mArb, r8, b8);   // Arb[t][s] = R~_t . B~_s
+            mfma(mArbT, b8, r8);  // Arb^T
+            mfma(mArk, r8, k8);   // Ark[t][s] = R~_t . K~_s
+        }
+        mA = mask4(mA, lr, lq, true, true);          // s < t
+        mAT = mask4(mAT, lr, lq, true, false);
+        mAak = mask4(mAak, lr, lq, true, true);
+        mAakT = mask4(mAakT, lr, lq, true, false);
+        mArb = mask4(mArb, lr, lq, false, true);     // s <= t
+        mArbT = mask4(mArbT, lr, lq, false, false);
+        mArk = mask4(mArk, lr, lq, false, true);
+        const i16x4_t kAakA = kq(mAakT);  // A operand: Aak
+        const i16x4_t kAakB = kq(mAak);   // B operand: Aak
+        const i16x4_t kArbTA = kq(mArb);  // A operand: Arb^T
+        const i16x4_t kArbA = kq(mArbT);  // A operand: Arb
+        const i16x4_t kArkB = kq(mArk);   // B operand: Ark
+
+        // ---- Minv = (I - Aab)^{-1} = (I + A)(I + A^2)(I + A^4)(I + A^8) ----
+        // kMinv = kq(D(Minv^T)): A operand Minv, B operand Minv^T;
+        // kMinvT = kq(D(Minv)): A operand Minv^T, B operand Minv
+        i16x4_t kMinv, kMinvT;
+        {
+            const i16x4_t pA = kq(mA), pT = kq(mAT);
+            f32x4_t x2 = zero4(), t2 = zero4();
+            mfma16(x2, pT, pA);  // A A
+            mfma16(t2, pA, pT);  // (A A)^T
+            const i16x4_t px2 = kq(x2), pt2 = kq(t2);
+            f32x4_t q1, q1t;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float one = (4 * lq + e == lr) ? 1.f : 0.f;
+                q1[e] = one + mA[e] + x2[e];
+                q1t[e] = one + mAT[e] + t2[e];
+            }
+            mfma16(q1, pT, px2);   // + A A^2
+            mfma16(q1t, px2, pT);  // + (A A^2)^T
+            f32x4_t x4 = zero4(), t4 = zero4();
+            mfma16(x4, pt2, px2);  // A^4
+            mfma16(t4, px2, pt2);  // (A^4)^T
+            const i16x4_t pq1t = kq(q1t), px4 = kq(x4), pt4 = kq(t4);
+            f32x4_t q2 = q1, q2t = q1t, x8 = zero4();
+            mfma16(q2, pq1t, px4);   // + Q1 A^4
+            mfma16(q2t, px4, pq1t);  // + (Q1 A^4)^T
+            mfma16(x8, pt4, px4);    // A^8
+            const i16x4_t pq2t = kq(q2t), px8 = kq(x8);
+            f32x4_t dM = q2, dMT = q2t;
+            mfma16(dM, pq2t, px8);   // Minv = Q2 + Q2 A^8
+            mfma16(dMT, px8, pq2t);  // Minv^T = Q2^T + (A^8)^T Q2^T
+            kMinv = kq(dMT);
+            kMinvT = kq(dM);
+        }
+
+        // ---- W^ = Minv A^, Q^ = R~ 2^{g_ref} + Arb W^ (J layout); the map -
+        if (wait_for(A.wait, &fl.map_taken[w], lane,
+                     [&](int x) { return x >= NCHAIN * kord; }) <= 0)
+            break;
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            const float erj = lds_eref[w][16 * jb + lr];
+            f32x4_t x = zero4();
+            mfma16(x, kMinv, to_j(tA[jb], kI));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] *= erj;
+            const i16x4_t kW = kq(x);
+            f32x4_t y = unpack_i16(to_j(tR[jb], kI));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] *= erj;
+            mfma16(y, kArbA, kW);
+            map.W[jb][lane] = kW;
+            map.Q[jb][lane] = kq(y);
+        }
+        const bf16x8_t Bhp0 = pk8(tBh[0], tBh[1]), Bhp1 = pk8(tBh[2], tBh[3]);
+        map.Bh[0][lane] = Bhp0;
+        map.Bh[1][lane] = Bhp1;
+        i16x4_t jdY[4];
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib) {
+            jdY[ib] = to_j(as_i16x4(raw[6][ib]), kI);
+            map.dY[ib][lane] = jdY[ib];
+        }
+        lds_drain();
+        if (lane == 0) lds_store(&fl.map_ready[w], kord + 1);
+
+        // ---- U = A^ S_0^T + Aak V, X = Minv U ------------------------------
+        if (!starts) {
+            if (wait_for(A.wait, &fl.s_ready[w], lane,
+                         [&](int x) { return x == c; }) <= 0)
+                break;
+        }
+        // the next chunk's start state, S_L = S_0 2^{g_L} + X^T B^ + V^T K^,
+        // goes to the worker of chunk c + 1 (tiles of S_L^T, formed per i
+        // block as X is)
+        i16x4_t kBh[4], kKh[4];
+        if (feeds) {
+            if (wait_for(A.wait, &fl.s_free[wfeed], lane,
+                         [&](int x) { return x == c + 1; }) <= 0)
+                break;
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+                const float elr = lds_eLR[w][16 * jb + lr];
+                f32x4_t bj = unpack_i16(to_j(tB[jb], kI));
+                f32x4_t kj = unpack_i16(to_j(tK[jb], kI));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    bj[e] *= elr;
+                    kj[e] *= elr;
+                }
+                kBh[jb] = kq(bj);
+                kKh[jb] = kq(kj);
+            }
+        }
+        const bf16x8_t Ahp0 = pk8(tAh[0], tAh[1]), Ahp1 = pk8(tAh[2], tAh[3]);
+        i16x4_t kXT[4];
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib) {
+            const i16x4_t jV = to_j(as_i16x4(raw[3][ib]), kI);
+            f32x4_t u = zero4(), av = zero4();
+            mfma(u, Ahp0, frag_rows(S, ib, 0, lane));
+            mfma(u, Ahp1, frag_rows(S, ib, 1, lane));
+            mfma16(av, kAakA, jV);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) u[e] += av[e];
+            const i16x4_t kU = kq(u);  // D(U_ib): B = U, A = U^T
+            f32x4_t xt = zero4();
+            mfma16(xt, kU, kMinv);  // X^T = U^T Minv^T
+            kXT[ib] = kq(xt);
+            if (feeds) {
+                f32x4_t xj = zero4();
+                mfma16(xj, kMinv, kU);  // X = Minv U
+                const i16x4_t kXJ = kq(xj);
+                bf16_t* const Sn = lds_S[wfeed];
+#pragma unroll
+                for (int jpb = 0; jpb < 4; ++jpb) {
+                    // lane: S_L[16 ib + lr][16 jpb + 4 lq + e]
+                    const f32x4_t el = *reinterpret_cast<const f32x4_t*>(
+                        &lds_eL[w][16 * jpb + 4 * lq]);
+                    const f32x4_t s0 = unpack4(
+                        sd_read4(S, 16 * ib + lr, 16 * jpb + 4 * lq));
+                    f32x4_t acc;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[e] = s0[e] * el[e];
+                    mfma16(acc, kBh[jpb], kXJ);
+                    mfma16(acc, kKh[jpb], jV);
+                    sd_write4(Sn, 16 * ib + lr, 16 * jpb + 4 * lq, pack4(acc));
+                }
+            }
+            fence_sched();
+        }
+        if (feeds) {
+            lds_drain();
+            if (lane == 0) lds_store(&fl.s_ready[wfeed], c + 1);
+        }
+
+        // ---- D arrives: dX = B^ D^T + Arb^T dY, dU = Minv^T dX (J and T),
+        // dV^T = D K^^T + dY^T Ark + dU^T Aak ---------------------------------
+        if (wait_for(A.wait, &fl.d_cnt[w], lane,
+                     [&](int x) { return x >= NCHAIN * (kord + 1); }) <= 0)
+            break;
+        const bf16x8_t Khp0 = pk8(tKh[0], tKh[1]), Khp1 = pk8(tKh[2], tKh[3]);
+        i16x4_t kdUT[4];
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib) {
+            const bf16x8_t d0 = frag_rows(D, ib, 0, lane);
+            const bf16x8_t d1 = frag_rows(D, ib, 1, lane);
+            f32x4_t dx = zero4(), dxy = zero4();
+            mfma(dx, Bhp0, d0);
+            mfma(dx, Bhp1, d1);
+            mfma16(dxy, kArbTA, jdY[ib]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dx[e] += dxy[e];
+            const i16x4_t kdX = kq(dx);
+            f32x4_t du = zero4(), dut = zero4();
+            mfma16(du, kMinvT, kdX);   // dU = Minv^T dX (J)
+            mfma16(dut, kdX, kMinvT);  // dU^T = dX^T Minv (T)
+            kdUT[ib] = kq(dut);
+            const i16x4_t kdUJ = kq(du);
+            f32x4_t dv = zero4(), dv16 = zero4();
+            mfma(dv, d0, Khp0);
+            mfma(dv, d1, Khp1);
+            mfma16(dv16, jdY[ib], kArkB);  // dY^T Ark
+            mfma16(dv16, kdUJ, kAakB);     // dU^T Aak
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dv[e] += dv16[e];
+            // lane: dV[t0 + lr][16 ib + 4 lq + e]
+            if (valid)
+                *reinterpret_cast<uint2*>(
+                    (A.dv + (t0 * A.lay.ts + hoff)) +
+                    (uint32_t(lr) * TS + 16 * ib + 4 * lq)) = pack4(dv);
+            fence_sched();
+        }
+
+        // ---- cotangents of the 16 x 16 matrices (K = 64 over i) -----------
+        bf16x8_t Xp[2], dUp[2];
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            Xp[kp] = pk8(kXT[2 * kp], kXT[2 * kp + 1]);
+            dUp[kp] = pk8(kdUT[2 * kp], kdUT[2 * kp + 1]);
+        }
+        f32x4_t gArb = zero4(), gArbT = zero4(), gArk = zero4(),
+                gArkT = zero4(), gAab = zero4(), gAabT = zero4(),
+                gAak = zero4(), gAakT = zero4();
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            mfma(gArb, dYp[kp], Xp[kp]);    // dArb[t][s] = dY_t . X_s
+            mfma(gArbT, Xp[kp], dYp[kp]);
+            mfma(gArk, dYp[kp], Vp[kp]);    // dArk[t][s] = dY_t . V_s
+            mfma(gArkT, Vp[kp], dYp[kp]);
+            mfma(gAab, dUp[kp], Xp[kp]);    // dAab[t][s] = dU_t . X_s
+            mfma(gAabT, Xp[kp], dUp[kp]);
+            mfma(gAak, dUp[kp], Vp[kp]);    // dAak[t][s] = dU_t . V_s
+            mfma(gAakT, Vp[kp], dUp[kp]);
+        }
+        const i16x4_t kgArb = kq(mask4(gArb, lr, lq, false, true));
+        const i16x4_t kgArbT = kq(mask4(gArbT, lr, lq, false, false));
+        const i16x4_t kgArk = kq(mask4(gArk, lr, lq, false, true));
+        const i16x4_t kgArkT = kq(mask4(gArkT, lr, lq, false, false));
+        const i16x4_t kgAab = kq(mask4(gAab, lr, lq, true, true));
+        const i16x4_t kgAabT = kq(mask4(gAabT, lr, lq, true, false));
+        const i16x4_t kgAak = kq(mask4(gAak, lr, lq, true, true));
+        const i16x4_t kgAakT = kq(mask4(gAakT, lr, lq, true, false));
+
+        // ---- the chains' shares of sum_i D_0 S_0 -------------------------
+        if (wait_for(A.wait, &fl.tail_cnt[w], lane,
+                     [&](int x) { return x >= NCHAIN * (kord + 1); }) <= 0)
+            break;
+
+        // ---- per column block: dR~, dA~, dB~, dK~ and the input gradients -
+        // (tiles of the transposes: lane holds token lr, columns
+        // 16 jb + 4 lq + e, the T layout)
+        const uint32_t goff = uint32_t(lr) * TS + 4 * lq;
+        const int64_t gbase = t0 * A.lay.ts + hoff;
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            const f32x4_t er = *reinterpret_cast<const f32x4_t*>(
+                &lds_eref[w][16 * jb + 4 * lq]);
+            const f32x4_t elr = *reinterpret_cast<const f32x4_t*>(
+                &lds_eLR[w][16 * jb + 4 * lq]);
+            f32x4_t tail = zero4();
+#pragma unroll
+            for (int ch = 0; ch < NCHAIN; ++ch) {
+                const f32x4_t x = *reinterpret_cast<const f32x4_t*>(
+                    &lds_tail[w][ch][16 * jb + 4 * lq]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) tail[e] += x[e];
+            }
+            f32x4_t gR = zero4(), gA = zero4(), gB = zero4(), gK = zero4();
+            {
+                const bf16x8_t s0 = frag_cols(S, jb, 0, lane);
+                const bf16x8_t s1 = frag_cols(S, jb, 1, lane);
+                mfma(gR, s0, dYp[0]);  // S_0^T dY^T
+                mfma(gR, s1, dYp[1]);
+                mfma(gA, s0, dUp[0]);  // S_0^T dU^T
+                mfma(gA, s1, dUp[1]);
+            }
+            {
+                const bf16x8_t d0 = frag_cols(D, jb, 0, lane);
+                const bf16x8_t d1 = frag_cols(D, jb, 1, lane);
+                mfma(gB, d0, Xp[0]);   // D^T X^T
+                mfma(gB, d1, Xp[1]);
+                mfma(gK, d0, Vp[0]);   // D^T V^T
+                mfma(gK, d1, Vp[1]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                gR[e] *= er[e];
+                gA[e] *= er[e];
+                gB[e] *= elr[e];
+                gK[e] *= elr[e];
+            }
+            const i16x4_t jA = to_j(tA[jb], kI), jB = to_j(tB[jb], kI);
+            const i16x4_t jK = to_j(tK[jb], kI), jR = to_j(tR[jb], kI);
+            mfma16(gR, jB, kgArbT);  // + B~^T dArb^T
+            mfma16(gR, jK, kgArkT);  // + K~^T dArk^T
+            mfma16(gA, jB, kgAabT);  // + B~^T dAab^T
+            mfma16(gA, jK, kgAakT);  // + K~^T dAak^T
+            mfma16(gB, jA, kgAab);   // + A~^T dAab
+            mfma16(gB, jR, kgArb);   // + R~^T dArb
+            mfma16(gK, jA, kgAak);   // + A~^T dAak
+            mfma16(gK, jR, kgArk);   // + R~^T dArk
+
+            // input gradients; the factors' exponentials are formed again
+            // exactly as in the factor pass, and the decay gradient's terms
+            // r dr, b db, k dk, a da are R~ dR~, B~ dB~, K~ dK~, A~ dA~
+            const f32x4_t wr = unpack4(wraw[jb]);
+            const f32x4_t fA = unpack_i16(tA[jb]), fR = unpack_i16(tR[jb]);
+            const f32x4_t fB = unpack_i16(tB[jb]), fK = unpack_i16(tK[jb]);
+            f32x4_t drv, dwv, dkv, dav, dbv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float ew = __builtin_amdgcn_exp2f(
+                    valid ? wr[e] * kLog2e : -__builtin_inff());
+                const float g = scan16(-ew * kLog2e);
+                const float gref = row_bcast<7>(g);
+                const float eg = __builtin_amdgcn_exp2f(g - gref);
+                const float eng = __builtin_amdgcn_exp2f(gref - g);
+                const float e0 = __builtin_amdgcn_exp2f(-gref);
+                const float eprev = row_prev(eg, e0);
+                drv[e] = gR[e] * eg;
+                dav[e] = gA[e] * eprev;
+                dbv[e] = gB[e] * eng;
+                dkv[e] = gK[e] * eng;
+                const float f1 = fB[e] * gB[e] + fK[e] * gK[e] - fR[e] * gR[e];
+                const float pre = scan16(f1) - f1;
+                const float ada = scan16(fA[e] * gA[e]);
+                dwv[e] = (pre - ada + tail[e]) * -ew;  // dlog d * (-e^w)
+            }
+            if (valid) {
+                const uint32_t o = goff + 16 * jb;
+                *reinterpret_cast<uint2*>((A.dr + gbase) + o) = pack4(drv);
+                *reinterpret_cast<uint2*>((A.dw + gbase) + o) = pack4(dwv);
+                *reinterpret_cast<uint2*>((A.dk + gbase) + o) = pack4(dkv);
+                *reinterpret_cast<uint2*>((A.da + gbase) + o) = pack4(dav);
+                *reinterpret_cast<uint2*>((A.db + gbase) + o) = pack4(dbv);
+            }
+            fence_sched();
+        }
+
+        // ---- release the buffers; the next chunk's start state ------------
+        lds_drain();
+        if (lane == 0) {
+            lds_store(&fl.d_done[w], kord + 1);
+            lds_store(&fl.s_free[w], cn);
+        }
+        if (cn >= 0 && cn % m == 0) fetch_state(A, w, cn, lane);
+    }
+}
+
+// A workgroup whose wait gave up overwrites every output of its head with
+// NaN.
+__device__ __forceinline__ void poison(const BwdArgs& A, int tid) {
+    const int64_t bh = blockIdx.x;
+    const int64_t hoff = A.lay.head(bh, WN);
+    const bf16_t nan16 = 0x7fc0;
+    bf16_t* const outs[6] = {A.dr, A.dw, A.dk, A.dv, A.da, A.db};
+    for (int g = 0; g < 6; ++g)
+        for (int64_t e = tid; e < A.T * WN; e += BTHREADS)
+            outs[g][(e / WN) * A.lay.ts + hoff + e % WN] = nan16;
+    for (int e = tid; e < NN; e += BTHREADS)
+        A.ds0[bh * NN + e] = __builtin_nanf("");
+}
+
+__global__ void __launch_bounds__(BTHREADS)
+wkv7_wave_bwd_kernel(BwdArgs A) {
+    BwdFlags& fl = lds_flags;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nch = int((A.T + WL - 1) / WL);
+    if (tid < NWORK) {
+        fl.map_ready[tid] = 0;
+        fl.map_taken[tid] = 0;
+        fl.d_cnt[tid] = 0;
+        fl.d_done[tid] = 0;
+        fl.tail_cnt[tid] = 0;
+        fl.s_ready[tid] = -1;
+        fl.s_free[tid] = nch - 1 - tid;
+    }
+    if (tid == 0) {
+        fl.abort = 0;
+        fl.failed = 0;
+    }
+    __syncthreads();
+    if (wv < NCHAIN)
+        chain(A, wv, lane);
+    else
+        work(A, wv - NCHAIN, lane);
+    // every wait is bounded, so every wave arrives here
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (lds_load(&fl.failed) != 0) poison(A, tid);
+}
+
+}  // namespace
+
+hipError_t launch_wave_backward(const WaveBwdArgs& p, hipStream_t stream) {
+    if (p.L % WL != 0 || p.L / WL < 1 || p.L / WL > 4 || p.L / WL == 3)
+        return hipErrorInvalidValue;
+    BwdArgs A;
+    A.T = p.T;
+    A.BH = p.B * p.H;
+    A.lay = p.lay;
+    A.r = static_cast<const bf16_t*>(p.r);
+    A.w = static_cast<const bf16_t*>(p.w);
+    A.k = static_cast<const bf16_t*>(p.k);
+    A.v = static_cast<const bf16_t*>(p.v);
+    A.a = static_cast<const bf16_t*>(p.a);
+    A.b = static_cast<const bf16_t*>(p.b);
+    A.dy = static_cast<const bf16_t*>(p.dy);
+    A.ds_t = p.ds_t;
+    A.ckpt = static_cast<const bf16_t*>(p.ckpt);
+    A.m = p.L / WL;
+    A.dr = static_cast<bf16_t*>(p.dr);
+    A.dw = static_cast<bf16_t*>(p.dw);
+    A.dk = static_cast<bf16_t*>(p.dk);
+    A.dv = static_cast<bf16_t*>(p.dv);
+    A.da = static_cast<bf16_t*>(p.da);
+    A.db = static_cast<bf16_t*>(p.db);
+    A.ds0 = p.ds0;
+    A.wait = p.wait;
+    if (A.BH <= 0 || A.T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(wkv7_wave_bwd_kernel, dim3(unsigned(A.BH)),
+                       dim3(BTHREADS), 0, stream, A);
+    return hipGetLastError();
+}
+
+}  // namespace rwkv7m

@@ -7,7 +7,8 @@
 //
 // acts on each row i of the state separately: row i needs only v_t[i] of
 // the value side and yields only y_t[i].  Over a chunk, in the closed form
-// of the chunked kernels (wkv7_chunk_common.h),
+// below (g = running log2-decay, g_ref its value at token 7; A~, R~, B~, K~
+// the decayed factors of wkv7_wave_bwd.hip),
 //
 //   S_L = S_0 diag(2^{g_L}) + bf16(S_0) M^ + C,   Y^T = bf16(S_0) Q^^T + P^T
 //
@@ -15,8 +16,8 @@
 // depending on the chunk's key-side vectors only, and C = U^T B^ + V^T K^,
 // P = Arb U + Ark V linear in the value rows.
 //
-// One workgroup of 8 waves per (batch, head):
-//   * waves 4..7, the producers: producer p builds chunks p, p + 4, ...:
+// One workgroup of 12 waves per (batch, head):
+//   * waves 4..11, the producers: producer p builds chunks p, p + 8, ...:
 //     the decayed factors, the 16 x 16 matrices, the inverse, W, U, M^ and
 //     Q^, all in registers, and hands them to a ring of three LDS slots;
 //   * waves 0..3, the chains: chain ib holds rows 16 ib .. 16 ib + 15 of the
@@ -44,31 +45,22 @@
 // 16x16x16 product never accumulates onto a 16x16x32 result or the other way
 // round: every such hand-over goes through a VALU operation.
 
-#include "wkv7_chunk_common.h"
-#include "wkv7_launch.h"
+#include "wkv7_wave_common.h"
 
 namespace rwkv7m {
 namespace {
 
-using chunk::kHalfRange;
-using chunk::kLog2e;
-using chunk::kq;
-using chunk::mfma16;
+using namespace wave;
 
-constexpr int WN = 64;       // head size
-constexpr int WL = 16;       // tokens per chunk
 constexpr int NCHAIN = 4;    // chain waves (16 state rows each)
 constexpr int NPROD = 8;     // producer waves
 constexpr int NSLOT = 3;     // hand-over ring
 constexpr int WTHREADS = 64 * (NCHAIN + NPROD);
-constexpr int XPITCH = WN + 8;  // bf16 transpose buffer row pitch
 // Every hand-over wait is bounded (WaitCfg::limit polls of ~64 cycles; a
 // wave waits for at most a few other chunks, and the default bound is orders
 // of magnitude above that), so every wave exits.  A wait that gives up marks
 // the workgroup failed: its outputs are then overwritten with NaN and the
 // device's failure counter is raised (wkv7_status.hip).
-
-typedef short i16x8_t __attribute__((ext_vector_type(8)));
 
 // Per producer: the next chunk's six vectors as loaded, and, once the
 // factors are formed, the four J-layout matrices on their way through the
@@ -105,87 +97,8 @@ struct WaveFwdSmem {
     int failed;             // a bounded wait of this workgroup gave up
 };
 
-__device__ __forceinline__ bf16x8_t pk8(const i16x4_t& lo, const i16x4_t& hi) {
-    const i16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    return __builtin_bit_cast(bf16x8_t, v);
-}
 
-// Value of lane n of each 16-lane row, in every lane of the row.
-template <int N>
-__device__ __forceinline__ float row_bcast(float x) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(
-        0, __float_as_int(x), 0x150 + N, 0xF, 0xF, false));
-}
 
-// The previous lane's value within each row; the row's first lane keeps
-// `first`.
-__device__ __forceinline__ float row_prev(float x, float first) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(
-        __float_as_int(first), __float_as_int(x), 0x111, 0xF, 0xF, false));
-}
-
-// X[4q + e][16 jb + r] (e = 0..3) of a [t][j] matrix in LDS (the J layout)
-// by one transposing read: lane s of each 16-lane group addresses row
-// 4q + s / 4, columns 16 jb + 4 (s % 4) .. + 3.
-__device__ __forceinline__ i16x4_t read_j(const bf16_t (*X)[XPITCH], int jb,
-                                          int lane) {
-    const int s = lane & 15, q = lane >> 4;
-    const bf16_t* p = &X[4 * q + (s >> 2)][16 * jb + 4 * (s & 3)];
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p));
-}
-
-// Keep X[4q + e][r] where (row_below: r < 4q + e; else 4q + e < r), with
-// equality kept unless strict.
-__device__ __forceinline__ f32x4_t mask4(f32x4_t x, int r, int q, bool strict,
-                                         bool row_below) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int m = 4 * q + e;
-        const bool keep = row_below ? (strict ? r < m : r <= m)
-                                    : (strict ? m < r : m <= r);
-        x[e] = keep ? x[e] : 0.f;
-    }
-    return x;
-}
-
-// Hand-over words in LDS are read and written as relaxed workgroup-scope
-// atomics: a volatile access would also make the wave wait for all its
-// outstanding global stores.  Ordering against the data they guard comes
-// from an explicit lgkmcnt(0) before each write and from the polling
-// reads' own completion before the guarded reads are issued.
-__device__ __forceinline__ int lds_load(int* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-__device__ __forceinline__ void lds_store(int* p, int x) {
-    __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-// Poll an LDS word until pred(value) holds, at most `limit` times; false if
-// it never did.
-template <typename Pred>
-__device__ __forceinline__ bool poll(int* p, int limit, Pred pred) {
-    bool ok = false;
-    for (int it = 0; it < limit; ++it) {
-        if (pred(__builtin_amdgcn_readfirstlane(lds_load(p)))) {
-            ok = true;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-    asm volatile("" ::: "memory");
-    return ok;
-}
-
-// A wait gave up: mark the workgroup failed (LDS) and count it on the device
-// (a per-lane global atomic from lane 0).
-__device__ __forceinline__ void wait_failed(int* failed, unsigned int* counter,
-                                         int lane) {
-    if (lane == 0) {
-        lds_store(failed, 1);
-        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
 
 struct FwdArgs {
     int64_t T, BH;
@@ -209,7 +122,7 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
     const int64_t T = A.T;
     const int64_t nch = (T + WL - 1) / WL;
     const uint32_t TS = uint32_t(A.lay.ts);
-    const chunk::VecPtrs src{A.r, A.w, A.k, A.v, A.a, A.b, nullptr};
+    const VecPtrs src{A.r, A.w, A.k, A.v, A.a, A.b, nullptr};
     ProdStage& stg = sm.st[p];
     bf16_t (*const xp)[WL][XPITCH] = stg.xp;
     int* const vdone = sm.done;
@@ -280,7 +193,7 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
             for (int e = 0; e < 4; ++e) {
                 const float ew = __builtin_amdgcn_exp2f(
                     valid ? wr[e] * kLog2e : -__builtin_inff());
-                const float g = chunk::scan_lanes<16>(-ew * kLog2e);
+                const float g = scan16(-ew * kLog2e);
                 const float gref = row_bcast<7>(g), gL = row_bcast<15>(g);
                 lo = fminf(lo, fminf(gref, gL - gref));
                 const float dg = g - gref;
@@ -292,7 +205,7 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
                     lr == 0 ? -gref : lr == 1 ? gref : gL);
                 const float eprev = row_prev(eg, sp);
                 sp4[e] = sp;
-                sLR[e] = chunk::pin_lanes(row_bcast<15>(eg));
+                sLR[e] = pin_lanes(row_bcast<15>(eg));
                 fA[kb][e] = ar[e] * eprev;
                 fR[kb][e] = rr[e] * eg;
                 fB[kb][e] = br[e] * eng;
@@ -383,7 +296,7 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
         const i16x4_t kMinv = kq(dMT);  // A operand: Minv
         const i16x4_t kAak = kq(mAakT), kArbT = kq(mArbT),
                       kArkT = kq(mArkT);
-        chunk::wave_lds_fence();
+        wave_lds_fence();
         i16x4_t jA[4], jB[4], jK[4], jV[4];
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {

@@ -225,7 +225,7 @@ def _layout(layout: str, r: torch.Tensor):
 
 def last_path() -> str:
     """Kernel path of the last successful WKV-7 call on this thread
-    ("wave_forward", "decode", "seq_forward", "chunk_backward",
+    ("wave_forward", "decode", "seq_forward", "wave_backward",
     "seq_backward" or "")."""
     return load_library().rwkv7m_wkv7_last_path().decode()
 

@@ -23,14 +23,14 @@ NAMES = ("r", "w", "k", "v", "neg_kk", "kka")
 GRAD_NAMES = ("dr", "dw", "dk", "dv", "dneg_kk", "dkka", "ds0")
 TOL = 2e-2
 THREADS = 8
-# checkpoint intervals (= backward chunk lengths) the MFMA kernels serve
-MFMA_INTERVALS = (16, 32)
+# checkpoint intervals the MFMA kernels serve (both directions)
+MFMA_INTERVALS = (16, 32, 64)
 
 
 def expected_paths(ci):
     """(forward, backward) kernel paths of a bf16 N = 64 training call."""
     if ci in MFMA_INTERVALS:
-        return ("wave_forward", "chunk_backward")
+        return ("wave_forward", "wave_backward")
     return ("seq_forward", "seq_backward")
 
 
@@ -108,7 +108,7 @@ def test_chunked_strong_decay_uses_exact_fallback(hip, ci):
     _run_case(hip, inp, ci, case)
 
 
-@pytest.mark.parametrize("ci", [16, 32])
+@pytest.mark.parametrize("ci", [16, 32, 64])
 def test_chunked_mixed_fast_and_fallback_chunks(hip, ci):
     # decay strong only in tokens 64..127 of head 1: chunks there take the
     # exact fallback, the rest the MFMA path, and the state crosses both
@@ -164,7 +164,7 @@ def test_config1_forward_backward_sequential_kernels(hip):
     _run_case(hip, inp, 128, case)
 
 
-@pytest.mark.parametrize("ci", [16, 32])
+@pytest.mark.parametrize("ci", [16, 32, 64])
 def test_config4_distributions_slow_decay_carry_state(hip, ci):
     # config 4's distributions (slow decay, S0 and dS_T ~ N(0, 0.1)) on a
     # reduced (B, H) at T = 2048; the full size is in

@@ -100,7 +100,7 @@ def _train_config(hip, index, case):
     print("case:", case, flush=True)
     inp = config_inputs(index, device="cuda", generator="torch")
     outs, paths = _train_call(hip, inp, 32)
-    assert paths == ("wave_forward", "chunk_backward"), paths
+    assert paths == ("wave_forward", "wave_backward"), paths
     bs, hs = _heads(B, H, seed=index)
     host = [_vec_slice(inp[n], bs, hs) for n in NAMES]
     s0 = _state_slice(inp["s0"], bs, hs)
@@ -115,7 +115,7 @@ def _train_config(hip, index, case):
         assert torch.isfinite(got).all(), f"{case} {name}: non-finite"
     # every head: the same call at L = 16 agrees with L = 32
     outs16, paths16 = _train_call(hip, inp, 16)
-    assert paths16 == ("wave_forward", "chunk_backward"), paths16
+    assert paths16 == ("wave_forward", "wave_backward"), paths16
     for name, a, b in zip(OUT_NAMES, outs16, outs):
         _check_dev(name, a, b, f"{case} L16 vs L32 (all heads)")
 

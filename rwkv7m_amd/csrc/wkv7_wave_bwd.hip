@@ -68,6 +68,7 @@ constexpr int NCHAIN = 4;
 constexpr int NWORK = 4;
 constexpr int BTHREADS = 64 * (NCHAIN + NWORK);
 constexpr int NN = WN * WN;
+constexpr float kLn2 = 0.6931471805599453f;
 
 // Element (i, j) of a 64 x 64 bf16 S/D buffer: 16-byte unit (i, j / 8) at
 // ((i / 8) * 8 + j / 8) * 8 + i % 8, so one global_load_lds of 64 lanes
@@ -156,7 +157,6 @@ struct BwdArgs {
     const bf16_t *r, *w, *k, *v, *a, *b, *dy;
     const float* ds_t;
     const bf16_t* ckpt;
-    int m;  // checkpoint interval / 16
     bf16_t *dr, *dw, *dk, *dv, *da, *db;
     float* ds0;
     WaitCfg wait;
@@ -203,6 +203,18 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
     const int row = 16 * ib + lr;
     BwdFlags& fl = lds_flags;
     __builtin_amdgcn_s_setprio(2);  // the serial path
+    // the identity and a matrix of ones as bf16 operands (B and A)
+    i16x4_t kI, kOne;
+    {
+        f32x4_t id, one;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            id[e] = (4 * lq + e == lr) ? 1.f : 0.f;
+            one[e] = 1.f;
+        }
+        kI = kq(id);
+        kOne = kq(one);
+    }
     // tiles D(D^T_{j'b, ib}): lane holds D[row][16 j'b + 4 lq + e]
     f32x4_t Dt[4];
 #pragma unroll
@@ -272,7 +284,11 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
             Dt[jb] = acc;
         }
 
-        // this block's share of sum_i D_0[i][j] S_0[i][j] for the worker
+        // this block's share of sum_i D_0[i][j] S_0[i][j] for the worker.
+        // P = D_0 * S_0 on the block's tiles D(P^T) is split into bf16 parts
+        // P = P_hi + P_lo (16 significant bits); each part is turned into
+        // D(P) by P I and summed over i by a product with ones (exact for
+        // bf16 values, fp32 accumulation)
         if (wait_for(A.wait, &fl.s_ready[w], lane,
                      [&](int x) { return x == c; }) <= 0) {
             done = false;
@@ -282,13 +298,19 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
         for (int jb = 0; jb < 4; ++jb) {
             const f32x4_t s0 =
                 unpack4(sd_read4(lds_S[w], row, 16 * jb + 4 * lq));
-            f32x4_t t4;
+            f32x4_t pt, plo;
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                t4[e] = row_sum16(Dt[jb][e] * s0[e]);
-            if (lr == 0)
-                *reinterpret_cast<f32x4_t*>(
-                    &lds_tail[w][ib][16 * jb + 4 * lq]) = t4;
+            for (int e = 0; e < 4; ++e) pt[e] = Dt[jb][e] * s0[e];
+            const i16x4_t khi = kq(pt);
+            const f32x4_t phi = unpack_i16(khi);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) plo[e] = pt[e] - phi[e];
+            f32x4_t ph = zero4(), pl = zero4(), cs = zero4();
+            mfma16(ph, khi, kI);       // D(P_hi)
+            mfma16(pl, kq(plo), kI);   // D(P_lo)
+            mfma16(cs, kOne, kq(ph));  // every row: sum_i P[i][j]
+            mfma16(cs, kOne, kq(pl));
+            if (lq == 0) lds_tail[w][ib][16 * jb + lr] = cs[0];
         }
         lds_drain();
         if (lane == 0) lds_add(&fl.tail_cnt[w], 1);
@@ -331,13 +353,14 @@ __device__ __forceinline__ void fetch_vecs(const BwdArgs& A, int w, int c,
     }
 }
 
-// Checkpoint c / m (chunk c starts an interval) straight to worker w's S
+// Checkpoint c / M (chunk c starts an interval) straight to worker w's S
 // buffer: load g fills rows 8g .. 8g + 7 (lane l: row 8g + l % 8, segment
 // l / 8).
+template <int M>
 __device__ __forceinline__ void fetch_state(const BwdArgs& A, int w, int c,
                                             int lane) {
     const bf16_t* base =
-        A.ckpt + (int64_t(c / A.m) * A.BH + int64_t(blockIdx.x)) * NN;
+        A.ckpt + (int64_t(c / M) * A.BH + int64_t(blockIdx.x)) * NN;
     const int ldu = lane & 7, ldseg = lane >> 3;
 #pragma unroll
     for (int g = 0; g < 8; ++g)
@@ -366,14 +389,16 @@ __device__ __forceinline__ i16x4_t to_j(const i16x4_t& t, const i16x4_t& kI) {
 }
 
 // ---------------------------------------------------------------------------
-// Worker w: chunks nch - 1 - w, nch - 1 - w - NWORK, ...
+// Worker w: chunks nch - 1 - w, nch - 1 - w - NWORK, ...; checkpoints every
+// M chunks.
+template <int M>
 __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
     const int64_t bh = blockIdx.x;
     const int64_t hoff = A.lay.head(bh, WN);
     const int64_t T = A.T;
     const int nch = int((T + WL - 1) / WL);
     const uint32_t TS = uint32_t(A.lay.ts);
-    const int m = A.m;
+    constexpr int m = M;
     // the worker of chunk c + 1 (one position earlier in the reverse order),
     // whose start state chunk c's end state is
     const int wfeed = (w + NWORK - 1) % NWORK;
@@ -384,7 +409,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
 
     if (nch - 1 - w >= 0) {
         fetch_vecs(A, w, nch - 1 - w, lane0);
-        if ((nch - 1 - w) % m == 0) fetch_state(A, w, nch - 1 - w, lane0);
+        if ((nch - 1 - w) % m == 0) fetch_state<M>(A, w, nch - 1 - w, lane0);
     }
 
     for (int kord = 0, p = w; p < nch; ++kord, p += NWORK) {
@@ -433,6 +458,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         // lam = log2 d_t, g its running sum over the chunk, g_ref = g at
         // token 7, g_L = g at token 15 (padding tokens decay by nothing)
         i16x4_t tA[4], tR[4], tB[4], tK[4], tAh[4], tBh[4], tKh[4];
+        f32x4_t g4[4];  // g, kept for the input gradients
         float lo = 0.f;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
@@ -445,6 +471,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 const float ew = __builtin_amdgcn_exp2f(
                     valid ? wr[e] * kLog2e : -__builtin_inff());
                 const float g = scan16(-ew * kLog2e);
+                g4[kb][e] = g;
                 const float gref = row_bcast<7>(g), gL = row_bcast<15>(g);
                 lo = fminf(lo, fminf(gref, gL - gref));
                 const float dg = g - gref;
@@ -491,12 +518,9 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             }
             break;
         }
-        // kept for the rest of the chunk: w (the decay gradient), and v, dy
-        // as T layout pairs (products over the value index)
-        uint2 wraw[4];
+        // kept for the rest of the chunk: v, dy as T layout pairs (products
+        // over the value index)
         bf16x8_t Vp[2], dYp[2];
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) wraw[kb] = raw[1][kb];
 #pragma unroll
         for (int kp = 0; kp < 2; ++kp) {
             Vp[kp] = pk8(as_i16x4(raw[3][2 * kp]), as_i16x4(raw[3][2 * kp + 1]));
@@ -797,31 +821,30 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             mfma16(gK, jA, kgAak);   // + A~^T dAak
             mfma16(gK, jR, kgArk);   // + R~^T dArk
 
-            // input gradients; the factors' exponentials are formed again
-            // exactly as in the factor pass, and the decay gradient's terms
-            // r dr, b db, k dk, a da are R~ dR~, B~ dB~, K~ dK~, A~ dA~
-            const f32x4_t wr = unpack4(wraw[jb]);
+            // input gradients.  The decay gradient's terms r dr, b db, k dk,
+            // a da are R~ dR~, B~ dB~, K~ dK~, A~ dA~, and
+            // dlog d_t = S_t - f1_t + tail with S the inclusive prefix sum of
+            // f1 - A~ dA~ (f1 = B~ dB~ + K~ dK~ - R~ dR~)
             const f32x4_t fA = unpack_i16(tA[jb]), fR = unpack_i16(tR[jb]);
             const f32x4_t fB = unpack_i16(tB[jb]), fK = unpack_i16(tK[jb]);
             f32x4_t drv, dwv, dkv, dav, dbv;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float ew = __builtin_amdgcn_exp2f(
-                    valid ? wr[e] * kLog2e : -__builtin_inff());
-                const float g = scan16(-ew * kLog2e);
+                const float g = g4[jb][e];
                 const float gref = row_bcast<7>(g);
                 const float eg = __builtin_amdgcn_exp2f(g - gref);
                 const float eng = __builtin_amdgcn_exp2f(gref - g);
                 const float e0 = __builtin_amdgcn_exp2f(-gref);
                 const float eprev = row_prev(eg, e0);
+                // -e^w = (g_t - g_{t-1}) ln 2
+                const float lam = (g - row_prev(g, 0.f)) * kLn2;
                 drv[e] = gR[e] * eg;
                 dav[e] = gA[e] * eprev;
                 dbv[e] = gB[e] * eng;
                 dkv[e] = gK[e] * eng;
                 const float f1 = fB[e] * gB[e] + fK[e] * gK[e] - fR[e] * gR[e];
-                const float pre = scan16(f1) - f1;
-                const float ada = scan16(fA[e] * gA[e]);
-                dwv[e] = (pre - ada + tail[e]) * -ew;  // dlog d * (-e^w)
+                const float sc = scan16(f1 - fA[e] * gA[e]);
+                dwv[e] = (sc - f1 + tail[e]) * lam;  // dlog d * (-e^w)
             }
             if (valid) {
                 const uint32_t o = goff + 16 * jb;
@@ -840,7 +863,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             lds_store(&fl.d_done[w], kord + 1);
             lds_store(&fl.s_free[w], cn);
         }
-        if (cn >= 0 && cn % m == 0) fetch_state(A, w, cn, lane);
+        if (cn >= 0 && cn % m == 0) fetch_state<M>(A, w, cn, lane);
     }
 }
 
@@ -858,6 +881,7 @@ __device__ __forceinline__ void poison(const BwdArgs& A, int tid) {
         A.ds0[bh * NN + e] = __builtin_nanf("");
 }
 
+template <int M>
 __global__ void __launch_bounds__(BTHREADS)
 wkv7_wave_bwd_kernel(BwdArgs A) {
     BwdFlags& fl = lds_flags;
@@ -881,7 +905,7 @@ wkv7_wave_bwd_kernel(BwdArgs A) {
     if (wv < NCHAIN)
         chain(A, wv, lane);
     else
-        work(A, wv - NCHAIN, lane);
+        work<M>(A, wv - NCHAIN, lane);
     // every wait is bounded, so every wave arrives here
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -906,7 +930,6 @@ hipError_t launch_wave_backward(const WaveBwdArgs& p, hipStream_t stream) {
     A.dy = static_cast<const bf16_t*>(p.dy);
     A.ds_t = p.ds_t;
     A.ckpt = static_cast<const bf16_t*>(p.ckpt);
-    A.m = p.L / WL;
     A.dr = static_cast<bf16_t*>(p.dr);
     A.dw = static_cast<bf16_t*>(p.dw);
     A.dk = static_cast<bf16_t*>(p.dk);
@@ -916,8 +939,20 @@ hipError_t launch_wave_backward(const WaveBwdArgs& p, hipStream_t stream) {
     A.ds0 = p.ds0;
     A.wait = p.wait;
     if (A.BH <= 0 || A.T <= 0) return hipSuccess;
-    hipLaunchKernelGGL(wkv7_wave_bwd_kernel, dim3(unsigned(A.BH)),
-                       dim3(BTHREADS), 0, stream, A);
+    switch (p.L / WL) {
+        case 1:
+            hipLaunchKernelGGL(wkv7_wave_bwd_kernel<1>, dim3(unsigned(A.BH)),
+                               dim3(BTHREADS), 0, stream, A);
+            break;
+        case 2:
+            hipLaunchKernelGGL(wkv7_wave_bwd_kernel<2>, dim3(unsigned(A.BH)),
+                               dim3(BTHREADS), 0, stream, A);
+            break;
+        default:
+            hipLaunchKernelGGL(wkv7_wave_bwd_kernel<4>, dim3(unsigned(A.BH)),
+                               dim3(BTHREADS), 0, stream, A);
+            break;
+    }
     return hipGetLastError();
 }
 

@@ -182,14 +182,6 @@ __device__ __forceinline__ int wait_for(const WaitCfg& wc, int* p, int lane,
     return -1;
 }
 
-// Keeps the scheduler from moving instructions across this point: placed
-// between the unrolled iterations of the worker's block loops, so that one
-// iteration's LDS reads are not all hoisted to the top (each would hold its
-// registers across the whole loop).
-__device__ __forceinline__ void fence_sched() {
-    __builtin_amdgcn_sched_barrier(0);
-}
-
 __device__ __forceinline__ f32x4_t unpack_i16(const i16x4_t& x) {
     return unpack4(__builtin_bit_cast(uint2, x));
 }
@@ -341,15 +333,12 @@ __device__ __forceinline__ void fetch_vecs(const BwdArgs& A, int w, int c,
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int t = 8 * h + ldu;
-        const uint32_t off = uint32_t(t < n ? t : n - 1) * TS + 8 * ldseg;
+        const uint32_t off =
+            (uint32_t(t < n ? t : n - 1) * TS + 8 * ldseg) * sizeof(bf16_t);
 #pragma unroll
         for (int vv = 0; vv < 7; ++vv)
-            __builtin_amdgcn_global_load_lds(
-                (const void __attribute__((address_space(1)))*)(
-                    (src.get(vv) + cbase) + off),
-                (void __attribute__((address_space(3)))*)(
-                    &lds_stage[w][vv][h][0][0]),
-                16, 0, 0);
+            dma16(src.get(vv) + cbase, off,
+                  lds_addr(&lds_stage[w][vv][h][0][0]));
     }
 }
 
@@ -362,13 +351,10 @@ __device__ __forceinline__ void fetch_state(const BwdArgs& A, int w, int c,
     const bf16_t* base =
         A.ckpt + (int64_t(c / M) * A.BH + int64_t(blockIdx.x)) * NN;
     const int ldu = lane & 7, ldseg = lane >> 3;
+    const uint32_t off = uint32_t(ldu * WN + 8 * ldseg) * sizeof(bf16_t);
 #pragma unroll
     for (int g = 0; g < 8; ++g)
-        __builtin_amdgcn_global_load_lds(
-            (const void __attribute__((address_space(1)))*)(
-                base + ((8 * g + ldu) * WN + 8 * ldseg)),
-            (void __attribute__((address_space(3)))*)(&lds_S[w][512 * g]),
-            16, 0, 0);
+        dma16(base + 8 * g * WN, off, lds_addr(&lds_S[w][512 * g]));
 }
 
 // The T layout read of vector vv from worker w's stage: token lr, columns
@@ -432,11 +418,20 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         const int64_t t0 = int64_t(c) * WL;
         const int n = int(T - t0 < WL ? T - t0 : WL);
         const bool valid = lr < n;
+        // this chunk's rows of the token-major outputs: the lanes of tokens
+        // past the end (lr >= n) store at or past obytes, dropped
+        const int64_t gbase = t0 * A.lay.ts + hoff;
+        const uint32_t obytes = (uint32_t(n - 1) * TS + WN) * 2;
         const bool starts = c % m == 0;  // S_0 is checkpoint c / m
         const bool feeds = c % m != m - 1 && c + 1 < nch;  // S_0 of c + 1
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): vectors (and S_0)
+        // the vectors: issued before the start state's 8 loads (when the
+        // chunk starts an interval), whose wait comes only before S_0's first
+        // use (vector memory operations complete in issue order)
+        if (starts)
+            __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8)
+        else
+            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
         asm volatile("" ::: "memory");
-        if (starts && lane == 0) lds_store(&fl.s_ready[w], c);
 
         uint2 raw[7][4];
 #pragma unroll
@@ -593,6 +588,17 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             kMinvT = kq(dM);
         }
 
+        // the start state: since its loads, only the next chunk's 14 vector
+        // loads (if any) were issued
+        if (starts) {
+            if (cn >= 0)
+                __builtin_amdgcn_s_waitcnt(0x0f7e);  // vmcnt(14)
+            else
+                __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+            asm volatile("" ::: "memory");
+            if (lane == 0) lds_store(&fl.s_ready[w], c);
+        }
+
         // ---- W^ = Minv A^, Q^ = R~ 2^{g_ref} + Arb W^ (J layout); the map -
         if (wait_for(A.wait, &fl.map_taken[w], lane,
                      [&](int x) { return x >= NCHAIN * kord; }) <= 0)
@@ -687,7 +693,6 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                     sd_write4(Sn, 16 * ib + lr, 16 * jpb + 4 * lq, pack4(acc));
                 }
             }
-            fence_sched();
         }
         if (feeds) {
             lds_drain();
@@ -700,6 +705,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                      [&](int x) { return x >= NCHAIN * (kord + 1); }) <= 0)
             break;
         const bf16x8_t Khp0 = pk8(tKh[0], tKh[1]), Khp1 = pk8(tKh[2], tKh[3]);
+        const __amdgpu_buffer_rsrc_t rs_dv = out_rsrc(A.dv + gbase, obytes);
         i16x4_t kdUT[4];
 #pragma unroll
         for (int ib = 0; ib < 4; ++ib) {
@@ -725,11 +731,8 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) dv[e] += dv16[e];
             // lane: dV[t0 + lr][16 ib + 4 lq + e]
-            if (valid)
-                *reinterpret_cast<uint2*>(
-                    (A.dv + (t0 * A.lay.ts + hoff)) +
-                    (uint32_t(lr) * TS + 16 * ib + 4 * lq)) = pack4(dv);
-            fence_sched();
+            store8(rs_dv, (uint32_t(lr) * TS + 16 * ib + 4 * lq) * 2,
+                   pack4(dv));
         }
 
         // ---- cotangents of the 16 x 16 matrices (K = 64 over i) -----------
@@ -770,8 +773,12 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         // ---- per column block: dR~, dA~, dB~, dK~ and the input gradients -
         // (tiles of the transposes: lane holds token lr, columns
         // 16 jb + 4 lq + e, the T layout)
-        const uint32_t goff = uint32_t(lr) * TS + 4 * lq;
-        const int64_t gbase = t0 * A.lay.ts + hoff;
+        const uint32_t goff = (uint32_t(lr) * TS + 4 * lq) * 2;
+        const __amdgpu_buffer_rsrc_t rs_dr = out_rsrc(A.dr + gbase, obytes),
+                                     rs_dw = out_rsrc(A.dw + gbase, obytes),
+                                     rs_dk = out_rsrc(A.dk + gbase, obytes),
+                                     rs_da = out_rsrc(A.da + gbase, obytes),
+                                     rs_db = out_rsrc(A.db + gbase, obytes);
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
             const f32x4_t er = *reinterpret_cast<const f32x4_t*>(
@@ -846,15 +853,12 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 const float sc = scan16(f1 - fA[e] * gA[e]);
                 dwv[e] = (sc - f1 + tail[e]) * lam;  // dlog d * (-e^w)
             }
-            if (valid) {
-                const uint32_t o = goff + 16 * jb;
-                *reinterpret_cast<uint2*>((A.dr + gbase) + o) = pack4(drv);
-                *reinterpret_cast<uint2*>((A.dw + gbase) + o) = pack4(dwv);
-                *reinterpret_cast<uint2*>((A.dk + gbase) + o) = pack4(dkv);
-                *reinterpret_cast<uint2*>((A.da + gbase) + o) = pack4(dav);
-                *reinterpret_cast<uint2*>((A.db + gbase) + o) = pack4(dbv);
-            }
-            fence_sched();
+            const uint32_t o = goff + 32 * jb;
+            store8(rs_dr, o, pack4(drv));
+            store8(rs_dw, o, pack4(dwv));
+            store8(rs_dk, o, pack4(dkv));
+            store8(rs_da, o, pack4(dav));
+            store8(rs_db, o, pack4(dbv));
         }
 
         // ---- release the buffers; the next chunk's start state ------------

@@ -213,6 +213,48 @@ __device__ __forceinline__ f32x4_t mask4(f32x4_t x, int r, int q, bool strict,
     return x;
 }
 
+// LDS DMA (global_load_lds_dwordx4): lane l's 16 bytes at gbase + voff (a
+// byte offset) land at LDS byte address lds + 16 l; gbase and lds are
+// wave-uniform.  Written as inline assembly so that the compiler does not
+// treat every later LDS access as a possible reader of the DMA's data (it
+// would wait for all outstanding vector memory operations, this load's and
+// every earlier store's, before each one): the caller orders the data's
+// use with explicit vmcnt waits.  M0 is set in the same statement; no other
+// code of these kernels uses it.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* gbase, uint32_t voff,
+                                      uint32_t lds) {
+    asm volatile(
+        "s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+        :
+        : "v"(voff), "s"(gbase), "s"(lds)
+        : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// A raw buffer resource over `bytes` bytes at `base`: stores through it at
+// byte offsets at or past `bytes` are dropped by the hardware, so masked
+// lanes need no branch.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t out_rsrc(void* base,
+                                                         uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(base, 0, int(bytes), 0x00020000);
+}
+
+// 8 bytes at byte offset `off` of the buffer.
+__device__ __forceinline__ void store8(__amdgpu_buffer_rsrc_t rs, uint32_t off,
+                                       uint2 v) {
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    const u32x2_t x = {v.x, v.y};
+    __builtin_amdgcn_raw_buffer_store_b64(x, rs, int(off), 0, 0);
+}
+
+// The LDS byte address of a __shared__ object.
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(const T* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
 // Hand-over words in LDS are read and written as relaxed workgroup-scope
 // atomics: a volatile access would also make the wave wait for all its
 // outstanding global stores.  Ordering against the data they guard comes

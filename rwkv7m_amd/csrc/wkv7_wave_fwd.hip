@@ -10,20 +10,21 @@
 // below (g = running log2-decay, g_ref its value at token 7; A~, R~, B~, K~
 // the decayed factors of wkv7_wave_bwd.hip),
 //
-//   S_L = S_0 diag(2^{g_L}) + bf16(S_0) M^ + C,   Y^T = bf16(S_0) Q^^T + P^T
+//   X = W^ bf16(S_0)^T + U,   S_L = S_0 diag(2^{g_L}) + X^T B^ + V^T K^,
+//   Y^T = bf16(S_0) Q^^T + P^T
 //
-// with M^ = diag(2^{g_ref}) W^T B^ and Q^ = diag(2^{g_ref}) (R~ + Arb W)^T
-// depending on the chunk's key-side vectors only, and C = U^T B^ + V^T K^,
+// with W^ = Minv A~ diag(2^{g_ref}) and Q^ = diag(2^{g_ref}) (R~ + Arb W)^T
+// depending on the chunk's key-side vectors only, and U = Minv Aak V,
 // P = Arb U + Ark V linear in the value rows.
 //
 // One workgroup of 12 waves per (batch, head):
 //   * waves 4..11, the producers: producer p builds chunks p, p + 8, ...:
-//     the decayed factors, the 16 x 16 matrices, the inverse, W, U, M^ and
-//     Q^, all in registers, and hands them to a ring of three LDS slots;
+//     the decayed factors, the 16 x 16 matrices, the inverse, W^, U and Q^,
+//     all in registers, and hands them to a ring of three LDS slots;
 //   * waves 0..3, the chains: chain ib holds rows 16 ib .. 16 ib + 15 of the
 //     fp32 state in registers for the whole sequence and, chunk after
-//     chunk, takes the slot, forms its rows of C and P, advances its rows
-//     (8 MFMAs) and writes its rows of y.
+//     chunk, takes the slot, forms its rows of X (2 MFMAs), advances its
+//     rows (8 MFMAs) and forms its rows of y (stored one chunk later).
 // The four chains run independent recurrences; each one's step per chunk is
 // short, so the kernel runs at the producers' rate.
 //
@@ -75,7 +76,7 @@ union ProdStage {
 // One chunk's hand-over from a producer to the chains, as register images
 // (element [..][lane] is that lane's operand).
 struct Slot {
-    bf16x8_t M[4][2][64];  // A operands of M^^T: tiles (2jp, j'b), (2jp+1, j'b)
+    bf16x8_t W[2][64];     // A operands of W^ (T layout pairs, K = 64)
     bf16x8_t Q[2][64];     // B operands of Q^^T: tiles 2jp, 2jp + 1
     i16x4_t B[4][64];      // B^ (J layout)
     i16x4_t K[4][64];      // K^ (J layout)
@@ -120,7 +121,7 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
     const int64_t bh = blockIdx.x;
     const int64_t hoff = A.lay.head(bh, WN);
     const int64_t T = A.T;
-    const int64_t nch = (T + WL - 1) / WL;
+    const int nch = int((T + WL - 1) / WL);
     const uint32_t TS = uint32_t(A.lay.ts);
     const VecPtrs src{A.r, A.w, A.k, A.v, A.a, A.b, nullptr};
     ProdStage& stg = sm.st[p];
@@ -133,21 +134,17 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
     // of load (vector, h) fetches segment l / 8 of token 8h + l % 8.  Tokens
     // past the end re-read the last token (zeroed when read).
     const int ldu = lane & 7, ldseg = lane >> 3;
-    auto fetch = [&](int64_t c) {
-        const int64_t cbase = c * WL * A.lay.ts + hoff;
-        const int n = int(T - c * WL < WL ? T - c * WL : WL);
+    auto fetch = [&](int c) {
+        const int64_t cbase = int64_t(c) * WL * A.lay.ts + hoff;
+        const int n = int(T - int64_t(c) * WL < WL ? T - int64_t(c) * WL : WL);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int t = 8 * h + ldu;
-            const uint32_t off = uint32_t(t < n ? t : n - 1) * TS + 8 * ldseg;
+            const uint32_t off = (uint32_t(t < n ? t : n - 1) * TS +
+                                  8 * ldseg) * sizeof(bf16_t);
 #pragma unroll
             for (int vv = 0; vv < 6; ++vv)
-                __builtin_amdgcn_global_load_lds(
-                    (const void __attribute__((address_space(1)))*)(
-                        (src.get(vv) + cbase) + off),
-                    (void __attribute__((address_space(3)))*)(
-                        &stg.raw[vv][h][0][0]),
-                    16, 0, 0);
+                dma16(src.get(vv) + cbase, off, lds_addr(&stg.raw[vv][h][0][0]));
         }
     };
     // the T layout read of vector vv: token lr, columns 16 kb + 4 lq .. + 3
@@ -160,8 +157,8 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
     };
     if (p < nch) fetch(p);
 
-    for (int64_t c = p; c < nch; c += NPROD) {
-        const int n = int(T - c * WL < WL ? T - c * WL : WL);
+    for (int c = p; c < nch; c += NPROD) {
+        const int n = int(T - int64_t(c) * WL < WL ? T - int64_t(c) * WL : WL);
         const bool valid = lr < n;
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this chunk's vectors
         asm volatile("" ::: "memory");
@@ -294,6 +291,7 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
 
         // ---- products over the chunk (K = 16) ------------------------------
         const i16x4_t kMinv = kq(dMT);  // A operand: Minv
+        const i16x4_t kMinvB = kMinv;   // B operand: Minv^T
         const i16x4_t kAak = kq(mAakT), kArbT = kq(mArbT),
                       kArkT = kq(mArkT);
         wave_lds_fence();
@@ -305,6 +303,11 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
             jK[jb] = read_j(xp[2], jb, lane);
             jV[jb] = read_j(xp[3], jb, lane);
         }
+        // the stage is free once these reads are done: the next chunk's
+        // vectors load during the rest of this one
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        asm volatile("" ::: "memory");
+        if (c + NPROD < nch) fetch(c + NPROD);
 
         // 2^{g_ref} of column 16 jb + lr (W's columns in the J layout) and
         // of rows 16 jb + 4 lq + e (the T layout): folded into W and R~, so
@@ -341,34 +344,27 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
             kQ[jb] = kq(x);
         }
 
-        // M^ = (W diag(2^{g_ref}))^T B^ : D(M^_{jb, j'b}), as the chains'
-        // A operands (tiles 2jp, 2jp + 1 of column block j'b)
-        bf16x8_t M8[4][2];
+        // W^ = W diag(2^{g_ref}) in the T layout, D(W^T_kb) = A~_kb^T
+        // Minv^T scaled per column: the chains' A operands of W^ bf16(S_0)^T
+        i16x4_t wt[4];
 #pragma unroll
-        for (int jpb = 0; jpb < 4; ++jpb) {
-            i16x4_t m4[4];
+        for (int kb = 0; kb < 4; ++kb) {
+            f32x4_t x = zero4();
+            mfma16(x, jA[kb], kMinvB);
 #pragma unroll
-            for (int jb = 0; jb < 4; ++jb) {
-                f32x4_t x = zero4();
-                mfma16(x, kW[jb], jB[jpb]);
-                m4[jb] = kq(x);
-            }
-            M8[jpb][0] = pk8(m4[0], m4[1]);
-            M8[jpb][1] = pk8(m4[2], m4[3]);
+            for (int e = 0; e < 4; ++e) x[e] *= ert[kb][e];
+            wt[kb] = kq(x);
         }
 
         // ---- hand the chunk to the chains ---------------------------------
-        const int s = int(c % NSLOT);
-        const int uses = int(c / NSLOT);  // earlier uses of this slot
+        const int s = c % NSLOT;
+        const int uses = c / NSLOT;  // earlier uses of this slot
         if (!poll(vdone + s, A.wait.limit,
                   [&](int d) { return d >= NCHAIN * uses; }))
             wait_failed(&sm.failed, A.wait.failures, lane);
         Slot& sl = sm.slot[s];
-#pragma unroll
-        for (int jpb = 0; jpb < 4; ++jpb) {
-            sl.M[jpb][0][lane] = M8[jpb][0];
-            sl.M[jpb][1][lane] = M8[jpb][1];
-        }
+        sl.W[0][lane] = pk8(wt[0], wt[1]);
+        sl.W[1][lane] = pk8(wt[2], wt[3]);
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
             sl.B[jb][lane] = jB[jb];
@@ -386,10 +382,7 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
         if (lane == 0) sl.exact = exact ? 1 : 0;
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
         asm volatile("" ::: "memory");
-        if (lane == 0) lds_store(vready + s, int(c));
-        // the producer's next chunk: its loads are issued only now, so that
-        // no wait on them delays a hand-over (producers have time to spare)
-        if (c + NPROD < nch) fetch(c + NPROD);
+        if (lane == 0) lds_store(vready + s, c);
     }
 }
 
@@ -402,7 +395,7 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
     const int64_t sbase = bh * WN * WN;
     const int64_t hoff = A.lay.head(bh, WN);
     const int64_t T = A.T;
-    const int64_t nch = (T + WL - 1) / WL;
+    const int nch = int((T + WL - 1) / WL);
     const int64_t NN = WN * WN;
     const uint32_t TS = uint32_t(A.lay.ts);
     int* const vready = sm.ready;
@@ -421,94 +414,93 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
     // loads complete here, no wait for those stores lands inside the loop
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
 
-    for (int64_t c = 0; c < nch; ++c) {
-        const int64_t t0 = c * WL;
+    // running counters instead of divisions by the slot count and the
+    // checkpoint stride: the ring slot of chunk c, c modulo the stride, and
+    // the element offset of checkpoint c / stride
+    int s = 0, cph = 0;
+    int64_t ckoff = sbase;
+    // y of the previous chunk, stored one iteration late (its products are
+    // complete by then): rows of chunk yc (yc < 0: none pending)
+    f32x4_t ypend = zero4();
+    int yc = -1;
+    auto store_y = [&](int cc, const f32x4_t& yy) {
+        const int64_t ty = int64_t(cc) * WL;
+        const int ny = int(T - ty < WL ? T - ty : WL);
+        // lanes of tokens past the end store at or past the bound: dropped
+        const __amdgpu_buffer_rsrc_t rs = out_rsrc(
+            A.y + (ty * A.lay.ts + hoff), (uint32_t(ny - 1) * TS + WN) * 2);
+        store8(rs, (uint32_t(lr) * TS + 16 * ib + 4 * lq) * 2, pack4(yy));
+    };
+    for (int c = 0; c < nch; ++c) {
+        const int64_t t0 = int64_t(c) * WL;
         const int n = int(T - t0 < WL ? T - t0 : WL);
-
-        // per-lane store offsets, recomputed in every iteration rather than
-        // kept as 64-bit addresses across the loop
-        uint32_t yoff = uint32_t(lr) * TS + 16 * ib + 4 * lq;
-        uint32_t coff = uint32_t(row) * WN + 4 * lq;
-        asm volatile("" : "+v"(yoff), "+v"(coff));
 
         // bf16(S_0): the operand of the state step and checkpoint c
         i16x4_t sb[4];
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) sb[jb] = kq(S[jb]);
         const bf16x8_t Sb0 = pk8(sb[0], sb[1]), Sb1 = pk8(sb[2], sb[3]);
+        if (A.ckpt && cph == 0) {
+            // rows 16 ib .. + 15 of checkpoint c / stride
+            const uint32_t coff = uint32_t(row) * WN + 4 * lq;
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb)
+                *reinterpret_cast<i16x4_t*>((A.ckpt + ckoff) +
+                                            (coff + 16 * jb)) = sb[jb];
+        }
+        if (yc >= 0) store_y(yc, ypend);
+        yc = -1;
 
-        const int s = int(c % NSLOT);
         if (!poll(vready + s, A.wait.limit,
-                  [&](int x) { return x == int(c); }))
+                  [&](int x) { return x == c; }))
             wait_failed(&sm.failed, A.wait.failures, lane);
         const Slot& sl = sm.slot[s];
-        bf16x8_t M[4][2], Q[2];
-        i16x4_t B[4], K[4];
-        f32x4_t eL[4];
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb) {
-            M[jb][0] = sl.M[jb][0][lane];
-            M[jb][1] = sl.M[jb][1][lane];
-            B[jb] = sl.B[jb][lane];
-            K[jb] = sl.K[jb][lane];
-            eL[jb] = *reinterpret_cast<const f32x4_t*>(&sl.eL[16 * jb + 4 * lq]);
-        }
-        Q[0] = sl.Q[0][lane];
-        Q[1] = sl.Q[1][lane];
-        const i16x4_t U = sl.U[ib][lane], V = sl.V[ib][lane];
-        const i16x4_t Arb = sl.Arb[lane], Ark = sl.Ark[lane];
         const int exact = __builtin_amdgcn_readfirstlane(sl.exact);
-        // the slot's data is in registers: release it to the producers
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-        asm volatile("" ::: "memory");
-        if (lane == 0)
-            __hip_atomic_fetch_add(&sm.done[s], 1, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+        // the slot's data is read as the step uses it; the slot goes back
+        // to the producers once every read has completed
+        auto release = [&]() {
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            asm volatile("" ::: "memory");
+            if (lane == 0)
+                __hip_atomic_fetch_add(&sm.done[s], 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
+        };
 
         if (!exact) {
-            // S_L^T = S_0^T diag(2^{g_L}) + C^T + M^^T bf16(S_0)^T, rows of
-            // block ib; C^T_{j'b, ib} = B^^T U + K^^T V
+            // X^T_ib = W^ bf16(S_0)^T + U (rows of block ib, as D(X_ib)),
+            // then S_L^T = S_0^T diag(2^{g_L}) + B^^T X + K^^T V
+            f32x4_t xt = unpack4(__builtin_bit_cast(uint2, sl.U[ib][lane]));
+            mfma(xt, sl.W[0][lane], Sb0);
+            mfma(xt, sl.W[1][lane], Sb1);
+            const i16x4_t X = kq(xt), V = sl.V[ib][lane];
 #pragma unroll
             for (int jpb = 0; jpb < 4; ++jpb) {
-                f32x4_t cc = zero4();
-                mfma16(cc, B[jpb], U);
-                mfma16(cc, K[jpb], V);
+                const f32x4_t eL = *reinterpret_cast<const f32x4_t*>(
+                    &sl.eL[16 * jpb + 4 * lq]);
                 f32x4_t acc;
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    acc[e] = S[jpb][e] * eL[jpb][e] + cc[e];
-                mfma(acc, M[jpb][0], Sb0);
-                mfma(acc, M[jpb][1], Sb1);
+                for (int e = 0; e < 4; ++e) acc[e] = S[jpb][e] * eL[e];
+                mfma16(acc, sl.B[jpb][lane], X);
+                mfma16(acc, sl.K[jpb][lane], V);
                 S[jpb] = acc;
             }
-            // Y^T_ib = bf16(S_0) Q^^T + U^T Arb^T + V^T Ark^T, stored as
-            // y[t][16 ib + 4 lq ..]
+            const i16x4_t U = sl.U[ib][lane];
+            const bf16x8_t Q0 = sl.Q[0][lane], Q1 = sl.Q[1][lane];
+            const i16x4_t Arb = sl.Arb[lane], Ark = sl.Ark[lane];
+            // Y^T_ib = bf16(S_0) Q^^T + U^T Arb^T + V^T Ark^T, lane:
+            // y[t0 + lr][16 ib + 4 lq ..] (stored in the next iteration)
             f32x4_t pp = zero4();
             mfma16(pp, U, Arb);
             mfma16(pp, V, Ark);
             f32x4_t yy = zero4();
-            mfma(yy, Sb0, Q[0]);
-            mfma(yy, Sb1, Q[1]);
+            mfma(yy, Sb0, Q0);
+            mfma(yy, Sb1, Q1);
+            release();
 #pragma unroll
-            for (int e = 0; e < 4; ++e) yy[e] += pp[e];
-            if (lr < n)
-                *reinterpret_cast<uint2*>((A.y + (t0 * A.lay.ts + hoff)) +
-                                          yoff) = pack4(yy);
-            if (A.ckpt && c % A.cstride == 0) {
-#pragma unroll
-                for (int jb = 0; jb < 4; ++jb)
-                    *reinterpret_cast<i16x4_t*>(
-                        (A.ckpt + ((c / A.cstride) * A.BH * NN + sbase)) +
-                        (coff + 16 * jb)) = sb[jb];
-            }
+            for (int e = 0; e < 4; ++e) ypend[e] = yy[e] + pp[e];
+            yc = c;
         } else {
-            if (A.ckpt && c % A.cstride == 0) {
-#pragma unroll
-                for (int jb = 0; jb < 4; ++jb)
-                    *reinterpret_cast<i16x4_t*>(
-                        (A.ckpt + ((c / A.cstride) * A.BH * NN + sbase)) +
-                        (coff + 16 * jb)) = sb[jb];
-            }
+            release();
             // exact fp32 sequential pass over the chunk for the rows of
             // block ib (a chunk outside the factored form's range, far
             // beyond the model's clamped decays): sums over the lane's 16
@@ -541,7 +533,13 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
                 if (lq == 0) A.y[off + row] = to_bf16(acc);
             }
         }
+        s = s + 1 == NSLOT ? 0 : s + 1;
+        if (++cph == A.cstride) {
+            cph = 0;
+            ckoff += A.BH * NN;
+        }
     }
+    if (yc >= 0) store_y(yc, ypend);
 
     // final state (fp32) and the last checkpoint
 #pragma unroll
@@ -597,7 +595,9 @@ wkv7_wave_fwd_kernel(FwdArgs A) {
         chain(A, sm, wv, lane);
     else
         produce(A, sm, wv - NCHAIN, lane);
-    // every wait is bounded, so every wave arrives here
+    // every wait is bounded, so every wave arrives here (with no LDS DMA
+    // in flight)
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (lds_load(&sm.failed) != 0) poison(A, tid);
 }

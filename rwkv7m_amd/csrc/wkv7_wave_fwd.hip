@@ -88,13 +88,20 @@ struct Slot {
     int exact;             // the chunk needs the exact sequential pass
 };
 
+// Checkpoints on their way from the chains to global memory: two buffers of
+// bf16 rows (pitch XPITCH), used in turn.  The chains write their rows in
+// their register layout; a producer stores whole rows, 16 bytes per lane.
+typedef bf16_t CkBuf[WN][XPITCH];
+
 struct WaveFwdSmem {
     Slot slot[NSLOT];
+    CkBuf ck[2];
     ProdStage st[NPROD];
     float eref[NPROD][WN];  // per producer: 2^{g_ref} per column
     float eL[NPROD][WN];    // per producer: 2^{g_L} per column
     int ready[NSLOT];       // chunk held by the slot (-1: none yet)
     int done[NSLOT];        // chains finished with the slot, over all uses
+    int ck_done[2];         // checkpoints stored from each buffer so far
     int failed;             // a bounded wait of this workgroup gave up
 };
 
@@ -110,6 +117,7 @@ struct FwdArgs {
     float* s_t;
     bf16_t* ckpt;  // nullptr, or bf16 checkpoints every cstride chunks
     int cstride;   // checkpoint interval / 16
+    int cshift;    // log2(cstride)
     WaitCfg wait;
 };
 
@@ -362,6 +370,24 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
         if (!poll(vdone + s, A.wait.limit,
                   [&](int d) { return d >= NCHAIN * uses; }))
             wait_failed(&sm.failed, A.wait.failures, lane);
+        // the chains staged checkpoint (c - NSLOT) / stride before releasing
+        // this slot after chunk c - NSLOT: store it, then free its buffer
+        const int cc = c - NSLOT;
+        if (A.ckpt && cc >= 0 && (cc & (A.cstride - 1)) == 0) {
+            const int k = cc >> A.cshift;
+            const int b = k & 1;
+            bf16_t* const dst =
+                A.ckpt + (int64_t(k) * A.BH + bh) * (WN * WN) +
+                ((lane >> 3) * WN + 8 * (lane & 7));
+#pragma unroll
+            for (int g = 0; g < 8; ++g)
+                *reinterpret_cast<uint4*>(dst + 8 * g * WN) =
+                    *reinterpret_cast<const uint4*>(
+                        &sm.ck[b][8 * g + (lane >> 3)][8 * (lane & 7)]);
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): reads done
+            asm volatile("" ::: "memory");
+            if (lane == 0) lds_add(&sm.ck_done[b], 1);
+        }
         Slot& sl = sm.slot[s];
         sl.W[0][lane] = pk8(wt[0], wt[1]);
         sl.W[1][lane] = pk8(wt[2], wt[3]);
@@ -417,7 +443,7 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
     // running counters instead of divisions by the slot count and the
     // checkpoint stride: the ring slot of chunk c, c modulo the stride, and
     // the element offset of checkpoint c / stride
-    int s = 0, cph = 0;
+    int s = 0, cph = 0, kck = 0;
     int64_t ckoff = sbase;
     // y of the previous chunk, stored one iteration late (its products are
     // complete by then): rows of chunk yc (yc < 0: none pending)
@@ -441,12 +467,27 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
         for (int jb = 0; jb < 4; ++jb) sb[jb] = kq(S[jb]);
         const bf16x8_t Sb0 = pk8(sb[0], sb[1]), Sb1 = pk8(sb[2], sb[3]);
         if (A.ckpt && cph == 0) {
-            // rows 16 ib .. + 15 of checkpoint c / stride
-            const uint32_t coff = uint32_t(row) * WN + 4 * lq;
+            // rows 16 ib .. + 15 of checkpoint kck = c / stride.  While a
+            // producer has a later chunk (c + NSLOT) to hand over, it stores
+            // the checkpoint from buffer kck % 2 (this slot's release
+            // publishes the rows); the last ones are stored here
+            if (c + NSLOT < nch) {
+                const int b = kck & 1, u = kck >> 1;
+                if (!poll(&sm.ck_done[b], A.wait.limit,
+                          [&](int x) { return x >= u; }))
+                    wait_failed(&sm.failed, A.wait.failures, lane);
 #pragma unroll
-            for (int jb = 0; jb < 4; ++jb)
-                *reinterpret_cast<i16x4_t*>((A.ckpt + ckoff) +
-                                            (coff + 16 * jb)) = sb[jb];
+                for (int jb = 0; jb < 4; ++jb)
+                    *reinterpret_cast<i16x4_t*>(
+                        &sm.ck[b][row][16 * jb + 4 * lq]) = sb[jb];
+            } else {
+                const uint32_t coff = uint32_t(row) * WN + 4 * lq;
+#pragma unroll
+                for (int jb = 0; jb < 4; ++jb)
+                    *reinterpret_cast<i16x4_t*>((A.ckpt + ckoff) +
+                                                (coff + 16 * jb)) = sb[jb];
+            }
+            ++kck;
         }
         if (yc >= 0) store_y(yc, ypend);
         yc = -1;
@@ -589,6 +630,7 @@ wkv7_wave_fwd_kernel(FwdArgs A) {
         sm.ready[tid] = -1;
         sm.done[tid] = 0;
     }
+    if (tid < 2) sm.ck_done[tid] = 0;
     if (tid == 0) sm.failed = 0;
     __syncthreads();
     if (wv < NCHAIN)
@@ -623,6 +665,7 @@ hipError_t launch_wave_forward(const ChunkFwdArgs& p, hipStream_t stream) {
     A.s_t = p.s_t;
     A.ckpt = static_cast<bf16_t*>(p.ckpt);
     A.cstride = p.L / WL;
+    A.cshift = A.cstride == 4 ? 2 : A.cstride == 2 ? 1 : 0;
     A.wait = p.wait;
     if (A.BH <= 0) return hipSuccess;
     hipLaunchKernelGGL(wkv7_wave_fwd_kernel, dim3(unsigned(A.BH)),

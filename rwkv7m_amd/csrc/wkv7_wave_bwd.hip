@@ -442,11 +442,16 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         // the stage is free: the next chunk's vectors load during this one
         if (cn >= 0) fetch_vecs(A, w, cn, lane);
         if (n < WL) {
+            // padding tokens: zero vectors and w = -inf (bf16), so that
+            // they decay by nothing
 #pragma unroll
-            for (int vv = 0; vv < 7; ++vv)
+            for (int vv = 0; vv < 7; ++vv) {
+                const uint2 pad = vv == 1 ? make_uint2(0xff80ff80u, 0xff80ff80u)
+                                          : make_uint2(0, 0);
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb)
-                    raw[vv][kb] = valid ? raw[vv][kb] : make_uint2(0, 0);
+                    raw[vv][kb] = valid ? raw[vv][kb] : pad;
+            }
         }
 
         // ---- factors (T layout) ------------------------------------------
@@ -463,8 +468,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             f32x4_t sp4, lr4, fA, fR, fB, fK, eh, bh4, kh4;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float ew = __builtin_amdgcn_exp2f(
-                    valid ? wr[e] * kLog2e : -__builtin_inff());
+                const float ew = __builtin_amdgcn_exp2f(wr[e] * kLog2e);
                 const float g = scan16(-ew * kLog2e);
                 g4[kb][e] = g;
                 const float gref = row_bcast<7>(g), gL = row_bcast<15>(g);
@@ -779,37 +783,49 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                                      rs_dk = out_rsrc(A.dk + gbase, obytes),
                                      rs_da = out_rsrc(A.da + gbase, obytes),
                                      rs_db = out_rsrc(A.db + gbase, obytes);
+        // the products over i of column block jb, issued one block ahead
+        // of their use: their latency is hidden by the previous block's
+        // element-wise work
+        struct Acc4 {
+            f32x4_t R, A, B, K;
+        };
+        auto products = [&](int jb) {
+            Acc4 g;
+            g.R = g.A = g.B = g.K = zero4();
+            const bf16x8_t s0 = frag_cols(S, jb, 0, lane);
+            const bf16x8_t s1 = frag_cols(S, jb, 1, lane);
+            mfma(g.R, s0, dYp[0]);  // S_0^T dY^T
+            mfma(g.R, s1, dYp[1]);
+            mfma(g.A, s0, dUp[0]);  // S_0^T dU^T
+            mfma(g.A, s1, dUp[1]);
+            const bf16x8_t d0 = frag_cols(D, jb, 0, lane);
+            const bf16x8_t d1 = frag_cols(D, jb, 1, lane);
+            mfma(g.B, d0, Xp[0]);   // D^T X^T
+            mfma(g.B, d1, Xp[1]);
+            mfma(g.K, d0, Vp[0]);   // D^T V^T
+            mfma(g.K, d1, Vp[1]);
+            return g;
+        };
+        Acc4 cur = products(0);
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
             const f32x4_t er = *reinterpret_cast<const f32x4_t*>(
                 &lds_eref[w][16 * jb + 4 * lq]);
             const f32x4_t elr = *reinterpret_cast<const f32x4_t*>(
                 &lds_eLR[w][16 * jb + 4 * lq]);
+            f32x4_t tl[NCHAIN];
+#pragma unroll
+            for (int ch = 0; ch < NCHAIN; ++ch)
+                tl[ch] = *reinterpret_cast<const f32x4_t*>(
+                    &lds_tail[w][ch][16 * jb + 4 * lq]);
+            Acc4 nxt;
+            if (jb < 3) nxt = products(jb + 1);
             f32x4_t tail = zero4();
 #pragma unroll
-            for (int ch = 0; ch < NCHAIN; ++ch) {
-                const f32x4_t x = *reinterpret_cast<const f32x4_t*>(
-                    &lds_tail[w][ch][16 * jb + 4 * lq]);
+            for (int ch = 0; ch < NCHAIN; ++ch)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) tail[e] += x[e];
-            }
-            f32x4_t gR = zero4(), gA = zero4(), gB = zero4(), gK = zero4();
-            {
-                const bf16x8_t s0 = frag_cols(S, jb, 0, lane);
-                const bf16x8_t s1 = frag_cols(S, jb, 1, lane);
-                mfma(gR, s0, dYp[0]);  // S_0^T dY^T
-                mfma(gR, s1, dYp[1]);
-                mfma(gA, s0, dUp[0]);  // S_0^T dU^T
-                mfma(gA, s1, dUp[1]);
-            }
-            {
-                const bf16x8_t d0 = frag_cols(D, jb, 0, lane);
-                const bf16x8_t d1 = frag_cols(D, jb, 1, lane);
-                mfma(gB, d0, Xp[0]);   // D^T X^T
-                mfma(gB, d1, Xp[1]);
-                mfma(gK, d0, Vp[0]);   // D^T V^T
-                mfma(gK, d1, Vp[1]);
-            }
+                for (int e = 0; e < 4; ++e) tail[e] += tl[ch][e];
+            f32x4_t gR = cur.R, gA = cur.A, gB = cur.B, gK = cur.K;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 gR[e] *= er[e];
@@ -859,6 +875,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             store8(rs_dk, o, pack4(dkv));
             store8(rs_da, o, pack4(dav));
             store8(rs_db, o, pack4(dbv));
+            if (jb < 3) cur = nxt;
         }
 
         // ---- release the buffers; the next chunk's start state ------------

@@ -175,11 +175,12 @@ __device__ __forceinline__ i16x4_t as_i16x4(uint2 u) {
     return __builtin_bit_cast(i16x4_t, u);
 }
 
-// Value of lane n of each 16-lane row, in every lane of the row.
+// Value of lane n of each 16-lane row, in every lane of the row (every
+// lane reads a valid source, so no old value is needed).
 template <int N>
 __device__ __forceinline__ float row_bcast(float x) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(
-        0, __float_as_int(x), 0x150 + N, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x),
+                                                   0x150 + N, 0xF, 0xF, true));
 }
 
 // The previous lane's value within each row; the row's first lane keeps

@@ -176,11 +176,16 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) raw[vv][kb] = read_t(vv, kb);
         if (n < WL) {
+            // padding tokens: zero vectors and w = -inf (bf16), so that
+            // they decay by nothing
 #pragma unroll
-            for (int vv = 0; vv < 6; ++vv)
+            for (int vv = 0; vv < 6; ++vv) {
+                const uint2 pad = vv == 1 ? make_uint2(0xff80ff80u, 0xff80ff80u)
+                                          : make_uint2(0, 0);
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb)
-                    raw[vv][kb] = valid ? raw[vv][kb] : make_uint2(0, 0);
+                    raw[vv][kb] = valid ? raw[vv][kb] : pad;
+            }
         }
 
         // ---- factors (T layout, fp32) --------------------------------------
@@ -196,8 +201,7 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
             f32x4_t sLR, sp4;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float ew = __builtin_amdgcn_exp2f(
-                    valid ? wr[e] * kLog2e : -__builtin_inff());
+                const float ew = __builtin_amdgcn_exp2f(wr[e] * kLog2e);
                 const float g = scan16(-ew * kLog2e);
                 const float gref = row_bcast<7>(g), gL = row_bcast<15>(g);
                 lo = fminf(lo, fminf(gref, gL - gref));

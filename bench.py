@@ -99,12 +99,30 @@ def measured_traffic(kernel, config, chunk, layout="tbhn"):
     return None
 
 
+def mfma_diagnostic(kernel, config, chunk):
+    """MFMA utilisation of ``kernel`` from the committed rocprofv3 counter
+    run (profiles/mfma_util.json), or None if none matches."""
+    path = os.path.join(ROOT, "profiles", "mfma_util.json")
+    try:
+        with open(path) as f:
+            rows = json.load(f)["measurements"]
+    except (OSError, ValueError, KeyError):
+        return None
+    for row in rows:
+        if (row.get("kernel") == kernel and row.get("config") == config
+                and row.get("chunk") == chunk):
+            return {"tflops": row["mfma_tflops"], "util": row["mfma_util"],
+                    "busy": row["mfma_busy"],
+                    "peak_tflops": 2500.0,
+                    "source": "profiles/mfma_util.json (rocprofv3 --pmc)"}
+    return None
+
+
 def cpu_threads():
-    """(threads used, CPUs in this process's affinity set).  The threads are
-    the affinity set, capped at 16: the GPU boxes give one GPU a 16-CPU
-    share whatever the affinity mask shows."""
+    """(threads used, CPUs in this process's affinity set): the thread pool
+    is pinned to the affinity set, one thread per CPU in it."""
     cpus = len(os.sched_getaffinity(0))
-    return min(cpus, 16), cpus
+    return cpus, cpus
 
 
 def timing_summary(samples_ms):
@@ -136,8 +154,9 @@ def per_call_timing(fn, iters, warmup=3):
 
 def cpu_baseline(cfg, target_s):
     """Time the CPU restatement (oracle, fp32, OpenMP over (b, h)) on the
-    config's (B, H, N): a reduced T chosen to take about ``target_s``, or
-    the full T repeated until ``target_s`` has passed."""
+    config's (B, H, N) the reference's way (one warmup, then synchronised
+    iterations, median; forward and forward+backward separately), at a
+    reduced T chosen so that the iterations take about ``target_s``."""
     import numpy as np
 
     import oracle
@@ -147,6 +166,7 @@ def cpu_baseline(cfg, target_s):
     B, H, N = cfg["B"], cfg["H"], cfg["N"]
 
     def run(T):
+        """(forward seconds, backward seconds) of one iteration."""
         inp = make_inputs(T, B, H, N, dtype=cfg["dtype"], seed=7,
                           state_std=cfg.get("state_std", 0.0),
                           dstate_std=cfg.get("dstate_std", 0.0),
@@ -155,27 +175,32 @@ def cpu_baseline(cfg, target_s):
         vecs = [arrs[n] for n in ("r", "w", "k", "v", "neg_kk", "kka")]
         t0 = time.perf_counter()
         oracle.forward(*vecs, arrs["s0"], precision="f32", threads=threads)
+        t1 = time.perf_counter()
         oracle.backward(*vecs, arrs["s0"], arrs["dy"], arrs["ds_t"],
                         precision="f32", threads=threads)
-        return time.perf_counter() - t0
+        return t1 - t0, time.perf_counter() - t1
 
+    import statistics
     probe_T = 16
-    dt = run(probe_T)
-    T = int(max(probe_T, min(cfg["T"], probe_T * target_s / max(dt, 1e-6))))
-    reps, dt = 0, 0.0
-    while reps == 0 or dt < 0.8 * target_s:
-        dt += run(T)
-        reps += 1
+    dt = sum(run(probe_T))
+    # one warmup and three timed iterations in about target_s
+    T = int(max(probe_T,
+                min(cfg["T"], probe_T * target_s / 4 / max(dt, 1e-6))))
+    run(T)
+    iters = [run(T) for _ in range(3)]
+    fwd = statistics.median(f for f, _ in iters)
+    step = statistics.median(f + b for f, b in iters)
     return {
-        "value": reps * B * T / dt,
+        "value": B * T / step,
         "unit": "tokens/s",
+        "forward_tokens_per_s": B * T / fwd,
         "cores": threads,
-        "affinity_cpus": cpus,
+        "threads": threads,
         "kind": "port",
-        "sample": (f"fp32 C restatement of the reference scan fwd+bwd, "
-                   f"B={B} T={T} H={H} N={N}, {reps} run(s), {dt:.1f} s "
-                   f"on {threads} threads ({cpus} CPUs in the affinity "
-                   f"set)"),
+        "sample": (f"fp32 C restatement of the reference scan, B={B} T={T} "
+                   f"H={H} N={N}: 1 warmup + 3 iterations, median fwd+bwd "
+                   f"{step:.2f} s (fwd {fwd:.2f} s), one thread per CPU of "
+                   f"the affinity set ({cpus})"),
     }
 
 
@@ -831,6 +856,7 @@ def main():
                                         args.layout),
             "algorithmic_bytes": dom_bytes,
             "avg_ms": dom_ms,
+            "mfma": mfma_diagnostic(dominant, args.config, ci),
         },
         "kernels_ms": {"forward": fwd_ms, "backward": bwd_ms},
         "step_roofline_frac": step_gbs / HBM_PEAK_GBS,

@@ -51,6 +51,8 @@ def _check(name, got, expected, case, tol=TOL):
 
 
 def _run_case(hip, inp, ci, case, check_grads=True):
+    """ci is passed to the library as is (0: its default); the checks use
+    the interval in effect."""
     dev = {k: v.cuda() for k, v in inp.items()}
     vecs = [dev[n] for n in NAMES]
     (y, s_t), aux = hip.forward_with_aux(*vecs, dev["s0"],
@@ -62,10 +64,11 @@ def _run_case(hip, inp, ci, case, check_grads=True):
         paths.append(hip.last_path())
     torch.cuda.synchronize()
     hip.device_status()
-    assert tuple(paths) == expected_paths(ci)[:len(paths)], (case, paths)
+    eff = ci or hip.default_checkpoint_interval(torch.bfloat16, 64)
+    assert tuple(paths) == expected_paths(eff)[:len(paths)], (case, paths)
     host = [_np(inp[n]) for n in NAMES]
     ey, es, eck = oracle.forward(*host, _np(inp["s0"]),
-                                 checkpoint_interval=ci, threads=THREADS)
+                                 checkpoint_interval=eff, threads=THREADS)
     assert y.dtype == torch.bfloat16 and s_t.dtype == torch.float32
     _check("y", y, ey, case)
     _check("s_t", s_t, es, case)
@@ -73,7 +76,7 @@ def _run_case(hip, inp, ci, case, check_grads=True):
     # MFMA interval): S0 and S_T rounded to nearest even
     cdt = hip.checkpoint_dtype(torch.bfloat16, 64, ci)
     assert aux[0].dtype == cdt
-    if ci in MFMA_INTERVALS:
+    if eff in MFMA_INTERVALS:
         assert cdt == torch.bfloat16
     _check("checkpoints", aux[0], eck, case)
     assert torch.equal(aux[0][0], dev["s0"].to(cdt))
@@ -149,11 +152,14 @@ def test_chunked_plain_forward_and_in_place_state(hip):
 
 
 def test_config1_forward_backward_default_path(hip):
-    # config 1 in full on the library's default (MFMA) path
-    case = "config 1: B8 T512 H12 N64 bf16 L32"
-    print("case:", case, flush=True)
+    # config 1 in full on the library's default (MFMA) path, interval 0
+    # (the library default, 16), and at interval 32
+    assert hip.default_checkpoint_interval(torch.bfloat16, 64) == 16
     inp = config_inputs(1)
-    _run_case(hip, inp, 32, case)
+    for ci in (0, 32):
+        case = f"config 1: B8 T512 H12 N64 bf16 L{ci or 'default'}"
+        print("case:", case, flush=True)
+        _run_case(hip, inp, ci, case)
 
 
 def test_config1_forward_backward_sequential_kernels(hip):

@@ -275,7 +275,7 @@ def test_library_host_queries(lib):
     assert lib.rwkv7m_wkv7_checkpoint_count(4096, 32) == 129
     assert lib.rwkv7m_wkv7_checkpoint_count(-1, 16) == -1
     assert lib.rwkv7m_wkv7_checkpoint_count(5, 0) == -1
-    assert lib.rwkv7m_wkv7_default_checkpoint_interval(1, 64) == 32
+    assert lib.rwkv7m_wkv7_default_checkpoint_interval(1, 64) == 16
     assert lib.rwkv7m_wkv7_default_checkpoint_interval(0, 64) == 16
     # bf16 checkpoints exactly for the MFMA-served intervals
     for ci in (0, 16, 32, 64):

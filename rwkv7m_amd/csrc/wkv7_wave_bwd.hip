@@ -68,7 +68,6 @@ constexpr int NCHAIN = 4;
 constexpr int NWORK = 4;
 constexpr int BTHREADS = 64 * (NCHAIN + NWORK);
 constexpr int NN = WN * WN;
-constexpr float kLn2 = 0.6931471805599453f;
 
 // Element (i, j) of a 64 x 64 bf16 S/D buffer: 16-byte unit (i, j / 8) at
 // ((i / 8) * 8 + j / 8) * 8 + i % 8, so one global_load_lds of 64 lanes
@@ -117,7 +116,7 @@ __device__ __forceinline__ bf16x8_t frag_cols(const bf16_t* buf, int cb,
 // A chunk's hand-over from its worker to the chains, as register images
 // (element [..][lane] is that lane's operand).
 struct BMap {
-    bf16x8_t Bh[2][64];  // B^ (T layout pairs): x32 A operands (m = t, k = j)
+    bf16x8_t Bh[2][64];  // B~ (T layout pairs): x32 A operands (m = t, k = j)
     i16x4_t W[4][64];    // D(W^_jb)
     i16x4_t Q[4][64];    // D(Q^_jb)
     i16x4_t dY[4][64];   // D(dY_ib)
@@ -223,14 +222,26 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
         const int c = nch - 1 - p;
         const int w = p % NWORK, kord = p / NWORK;
 
-        // bf16(D): the step's operand and the worker's D buffer
-        i16x4_t sb[4];
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb) sb[jb] = kq(Dt[jb]);
+        // the chunk's map (its per-column factors are in LDS by then)
         if (wait_for(A.wait, &fl.d_done[w], lane,
-                     [&](int x) { return x >= kord; }) <= 0) {
+                     [&](int x) { return x >= kord; }) <= 0 ||
+            wait_for(A.wait, &fl.map_ready[w], lane,
+                     [&](int x) { return x >= kord + 1; }) <= 0) {
             done = false;
             break;
+        }
+        // bf16(D diag(2^{g_L - g_ref})): the step's operand and the
+        // worker's D buffer (folding the per-column factor in here takes it
+        // out of every product of D with B~ and K~)
+        i16x4_t sb[4];
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            const f32x4_t elr = *reinterpret_cast<const f32x4_t*>(
+                &lds_eLR[w][16 * jb + 4 * lq]);
+            f32x4_t x;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = Dt[jb][e] * elr[e];
+            sb[jb] = kq(x);
         }
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb)
@@ -238,13 +249,6 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
                       __builtin_bit_cast(uint2, sb[jb]));
         lds_drain();
         if (lane == 0) lds_add(&fl.d_cnt[w], 1);
-
-        // the chunk's map
-        if (wait_for(A.wait, &fl.map_ready[w], lane,
-                     [&](int x) { return x >= kord + 1; }) <= 0) {
-            done = false;
-            break;
-        }
         const BMap& mp = lds_map[w];
         const bf16x8_t Bh0 = mp.Bh[0][lane], Bh1 = mp.Bh[1][lane];
         i16x4_t Wt[4], Qt[4];
@@ -260,7 +264,7 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
         lds_drain();
         if (lane == 0) lds_add(&fl.map_taken[w], 1);
 
-        // Z = B^ bf16(D)^T ([t][i]), then
+        // Z = B~ bf16(D diag(2^{g_L - g_ref}))^T = B^ D^T ([t][i]), then
         // D_0^T = 2^{g_L} D^T + Q^^T dY + W^^T Z (rows of block ib)
         f32x4_t z = zero4();
         mfma(z, Bh0, pk8(sb[0], sb[1]));
@@ -457,20 +461,23 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         // ---- factors (T layout) ------------------------------------------
         // lam = log2 d_t, g its running sum over the chunk, g_ref = g at
         // token 7, g_L = g at token 15 (padding tokens decay by nothing)
-        i16x4_t tA[4], tR[4], tB[4], tK[4], tAh[4], tBh[4], tKh[4];
-        f32x4_t g4[4];  // g, kept for the input gradients
+        i16x4_t tA[4], tR[4], tB[4], tK[4], tAh[4];
+        // kept for the input gradients: 2^{g_t - g_ref}, 2^{g_ref - g_t},
+        // 2^{g_{t-1} - g_ref} (bf16) and -e^w (the decay gradient's factor)
+        i16x4_t keg[4], keng[4], kep[4];
+        f32x4_t lam4[4];
         float lo = 0.f;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
             const f32x4_t wr = unpack4(raw[1][kb]);
             const f32x4_t ar = unpack4(raw[4][kb]), br = unpack4(raw[5][kb]);
             const f32x4_t rr = unpack4(raw[0][kb]), kr = unpack4(raw[2][kb]);
-            f32x4_t sp4, lr4, fA, fR, fB, fK, eh, bh4, kh4;
+            f32x4_t sp4, lr4, fA, fR, fB, fK, eh, eg4, eng4, ep4;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float ew = __builtin_amdgcn_exp2f(wr[e] * kLog2e);
                 const float g = scan16(-ew * kLog2e);
-                g4[kb][e] = g;
+                lam4[kb][e] = -ew;
                 const float gref = row_bcast<7>(g), gL = row_bcast<15>(g);
                 lo = fminf(lo, fminf(gref, gL - gref));
                 const float dg = g - gref;
@@ -481,6 +488,9 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 const float sp = __builtin_amdgcn_exp2f(
                     lr == 0 ? -gref : lr == 1 ? gref : gL);
                 const float eprev = row_prev(eg, sp);
+                eg4[e] = eg;
+                eng4[e] = eng;
+                ep4[e] = eprev;
                 sp4[e] = sp;
                 const float sLR = pin_lanes(row_bcast<15>(eg));
                 lr4[e] = sLR;
@@ -489,16 +499,15 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 fB[e] = br[e] * eng;
                 fK[e] = kr[e] * eng;
                 eh[e] = fA[e] * pin_lanes(row_bcast<1>(sp));
-                bh4[e] = fB[e] * sLR;
-                kh4[e] = fK[e] * sLR;
             }
             tA[kb] = kq(fA);
             tR[kb] = kq(fR);
             tB[kb] = kq(fB);
             tK[kb] = kq(fK);
             tAh[kb] = kq(eh);
-            tBh[kb] = kq(bh4);
-            tKh[kb] = kq(kh4);
+            keg[kb] = kq(eg4);
+            keng[kb] = kq(eng4);
+            kep[kb] = kq(ep4);
             if (lr == 1)
                 *reinterpret_cast<f32x4_t*>(&lds_eref[w][16 * kb + 4 * lq]) =
                     sp4;
@@ -622,7 +631,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             map.W[jb][lane] = kW;
             map.Q[jb][lane] = kq(y);
         }
-        const bf16x8_t Bhp0 = pk8(tBh[0], tBh[1]), Bhp1 = pk8(tBh[2], tBh[3]);
+        const bf16x8_t Bhp0 = pk8(tB[0], tB[1]), Bhp1 = pk8(tB[2], tB[3]);
         map.Bh[0][lane] = Bhp0;
         map.Bh[1][lane] = Bhp1;
         i16x4_t jdY[4];
@@ -704,11 +713,13 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         }
 
         // ---- D arrives: dX = B^ D^T + Arb^T dY, dU = Minv^T dX (J and T),
-        // dV^T = D K^^T + dY^T Ark + dU^T Aak ---------------------------------
+        // dV^T = D K^^T + dY^T Ark + dU^T Aak.  The buffer holds
+        // D' = bf16(D diag(2^{g_L - g_ref})), so B^ D^T = B~ D'^T and
+        // K^ D^T = K~ D'^T -------------------------------------------------
         if (wait_for(A.wait, &fl.d_cnt[w], lane,
                      [&](int x) { return x >= NCHAIN * (kord + 1); }) <= 0)
             break;
-        const bf16x8_t Khp0 = pk8(tKh[0], tKh[1]), Khp1 = pk8(tKh[2], tKh[3]);
+        const bf16x8_t Khp0 = pk8(tK[0], tK[1]), Khp1 = pk8(tK[2], tK[3]);
         const __amdgpu_buffer_rsrc_t rs_dv = out_rsrc(A.dv + gbase, obytes);
         i16x4_t kdUT[4];
 #pragma unroll
@@ -800,9 +811,9 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             mfma(g.A, s1, dUp[1]);
             const bf16x8_t d0 = frag_cols(D, jb, 0, lane);
             const bf16x8_t d1 = frag_cols(D, jb, 1, lane);
-            mfma(g.B, d0, Xp[0]);   // D^T X^T
+            mfma(g.B, d0, Xp[0]);   // D'^T X^T = (D^T X^T) 2^{g_L - g_ref}
             mfma(g.B, d1, Xp[1]);
-            mfma(g.K, d0, Vp[0]);   // D^T V^T
+            mfma(g.K, d0, Vp[0]);   // D'^T V^T
             mfma(g.K, d1, Vp[1]);
             return g;
         };
@@ -811,8 +822,6 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         for (int jb = 0; jb < 4; ++jb) {
             const f32x4_t er = *reinterpret_cast<const f32x4_t*>(
                 &lds_eref[w][16 * jb + 4 * lq]);
-            const f32x4_t elr = *reinterpret_cast<const f32x4_t*>(
-                &lds_eLR[w][16 * jb + 4 * lq]);
             f32x4_t tl[NCHAIN];
 #pragma unroll
             for (int ch = 0; ch < NCHAIN; ++ch)
@@ -830,8 +839,6 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             for (int e = 0; e < 4; ++e) {
                 gR[e] *= er[e];
                 gA[e] *= er[e];
-                gB[e] *= elr[e];
-                gK[e] *= elr[e];
             }
             const i16x4_t jA = to_j(tA[jb], kI), jB = to_j(tB[jb], kI);
             const i16x4_t jK = to_j(tK[jb], kI), jR = to_j(tR[jb], kI);
@@ -850,24 +857,18 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             // f1 - A~ dA~ (f1 = B~ dB~ + K~ dK~ - R~ dR~)
             const f32x4_t fA = unpack_i16(tA[jb]), fR = unpack_i16(tR[jb]);
             const f32x4_t fB = unpack_i16(tB[jb]), fK = unpack_i16(tK[jb]);
+            const f32x4_t eg = unpack_i16(keg[jb]), eng = unpack_i16(keng[jb]);
+            const f32x4_t ep = unpack_i16(kep[jb]);
             f32x4_t drv, dwv, dkv, dav, dbv;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float g = g4[jb][e];
-                const float gref = row_bcast<7>(g);
-                const float eg = __builtin_amdgcn_exp2f(g - gref);
-                const float eng = __builtin_amdgcn_exp2f(gref - g);
-                const float e0 = __builtin_amdgcn_exp2f(-gref);
-                const float eprev = row_prev(eg, e0);
-                // -e^w = (g_t - g_{t-1}) ln 2
-                const float lam = (g - row_prev(g, 0.f)) * kLn2;
-                drv[e] = gR[e] * eg;
-                dav[e] = gA[e] * eprev;
-                dbv[e] = gB[e] * eng;
-                dkv[e] = gK[e] * eng;
+                drv[e] = gR[e] * eg[e];
+                dav[e] = gA[e] * ep[e];
+                dbv[e] = gB[e] * eng[e];
+                dkv[e] = gK[e] * eng[e];
                 const float f1 = fB[e] * gB[e] + fK[e] * gK[e] - fR[e] * gR[e];
                 const float sc = scan16(f1 - fA[e] * gA[e]);
-                dwv[e] = (sc - f1 + tail[e]) * lam;  // dlog d * (-e^w)
+                dwv[e] = (sc - f1 + tail[e]) * lam4[jb][e];  // dlog d (-e^w)
             }
             const uint32_t o = goff + 32 * jb;
             store8(rs_dr, o, pack4(drv));

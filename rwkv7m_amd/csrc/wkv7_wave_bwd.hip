@@ -428,13 +428,22 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         const uint32_t obytes = (uint32_t(n - 1) * TS + WN) * 2;
         const bool starts = c % m == 0;  // S_0 is checkpoint c / m
         const bool feeds = c % m != m - 1 && c + 1 < nch;  // S_0 of c + 1
-        // the vectors: issued before the start state's 8 loads (when the
-        // chunk starts an interval), whose wait comes only before S_0's first
-        // use (vector memory operations complete in issue order)
-        if (starts)
-            __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8)
-        else
-            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+        // the vectors.  Vector memory operations complete in issue order, and
+        // since the vectors' loads this worker issued the previous chunk's 24
+        // gradient stores (4 of dv, 20 of the column blocks) and, when this
+        // chunk starts an interval, its start state's 8 loads, whose wait
+        // comes only before S_0's first use
+        if (kord == 0) {
+            if (starts)
+                __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8)
+            else
+                __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+        } else {
+            if (starts)
+                __builtin_amdgcn_s_waitcnt(0x8f70);  // vmcnt(32)
+            else
+                __builtin_amdgcn_s_waitcnt(0x4f78);  // vmcnt(24)
+        }
         asm volatile("" ::: "memory");
 
         uint2 raw[7][4];
@@ -601,17 +610,6 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             kMinvT = kq(dM);
         }
 
-        // the start state: since its loads, only the next chunk's 14 vector
-        // loads (if any) were issued
-        if (starts) {
-            if (cn >= 0)
-                __builtin_amdgcn_s_waitcnt(0x0f7e);  // vmcnt(14)
-            else
-                __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-            asm volatile("" ::: "memory");
-            if (lane == 0) lds_store(&fl.s_ready[w], c);
-        }
-
         // ---- W^ = Minv A^, Q^ = R~ 2^{g_ref} + Arb W^ (J layout); the map -
         if (wait_for(A.wait, &fl.map_taken[w], lane,
                      [&](int x) { return x >= NCHAIN * kord; }) <= 0)
@@ -644,10 +642,18 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         if (lane == 0) lds_store(&fl.map_ready[w], kord + 1);
 
         // ---- U = A^ S_0^T + Aak V, X = Minv U ------------------------------
-        if (!starts) {
-            if (wait_for(A.wait, &fl.s_ready[w], lane,
-                         [&](int x) { return x == c; }) <= 0)
-                break;
+        if (starts) {
+            // the start state: since its loads, only the next chunk's 14
+            // vector loads (if any) were issued
+            if (cn >= 0)
+                __builtin_amdgcn_s_waitcnt(0x0f7e);  // vmcnt(14)
+            else
+                __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+            asm volatile("" ::: "memory");
+            if (lane == 0) lds_store(&fl.s_ready[w], c);
+        } else if (wait_for(A.wait, &fl.s_ready[w], lane,
+                            [&](int x) { return x == c; }) <= 0) {
+            break;
         }
         // the next chunk's start state, S_L = S_0 2^{g_L} + X^T B^ + V^T K^,
         // goes to the worker of chunk c + 1 (tiles of S_L^T, formed per i

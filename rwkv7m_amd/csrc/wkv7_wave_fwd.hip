@@ -23,10 +23,13 @@
 //     all in registers, and hands them to a ring of three LDS slots;
 //   * waves 0..3, the chains: chain ib holds rows 16 ib .. 16 ib + 15 of the
 //     fp32 state in registers for the whole sequence and, chunk after
-//     chunk, takes the slot, forms its rows of X (2 MFMAs), advances its
-//     rows (8 MFMAs) and forms its rows of y (stored one chunk later).
-// The four chains run independent recurrences; each one's step per chunk is
-// short, so the kernel runs at the producers' rate.
+//     chunk, forms its rows of X (2 MFMAs), advances its rows (8 MFMAs),
+//     forms its rows of y (4 MFMAs) and stores them with its rows of the
+//     checkpoint when one is due.  A chain reads a chunk's operands from
+//     the slot while the previous chunk's products run, so that its step
+//     waits on no LDS read.
+// The four chains run independent recurrences; the kernel runs at the
+// producers' rate.
 //
 // Register layouts (lane l, r = l % 16, q = l / 16).  A 16 x 16 accumulator
 // tile D(X) holds X[4q + e][r] (e = 0..3).  As operands of
@@ -88,24 +91,21 @@ struct Slot {
     int exact;             // the chunk needs the exact sequential pass
 };
 
-// Checkpoints on their way from the chains to global memory: two buffers of
-// bf16 rows (pitch XPITCH), used in turn.  The chains write their rows in
-// their register layout; a producer stores whole rows, 16 bytes per lane.
-typedef bf16_t CkBuf[WN][XPITCH];
+// A chain's 16 rows of a checkpoint on their way to global memory: written
+// in the chain's register layout, read back as whole rows (16 bytes per
+// lane) and stored one chunk later.  Each chain uses only its own rows.
+typedef bf16_t CkRows[16][XPITCH];
 
 struct WaveFwdSmem {
     Slot slot[NSLOT];
-    CkBuf ck[2];
+    CkRows ck[NCHAIN];
     ProdStage st[NPROD];
     float eref[NPROD][WN];  // per producer: 2^{g_ref} per column
     float eL[NPROD][WN];    // per producer: 2^{g_L} per column
     int ready[NSLOT];       // chunk held by the slot (-1: none yet)
     int done[NSLOT];        // chains finished with the slot, over all uses
-    int ck_done[2];         // checkpoints stored from each buffer so far
     int failed;             // a bounded wait of this workgroup gave up
 };
-
-
 
 
 struct FwdArgs {
@@ -374,24 +374,6 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
         if (!poll(vdone + s, A.wait.limit,
                   [&](int d) { return d >= NCHAIN * uses; }))
             wait_failed(&sm.failed, A.wait.failures, lane);
-        // the chains staged checkpoint (c - NSLOT) / stride before releasing
-        // this slot after chunk c - NSLOT: store it, then free its buffer
-        const int cc = c - NSLOT;
-        if (A.ckpt && cc >= 0 && (cc & (A.cstride - 1)) == 0) {
-            const int k = cc >> A.cshift;
-            const int b = k & 1;
-            bf16_t* const dst =
-                A.ckpt + (int64_t(k) * A.BH + bh) * (WN * WN) +
-                ((lane >> 3) * WN + 8 * (lane & 7));
-#pragma unroll
-            for (int g = 0; g < 8; ++g)
-                *reinterpret_cast<uint4*>(dst + 8 * g * WN) =
-                    *reinterpret_cast<const uint4*>(
-                        &sm.ck[b][8 * g + (lane >> 3)][8 * (lane & 7)]);
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): reads done
-            asm volatile("" ::: "memory");
-            if (lane == 0) lds_add(&sm.ck_done[b], 1);
-        }
         Slot& sl = sm.slot[s];
         sl.W[0][lane] = pk8(wt[0], wt[1]);
         sl.W[1][lane] = pk8(wt[2], wt[3]);
@@ -444,11 +426,35 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
     // loads complete here, no wait for those stores lands inside the loop
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
 
-    // running counters instead of divisions by the slot count and the
-    // checkpoint stride: the ring slot of chunk c, c modulo the stride, and
-    // the element offset of checkpoint c / stride
-    int s = 0, cph = 0, kck = 0;
-    int64_t ckoff = sbase;
+    // A chunk's operands, read from its slot at the end of the previous
+    // chunk's step, while that step's products run
+    struct SlotRegs {
+        bf16x8_t W0, W1, Q0, Q1;
+        i16x4_t U, V, Arb, Ark, B[4], K[4];
+        f32x4_t eL[4];
+        int exact;
+    };
+    auto take = [&](int c, int s, SlotRegs& r) {
+        if (!poll(vready + s, A.wait.limit, [&](int x) { return x == c; }))
+            wait_failed(&sm.failed, A.wait.failures, lane);
+        const Slot& sl = sm.slot[s];
+        r.exact = __builtin_amdgcn_readfirstlane(sl.exact);
+        r.W0 = sl.W[0][lane];
+        r.W1 = sl.W[1][lane];
+        r.U = sl.U[ib][lane];
+        r.V = sl.V[ib][lane];
+#pragma unroll
+        for (int jpb = 0; jpb < 4; ++jpb) {
+            r.B[jpb] = sl.B[jpb][lane];
+            r.K[jpb] = sl.K[jpb][lane];
+            r.eL[jpb] = *reinterpret_cast<const f32x4_t*>(
+                &sl.eL[16 * jpb + 4 * lq]);
+        }
+        r.Q0 = sl.Q[0][lane];
+        r.Q1 = sl.Q[1][lane];
+        r.Arb = sl.Arb[lane];
+        r.Ark = sl.Ark[lane];
+    };
     // y of the previous chunk, stored one iteration late (its products are
     // complete by then): rows of chunk yc (yc < 0: none pending)
     f32x4_t ypend = zero4();
@@ -461,91 +467,94 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
             A.y + (ty * A.lay.ts + hoff), (uint32_t(ny - 1) * TS + WN) * 2);
         store8(rs, (uint32_t(lr) * TS + 16 * ib + 4 * lq) * 2, pack4(yy));
     };
+    // this chain's rows of a checkpoint, staged in the previous iteration,
+    // as whole rows: lane l stores 16-byte units l and l + 64 (row u / 8,
+    // columns 8 (u % 8) ..) at element offset ckp (ckp < 0: none pending)
+    CkRows& ckr = sm.ck[ib];
+    int64_t ckp = -1;
+    auto store_ck = [&]() {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int u = lane + 64 * k;
+            *reinterpret_cast<uint4*>(A.ckpt + ckp + (16 * ib + (u >> 3)) * WN +
+                                      8 * (u & 7)) =
+                *reinterpret_cast<const uint4*>(&ckr[u >> 3][8 * (u & 7)]);
+        }
+    };
+
+    // running counters instead of divisions by the slot count and the
+    // checkpoint stride: the slot of chunk c, c modulo the stride, and the
+    // element offset of checkpoint c / stride
+    int s = 0, cph = 0;
+    int64_t ckoff = sbase;
+    SlotRegs cur;
+    if (nch > 0) take(0, 0, cur);
     for (int c = 0; c < nch; ++c) {
         const int64_t t0 = int64_t(c) * WL;
         const int n = int(T - t0 < WL ? T - t0 : WL);
+        const int exact = cur.exact;
 
-        // bf16(S_0): the operand of the state step and checkpoint c
+        // bf16(S_0): the operand of the state step and of y, and the
+        // checkpoint's rows
         i16x4_t sb[4];
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) sb[jb] = kq(S[jb]);
         const bf16x8_t Sb0 = pk8(sb[0], sb[1]), Sb1 = pk8(sb[2], sb[3]);
-        if (A.ckpt && cph == 0) {
-            // rows 16 ib .. + 15 of checkpoint kck = c / stride.  While a
-            // producer has a later chunk (c + NSLOT) to hand over, it stores
-            // the checkpoint from buffer kck % 2 (this slot's release
-            // publishes the rows); the last ones are stored here
-            if (c + NSLOT < nch) {
-                const int b = kck & 1, u = kck >> 1;
-                if (!poll(&sm.ck_done[b], A.wait.limit,
-                          [&](int x) { return x >= u; }))
-                    wait_failed(&sm.failed, A.wait.failures, lane);
-#pragma unroll
-                for (int jb = 0; jb < 4; ++jb)
-                    *reinterpret_cast<i16x4_t*>(
-                        &sm.ck[b][row][16 * jb + 4 * lq]) = sb[jb];
-            } else {
-                const uint32_t coff = uint32_t(row) * WN + 4 * lq;
-#pragma unroll
-                for (int jb = 0; jb < 4; ++jb)
-                    *reinterpret_cast<i16x4_t*>((A.ckpt + ckoff) +
-                                                (coff + 16 * jb)) = sb[jb];
-            }
-            ++kck;
-        }
-        if (yc >= 0) store_y(yc, ypend);
-        yc = -1;
-
-        if (!poll(vready + s, A.wait.limit,
-                  [&](int x) { return x == c; }))
-            wait_failed(&sm.failed, A.wait.failures, lane);
-        const Slot& sl = sm.slot[s];
-        const int exact = __builtin_amdgcn_readfirstlane(sl.exact);
-        // the slot's data is read as the step uses it; the slot goes back
-        // to the producers once every read has completed
-        auto release = [&]() {
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-            asm volatile("" ::: "memory");
-            if (lane == 0)
-                __hip_atomic_fetch_add(&sm.done[s], 1, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_WORKGROUP);
-        };
-
         if (!exact) {
             // X^T_ib = W^ bf16(S_0)^T + U (rows of block ib, as D(X_ib)),
             // then S_L^T = S_0^T diag(2^{g_L}) + B^^T X + K^^T V
-            f32x4_t xt = unpack4(__builtin_bit_cast(uint2, sl.U[ib][lane]));
-            mfma(xt, sl.W[0][lane], Sb0);
-            mfma(xt, sl.W[1][lane], Sb1);
-            const i16x4_t X = kq(xt), V = sl.V[ib][lane];
+            f32x4_t xt = unpack4(__builtin_bit_cast(uint2, cur.U));
+            mfma(xt, cur.W0, Sb0);
+            mfma(xt, cur.W1, Sb1);
+            const i16x4_t X = kq(xt);
 #pragma unroll
             for (int jpb = 0; jpb < 4; ++jpb) {
-                const f32x4_t eL = *reinterpret_cast<const f32x4_t*>(
-                    &sl.eL[16 * jpb + 4 * lq]);
                 f32x4_t acc;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[e] = S[jpb][e] * eL[e];
-                mfma16(acc, sl.B[jpb][lane], X);
-                mfma16(acc, sl.K[jpb][lane], V);
+                for (int e = 0; e < 4; ++e)
+                    acc[e] = S[jpb][e] * cur.eL[jpb][e];
+                mfma16(acc, cur.B[jpb], X);
+                mfma16(acc, cur.K[jpb], cur.V);
                 S[jpb] = acc;
             }
-            const i16x4_t U = sl.U[ib][lane];
-            const bf16x8_t Q0 = sl.Q[0][lane], Q1 = sl.Q[1][lane];
-            const i16x4_t Arb = sl.Arb[lane], Ark = sl.Ark[lane];
+        }
+        if (yc >= 0) store_y(yc, ypend);
+        yc = -1;
+        if (ckp >= 0) store_ck();
+        ckp = -1;
+        if (A.ckpt && cph == 0) {
+            // rows 16 ib .. + 15 of checkpoint c / stride (the reads of the
+            // previous one, above, precede these writes)
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb)
+                *reinterpret_cast<i16x4_t*>(&ckr[lr][16 * jb + 4 * lq]) =
+                    sb[jb];
+            ckp = ckoff;
+        }
+        if (!exact) {
             // Y^T_ib = bf16(S_0) Q^^T + U^T Arb^T + V^T Ark^T, lane:
             // y[t0 + lr][16 ib + 4 lq ..] (stored in the next iteration)
-            f32x4_t pp = zero4();
-            mfma16(pp, U, Arb);
-            mfma16(pp, V, Ark);
-            f32x4_t yy = zero4();
-            mfma(yy, Sb0, Q0);
-            mfma(yy, Sb1, Q1);
-            release();
+            f32x4_t pp = zero4(), yy = zero4();
+            mfma16(pp, cur.U, cur.Arb);
+            mfma16(pp, cur.V, cur.Ark);
+            mfma(yy, Sb0, cur.Q0);
+            mfma(yy, Sb1, cur.Q1);
 #pragma unroll
             for (int e = 0; e < 4; ++e) ypend[e] = yy[e] + pp[e];
             yc = c;
-        } else {
-            release();
+        }
+        // the slot goes back to the producers once its reads have completed
+        lds_drain();
+        if (lane == 0)
+            __hip_atomic_fetch_add(&sm.done[s], 1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+        s = s + 1 == NSLOT ? 0 : s + 1;
+        if (++cph == A.cstride) {
+            cph = 0;
+            ckoff += A.BH * NN;
+        }
+        if (c + 1 < nch) take(c + 1, s, cur);
+        if (exact) {
             // exact fp32 sequential pass over the chunk for the rows of
             // block ib (a chunk outside the factored form's range, far
             // beyond the model's clamped decays): sums over the lane's 16
@@ -578,13 +587,9 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
                 if (lq == 0) A.y[off + row] = to_bf16(acc);
             }
         }
-        s = s + 1 == NSLOT ? 0 : s + 1;
-        if (++cph == A.cstride) {
-            cph = 0;
-            ckoff += A.BH * NN;
-        }
     }
     if (yc >= 0) store_y(yc, ypend);
+    if (ckp >= 0) store_ck();
 
     // final state (fp32) and the last checkpoint
 #pragma unroll
@@ -634,7 +639,7 @@ wkv7_wave_fwd_kernel(FwdArgs A) {
         sm.ready[tid] = -1;
         sm.done[tid] = 0;
     }
-    if (tid < 2) sm.ck_done[tid] = 0;
+
     if (tid == 0) sm.failed = 0;
     __syncthreads();
     if (wv < NCHAIN)

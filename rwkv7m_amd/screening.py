@@ -100,7 +100,10 @@ class ScreeningConfig:
         for hl in (self.short_half_life_tokens, self.mid_half_life_tokens,
                    self.long_half_life_tokens):
             if hl is not None and hl <= 0.0:
-                raise ValueError("half-life values must be positive")
+                raise ValueError(
+                    "memory half-life values must be positive when provided")
+        if not 0.0 <= self.usage_ema_decay < 1.0:
+            raise ValueError("usage_ema_decay must be in [0, 1)")
 
 
 class ScreenState(NamedTuple):
@@ -245,7 +248,8 @@ class StateLevelScreening(torch.nn.Module):
     """NNXStateLevelScreening's parameters (nnx_model.py:885-999, linear
     kernels in the flax ``[in, out]`` layout) and its read-only call."""
 
-    def __init__(self, config: ScreeningConfig, *, compute_dtype=None,
+    def __init__(self, config: ScreeningConfig, *,
+                 compute_dtype=torch.float32,
                  param_dtype=torch.float32, device=None, seed: int = 0):
         super().__init__()
         self.config = config

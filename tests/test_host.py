@@ -472,3 +472,29 @@ def test_screening_write_abi_checks_requests_before_any_device_call(lib):
     assert bwd(1, 2, 8, 4, 128, 64, *ins, 0.05, 1e-6, *cots, None,
                *no_dpre, None) == 1
     assert b"d_pre is NULL" in lib.rwkv7m_last_error()
+
+
+def test_screening_config_checks_follow_the_reference():
+    """ScreeningConfig.__post_init__ rejects what the reference's does, with
+    its messages (src/rwkv7m/model/screening.py:124-140), and the module's
+    compute dtype defaults to float32 as NNXStateLevelScreening's does."""
+    from rwkv7m_amd.screening import ScreeningConfig, StateLevelScreening
+    base = dict(d_model=16, d_slot=8, d_k=4, d_v=4, n_slots=2)
+    for bad in (1.0, -0.1, 1.5):
+        with pytest.raises(ValueError, match=r"usage_ema_decay must be in "
+                                             r"\[0, 1\)"):
+            ScreeningConfig(**base, usage_ema_decay=bad)
+    ScreeningConfig(**base, usage_ema_decay=0.0)
+    for field in ("short_half_life_tokens", "mid_half_life_tokens",
+                  "long_half_life_tokens"):
+        with pytest.raises(ValueError, match="memory half-life values must "
+                                             "be positive when provided"):
+            ScreeningConfig(**base, **{field: 0.0})
+    with pytest.raises(ValueError, match="bank_ids must have length n_slots"):
+        ScreeningConfig(**base, bank_ids=(0,))
+    with pytest.raises(ValueError, match="bank_ids values must be only"):
+        ScreeningConfig(**base, bank_ids=(0, 3))
+    with pytest.raises(ValueError, match="write_rel_floor must be"):
+        ScreeningConfig(**base, write_rel_floor=-1.0)
+    mod = StateLevelScreening(ScreeningConfig(**base))
+    assert mod.compute_dtype == torch.float32

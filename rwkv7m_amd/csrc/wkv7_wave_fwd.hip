@@ -88,7 +88,6 @@ struct Slot {
     i16x4_t Arb[64];       // D(Arb^T)
     i16x4_t Ark[64];       // D(Ark^T)
     float eL[WN];          // 2^{g_L} per column
-    int exact;             // the chunk needs the exact sequential pass
 };
 
 // A chain's 16 rows of a checkpoint on their way to global memory: written
@@ -102,7 +101,9 @@ struct WaveFwdSmem {
     ProdStage st[NPROD];
     float eref[NPROD][WN];  // per producer: 2^{g_ref} per column
     float eL[NPROD][WN];    // per producer: 2^{g_L} per column
-    int ready[NSLOT];       // chunk held by the slot (-1: none yet)
+    int ready[NSLOT];       // 2 c + exact for the chunk c the slot holds
+                            // (exact: it needs the exact sequential pass;
+                            // -1: none yet)
     int done[NSLOT];        // chains finished with the slot, over all uses
     int failed;             // a bounded wait of this workgroup gave up
 };
@@ -391,10 +392,9 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
         if (lane < 16)
             *reinterpret_cast<f32x4_t*>(&sl.eL[4 * lane]) =
                 *reinterpret_cast<const f32x4_t*>(&sm.eL[p][4 * lane]);
-        if (lane == 0) sl.exact = exact ? 1 : 0;
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
         asm volatile("" ::: "memory");
-        if (lane == 0) lds_store(vready + s, c);
+        if (lane == 0) lds_store(vready + s, 2 * c + (exact ? 1 : 0));
     }
 }
 
@@ -427,18 +427,24 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
 
     // A chunk's operands, read from its slot at the end of the previous
-    // chunk's step, while that step's products run
+    // chunk's step, while that step's products run.  The slot's ready word
+    // (2 c + exact) is loaded at the start of that step, so the check
+    // rarely waits.
     struct SlotRegs {
         bf16x8_t W0, W1, Q0, Q1;
         i16x4_t U, V, Arb, Ark, B[4], K[4];
         f32x4_t eL[4];
         int exact;
     };
-    auto take = [&](int c, int s, SlotRegs& r) {
-        if (!poll(vready + s, A.wait.limit, [&](int x) { return x == c; }))
+    auto take = [&](int c, int s, int word, SlotRegs& r) {
+        if ((word >> 1) != c &&
+            !poll(vready + s, A.wait.limit, [&](int x) {
+                word = x;
+                return (x >> 1) == c;
+            }))
             wait_failed(&sm.failed, A.wait.failures, lane);
         const Slot& sl = sm.slot[s];
-        r.exact = __builtin_amdgcn_readfirstlane(sl.exact);
+        r.exact = word & 1;
         r.W0 = sl.W[0][lane];
         r.W1 = sl.W[1][lane];
         r.U = sl.U[ib][lane];
@@ -455,13 +461,16 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
         r.Arb = sl.Arb[lane];
         r.Ark = sl.Ark[lane];
     };
-    // y of the previous chunk, stored one iteration late (its products are
-    // complete by then): rows of chunk yc (yc < 0: none pending)
-    f32x4_t ypend = zero4();
+    // y of the previous chunk as its two products, added and stored one
+    // iteration late (complete by then): rows of chunk yc (yc < 0: none)
+    f32x4_t yq = zero4(), yp = zero4();
     int yc = -1;
-    auto store_y = [&](int cc, const f32x4_t& yy) {
-        const int64_t ty = int64_t(cc) * WL;
+    auto store_y = [&]() {
+        const int64_t ty = int64_t(yc) * WL;
         const int ny = int(T - ty < WL ? T - ty : WL);
+        f32x4_t yy;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) yy[e] = yq[e] + yp[e];
         // lanes of tokens past the end store at or past the bound: dropped
         const __amdgpu_buffer_rsrc_t rs = out_rsrc(
             A.y + (ty * A.lay.ts + hoff), (uint32_t(ny - 1) * TS + WN) * 2);
@@ -473,13 +482,13 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
     CkRows& ckr = sm.ck[ib];
     int64_t ckp = -1;
     auto store_ck = [&]() {
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int u = lane + 64 * k;
-            *reinterpret_cast<uint4*>(A.ckpt + ckp + (16 * ib + (u >> 3)) * WN +
-                                      8 * (u & 7)) =
-                *reinterpret_cast<const uint4*>(&ckr[u >> 3][8 * (u & 7)]);
-        }
+        bf16_t* const dst =
+            A.ckpt + ckp + (16 * ib + (lane >> 3)) * WN + 8 * (lane & 7);
+        *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(
+            &ckr[lane >> 3][8 * (lane & 7)]);
+        *reinterpret_cast<uint4*>(dst + 8 * WN) =
+            *reinterpret_cast<const uint4*>(
+                &ckr[8 + (lane >> 3)][8 * (lane & 7)]);
     };
 
     // running counters instead of divisions by the slot count and the
@@ -488,11 +497,14 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
     int s = 0, cph = 0;
     int64_t ckoff = sbase;
     SlotRegs cur;
-    if (nch > 0) take(0, 0, cur);
+    if (nch > 0) take(0, 0, -1, cur);
     for (int c = 0; c < nch; ++c) {
         const int64_t t0 = int64_t(c) * WL;
         const int n = int(T - t0 < WL ? T - t0 : WL);
         const int exact = cur.exact;
+        const int sn = s + 1 == NSLOT ? 0 : s + 1;  // the next chunk's slot
+        // the next chunk's ready word, used after this chunk's step
+        const int word = c + 1 < nch ? lds_load(vready + sn) : 0;
 
         // bf16(S_0): the operand of the state step and of y, and the
         // checkpoint's rows
@@ -518,7 +530,7 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
                 S[jpb] = acc;
             }
         }
-        if (yc >= 0) store_y(yc, ypend);
+        if (yc >= 0) store_y();
         yc = -1;
         if (ckp >= 0) store_ck();
         ckp = -1;
@@ -533,27 +545,30 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
         }
         if (!exact) {
             // Y^T_ib = bf16(S_0) Q^^T + U^T Arb^T + V^T Ark^T, lane:
-            // y[t0 + lr][16 ib + 4 lq ..] (stored in the next iteration)
-            f32x4_t pp = zero4(), yy = zero4();
-            mfma16(pp, cur.U, cur.Arb);
-            mfma16(pp, cur.V, cur.Ark);
-            mfma(yy, Sb0, cur.Q0);
-            mfma(yy, Sb1, cur.Q1);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) ypend[e] = yy[e] + pp[e];
+            // y[t0 + lr][16 ib + 4 lq ..] (added and stored in the next
+            // iteration)
+            yp = zero4();
+            yq = zero4();
+            mfma16(yp, cur.U, cur.Arb);
+            mfma16(yp, cur.V, cur.Ark);
+            mfma(yq, Sb0, cur.Q0);
+            mfma(yq, Sb1, cur.Q1);
             yc = c;
+        } else {
+            lds_drain();  // the slot's reads (unused) have completed
         }
-        // the slot goes back to the producers once its reads have completed
-        lds_drain();
+        // the slot goes back to the producers: its reads completed before
+        // their values were used
         if (lane == 0)
             __hip_atomic_fetch_add(&sm.done[s], 1, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_WORKGROUP);
-        s = s + 1 == NSLOT ? 0 : s + 1;
+        s = sn;
         if (++cph == A.cstride) {
             cph = 0;
             ckoff += A.BH * NN;
         }
-        if (c + 1 < nch) take(c + 1, s, cur);
+        if (c + 1 < nch)
+            take(c + 1, s, __builtin_amdgcn_readfirstlane(word), cur);
         if (exact) {
             // exact fp32 sequential pass over the chunk for the rows of
             // block ib (a chunk outside the factored form's range, far
@@ -588,7 +603,7 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
             }
         }
     }
-    if (yc >= 0) store_y(yc, ypend);
+    if (yc >= 0) store_y();
     if (ckp >= 0) store_ck();
 
     // final state (fp32) and the last checkpoint

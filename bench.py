@@ -861,6 +861,30 @@ def main():
         "kernels_ms": {"forward": fwd_ms, "backward": bwd_ms},
         "step_roofline_frac": step_gbs / HBM_PEAK_GBS,
     }
+    # the same step captured once in a HIP graph and replayed K times (the
+    # reference's step runs as one compiled XLA program, with no host work
+    # between its kernels): the step without launch gaps
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    graph_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    result["graph"] = {"ms_per_step": graph_ms,
+                       "tokens_per_s": tokens / (graph_ms / 1e3)}
+    del graph
     if args.ref_iters > 0:
         # the reference's method: every call host-synchronised, median over
         # the iterations, forward alone and forward+backward

@@ -7,13 +7,17 @@ callables the reference's FFI registry binds (src/rwkv7m/kernels/
 wkv_ffi.py:21-34).  Inputs (vectors, S0, dy, dS_T) are synthetic, with the
 model's input distributions, and resident in HBM before timing starts.
 
-Two timings.  The headline: W untimed warmup steps, then K steps back to
-back between two device synchronisations; tokens/s = B*T / seconds per
-step, with kernel durations from HIP events recorded on the stream the
-kernels run on.  Beside it, ``reference_method`` repeats the reference's WKV
-microbenchmark (scripts/benchmark_wkv_accelerator.py:88-97, :162-185):
-each call host-synchronised, median / p95 / min over ``--ref-iters``
-iterations, for the forward alone and for forward+backward.
+Three timings.  The headline: ``--settle`` untimed steps (the first few
+dozen steps over freshly allocated device memory run slower), W untimed
+warmup steps, then K steps back to back between two device
+synchronisations; tokens/s = B*T / seconds per step, with kernel durations
+from HIP events recorded on the stream the kernels run on.  ``graph``: the
+same step captured once in a HIP graph and replayed (no host work between
+kernels, as in the reference's compiled step).  ``reference_method``
+repeats the reference's WKV microbenchmark
+(scripts/benchmark_wkv_accelerator.py:88-97, :162-185): each call
+host-synchronised, median / p95 / min over ``--ref-iters`` iterations, for
+the forward alone and for forward+backward.
 ``cpu_baseline`` times the CPU restatement of the reference scan (oracle/,
 fp32, OpenMP over (b, h)) on a bounded sample of the same workload on the
 host cores.
@@ -41,6 +45,13 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--settle", type=int, default=40,
+                   help="untimed steps before the warmup (the first few "
+                        "dozen steps over fresh device allocations are "
+                        "slower)")
+    p.add_argument("--graph-steps", type=int, default=-1,
+                   help="replays of the HIP-graph-captured step to time "
+                        "(-1: as many as --steps; 0: skip)")
     p.add_argument("--config", type=int, default=2,
                    help="BASELINE config index (2 = the headline shape; "
                         "3 = the decode loop)")
@@ -736,6 +747,33 @@ def bench_screening(args):
     print(json.dumps(result), flush=True)
 
 
+def graph_step_ms(step, settle_calls: int, warmup: int, steps: int) -> float:
+    """Milliseconds per replay of `step` captured once in a HIP graph (its
+    own memory pool, so settled again), after `warmup` untimed replays."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    settle(graph.replay, settle_calls)
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    del graph
+    return ms
+
+
 def settle(fn, calls: int = 40) -> None:
     """Run fn `calls` times, untimed: the first few dozen uses of freshly
     allocated device memory are slower, a one-off cost that a training loop
@@ -811,7 +849,7 @@ def main():
     # same drift follows a graph capture's new pool; buffers already in use
     # show none).  A training loop pays this once; the settling steps come
     # before the warmup proper.
-    settle(step)
+    settle(step, args.settle)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -878,31 +916,14 @@ def main():
         "kernels_ms": {"forward": fwd_ms, "backward": bwd_ms},
         "step_roofline_frac": step_gbs / HBM_PEAK_GBS,
     }
-    # the same step captured once in a HIP graph and replayed K times (the
+    # the same step captured once in a HIP graph and replayed (the
     # reference's step runs as one compiled XLA program, with no host work
     # between its kernels): the step without launch gaps
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for _ in range(2):
-            step()
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
-    settle(graph.replay)
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        graph.replay()
-    torch.cuda.synchronize()
-    graph_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    result["graph"] = {"ms_per_step": graph_ms,
-                       "tokens_per_s": tokens / (graph_ms / 1e3)}
-    del graph
+    gsteps = args.steps if args.graph_steps < 0 else args.graph_steps
+    if gsteps > 0:
+        graph_ms = graph_step_ms(step, args.settle, args.warmup, gsteps)
+        result["graph"] = {"ms_per_step": graph_ms, "steps": gsteps,
+                           "tokens_per_s": tokens / (graph_ms / 1e3)}
     if args.ref_iters > 0:
         # the reference's method: every call host-synchronised, median over
         # the iterations, forward alone and forward+backward

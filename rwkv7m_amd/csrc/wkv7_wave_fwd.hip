@@ -428,8 +428,8 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
 
     // A chunk's operands, read from its slot at the end of the previous
     // chunk's step, while that step's products run.  The slot's ready word
-    // (2 c + exact) is loaded at the start of that step, so the check
-    // rarely waits.
+    // (2 c + exact) is loaded as that step is issued, so the check rarely
+    // waits.
     struct SlotRegs {
         bf16x8_t W0, W1, Q0, Q1;
         i16x4_t U, V, Arb, Ark, B[4], K[4];
@@ -476,19 +476,18 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
             A.y + (ty * A.lay.ts + hoff), (uint32_t(ny - 1) * TS + WN) * 2);
         store8(rs, (uint32_t(lr) * TS + 16 * ib + 4 * lq) * 2, pack4(yy));
     };
-    // this chain's rows of a checkpoint, staged in the previous iteration,
-    // as whole rows: lane l stores 16-byte units l and l + 64 (row u / 8,
-    // columns 8 (u % 8) ..) at element offset ckp (ckp < 0: none pending)
+    // this chain's rows of a checkpoint: written to its LDS rows in the
+    // register layout, read back at once as whole rows (lane l: 16-byte
+    // units l and l + 64, row u / 8, columns 8 (u % 8) ..) and stored in the
+    // next iteration, at element offset ckp (ckp < 0: none pending)
     CkRows& ckr = sm.ck[ib];
     int64_t ckp = -1;
+    uint4 ckd0 = {}, ckd1 = {};
     auto store_ck = [&]() {
         bf16_t* const dst =
             A.ckpt + ckp + (16 * ib + (lane >> 3)) * WN + 8 * (lane & 7);
-        *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(
-            &ckr[lane >> 3][8 * (lane & 7)]);
-        *reinterpret_cast<uint4*>(dst + 8 * WN) =
-            *reinterpret_cast<const uint4*>(
-                &ckr[8 + (lane >> 3)][8 * (lane & 7)]);
+        *reinterpret_cast<uint4*>(dst) = ckd0;
+        *reinterpret_cast<uint4*>(dst + 8 * WN) = ckd1;
     };
 
     // running counters instead of divisions by the slot count and the
@@ -503,8 +502,6 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
         const int n = int(T - t0 < WL ? T - t0 : WL);
         const int exact = cur.exact;
         const int sn = s + 1 == NSLOT ? 0 : s + 1;  // the next chunk's slot
-        // the next chunk's ready word, used after this chunk's step
-        const int word = c + 1 < nch ? lds_load(vready + sn) : 0;
 
         // bf16(S_0): the operand of the state step and of y, and the
         // checkpoint's rows
@@ -530,17 +527,25 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
                 S[jpb] = acc;
             }
         }
+        // the next chunk's ready word (read for every chunk; unused after
+        // the last), used after this chunk's step
+        const int word = lds_load(vready + sn);
         if (yc >= 0) store_y();
         yc = -1;
         if (ckp >= 0) store_ck();
         ckp = -1;
         if (A.ckpt && cph == 0) {
-            // rows 16 ib .. + 15 of checkpoint c / stride (the reads of the
-            // previous one, above, precede these writes)
+            // rows 16 ib .. + 15 of checkpoint c / stride, and at once their
+            // whole-row read-back (the same wave's LDS accesses complete in
+            // order)
 #pragma unroll
             for (int jb = 0; jb < 4; ++jb)
                 *reinterpret_cast<i16x4_t*>(&ckr[lr][16 * jb + 4 * lq]) =
                     sb[jb];
+            ckd0 = *reinterpret_cast<const uint4*>(
+                &ckr[lane >> 3][8 * (lane & 7)]);
+            ckd1 = *reinterpret_cast<const uint4*>(
+                &ckr[8 + (lane >> 3)][8 * (lane & 7)]);
             ckp = ckoff;
         }
         if (!exact) {

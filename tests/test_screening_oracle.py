@@ -14,10 +14,14 @@ statistics) and torch float64 (for autograd, the gradient oracle).  Pins:
   nothing at the first step (tau = 0), so h_0 = h_base_0;
 * the torch restatement's autograd against central finite differences of
   the numpy forward, for every input and parameter;
+* hand-built cases (two channels, three unit slots) whose relevances,
+  read, gated residual, final slots, usage, ages and twelve statistics
+  have short closed forms, for every option and the write phase;
 * planted mistakes fail those pins: the read taken after the slot update
-  (zero slots then read something), and a wrong per-slot rate in the numpy
+  (zero slots then read something), a wrong per-slot rate in the numpy
   restatement (the torch restatement, which derives the rates on its own,
-  disagrees).
+  disagrees), and tanh_norm, the trim's square, softplus, the gate's sigmoid
+  or the LayerNorm dropped (the hand-built case disagrees).
 """
 
 import numpy as np
@@ -294,3 +298,221 @@ def test_write_phase_autograd_matches_finite_differences():
             fd = (fp - fm) / (2 * eps)
             assert abs(fd - g[i]) < 1e-6 * max(1.0, abs(fd)), (n, i, fd,
                                                                 g[i])
+
+
+# ---------------------------------------------------------------------------
+# Hand-built cases: every quantity below is worked out from the definitions
+# (reference screening.py:21-58, nnx_model.py:1062-1137) with numbers chosen
+# so that it has a short closed form, not by re-running the oracle's steps.
+#
+#   x = [3, -1]: LayerNorm mean 1, variance 4, so x_ln = [s, -s] with
+#   s = 2 / sqrt(4 + 1e-6); q_proj_r keeps x_ln's first channel, so the read
+#   query is e1.  k_proj_r = I and unit slots make the keys the slots; the
+#   three slots e1, [0.6, 0.8], e2 then have similarities 1, 0.6, 0.
+#   tau_r_raw = log 1.5 gives tau = 2 * 0.6 - 1 = 0.2; lambda_raw =
+#   log(e^0.5 - 1) gives lambda = 0.5; v_proj = 2 I, so the unit-normed
+#   values are the slots (and twice the slots without the unit norm).
+# ---------------------------------------------------------------------------
+
+S_LN = 2.0 / np.sqrt(4.0 + 1e-6)
+SLOTS3 = np.array([[1.0, 0.0], [0.6, 0.8], [0.0, 1.0]])
+OUT3 = np.array([[1.0, -2.0], [0.5, 3.0]])
+DELTA3 = np.tanh(np.array([0.3, -0.2]))
+MU3 = np.array([0.05, 0.02, 0.005]) / 2.0     # mu_max * sigmoid(0), banks 0-2
+AGES3 = np.array([32.0, 32.0 + 8.0 * np.log(3.0), 0.0])
+USAGE3 = np.array([0.1, 0.0, 0.2])
+
+
+def _hand(T=1, delta_bias=(0.3, -0.2), **opt):
+    cfg = so.default_config(d_model=2, d_slot=2, d_k=2, d_v=2, n_slots=3,
+                            bank_ids=(0, 1, 2), eps=1e-12, **opt)
+    P = {"ln_scale": np.ones(2), "ln_bias": np.zeros(2),
+         "q_proj_r": np.array([[1.0, 0.0], [0.0, 0.0]]),
+         "k_proj_r": np.eye(2), "v_proj": 2.0 * np.eye(2), "out_proj": OUT3,
+         "gate_kernel": np.array([[0.7, 0.0], [0.0, 0.0]]),
+         "gate_bias": np.array([0.1, -0.4]),
+         "delta_kernel": np.zeros((6, 2)),
+         "delta_bias": np.array(delta_bias, np.float64),
+         "tau_r_raw": np.array(np.log(1.5)),
+         "lambda_raw": np.array(np.log(np.expm1(0.5))),
+         "slot_embed": np.zeros((3, 2)), "mu_by_bank_raw": np.zeros(3),
+         # write path: the write query is unit(h) = e2 (x's part is zero),
+         # the write keys are the slots, tau_w = 0.2 as tau
+         "q_proj_w": np.vstack([np.zeros((2, 2)), np.eye(2)]),
+         "k_proj_w": np.eye(2), "tau_w_raw": np.array(np.log(1.5))}
+    x = np.tile(np.array([3.0, -1.0]), (1, T, 1))
+    h = np.tile(np.array([0.0, 2.0]), (1, T, 1))
+    return (x, h, SLOTS3[None].copy(), AGES3[None].copy(),
+            USAGE3[None].copy(), P, cfg)
+
+
+def _hand_read(rel, value_scale=1.0):
+    """h at a step whose relevances are ``rel``: z = sum_m rel_m v_m,
+    u = tanh(|z|) z / |z| (cap 1), h = h_base + lambda * gate * u @ out."""
+    z = value_scale * rel @ SLOTS3
+    nz = np.linalg.norm(z)
+    u = np.tanh(nz) / nz * z
+    gate = 1.0 / (1.0 + np.exp(-np.array([0.7 * S_LN + 0.1, -0.4])))
+    return np.array([0.0, 2.0]) + 0.5 * gate * (u @ OUT3), z, u
+
+
+def _check_hand(opt, rel, value_scale=1.0, torch_too=True):
+    x, h, slots, ages, usage, P, cfg = _hand(**opt)
+    want_h, z, u = _hand_read(rel, value_scale)
+    hn, (sn, an, un), stats = so.read_forward(x, h, slots, ages, usage, P,
+                                              cfg)
+    np.testing.assert_allclose(hn[0, 0], want_h, rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(sn[0], SLOTS3 + MU3[:, None]
+                               * (DELTA3 - SLOTS3), rtol=1e-9, atol=1e-15)
+    np.testing.assert_allclose(un[0], 0.99 * USAGE3 + 0.01 * rel,
+                               rtol=1e-9, atol=1e-15)
+    np.testing.assert_array_equal(an, ages)
+    if torch_too:
+        ht, st, ut = so.read_forward_torch(
+            _t(x), _t(h), _t(slots), _t(ages), _t(usage),
+            {k: _t(v) for k, v in P.items()}, cfg)
+        np.testing.assert_allclose(ht.numpy()[0, 0], want_h, rtol=1e-9,
+                                   atol=1e-12)
+        np.testing.assert_allclose(ut.numpy()[0], un[0], rtol=1e-9)
+    return stats, z, u
+
+
+def test_hand_built_read():
+    # trim-square relevances ((sim - 0.2) / 0.8)^2 of 1, 0.6, 0
+    _check_hand({}, np.array([1.0, 0.25, 0.0]))
+    # a one-hot slot gives z = rel * v: only e1 clears tau = 0.7
+    # (tau_r_raw = log(0.85 / 0.15))
+    x, h, slots, ages, usage, P, cfg = _hand()
+    P["tau_r_raw"] = np.array(np.log(0.85 / 0.15))
+    hn, _, stats = so.read_forward(x, h, slots, ages, usage, P, cfg)
+    rel = np.array([1.0, 0.0, 0.0])
+    want_h, z, _ = _hand_read(rel)
+    np.testing.assert_allclose(z, [1.0, 0.0])
+    np.testing.assert_allclose(hn[0, 0], want_h, rtol=1e-9)
+    assert stats["active_slots_mean"] == 1.0
+    # without the value unit norm the values are 2 * slots
+    _check_hand(dict(use_value_unit_norm=False), np.array([1.0, 0.25, 0.0]),
+                value_scale=2.0)
+    # age weights sigmoid((32 - age) / 8): 1/2 at age 32, 1/4 at
+    # 32 + 8 ln 3, and e2's relevance is 0 whatever its weight
+    _check_hand(dict(use_age_mask=True), np.array([0.5, 0.0625, 0.0]))
+    # leaky warm-up: 0.7 * trim (reference eps 1e-6) + 0.3 * sigmoid(8 (sim
+    # - tau)); e2 (sim 0, below tau) still reads through the soft term
+    hard = np.array([0.8, 0.4, 0.0]) ** 2 / (0.8 + 1e-6) ** 2
+    soft = 1.0 / (1.0 + np.exp(-8.0 * np.array([0.8, 0.4, -0.2])))
+    _check_hand(dict(use_leaky_warmup=True, leaky_alpha=0.3),
+                0.7 * hard + 0.3 * soft)
+
+
+def test_hand_built_statistics():
+    rel = np.array([1.0, 0.25, 0.0])
+    stats, z, u = _check_hand({}, rel)
+    upd = MU3 * np.linalg.norm(DELTA3 - SLOTS3, axis=-1)
+    want = {"rel_read_mean": 1.25 / 3.0, "rel_read_max": 1.0,
+            "active_slots_mean": 2.0, "z_norm_mean": np.sqrt(1.3625),
+            "u_norm_mean": np.tanh(np.sqrt(1.3625)), "tau_r": 0.2,
+            "lambda_screen": 0.5, "rel_write_mean": 0.0,
+            "rel_write_effective_mean": 0.0,
+            "slot_update_norm_mean": upd.mean(),
+            "slot_usage_ema_mean": (0.99 * USAGE3 + 0.01 * rel).mean(),
+            "tau_w": 0.0}
+    np.testing.assert_allclose(z, [1.15, 0.2])
+    assert set(stats) == set(want)
+    for k, v in want.items():
+        np.testing.assert_allclose(stats[k], v, rtol=1e-9, atol=1e-15,
+                                   err_msg=k)
+
+
+def test_hand_built_steps_average_the_statistics():
+    # delta = tanh(0) = 0 shrinks each slot by (1 - mu) per step without
+    # turning it, so every step reads the same; the usage follows the EMA in
+    # closed form and the update norms are mu (1 - mu)^t
+    T = 3
+    x, h, slots, ages, usage, P, cfg = _hand(T=T, delta_bias=(0.0, 0.0))
+    hn, (sn, _, un), stats = so.read_forward(x, h, slots, ages, usage, P,
+                                             cfg)
+    rel = np.array([1.0, 0.25, 0.0])
+    want_h, _, _ = _hand_read(rel)
+    np.testing.assert_allclose(hn[0], np.tile(want_h, (T, 1)), rtol=1e-9)
+    np.testing.assert_allclose(sn[0], (1 - MU3[:, None]) ** T * SLOTS3,
+                               rtol=1e-9)
+    usage_t = [0.99 ** t * USAGE3 + (1 - 0.99 ** t) * rel
+               for t in range(1, T + 1)]
+    np.testing.assert_allclose(un[0], usage_t[-1], rtol=1e-9)
+    np.testing.assert_allclose(stats["slot_usage_ema_mean"],
+                               np.mean([u.mean() for u in usage_t]),
+                               rtol=1e-9)
+    np.testing.assert_allclose(
+        stats["slot_update_norm_mean"],
+        np.mean([(MU3 * (1 - MU3) ** t).mean() for t in range(T)]),
+        rtol=1e-9)
+    np.testing.assert_allclose(stats["rel_read_mean"], 1.25 / 3.0,
+                               rtol=1e-9)
+
+
+def test_hand_built_write():
+    # write query e2 against the slots: similarities 0, 0.8, 1, so with
+    # tau_w = 0.2 the write relevances are 0, 0.5625, 1; e1 is written at
+    # the floor and ages, the others reset to age 0
+    x, h, slots, ages, usage, P, cfg = _hand(use_write_screening=True,
+                                             write_rel_floor=0.05)
+    hn, (sn, an, un), stats = so.read_forward(x, h, slots, ages, usage, P,
+                                              cfg, phase="read_write")
+    rel = np.array([1.0, 0.25, 0.0])
+    rel_w = np.array([0.0, 0.5625, 1.0])
+    strength = MU3 * np.maximum(rel_w, 0.05)
+    want_h, _, _ = _hand_read(rel)
+    np.testing.assert_allclose(hn[0, 0], want_h, rtol=1e-9)
+    np.testing.assert_allclose(
+        sn[0], SLOTS3 + strength[:, None] * (DELTA3 - SLOTS3), rtol=1e-9,
+        atol=1e-14)
+    np.testing.assert_array_equal(an[0], [AGES3[0] + 1.0, 0.0, 0.0])
+    activity = np.array([1.0, 0.5625, 1.0])
+    np.testing.assert_allclose(un[0], 0.99 * USAGE3 + 0.01 * activity,
+                               rtol=1e-9)
+    np.testing.assert_allclose(stats["rel_write_mean"], 1.5625 / 3.0,
+                               rtol=1e-9)
+    np.testing.assert_allclose(stats["rel_write_effective_mean"],
+                               1.6125 / 3.0, rtol=1e-9)
+    np.testing.assert_allclose(stats["tau_w"], 0.2, rtol=1e-9)
+    np.testing.assert_allclose(
+        stats["slot_update_norm_mean"],
+        (strength * np.linalg.norm(DELTA3 - SLOTS3, axis=-1)).mean(),
+        rtol=1e-9)
+    ht, st, ut = so.read_forward_torch(
+        _t(x), _t(h), _t(slots), _t(ages), _t(usage),
+        {k: _t(v) for k, v in P.items()}, cfg, phase="read_write")
+    np.testing.assert_allclose(ht.numpy(), hn, rtol=1e-9)
+    np.testing.assert_allclose(st.numpy(), sn, rtol=1e-9)
+    np.testing.assert_allclose(ut.numpy(), un, rtol=1e-9)
+
+
+def test_half_life_rates():
+    # a half-life H gives the rate mu with (1 - mu)^H = 1/2; banks without
+    # one keep mu_max * sigmoid(raw)
+    cfg = so.default_config(short_half_life_tokens=4.0,
+                            long_half_life_tokens=50.0, bank_ids=(0, 1, 2))
+    mu = so.compute_mu(cfg, np.array([5.0, np.log(3.0), -5.0]))
+    np.testing.assert_allclose((1.0 - mu[[0, 2]]) ** np.array([4.0, 50.0]),
+                               0.5, rtol=1e-13)
+    np.testing.assert_allclose(mu[1], 0.02 * 0.75, rtol=1e-13)
+
+
+@pytest.mark.parametrize("plant", ["no_squash", "no_square", "exp_lambda",
+                                   "gate_without_sigmoid", "no_layer_norm"])
+def test_hand_pins_catch_planted_mistakes(monkeypatch, plant):
+    if plant == "no_squash":
+        monkeypatch.setattr(so, "tanh_norm", lambda z, cap, eps: z)
+    elif plant == "no_square":
+        monkeypatch.setattr(so, "trim_square", lambda s, t, e: np.maximum(
+            (s - t) / (1.0 - t + e), 0.0))
+    elif plant == "exp_lambda":
+        monkeypatch.setattr(so, "softplus", np.exp)
+    elif plant == "gate_without_sigmoid":   # the only [B, T, C] sigmoid
+        real = so.sigmoid
+        monkeypatch.setattr(so, "sigmoid",
+                            lambda v: v if np.ndim(v) == 3 else real(v))
+    else:   # gate and query fed the raw input: the gate sees 3, not ~1
+        monkeypatch.setattr(so, "layer_norm", lambda x, sc, b, eps=1e-6: x)
+    with pytest.raises(AssertionError):
+        _check_hand({}, np.array([1.0, 0.25, 0.0]), torch_too=False)

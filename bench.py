@@ -420,10 +420,11 @@ def bench_timemix(args, cfg):
     """The fused WKV section of the time mix (src/rwkv7m/model/
     nnx_model.py:630-727 without the projections) on batch-major [B, T, C]
     activations: producers, batch-major WKV forward_with_aux, consumer, then
-    consumer, WKV and producer backward and the two cotangent sums of r and
-    v -- the calls ``rwkv7m_amd.time_mix_wkv`` makes.  Each stage is
-    bracketed by HIP events on the launch stream; the algorithmic bytes of a
-    fused kernel are its activation reads and writes."""
+    consumer, WKV (with the consumer's cotangents of r, k' and v summed into
+    its stores) and producer backward -- the calls
+    ``rwkv7m_amd.time_mix_wkv`` makes.  Each stage is bracketed by HIP
+    events on the launch stream; the algorithmic bytes of a fused kernel
+    are its activation reads and writes."""
     import torch
 
     from rwkv7m_amd.kernels import timemix_hip, wkv_hip
@@ -452,7 +453,7 @@ def bench_timemix(args, cfg):
     stream = torch.cuda.current_stream(dev)
     torch.cuda.synchronize()
     stages = ("inputs_fwd", "wkv_fwd", "output_fwd", "output_bwd", "wkv_bwd",
-              "inputs_bwd", "sums")
+              "inputs_bwd")
 
     def step(evs=None):
         def mark(i):
@@ -475,21 +476,20 @@ def bench_timemix(args, cfg):
             x["dout"], N)
         mark(4)
         dr, dw, dk_w, dv, dnkk, dkka, ds0 = wkv_hip.backward(
-            *vecs, dy, ds_t, *aux, layout="bthn")
+            *vecs, dy, ds_t, *aux, layout="bthn",
+            add=(dr_c.view(hv), dk_c.view(hv), dv_c.view(hv)))
         mark(5)
         gi = timemix_hip.inputs_backward(
             x["w_raw"], x["k"], x["a"], par["k_k"], par["k_a"], dw, dk_w,
-            dnkk, dkka, N, dk_out2=dk_c)
+            dnkk, dkka, N)
         mark(6)
-        dr = dr + dr_c
-        dv = dv + dv_c
-        mark(7)
         return out, s_t, dr, dv, dg, gi, pg, ds0
 
+    settle(step, args.settle)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(8)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(7)]
            for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -502,8 +502,10 @@ def bench_timemix(args, cfg):
     ms_per_step = elapsed * 1e3 / args.steps
     eb = 2 if dtype == torch.bfloat16 else 4
     M = B * T * C * eb
+    # activations each fused kernel reads and writes (the producers'
+    # backward: w_raw, k, a and the four WKV input cotangents in, three out)
     moved = {"inputs_fwd": 7 * M, "output_fwd": 6 * M, "output_bwd": 11 * M,
-             "inputs_bwd": 11 * M}
+             "inputs_bwd": 10 * M}
     kernels = {name: {"ms": stage_ms[name],
                       "algorithmic_bytes": moved[name],
                       "GB/s": moved[name] / (stage_ms[name] / 1e3) / 1e9}

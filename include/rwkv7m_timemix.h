@@ -120,6 +120,28 @@ int rwkv7m_timemix_wkv_output_backward_noalloc(
     const void *dout, void *dy, void *dr, void *dk, void *dv, void *dg,
     float *dr_k, float *dln_scale, float *dln_bias, void *stream);
 
+/*
+ * The WKV-7 backward as the time mix needs it: rwkv7m_wkv7_backward_bthn
+ * (batch-major vectors, the same arguments and checks) with the consumer's
+ * cotangents of r, k' and v (dr_add, dk_add, dv_add, each batch-major in
+ * the vector dtype, or NULL for none) added to dr, dk and dv.  r, k' and v
+ * feed both the WKV call and the consumer's bonus term, so jax autodiff
+ * sums the two cotangents of each (nnx_model.py:695-727; the reference's
+ * training step differentiates the time mix as a whole).  The sums are
+ * formed in fp32 and rounded once, inside the backward's own stores, so no
+ * separate pass re-reads the three gradients.  The added cotangents must
+ * not overlap an output buffer (RWKV7M_ERR_INVALID_ARGUMENT when one is
+ * the same pointer).
+ */
+int rwkv7m_timemix_wkv_backward(
+    int dtype, int64_t T, int64_t B, int64_t H, int64_t N, const void *r,
+    const void *w, const void *k, const void *v, const void *neg_kk,
+    const void *kka, const float *initial_state, const void *dy,
+    const float *ds_t, const void *checkpoints, int64_t checkpoint_interval,
+    const void *dr_add, const void *dk_add, const void *dv_add, void *dr,
+    void *dw, void *dk, void *dv, void *dneg_kk, void *dkka, float *ds0,
+    void *stream);
+
 #ifdef __cplusplus
 }
 #endif

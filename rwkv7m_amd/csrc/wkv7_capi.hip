@@ -251,7 +251,10 @@ int backward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
                          const void* checkpoints,
                          int64_t checkpoint_interval, void* dr, void* dw,
                          void* dk, void* dv, void* dneg_kk, void* dkka,
-                         float* ds0, hipStream_t s, bool batch_major) {
+                         float* ds0, hipStream_t s, bool batch_major,
+                         const void* add_dr = nullptr,
+                         const void* add_dk = nullptr,
+                         const void* add_dv = nullptr) {
     (void)initial_state;  // checkpoints[0] holds it
     g_last_path = "";
     Dims d;
@@ -277,6 +280,16 @@ int backward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     RWKV7M_TRY(need(dkka, vecs, fn, "dkka"));
     RWKV7M_TRY(need(ds0, st, fn, "ds0"));
     RWKV7M_TRY(need(checkpoints, vecs, fn, "checkpoints"));
+    // an added cotangent is read while the gradients are written: it may
+    // not be an output buffer (a head handed to the exact pass is written
+    // twice)
+    for (const void* a : {add_dr, add_dk, add_dv})
+        for (const void* o : {dr, dw, dk, dv, dneg_kk, dkka})
+            if (a && a == o)
+                return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                            std::string(fn) +
+                                ": an added cotangent may not be an output "
+                                "buffer");
     if (d.state_elems == 0) return RWKV7M_OK;
     if (T == 0) return copy_or_clear(ds0, ds_t, d.state_elems, s);
     const rwkv7m::VecLayout lay = vec_layout(batch_major, T, B, H, N);
@@ -305,9 +318,12 @@ int backward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     p.da = dneg_kk;
     p.db = dkka;
     p.ds0 = ds0;
+    p.add_dr = add_dr;
+    p.add_dk = add_dk;
+    p.add_dv = add_dv;
     if (use_chunked(dtype, N, ci, T, lay.ts,
                     {r, w, k, v, neg_kk, kka, dy, ds_t, checkpoints, dr, dw,
-                     dk, dv, dneg_kk, dkka, ds0})) {
+                     dk, dv, dneg_kk, dkka, ds0, add_dr, add_dk, add_dv})) {
         rwkv7m::WaveBwdArgs c{};
         c.L = int(ci);
         c.T = T;
@@ -330,6 +346,9 @@ int backward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
         c.da = dneg_kk;
         c.db = dkka;
         c.ds0 = ds0;
+        c.add_dr = add_dr;
+        c.add_dk = add_dk;
+        c.add_dv = add_dv;
         RWKV7M_TRY(hip_status("device wait configuration",
                               rwkv7m::wait_config(&c.wait)));
         RWKV7M_TRY(hip_status("wave backward launch",
@@ -907,6 +926,22 @@ int rwkv7m_timemix_wkv_output_backward_noalloc(
         k, v, g, r_k, ln_scale, ln_bias, eps, dout, dy, dr, dk, dv, dg, dr_k,
         dln_scale, dln_bias, nullptr, 0, true,
         static_cast<hipStream_t>(stream));
+}
+
+int rwkv7m_timemix_wkv_backward(
+    int dtype, int64_t T, int64_t B, int64_t H, int64_t N, const void* r,
+    const void* w, const void* k, const void* v, const void* neg_kk,
+    const void* kka, const float* initial_state, const void* dy,
+    const float* ds_t, const void* checkpoints, int64_t checkpoint_interval,
+    const void* dr_add, const void* dk_add, const void* dv_add, void* dr,
+    void* dw, void* dk, void* dv, void* dneg_kk, void* dkka, float* ds0,
+    void* stream) {
+    g_last_error.clear();
+    return backward_impl("rwkv7m_timemix_wkv_backward", dtype, T, B, H, N, r,
+                         w, k, v, neg_kk, kka, initial_state, dy, ds_t,
+                         checkpoints, checkpoint_interval, dr, dw, dk, dv,
+                         dneg_kk, dkka, ds0, static_cast<hipStream_t>(stream),
+                         true, dr_add, dk_add, dv_add);
 }
 
 int64_t rwkv7m_screen_slot_scan_workspace_floats(int64_t B, int64_t T,

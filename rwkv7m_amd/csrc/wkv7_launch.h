@@ -51,6 +51,9 @@ struct SeqBwdArgs {
     // only the heads whose ds0[b][h][0][0] holds kExactPassMark (left by the
     // wave backward to this exact pass); others are untouched
     bool marked_only;
+    // nullptr, or cotangents (vector layout and dtype) added to dr, dk, dv
+    // in fp32 before they are rounded and stored
+    const void *add_dr, *add_dk, *add_dv;
 };
 
 // Bit pattern (a NaN no arithmetic produces) that the wave backward leaves in
@@ -88,6 +91,10 @@ struct WaveBwdArgs {
     void *dr, *dw, *dk, *dv, *da, *db;
     float* ds0;
     WaitCfg wait;
+    // nullptr, or bf16 cotangents added to dr, dk, dv (as SeqBwdArgs); any
+    // non-null one selects the accumulating kernel, which takes all three
+    // (a null one reads as zeros)
+    const void *add_dr, *add_dk, *add_dv;
 };
 
 hipError_t launch_wave_backward(const WaveBwdArgs& p, hipStream_t stream);

@@ -143,7 +143,9 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
                     const float* __restrict__ ds_t,
                     const CT* __restrict__ ckpt, int64_t ci, VT* dr,
                     VT* dw, VT* dk, VT* dv, VT* da, VT* db, float* ds0,
-                    int marked_only) {
+                    int marked_only, const VT* __restrict__ add_dr,
+                    const VT* __restrict__ add_dk,
+                    const VT* __restrict__ add_dv) {
     using Sh = SeqShape<N>;
     constexpr int G = Sh::G, C = Sh::C, SUB = Sh::SUB, TH = Sh::THREADS;
     constexpr int WL = Sh::WAVE_LANES, NW = Sh::NWAVES;
@@ -265,7 +267,12 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
 #pragma unroll
                         for (int ww = 0; ww < NW; ++ww) acc += red[buf][ww][q][j];
                         if (q == 1) acc *= -sh[7][u][j] * sh[1][u][j];
-                        store_f(gout[q] + t * lay.ts + hoff + j, acc);
+                        const int64_t off = t * lay.ts + hoff + j;
+                        // cotangents of r and k from other uses, added in
+                        // fp32 before rounding
+                        if (q == 0 && add_dr) acc += load_f(add_dr + off);
+                        if (q == 3 && add_dk) acc += load_f(add_dk + off);
+                        store_f(gout[q] + off, acc);
                     }
                     buf ^= 1;
                 }
@@ -273,7 +280,9 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
             __syncthreads();
             for (int e = tid; e < nt * N; e += TH) {
                 const int u = e / N, i = e - u * N;
-                store_f(dv + (ts + u) * lay.ts + hoff + i, sh_dv[u][i]);
+                const int64_t off = (ts + u) * lay.ts + hoff + i;
+                store_f(dv + off,
+                        sh_dv[u][i] + (add_dv ? load_f(add_dv + off) : 0.f));
             }
             __syncthreads();
         }
@@ -320,7 +329,10 @@ hipError_t launch_bwd_nc(const SeqBwdArgs& p, hipStream_t stream) {
                        static_cast<VT*>(p.dr), static_cast<VT*>(p.dw),
                        static_cast<VT*>(p.dk), static_cast<VT*>(p.dv),
                        static_cast<VT*>(p.da), static_cast<VT*>(p.db),
-                       p.ds0, p.marked_only ? 1 : 0);
+                       p.ds0, p.marked_only ? 1 : 0,
+                       static_cast<const VT*>(p.add_dr),
+                       static_cast<const VT*>(p.add_dk),
+                       static_cast<const VT*>(p.add_dv));
     return hipGetLastError();
 }
 

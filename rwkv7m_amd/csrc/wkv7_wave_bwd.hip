@@ -159,6 +159,8 @@ struct BwdArgs {
     bf16_t *dr, *dw, *dk, *dv, *da, *db;
     float* ds0;
     WaitCfg wait;
+    // cotangents added to dr, dk, dv (the accumulating kernel; null: zeros)
+    const bf16_t *add_dr, *add_dk, *add_dv;
 };
 
 // Wait until pred(*p) holds: 1 when it does, 0 when the workgroup aborted
@@ -183,6 +185,25 @@ __device__ __forceinline__ int wait_for(const WaitCfg& wc, int* p, int lane,
 
 __device__ __forceinline__ f32x4_t unpack_i16(const i16x4_t& x) {
     return unpack4(__builtin_bit_cast(uint2, x));
+}
+
+// A buffer resource over `bytes` bytes at p + off for loads (null p: an
+// empty range, so every load returns zeros); loads at or past the range
+// return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t in_rsrc(const bf16_t* p,
+                                                        int64_t off,
+                                                        uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16_t*>(p ? p + off : nullptr), 0, p ? int(bytes) : 0,
+        0x00020000);
+}
+
+// 8 bytes at byte offset `off` of the buffer.
+__device__ __forceinline__ uint2 load8(__amdgpu_buffer_rsrc_t rs,
+                                       uint32_t off) {
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(rs, int(off), 0, 0);
+    return make_uint2(x[0], x[1]);
 }
 
 // ---------------------------------------------------------------------------
@@ -380,8 +401,11 @@ __device__ __forceinline__ i16x4_t to_j(const i16x4_t& t, const i16x4_t& kI) {
 
 // ---------------------------------------------------------------------------
 // Worker w: chunks nch - 1 - w, nch - 1 - w - NWORK, ...; checkpoints every
-// M chunks.
-template <int M>
+// M chunks.  ACC: the cotangents add_dr, add_dk, add_dv are added to dr, dk,
+// dv before they are rounded; their 12 loads are issued just before the next
+// chunk's vector loads (so that waiting for them does not wait for those)
+// and count in the waits below.
+template <int M, bool ACC>
 __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
     const int64_t bh = blockIdx.x;
     const int64_t hoff = A.lay.head(bh, WN);
@@ -452,6 +476,22 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) raw[vv][kb] = read_t(w, vv, kb, lane);
         lds_drain();
+        // the cotangents added to this chunk's dv (value blocks ib) and dr,
+        // dk (key blocks jb), at the lanes' own output offsets
+        uint2 adv[4], adr[4], adk[4];
+        if constexpr (ACC) {
+            const __amdgpu_buffer_rsrc_t rv = in_rsrc(A.add_dv, gbase, obytes),
+                                         rr = in_rsrc(A.add_dr, gbase, obytes),
+                                         rk = in_rsrc(A.add_dk, gbase, obytes);
+            const uint32_t lo0 = (uint32_t(lr) * TS + 4 * lq) * 2;
+#pragma unroll
+            for (int ib = 0; ib < 4; ++ib) adv[ib] = load8(rv, lo0 + 32 * ib);
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+                adr[jb] = load8(rr, lo0 + 32 * jb);
+                adk[jb] = load8(rk, lo0 + 32 * jb);
+            }
+        }
         // the stage is free: the next chunk's vectors load during this one
         if (cn >= 0) fetch_vecs(A, w, cn, lane);
         if (n < WL) {
@@ -645,10 +685,18 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         if (starts) {
             // the start state: since its loads, only the next chunk's 14
             // vector loads (if any) were issued
-            if (cn >= 0)
-                __builtin_amdgcn_s_waitcnt(0x0f7e);  // vmcnt(14)
-            else
-                __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+            if constexpr (ACC) {
+                // and the 12 cotangent loads
+                if (cn >= 0)
+                    __builtin_amdgcn_s_waitcnt(0x4f7a);  // vmcnt(26)
+                else
+                    __builtin_amdgcn_s_waitcnt(0x0f7c);  // vmcnt(12)
+            } else {
+                if (cn >= 0)
+                    __builtin_amdgcn_s_waitcnt(0x0f7e);  // vmcnt(14)
+                else
+                    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+            }
             asm volatile("" ::: "memory");
             if (lane == 0) lds_store(&fl.s_ready[w], c);
         } else if (wait_for(A.wait, &fl.s_ready[w], lane,
@@ -727,6 +775,15 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             break;
         const bf16x8_t Khp0 = pk8(tK[0], tK[1]), Khp1 = pk8(tK[2], tK[3]);
         const __amdgpu_buffer_rsrc_t rs_dv = out_rsrc(A.dv + gbase, obytes);
+        if constexpr (ACC) {
+            // the dv cotangents: the 8 dr, dk loads and the next chunk's 14
+            // vector loads (if any) came after them
+            if (cn >= 0)
+                __builtin_amdgcn_s_waitcnt(0x4f76);  // vmcnt(22)
+            else
+                __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8)
+            asm volatile("" ::: "memory");
+        }
         i16x4_t kdUT[4];
 #pragma unroll
         for (int ib = 0; ib < 4; ++ib) {
@@ -751,6 +808,11 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             mfma16(dv16, kdUJ, kAakB);     // dU^T Aak
 #pragma unroll
             for (int e = 0; e < 4; ++e) dv[e] += dv16[e];
+            if constexpr (ACC) {
+                const f32x4_t ad = unpack4(adv[ib]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dv[e] += ad[e];
+            }
             // lane: dV[t0 + lr][16 ib + 4 lq + e]
             store8(rs_dv, (uint32_t(lr) * TS + 16 * ib + 4 * lq) * 2,
                    pack4(dv));
@@ -823,6 +885,15 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             mfma(g.K, d1, Vp[1]);
             return g;
         };
+        if constexpr (ACC) {
+            // the dr and dk cotangents: the next chunk's vector loads (if
+            // any) and the 4 dv stores came after them
+            if (cn >= 0)
+                __builtin_amdgcn_s_waitcnt(0x4f72);  // vmcnt(18)
+            else
+                __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4)
+            asm volatile("" ::: "memory");
+        }
         Acc4 cur = products(0);
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
@@ -876,6 +947,14 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 const float sc = scan16(f1 - fA[e] * gA[e]);
                 dwv[e] = (sc - f1 + tail[e]) * lam4[jb][e];  // dlog d (-e^w)
             }
+            if constexpr (ACC) {
+                const f32x4_t ar = unpack4(adr[jb]), ak = unpack4(adk[jb]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    drv[e] += ar[e];
+                    dkv[e] += ak[e];
+                }
+            }
             const uint32_t o = goff + 32 * jb;
             store8(rs_dr, o, pack4(drv));
             store8(rs_dw, o, pack4(dwv));
@@ -909,7 +988,7 @@ __device__ __forceinline__ void poison(const BwdArgs& A, int tid) {
         A.ds0[bh * NN + e] = __builtin_nanf("");
 }
 
-template <int M>
+template <int M, bool ACC>
 __global__ void __launch_bounds__(BTHREADS)
 wkv7_wave_bwd_kernel(BwdArgs A) {
     BwdFlags& fl = lds_flags;
@@ -933,7 +1012,7 @@ wkv7_wave_bwd_kernel(BwdArgs A) {
     if (wv < NCHAIN)
         chain(A, wv, lane);
     else
-        work<M>(A, wv - NCHAIN, lane);
+        work<M, ACC>(A, wv - NCHAIN, lane);
     // every wait is bounded, so every wave arrives here
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -966,19 +1045,36 @@ hipError_t launch_wave_backward(const WaveBwdArgs& p, hipStream_t stream) {
     A.db = static_cast<bf16_t*>(p.db);
     A.ds0 = p.ds0;
     A.wait = p.wait;
+    A.add_dr = static_cast<const bf16_t*>(p.add_dr);
+    A.add_dk = static_cast<const bf16_t*>(p.add_dk);
+    A.add_dv = static_cast<const bf16_t*>(p.add_dv);
     if (A.BH <= 0 || A.T <= 0) return hipSuccess;
+    const bool acc = A.add_dr || A.add_dk || A.add_dv;
+    const dim3 grid(unsigned(A.BH)), block(BTHREADS);
     switch (p.L / WL) {
         case 1:
-            hipLaunchKernelGGL(wkv7_wave_bwd_kernel<1>, dim3(unsigned(A.BH)),
-                               dim3(BTHREADS), 0, stream, A);
+            if (acc)
+                hipLaunchKernelGGL((wkv7_wave_bwd_kernel<1, true>), grid,
+                                   block, 0, stream, A);
+            else
+                hipLaunchKernelGGL((wkv7_wave_bwd_kernel<1, false>), grid,
+                                   block, 0, stream, A);
             break;
         case 2:
-            hipLaunchKernelGGL(wkv7_wave_bwd_kernel<2>, dim3(unsigned(A.BH)),
-                               dim3(BTHREADS), 0, stream, A);
+            if (acc)
+                hipLaunchKernelGGL((wkv7_wave_bwd_kernel<2, true>), grid,
+                                   block, 0, stream, A);
+            else
+                hipLaunchKernelGGL((wkv7_wave_bwd_kernel<2, false>), grid,
+                                   block, 0, stream, A);
             break;
         default:
-            hipLaunchKernelGGL(wkv7_wave_bwd_kernel<4>, dim3(unsigned(A.BH)),
-                               dim3(BTHREADS), 0, stream, A);
+            if (acc)
+                hipLaunchKernelGGL((wkv7_wave_bwd_kernel<4, true>), grid,
+                                   block, 0, stream, A);
+            else
+                hipLaunchKernelGGL((wkv7_wave_bwd_kernel<4, false>), grid,
+                                   block, 0, stream, A);
             break;
     }
     return hipGetLastError();

@@ -69,6 +69,7 @@ EXPORTED_SYMBOLS = (
     "rwkv7m_timemix_wkv_output",
     "rwkv7m_timemix_wkv_output_backward",
     "rwkv7m_timemix_wkv_output_backward_noalloc",
+    "rwkv7m_timemix_wkv_backward",
     "rwkv7m_screen_slot_scan_workspace_floats",
     "rwkv7m_screen_slot_scan",
     "rwkv7m_screen_slot_scan_backward",
@@ -146,6 +147,9 @@ def load_library(path: str | None = None):
         lib.rwkv7m_timemix_wkv_output_backward_noalloc.restype = i32
         lib.rwkv7m_timemix_wkv_output_backward_noalloc.argtypes = (
             dims + [vp] * 8 + [f64] + [vp] * 9 + [vp])
+        lib.rwkv7m_timemix_wkv_backward.restype = i32
+        lib.rwkv7m_timemix_wkv_backward.argtypes = (
+            [i32] + [i64] * 4 + [vp] * 10 + [i64] + [vp] * 11)
         sdims = [i32, i64, i64, i64, i64]
         lib.rwkv7m_screen_slot_scan_workspace_floats.restype = i64
         lib.rwkv7m_screen_slot_scan_workspace_floats.argtypes = [i64] * 4
@@ -309,8 +313,13 @@ def forward_with_aux(r, w, k, v, neg_kk, kka, initial_state, *,
 
 
 def backward(r, w, k, v, neg_kk, kka, initial_state, dy, ds_t, checkpoints,
-             interval, *, layout: str = "tbhn"):
-    """Seven input cotangents (primal order, primal dtypes)."""
+             interval, *, layout: str = "tbhn", add=None):
+    """Seven input cotangents (primal order, primal dtypes).
+
+    ``add``: ``(dr_add, dk_add, dv_add)`` (each a vector-shaped tensor or
+    None), cotangents of r, k and v from their other uses, summed into dr,
+    dk and dv in fp32 before rounding (``rwkv7m_timemix_wkv_backward``;
+    batch-major vectors only)."""
     lib = load_library()
     r, w, k, v, a, b = _vecs(r, w, k, v, neg_kk, kka)
     s0 = initial_state.contiguous()
@@ -325,6 +334,25 @@ def backward(r, w, k, v, neg_kk, kka, initial_state, dy, ds_t, checkpoints,
     ds_c = None if ds_t is None else ds_t.to(torch.float32).contiguous()
     grads = [torch.empty_like(r) for _ in range(6)]
     ds0 = torch.empty_like(s0)
+    if add is not None:
+        if layout != "bthn":
+            raise ValueError("added cotangents need batch-major vectors "
+                             "(layout='bthn')")
+        adds = []
+        for t, name in zip(add, ("dr_add", "dk_add", "dv_add")):
+            if t is not None and tuple(t.shape) != tuple(r.shape):
+                raise ValueError(f"{name} has shape {tuple(t.shape)}; "
+                                 f"expected {tuple(r.shape)}")
+            adds.append(None if t is None else t.to(r.dtype).contiguous())
+        fn = "rwkv7m_timemix_wkv_backward"
+        with torch.cuda.device(dev):
+            rc = lib.rwkv7m_timemix_wkv_backward(
+                _dtype_code(r), T, B, H, N, _p(r), _p(w), _p(k), _p(v),
+                _p(a), _p(b), _p(s0), _p(dy_c), _p(ds_c), _p(ckpt), ci,
+                *(_p(t) for t in adds), *(_p(g) for g in grads), _p(ds0),
+                _stream(dev))
+        _check(rc, fn)
+        return (*grads, ds0)
     fn = "rwkv7m_wkv7_backward" + sfx
     with torch.cuda.device(dev):
         rc = getattr(lib, fn)(

@@ -18,8 +18,9 @@ fuses and jax autodiff differentiates:
 Here each of those pieces is one HIP kernel per direction
 (``kernels/timemix_hip.py``), and ``time_mix_wkv`` chains producers, the
 batch-major WKV kernels and the consumer with no transpose and no
-intermediate elementwise pass: in the backward the consumer's cotangent of
-``k'`` is folded into the producers' backward kernel.
+intermediate elementwise pass: in the backward the consumer's cotangents of
+``r``, ``k'`` and ``v`` are summed into the WKV backward's own stores
+(``rwkv7m_timemix_wkv_backward``).
 
 Activations are batch-major ``[B, T, C]`` (C = H * N) as in the reference
 model, bf16 or fp32; parameters any float dtype, their gradients returned
@@ -113,7 +114,7 @@ def wkv7_output(y, r, k, v, g, r_k, ln_scale, ln_bias,
 class _TimeMixWKV(torch.autograd.Function):
     """Producers -> batch-major WKV -> consumer as one custom VJP; the
     backward runs consumer, WKV and producer kernels in turn, with the
-    consumer's cotangent of k' added inside the producers' kernel."""
+    consumer's cotangents of r, k' and v added inside the WKV backward."""
 
     @staticmethod
     def forward(ctx, r, w_raw, k, v, a, g, k_k, k_a, r_k, ln_scale, ln_bias,
@@ -150,11 +151,13 @@ class _TimeMixWKV(torch.autograd.Function):
         dy, dr_c, dk_c, dv_c, dg, drk, dsc, dbi = timemix_hip.output_backward(
             y, r_h, kp, v_h, g, r_k, ln_scale, ln_bias, dout, N, eps)
         dr, dw, dk_w, dv, dnkk, dkka, ds0 = wkv_hip.backward(
-            r_h, w, kp, v_h, nkk, kka, s0, dy, ds_t, *aux, layout="bthn")
+            r_h, w, kp, v_h, nkk, kka, s0, dy, ds_t, *aux, layout="bthn",
+            add=(dr_c.view(r_h.shape), dk_c.view(r_h.shape),
+                 dv_c.view(r_h.shape)))
         dx, dk, da, dkk_p, dka_p = timemix_hip.inputs_backward(
-            w_raw, k, a, k_k, k_a, dw, dk_w, dnkk, dkka, N, dk_out2=dk_c)
-        dr = (dr + dr_c).reshape(w_raw.shape)
-        dv = (dv + dv_c).reshape(w_raw.shape)
+            w_raw, k, a, k_k, k_a, dw, dk_w, dnkk, dkka, N)
+        dr = dr.reshape(w_raw.shape)
+        dv = dv.reshape(w_raw.shape)
         return (dr, dx, dk, dv, da, dg, _pgrad(dkk_p, k_k),
                 _pgrad(dka_p, k_a), _pgrad(drk, r_k), _pgrad(dsc, ln_scale),
                 _pgrad(dbi, ln_bias), ds0, None, None, None)

@@ -306,6 +306,27 @@ def test_library_rejects_bad_requests_before_any_device_call(lib):
     assert b"rwkv7m_wkv7_backward_bthn" in lib.rwkv7m_last_error()
 
 
+def test_summed_backward_checks_its_arguments_before_any_device_call(lib):
+    # rwkv7m_timemix_wkv_backward: the backward's own checks (named after
+    # the entry point), then an added cotangent that is an output buffer is
+    # refused; the fake addresses below are never dereferenced
+    fake = [ctypes.c_void_p(0x1000 * (i + 1)) for i in range(10)]
+    outs = [ctypes.c_void_p(0x100000 * (i + 1)) for i in range(7)]
+    fn = lib.rwkv7m_timemix_wkv_backward
+    assert fn(1, 2, 1, 1, 64, *fake, -1, None, None, None, *outs, None) == 1
+    assert b"rwkv7m_timemix_wkv_backward: checkpoint_interval" in \
+        lib.rwkv7m_last_error()
+    assert fn(1, 2, 1, 1, 64, *fake, 16, None, None, None, *outs[:6], None,
+              None) == 1
+    assert b"ds0 is NULL" in lib.rwkv7m_last_error()
+    for i, o in ((0, 0), (1, 2), (2, 3), (0, 3), (2, 5)):
+        adds = [None, None, None]
+        adds[i] = outs[o]
+        assert fn(1, 2, 1, 1, 64, *fake, 16, *adds, *outs, None) == 1
+        assert b"may not be an output buffer" in lib.rwkv7m_last_error()
+    assert lib.rwkv7m_wkv7_last_path() == b""
+
+
 def test_noalloc_consumer_backward_rejects_sizes_beyond_its_scratch(lib):
     # 2^22 channels need more partial rows than the built-in scratch holds:
     # rejected by the size check, before any pointer is used or any device

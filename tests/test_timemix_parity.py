@@ -323,8 +323,9 @@ def test_time_mix_wkv_matches_oracle_chain(hip_lib, dtype, T, H, N):
 
 def test_time_mix_wkv_equals_separate_ops(hip_lib):
     # producers, batch-major WKV and consumer as three autograd ops give the
-    # fused section's results (the fused backward adds the two cotangents of
-    # k' in fp32 inside the producers' kernel, the separate ops in bf16)
+    # fused section's results (the fused backward adds the consumer's
+    # cotangents of r, k' and v in fp32 inside the WKV backward, the
+    # separate ops in bf16)
     import rwkv7m_amd
     from rwkv7m_amd.kernels.wkv_ffi import unregister_wkv_ffi_backend
     from rwkv7m_amd.timemix import time_mix_wkv, wkv7_inputs, wkv7_output

@@ -213,7 +213,24 @@ def _vecs(r, w, k, v, neg_kk, kka):
     if out[0].dim() != 4:
         raise ValueError(f"r must have shape [time, batch, heads, head_size]"
                          f" (or [batch, time, ...]), got {tuple(out[0].shape)}")
+    # the kernels take bare pointers: every vector must have r's shape and
+    # dtype, or they would read past a shorter one
+    for x, name in zip(out[1:], ("w", "k", "v", "neg_kk", "kka")):
+        if x.shape != out[0].shape or x.dtype != out[0].dtype:
+            raise ValueError(f"{name} has shape {tuple(x.shape)} and dtype "
+                             f"{x.dtype}; expected {tuple(out[0].shape)} "
+                             f"{out[0].dtype} like r")
     return out
+
+
+def _state(s, shape, name):
+    """A contiguous fp32 state of ``shape`` ([B, H, N, N]) or raise."""
+    if tuple(s.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(s.shape)}; expected "
+                         f"{tuple(shape)}")
+    if s.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32, got {s.dtype}")
+    return s.contiguous()
 
 
 def _layout(layout: str, r: torch.Tensor):
@@ -275,11 +292,16 @@ def forward(r, w, k, v, neg_kk, kka, initial_state, *, out_state=None,
     """y, S_T = WKV(...). ``out_state`` may be ``initial_state`` (in place)."""
     lib = load_library()
     r, w, k, v, a, b = _vecs(r, w, k, v, neg_kk, kka)
-    s0 = initial_state.contiguous()
-    dev = _dev((r, w, k, v, a, b, s0))
     sfx, T, B, H, N = _layout(layout, r)
+    s0 = _state(initial_state, (B, H, N, N), "initial_state")
     y = torch.empty_like(r)
+    if out_state is not None:
+        if out_state.shape != s0.shape or out_state.dtype != torch.float32 \
+                or not out_state.is_contiguous():
+            raise ValueError("out_state must be a contiguous float32 state "
+                             "like initial_state")
     s_t = out_state if out_state is not None else torch.empty_like(s0)
+    dev = _dev((r, w, k, v, a, b, s0, s_t))
     fn = "rwkv7m_wkv7_forward" + sfx
     with torch.cuda.device(dev):
         rc = getattr(lib, fn)(
@@ -294,9 +316,9 @@ def forward_with_aux(r, w, k, v, neg_kk, kka, initial_state, *,
     """((y, S_T), (checkpoints, interval)) for the backward pass."""
     lib = load_library()
     r, w, k, v, a, b = _vecs(r, w, k, v, neg_kk, kka)
-    s0 = initial_state.contiguous()
-    dev = _dev((r, w, k, v, a, b, s0))
     sfx, T, B, H, N = _layout(layout, r)
+    s0 = _state(initial_state, (B, H, N, N), "initial_state")
+    dev = _dev((r, w, k, v, a, b, s0))
     ci = int(checkpoint_interval) or default_checkpoint_interval(r.dtype, N)
     nck = checkpoint_count(T, ci)
     y = torch.empty_like(r)
@@ -322,16 +344,21 @@ def backward(r, w, k, v, neg_kk, kka, initial_state, dy, ds_t, checkpoints,
     batch-major vectors only)."""
     lib = load_library()
     r, w, k, v, a, b = _vecs(r, w, k, v, neg_kk, kka)
-    s0 = initial_state.contiguous()
-    dev = _dev((r, w, k, v, a, b, s0, checkpoints))
     sfx, T, B, H, N = _layout(layout, r)
+    s0 = _state(initial_state, (B, H, N, N), "initial_state")
+    dev = _dev((r, w, k, v, a, b, s0, checkpoints))
     ci = int(interval)
     if checkpoints.shape != (checkpoint_count(T, ci), B, H, N, N) or \
             checkpoints.dtype != checkpoint_dtype(r.dtype, N, ci):
         raise ValueError("checkpoints do not match time, shape and interval")
     ckpt = checkpoints.contiguous()
+    if dy is not None and tuple(dy.shape) != tuple(r.shape):
+        raise ValueError(f"dy has shape {tuple(dy.shape)}; expected "
+                         f"{tuple(r.shape)}")
     dy_c = None if dy is None else dy.to(r.dtype).contiguous()
-    ds_c = None if ds_t is None else ds_t.to(torch.float32).contiguous()
+    ds_c = None if ds_t is None else _state(ds_t.to(torch.float32),
+                                            (B, H, N, N), "ds_t")
+    _dev([t for t in (r, dy_c, ds_c) if t is not None])
     grads = [torch.empty_like(r) for _ in range(6)]
     ds0 = torch.empty_like(s0)
     if add is not None:
@@ -344,6 +371,7 @@ def backward(r, w, k, v, neg_kk, kka, initial_state, dy, ds_t, checkpoints,
                 raise ValueError(f"{name} has shape {tuple(t.shape)}; "
                                  f"expected {tuple(r.shape)}")
             adds.append(None if t is None else t.to(r.dtype).contiguous())
+        _dev([r] + [t for t in adds if t is not None])
         fn = "rwkv7m_timemix_wkv_backward"
         with torch.cuda.device(dev):
             rc = lib.rwkv7m_timemix_wkv_backward(
@@ -368,13 +396,16 @@ def decode_inplace(r, w, k, v, neg_kk, kka, state):
     [1,B,H,N]. Returns y with the vectors' shape."""
     lib = load_library()
     shape = r.shape
-    r, w, k, v, a, b = (x.reshape(-1, *x.shape[-3:]).contiguous()
-                        for x in (r, w, k, v, neg_kk, kka))
+    r, w, k, v, a, b = _vecs(*(x.reshape(-1, *x.shape[-3:])
+                               for x in (r, w, k, v, neg_kk, kka)))
     if r.shape[0] != 1 or not state.is_contiguous():
         raise ValueError("decode_inplace takes one token and a contiguous "
                          "state")
-    dev = _dev((r, w, k, v, a, b, state))
     _, B, H, N = r.shape
+    if tuple(state.shape) != (B, H, N, N) or state.dtype != torch.float32:
+        raise ValueError(f"state must be a float32 [{B}, {H}, {N}, {N}] "
+                         f"tensor, got {state.dtype} {tuple(state.shape)}")
+    dev = _dev((r, w, k, v, a, b, state))
     y = torch.empty_like(r)
     with torch.cuda.device(dev):
         rc = lib.rwkv7m_wkv7_decode_inplace(

@@ -519,3 +519,29 @@ def test_screening_config_checks_follow_the_reference():
         ScreeningConfig(**base, write_rel_floor=-1.0)
     mod = StateLevelScreening(ScreeningConfig(**base))
     assert mod.compute_dtype == torch.float32
+
+
+def test_hip_wrappers_check_shapes_dtypes_and_devices_first(lib):
+    # the ctypes wrappers hand the kernels bare pointers: a shorter vector,
+    # a state of the wrong shape or dtype, or a host tensor is refused
+    # before any call (no GPU needed)
+    from rwkv7m_amd.kernels import wkv_hip
+    T, B, H, N = 3, 2, 2, 64
+    vec = [torch.zeros(T, B, H, N, dtype=torch.bfloat16) for _ in range(6)]
+    s0 = torch.zeros(B, H, N, N)
+    short = list(vec)
+    short[1] = torch.zeros(T - 1, B, H, N, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="w has shape"):
+        wkv_hip.forward(*short, s0)
+    mixed = list(vec)
+    mixed[4] = vec[4].float()
+    with pytest.raises(ValueError, match="neg_kk has shape"):
+        wkv_hip.forward_with_aux(*mixed, s0)
+    with pytest.raises(ValueError, match="initial_state has shape"):
+        wkv_hip.forward(*vec, torch.zeros(B, H, N, N - 1))
+    with pytest.raises(TypeError, match="initial_state must be float32"):
+        wkv_hip.forward(*vec, s0.double())
+    with pytest.raises(RuntimeError, match="needs GPU tensors"):
+        wkv_hip.forward(*vec, s0)
+    with pytest.raises(ValueError, match="state must be a float32"):
+        wkv_hip.decode_inplace(*(v[:1] for v in vec), torch.zeros(B, H, N, 2))

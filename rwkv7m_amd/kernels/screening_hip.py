@@ -30,6 +30,22 @@ def _f32(t):
     return None if t is None else t.detach().to(torch.float32).contiguous()
 
 
+def _check(named):
+    """Each (name, tensor or None, shape): the exact shape, and every given
+    tensor on one GPU (the kernels take bare pointers)."""
+    for name, t, shape in named:
+        if t is not None and tuple(t.shape) != tuple(shape):
+            raise ValueError(f"{name} has shape {tuple(t.shape)}; expected "
+                             f"{tuple(shape)}")
+    return wkv_hip._dev([t for _, t, _ in named if t is not None])
+
+
+def _scalar(name, t):
+    if t.numel() != 1:
+        raise ValueError(f"{name} must hold one value, got shape "
+                         f"{tuple(t.shape)}")
+
+
 def _workspace(B, T, M, ds, dev):
     n = wkv_hip.load_library().rwkv7m_screen_slot_scan_workspace_floats(
         B, T, M, ds)
@@ -45,7 +61,8 @@ def slot_scan(base, slot_term, mu, slots0):
     base = _c(base)
     B, T, ds = base.shape
     M = slot_term.shape[0]
-    dev = wkv_hip._dev([base, slots0])
+    dev = _check([("base", base, (B, T, ds)), ("slot_term", slot_term, (M, ds)),
+                  ("mu", mu, (M,)), ("slots0", slots0, (B, M, ds))])
     st, mu_, s0 = _f32(slot_term), _f32(mu), _f32(slots0)
     seq = torch.empty(B, T, M, ds, dtype=base.dtype, device=dev)
     s_t = torch.empty(B, M, ds, dtype=torch.float32, device=dev)
@@ -68,7 +85,10 @@ def slot_scan_backward(base, slot_term, mu, slots_seq, d_slots_seq,
     d_slots_seq = _c(d_slots_seq).to(base.dtype)
     B, T, ds = base.shape
     M = slot_term.shape[0]
-    dev = wkv_hip._dev([base, slots_seq, d_slots_seq])
+    dev = _check([("base", base, (B, T, ds)), ("slot_term", slot_term, (M, ds)),
+                  ("mu", mu, (M,)), ("slots_seq", slots_seq, (B, T, M, ds)),
+                  ("d_slots_seq", d_slots_seq, (B, T, M, ds)),
+                  ("d_slots_T", d_slots_T, (B, M, ds))])
     st, mu_ = _f32(slot_term), _f32(mu)
     dst = _f32(d_slots_T)
     d_pre = torch.empty(B, T, M, ds, dtype=torch.float32, device=dev)
@@ -102,7 +122,10 @@ def read(q, proj, tau, age_w, cfg, dv):
     q, proj = _f32(q), _c(proj)
     B, T, M, kv = proj.shape
     dk = kv - dv
-    dev = wkv_hip._dev([q, proj])
+    _scalar("tau", tau)
+    dev = _check([("q", q, (B, T, dk)), ("proj", proj, (B, T, M, kv)),
+                  ("age_w", age_w, (B, T, M) if age_w is not None and
+                   age_w.dim() == 3 else (B, M)), ("tau", tau, tau.shape)])
     aw = _f32(age_w)
     u = torch.empty(B, T, dv, dtype=proj.dtype, device=dev)
     rel = torch.empty(B, T, M, dtype=torch.float32, device=dev)
@@ -124,7 +147,11 @@ def read_backward(q, proj, tau, age_w, cfg, dv, du, d_rel=None):
     du = _c(du).to(proj.dtype)
     B, T, M, kv = proj.shape
     dk = kv - dv
-    dev = wkv_hip._dev([q, proj, du])
+    _scalar("tau", tau)
+    dev = _check([("q", q, (B, T, dk)), ("proj", proj, (B, T, M, kv)),
+                  ("age_w", age_w, (B, T, M) if age_w is not None and
+                   age_w.dim() == 3 else (B, M)), ("tau", tau, tau.shape),
+                  ("du", du, (B, T, dv)), ("d_rel", d_rel, (B, T, M))])
     aw, dr = _f32(age_w), _f32(d_rel)
     dq = torch.empty(B, T, dk, dtype=torch.float32, device=dev)
     dproj = torch.empty_like(proj)
@@ -141,6 +168,13 @@ def read_backward(q, proj, tau, age_w, cfg, dv, du, d_rel=None):
 
 
 def _write_common(base, slot_term, slot_embed, kw, q_w, tau_w, mu):
+    B, T, ds = base.shape
+    M, dk = slot_term.shape[0], kw.shape[-1]
+    _scalar("tau_w", tau_w)
+    _check([("base", base, (B, T, ds)), ("slot_term", slot_term, (M, ds)),
+            ("slot_embed", slot_embed, (M, ds)), ("k_proj_w", kw, (ds, dk)),
+            ("q_w", q_w, (B, T, dk)), ("tau_w", tau_w, tau_w.shape),
+            ("mu", mu, (M,))])
     return (_c(base), _f32(slot_term), _f32(slot_embed), _f32(kw), _f32(q_w),
             tau_w.detach().to(torch.float32).reshape(1).contiguous(),
             _f32(mu))
@@ -157,7 +191,8 @@ def write(base, slot_term, slot_embed, kw, q_w, tau_w, mu, floor, eps,
                                                    mu)
     B, T, ds = base.shape
     M, dk = st.shape[0], kw_.shape[1]
-    dev = wkv_hip._dev([base, slots0])
+    dev = _check([("base", base, (B, T, ds)), ("slots0", slots0, (B, M, ds)),
+                  ("ages0", ages0, (B, M))])
     f = dict(dtype=torch.float32, device=dev)
     seq = torch.empty(B, T, M, ds, dtype=base.dtype, device=dev)
     s32 = torch.empty(B, T, M, ds, **f)
@@ -186,7 +221,13 @@ def write_backward(base, slot_term, slot_embed, kw, q_w, tau_w, mu, floor,
                                                    mu)
     B, T, ds = base.shape
     M, dk = st.shape[0], kw_.shape[1]
-    dev = wkv_hip._dev([base, slots32])
+    dev = _check([("base", base, (B, T, ds)),
+                  ("slots32", slots32, (B, T, M, ds)),
+                  ("d_slots_seq", d_slots_seq, (B, T, M, ds)),
+                  ("d_slots_T", d_slots_T, (B, M, ds)),
+                  ("d_rel_w", d_rel_w, (B, T, M)),
+                  ("d_ages_seq", d_ages_seq, (B, T, M)),
+                  ("d_ages_T", d_ages_T, (B, M))])
     f = dict(dtype=torch.float32, device=dev)
     d_seq = _c(d_slots_seq).to(base.dtype)
     outs = [torch.empty(B, T, M, ds, **f), torch.empty(B, M, ds, **f),

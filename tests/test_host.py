@@ -545,3 +545,30 @@ def test_hip_wrappers_check_shapes_dtypes_and_devices_first(lib):
         wkv_hip.forward(*vec, s0)
     with pytest.raises(ValueError, match="state must be a float32"):
         wkv_hip.decode_inplace(*(v[:1] for v in vec), torch.zeros(B, H, N, 2))
+
+
+def test_screening_wrappers_check_shapes_and_devices_first(lib):
+    # the screening entry points take bare pointers too: mismatched shapes
+    # and host tensors are refused before any call (no GPU needed)
+    from rwkv7m_amd.kernels import screening_hip as sh
+    B, T, M, ds, dk = 2, 5, 3, 8, 4
+    base = torch.zeros(B, T, ds)
+    with pytest.raises(ValueError, match="slots0 has shape"):
+        sh.slot_scan(base, torch.zeros(M, ds), torch.zeros(M),
+                     torch.zeros(B, M, ds + 1))
+    with pytest.raises(ValueError, match="mu has shape"):
+        sh.slot_scan(base, torch.zeros(M, ds), torch.zeros(M + 1),
+                     torch.zeros(B, M, ds))
+    with pytest.raises(RuntimeError, match="needs GPU tensors"):
+        sh.slot_scan(base, torch.zeros(M, ds), torch.zeros(M),
+                     torch.zeros(B, M, ds))
+    with pytest.raises(ValueError, match="k_proj_w has shape"):
+        sh.write(base, torch.zeros(M, ds), torch.zeros(M, ds),
+                 torch.zeros(ds + 1, dk), torch.zeros(B, T, dk),
+                 torch.zeros(()), torch.zeros(M), 1e-3, 1e-6,
+                 torch.zeros(B, M, ds), torch.zeros(B, M))
+    with pytest.raises(ValueError, match="tau_w must hold one value"):
+        sh.write(base, torch.zeros(M, ds), torch.zeros(M, ds),
+                 torch.zeros(ds, dk), torch.zeros(B, T, dk),
+                 torch.zeros(2), torch.zeros(M), 1e-3, 1e-6,
+                 torch.zeros(B, M, ds), torch.zeros(B, M))

@@ -114,3 +114,31 @@ def test_summed_backward_needs_batch_major_vectors(hip):
     with pytest.raises(ValueError, match="batch-major"):
         hip.backward(*vecs, s0, inp["dy"].cuda(), None, *aux,
                      add=(vecs[0], None, None))
+
+
+def test_summed_backward_at_the_headline_shape(hip):
+    # config 2's shape in the model's batch-major layout, the wave backward
+    # at the default interval, every head
+    from rwkv7m_amd.synthetic import config_inputs
+    case = "summed backward B8 T4096 H32 N64 bf16 batch-major"
+    print("case:", case, flush=True)
+    inp = config_inputs(2, device="cuda", generator="torch")
+    vecs = [inp[n].transpose(0, 1).contiguous() for n in NAMES]
+    dy = inp["dy"].transpose(0, 1).contiguous()
+    s0, ds_t = inp["s0"], inp["ds_t"]
+    del inp
+    (_, _), aux = hip.forward_with_aux(*vecs, s0, layout="bthn")
+    plain = hip.backward(*vecs, s0, dy, ds_t, *aux, layout="bthn")
+    g = torch.Generator(device="cuda").manual_seed(7)
+    adds = [torch.randn(vecs[0].shape, generator=g, device="cuda").mul_(
+        float(plain[i].float().abs().max())).to(torch.bfloat16)
+        for i in (0, 2, 3)]
+    summed = hip.backward(*vecs, s0, dy, ds_t, *aux, layout="bthn",
+                          add=tuple(adds))
+    assert hip.last_path() == "wave_backward"
+    torch.cuda.synchronize()
+    hip.device_status()
+    for i, name in ((1, "dw"), (4, "dneg_kk"), (5, "dkka"), (6, "ds0")):
+        assert torch.equal(summed[i], plain[i]), (case, name)
+    for j, (i, name) in enumerate(((0, "dr"), (2, "dk"), (3, "dv"))):
+        _check_sum(name, summed[i], plain[i], adds[j], 2.0 ** -8, case)

@@ -165,3 +165,29 @@ def test_config3_decode_128_steps_in_place(hip):
     _check("y", _vec_slice(y, bs, hs), ey, f"{case} sampled heads")
     _check("state", _state_slice(state, bs, hs), es, f"{case} sampled heads",
            tol=1e-4)
+
+
+def test_config2_batch_major_equals_time_major_every_head(hip):
+    # the model's own batch-major layout at the headline shape: the same
+    # kernels with a 4 KB token stride instead of 32 KB; every output of
+    # every head bit-identical to the time-major call
+    case = "config 2: B8 T4096 H32 N64 bf16 batch-major vs time-major"
+    print("case:", case, flush=True)
+    inp = config_inputs(2, device="cuda", generator="torch")
+    want, _ = _train_call(hip, inp, 16)
+    bt = {n: inp[n].transpose(0, 1).contiguous() for n in NAMES + ("dy",)}
+    del inp["dy"]
+    vecs = [bt[n] for n in NAMES]
+    (y, s_t), aux = hip.forward_with_aux(*vecs, inp["s0"],
+                                         checkpoint_interval=16,
+                                         layout="bthn")
+    assert hip.last_path() == "wave_forward"
+    grads = hip.backward(*vecs, inp["s0"], bt["dy"], inp["ds_t"], *aux,
+                         layout="bthn")
+    assert hip.last_path() == "wave_backward"
+    torch.cuda.synchronize()
+    hip.device_status()
+    got = (y, s_t, *grads)
+    for name, g, w in zip(OUT_NAMES, got, want):
+        g = g if name in STATE_OUTS else g.transpose(0, 1)
+        assert torch.equal(g, w), f"{case} {name} differs"

@@ -191,3 +191,23 @@ def test_config2_batch_major_equals_time_major_every_head(hip):
     for name, g, w in zip(OUT_NAMES, got, want):
         g = g if name in STATE_OUTS else g.transpose(0, 1)
         assert torch.equal(g, w), f"{case} {name} differs"
+
+
+def test_config2_inference_forward_and_repeats_are_bit_identical(hip):
+    # at the headline shape, every head: the inference forward (no
+    # checkpoints) gives the training forward's y and S_T bit for bit, and a
+    # second training call repeats every output bit for bit
+    case = "config 2: inference forward and repeated training call"
+    print("case:", case, flush=True)
+    inp = config_inputs(2, device="cuda", generator="torch")
+    first, _ = _train_call(hip, inp, 16)
+    again, _ = _train_call(hip, inp, 16)
+    for name, a, b in zip(OUT_NAMES, first, again):
+        assert torch.equal(a, b), f"{case} {name}: repeat differs"
+    del again
+    y, s_t = hip.forward(*(inp[n] for n in NAMES), inp["s0"])
+    assert hip.last_path() == "wave_forward"
+    torch.cuda.synchronize()
+    hip.device_status()
+    assert torch.equal(y, first[0]), f"{case} y"
+    assert torch.equal(s_t, first[1]), f"{case} s_t"

@@ -35,6 +35,10 @@ CASES = [
      "wave_backward"),
     ("exact pass L16 T80", 80, 1, 3, 64, torch.bfloat16, 16, True,
      "wave_backward"),
+    ("exact pass L32 T75", 75, 2, 3, 64, torch.bfloat16, 32, True,
+     "wave_backward"),
+    ("exact pass L64 T140", 140, 1, 3, 64, torch.bfloat16, 64, True,
+     "wave_backward"),
     ("sequential fp32 N16 T23", 23, 2, 2, 16, torch.float32, 16, False,
      "seq_backward"),
     ("sequential L128 T150", 150, 1, 2, 64, torch.bfloat16, 128, False,

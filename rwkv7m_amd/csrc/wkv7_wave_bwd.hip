@@ -165,16 +165,26 @@ struct BwdArgs {
 
 // Wait until pred(*p) holds: 1 when it does, 0 when the workgroup aborted
 // first, -1 when the poll budget ran out (then the workgroup is marked
-// failed and aborted).
+// failed and aborted).  A chain (raised issue priority) that has to wait
+// drops to normal priority until pred holds, so that its polls do not take
+// issue slots from the worker sharing its SIMD.  The abort word is read on
+// every eighth poll.
 template <typename Pred>
 __device__ __forceinline__ int wait_for(const WaitCfg& wc, int* p, int lane,
-                                        Pred pred) {
-    for (int it = 0; it < wc.limit; ++it) {
+                                        Pred pred, bool chain = false) {
+    if (pred(__builtin_amdgcn_readfirstlane(lds_load(p)))) {
+        asm volatile("" ::: "memory");
+        return 1;
+    }
+    if (chain) __builtin_amdgcn_s_setprio(0);
+    for (int it = 1; it < wc.limit; ++it) {  // wc.limit polls in all
         if (pred(__builtin_amdgcn_readfirstlane(lds_load(p)))) {
             asm volatile("" ::: "memory");
+            if (chain) __builtin_amdgcn_s_setprio(2);
             return 1;
         }
-        if (__builtin_amdgcn_readfirstlane(lds_load(&lds_flags.abort)) != 0)
+        if ((it & 7) == 7 &&
+            __builtin_amdgcn_readfirstlane(lds_load(&lds_flags.abort)) != 0)
             return 0;
         __builtin_amdgcn_s_sleep(1);
     }
@@ -245,9 +255,9 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
 
         // the chunk's map (its per-column factors are in LDS by then)
         if (wait_for(A.wait, &fl.d_done[w], lane,
-                     [&](int x) { return x >= kord; }) <= 0 ||
+                     [&](int x) { return x >= kord; }, true) <= 0 ||
             wait_for(A.wait, &fl.map_ready[w], lane,
-                     [&](int x) { return x >= kord + 1; }) <= 0) {
+                     [&](int x) { return x >= kord + 1; }, true) <= 0) {
             done = false;
             break;
         }
@@ -307,7 +317,7 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
         // D(P) by P I and summed over i by a product with ones (exact for
         // bf16 values, fp32 accumulation)
         if (wait_for(A.wait, &fl.s_ready[w], lane,
-                     [&](int x) { return x == c; }) <= 0) {
+                     [&](int x) { return x == c; }, true) <= 0) {
             done = false;
             break;
         }

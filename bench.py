@@ -53,7 +53,7 @@ def parse_args():
                    help="replays of the HIP-graph-captured step to time "
                         "(-1: as many as --steps; 0: skip)")
     p.add_argument("--config", type=int, default=2,
-                   help="BASELINE config index (2 = the headline shape; "
+                   help="benchmark configuration index (2 = the headline shape; "
                         "3 = the decode loop)")
     p.add_argument("--chunk", type=int, default=0,
                    help="checkpoint interval / chunk length (0 = library "

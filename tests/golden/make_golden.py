@@ -76,7 +76,7 @@ def kat_step():
 
 def main():
     kat_step()
-    # BASELINE config 0 (fp32 forward, tiny_config shape), full size.
+    # benchmark configuration 0 (fp32 forward, tiny_config shape), full size.
     _write("config0_fwd.npz", config_inputs(0), bf16=False, with_grads=False)
     # small bf16 fwd+bwd with ragged T (not a multiple of any chunk length)
     _write("bf16_t37_n16.npz",

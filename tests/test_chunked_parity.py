@@ -4,8 +4,8 @@ float64 CPU oracle.
 The MFMA path serves bf16 inputs with head size 64 and the checkpoint
 intervals in MFMA_INTERVALS; any other interval runs the sequential kernels.
 Every case asserts which kernels served it (rwkv7m_wkv7_last_path), so a
-case is labelled by the path it provably took.  Tolerance (BASELINE north
-star): max|diff| <= 2e-2 * max|oracle| per tensor.  Cases cover partial
+case is labelled by the path it provably took.  Tolerance (the bf16 bound
+of the path's accuracy target): max|diff| <= 2e-2 * max|oracle| per tensor.  Cases cover partial
 final chunks, every interval, nonzero initial state and state cotangent, and
 decays strong enough to force the in-kernel exact sequential fallback.
 """

@@ -1,12 +1,12 @@
-"""GPU parity at the full sizes of the benchmark configurations (BASELINE
-configs 2, 3 and 4), on the library's default kernel paths.
+"""GPU parity at the full sizes of the benchmark configurations 2, 3 and 4
+(rwkv7m_amd.synthetic.config_inputs), on the library's default kernel paths.
 
 Two checks per configuration:
 
 * Sampled (batch, head) slices at full T against the float64 oracle.  Heads
   are independent, so each slice is an exact sub-problem of the full call.
-  Tolerance: max|diff| <= 2e-2 * max|oracle| per tensor (BASELINE.json's
-  bf16 bound; the reference's accelerator tier uses the same order,
+  Tolerance: max|diff| <= 2e-2 * max|oracle| per tensor (the path's bf16
+  accuracy target; the reference's accelerator tier uses the same order,
   tests/test_wkv_pallas_accelerator.py:39-71).
 * Every head through a size-independent property: the same training call at
   two chunk lengths (configs 2 and 4), or the decode kernel against the

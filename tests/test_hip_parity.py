@@ -1,7 +1,7 @@
 """GPU parity of the HIP kernels (through the C ABI) against the CPU oracle
 and the committed golden fixtures.
 
-Tolerances: fp32 inputs -- max|diff| / max|oracle|
+Tolerances (the path's accuracy targets): fp32 inputs -- max|diff| / max|oracle|
 <= 1e-4 per tensor; bf16 inputs with an fp32 state -- <= 2e-2 of the
 oracle's max magnitude per tensor. The oracle is float64 on the same inputs.
 """

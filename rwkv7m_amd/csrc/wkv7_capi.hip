@@ -321,7 +321,13 @@ int backward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     p.add_dr = add_dr;
     p.add_dk = add_dk;
     p.add_dv = add_dv;
-    if (use_chunked(dtype, N, ci, T, lay.ts,
+    // the wave backward addresses vectors and checkpoints with 32-bit byte
+    // offsets below 2^31
+    const int64_t nck = (T + ci - 1) / ci + 1;
+    const bool small = d.vec_elems * 2 < (int64_t(1) << 31) &&
+                       nck * B * H * N * N * 2 < (int64_t(1) << 31);
+    if (small &&
+        use_chunked(dtype, N, ci, T, lay.ts,
                     {r, w, k, v, neg_kk, kka, dy, ds_t, checkpoints, dr, dw,
                      dk, dv, dneg_kk, dkka, ds0, add_dr, add_dk, add_dv})) {
         rwkv7m::WaveBwdArgs c{};

@@ -25,9 +25,14 @@
 // uses the chunk-start identity (S_0 and D_0 fixed; exact for the chunk)
 //
 //   dlog d_t = sum_{t' < t} (b db + k dk - r dr)_{t'} - sum_{t' <= t} (a da)_{t'}
-//              + sum_i D_0[i, :] S_0[i, :]
+//              + E_0,   E_0 = sum_i D_0[i, :] S_0[i, :]
 //
-// and dw = dlog d * (-e^w).  These are the reference's reverse equations
+// and dw = dlog d * (-e^w).  E is needed at every other chunk boundary
+// only: the chunk at an even position of the reverse order takes it at its
+// start; the chunk at the next (odd) position, one chunk earlier in time,
+// takes the same value as its end value E_L and recovers its own start
+// value through the same identity, E_0 = E_L - sum over the chunk of
+// (b db + k dk - r dr - a da).  These are the reference's reverse equations
 // (src/rwkv7m/kernels/wkv_pallas_gpu.py:221-257) summed over a chunk; states
 // come from checkpoints, never from dividing by the decay.  Inside an
 // interval of m chunks, the start state of chunk c + 1 is recomputed from
@@ -37,9 +42,10 @@
 //   * waves 0..3, the chains: chain ib holds rows 16 ib .. 16 ib + 15 of the
 //     fp32 cotangent D in registers and walks the chunks in reverse.  Per
 //     chunk it writes bf16(D) into the chunk's worker's D buffer, takes the
-//     worker's map (B^, W^, Q^, dY), advances D_0 (2 + 8 MFMAs: D_0 depends
-//     only on rows of D, so the four chains are independent) and adds its
-//     rows' share of sum_i D_0 S_0 for the worker;
+//     worker's map (B^, W^, Q^, dY), advances D_0 (2 + 4 MFMAs: D_0 depends
+//     only on rows of D, so the four chains are independent) and, at even
+//     positions, adds its rows' share of sum_i D_0 S_0 for the two workers
+//     that use it;
 //   * waves 4..7, the workers: worker w takes chunks nch - 1 - w,
 //     nch - 1 - w - 4, ...  It loads the chunk's vectors, forms the factors,
 //     the 16 x 16 matrices and the inverse in registers, publishes the map,
@@ -69,56 +75,11 @@ constexpr int NWORK = 4;
 constexpr int BTHREADS = 64 * (NCHAIN + NWORK);
 constexpr int NN = WN * WN;
 
-// Element (i, j) of a 64 x 64 bf16 S/D buffer: 16-byte unit (i, j / 8) at
-// ((i / 8) * 8 + j / 8) * 8 + i % 8, so one global_load_lds of 64 lanes
-// (16 bytes each, at consecutive units) fills rows 8g .. 8g + 7.
-__device__ __forceinline__ int sd_off(int i, int j) {
-    return ((((i >> 3) << 3) + (j >> 3)) * 8 + (i & 7)) * 8 + (j & 7);
-}
-
-__device__ __forceinline__ uint2 sd_read4(const bf16_t* buf, int i, int j) {
-    return *reinterpret_cast<const uint2*>(buf + sd_off(i, j));
-}
-
-__device__ __forceinline__ void sd_write4(bf16_t* buf, int i, int j, uint2 v) {
-    *reinterpret_cast<uint2*>(buf + sd_off(i, j)) = v;
-}
-
-// x32 fragment of rows 16 rb .. 16 rb + 15 over the 32 columns of pair p:
-// lane (q, r) takes row 16 rb + r, columns 32p + 4q .. + 3 (slots 0..3) and
-// 32p + 16 + 4q .. + 3 (slots 4..7).  As an A operand: the rows (m = i,
-// k = j); as a B operand: their transpose (k = j, n = i).
-__device__ __forceinline__ bf16x8_t frag_rows(const bf16_t* buf, int rb,
-                                              int p, int lane) {
-    const int r = lane & 15, q = lane >> 4;
-    const int i = 16 * rb + r, j = 32 * p + 4 * q;
-    return pk8(as_i16x4(sd_read4(buf, i, j)),
-               as_i16x4(sd_read4(buf, i, j + 16)));
-}
-
-// x32 fragment of columns 16 cb .. 16 cb + 15 over the 32 rows of pair p,
-// by two transposing reads: lane (q, r) takes column 16 cb + r at rows
-// 32p + 4q + e (slots 0..3) and 32p + 16 + 4q + e (slots 4..7).  Lane
-// s = a + 4e of each 16-lane group addresses row 32p + 4q + e, columns
-// 16 cb + 4a .. + 3.  As an A operand: the transpose (m = j, k = i); as a B
-// operand: the matrix (k = i, n = j).
-__device__ __forceinline__ bf16x8_t frag_cols(const bf16_t* buf, int cb,
-                                              int p, int lane) {
-    const int s = lane & 15, q = lane >> 4;
-    const int i = 32 * p + 4 * q + (s >> 2), j = 16 * cb + 4 * (s & 3);
-    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_i16x4_t*)(buf + sd_off(i, j)));
-    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_i16x4_t*)(buf + sd_off(i + 16, j)));
-    return pk8(lo, hi);
-}
-
 // A chunk's hand-over from its worker to the chains, as register images
 // (element [..][lane] is that lane's operand).
 struct BMap {
     bf16x8_t Bh[2][64];  // B~ (T layout pairs): x32 A operands (m = t, k = j)
-    i16x4_t W[4][64];    // D(W^_jb)
-    i16x4_t Q[4][64];    // D(Q^_jb)
+    bf16x8_t QW[4][64];  // D(Q^_jb) (slots 0..3), D(W^_jb) (slots 4..7)
     i16x4_t dY[4][64];   // D(dY_ib)
 };
 
@@ -128,6 +89,7 @@ struct BwdFlags {
     int d_cnt[NWORK];      // chain writes into its D buffer (NCHAIN per chunk)
     int d_done[NWORK];     // chunks whose D buffer the worker has finished
     int tail_cnt[NWORK];   // chain tail partials (NCHAIN per chunk)
+    int tail_used[NWORK];  // odd workers' reads of the even tail (count)
     int s_ready[NWORK];    // chunk whose start state the S buffer holds
     int s_free[NWORK];     // chunk whose start state the S buffer takes next
     int abort;             // a chunk needs the exact pass: every wave stops
@@ -144,15 +106,22 @@ __shared__ uint4 lds_stage[NWORK][7][2][8][8];
 __shared__ bf16_t lds_S[NWORK][NN];  // the chunk's start state (sd_off)
 __shared__ bf16_t lds_D[NWORK][NN];  // the cotangent of its end state
 __shared__ BMap lds_map[NWORK];
-__shared__ float lds_tail[NWORK][NCHAIN][WN];  // sum_i D_0 S_0 per chain
+// sum_i D_0 S_0 per chain, for the even positions' workers (0 and 2)
+__shared__ float lds_tail[NWORK][NCHAIN][WN];
 __shared__ float lds_eref[NWORK][WN];          // 2^{g_ref} per column
 __shared__ float lds_eLR[NWORK][WN];           // 2^{g_L - g_ref}
 __shared__ float lds_eL[NWORK][WN];            // 2^{g_L}
 __shared__ BwdFlags lds_flags;
 
+// Every byte offset into the vectors and the checkpoints is below 2^31
+// (checked by the host): addresses are a kernel-constant base plus a 32-bit
+// per-lane offset, and a lane with nothing to store or load uses the offset
+// kNoLane, past every buffer's 2^31-byte range.
+constexpr uint32_t kNoLane = 0x80000000u;
 struct BwdArgs {
     int64_t T, BH;
     VecLayout lay;
+    uint32_t ts2;  // bytes per token step of the vectors
     const bf16_t *r, *w, *k, *v, *a, *b, *dy;
     const float* ds_t;
     const bf16_t* ckpt;
@@ -197,15 +166,18 @@ __device__ __forceinline__ f32x4_t unpack_i16(const i16x4_t& x) {
     return unpack4(__builtin_bit_cast(uint2, x));
 }
 
-// A buffer resource over `bytes` bytes at p + off for loads (null p: an
-// empty range, so every load returns zeros); loads at or past the range
-// return zeros.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t in_rsrc(const bf16_t* p,
-                                                        int64_t off,
-                                                        uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<bf16_t*>(p ? p + off : nullptr), 0, p ? int(bytes) : 0,
-        0x00020000);
+// A buffer resource over a whole input tensor (null p: an empty range, so
+// every load returns zeros); loads at offset kNoLane return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t in_rsrc(const bf16_t* p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(p), 0,
+                                             p ? int(kNoLane) : 0,
+                                             0x00020000);
+}
+
+// A buffer resource over a whole output tensor: stores at offset kNoLane
+// are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t whole_rsrc(bf16_t* p) {
+    return __builtin_amdgcn_make_buffer_rsrc(p, 0, int(kNoLane), 0x00020000);
 }
 
 // 8 bytes at byte offset `off` of the buffer.
@@ -282,12 +254,11 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
         if (lane == 0) lds_add(&fl.d_cnt[w], 1);
         const BMap& mp = lds_map[w];
         const bf16x8_t Bh0 = mp.Bh[0][lane], Bh1 = mp.Bh[1][lane];
-        i16x4_t Wt[4], Qt[4];
+        bf16x8_t QW[4];
         f32x4_t eL[4];
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
-            Wt[jb] = mp.W[jb][lane];
-            Qt[jb] = mp.Q[jb][lane];
+            QW[jb] = mp.QW[jb][lane];
             eL[jb] = *reinterpret_cast<const f32x4_t*>(
                 &lds_eL[w][16 * jb + 4 * lq]);
         }
@@ -296,28 +267,36 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
         if (lane == 0) lds_add(&fl.map_taken[w], 1);
 
         // Z = B~ bf16(D diag(2^{g_L - g_ref}))^T = B^ D^T ([t][i]), then
-        // D_0^T = 2^{g_L} D^T + Q^^T dY + W^^T Z (rows of block ib)
+        // D_0^T = 2^{g_L} D^T + Q^^T dY + W^^T Z (rows of block ib), the
+        // two products over t as one K = 32 product: (Q^ | W^)^T (dY ; Z)
         f32x4_t z = zero4();
         mfma(z, Bh0, pk8(sb[0], sb[1]));
         mfma(z, Bh1, pk8(sb[2], sb[3]));
-        const i16x4_t kz = kq(z);
+        const bf16x8_t dYZ = pk8(dYt, kq(z));
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
             f32x4_t acc;
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[e] = Dt[jb][e] * eL[jb][e];
-            mfma16(acc, Qt[jb], dYt);
-            mfma16(acc, Wt[jb], kz);
+            mfma(acc, QW[jb], dYZ);
             Dt[jb] = acc;
         }
 
-        // this block's share of sum_i D_0[i][j] S_0[i][j] for the worker.
-        // P = D_0 * S_0 on the block's tiles D(P^T) is split into bf16 parts
-        // P = P_hi + P_lo (16 significant bits); each part is turned into
-        // D(P) by P I and summed over i by a product with ones (exact for
-        // bf16 values, fp32 accumulation)
+        // The decay gradient needs sum_i D_0[i][j] S_0[i][j] at every other
+        // chunk boundary only: the worker of an even position takes it as
+        // its chunk's start value, and the worker of the next (odd)
+        // position, one chunk earlier in time, as its chunk's end value.
+        if (p & 1) continue;
+        // this block's share for the worker.  P = D_0 * S_0 on the block's
+        // tiles D(P^T) is split into bf16 parts P = P_hi + P_lo (16
+        // significant bits); each part is turned into D(P) by P I and summed
+        // over i by a product with ones (exact for bf16 values, fp32
+        // accumulation)
         if (wait_for(A.wait, &fl.s_ready[w], lane,
-                     [&](int x) { return x == c; }, true) <= 0) {
+                     [&](int x) { return x == c; }, true) <= 0 ||
+            (kord > 0 && wait_for(A.wait, &fl.tail_used[w + 1], lane,
+                                  [&](int x) { return x >= kord; },
+                                  true) <= 0)) {
             done = false;
             break;
         }
@@ -356,24 +335,19 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
 // writes lane l's 16 bytes at 16 l): lane l of load (vector, h) fetches
 // segment l / 8 of token 8h + l % 8; tokens past the end re-read the last
 // token.
-__device__ __forceinline__ void fetch_vecs(const BwdArgs& A, int w, int c,
-                                           int lane) {
+// cb2: byte offset of the chunk's first token of this head; n: its tokens.
+__device__ __forceinline__ void fetch_vecs(const BwdArgs& A, int w,
+                                           uint32_t cb2, int n, int lane) {
     const VecPtrs src{A.r, A.w, A.k, A.v, A.a, A.b, A.dy};
-    const int64_t cbase = int64_t(c) * WL * A.lay.ts +
-                          A.lay.head(int64_t(blockIdx.x), WN);
-    const int64_t left = A.T - int64_t(c) * WL;
-    const int n = int(left < WL ? left : WL);
-    const uint32_t TS = uint32_t(A.lay.ts);
     const int ldu = lane & 7, ldseg = lane >> 3;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int t = 8 * h + ldu;
         const uint32_t off =
-            (uint32_t(t < n ? t : n - 1) * TS + 8 * ldseg) * sizeof(bf16_t);
+            cb2 + uint32_t(t < n ? t : n - 1) * A.ts2 + 16 * ldseg;
 #pragma unroll
         for (int vv = 0; vv < 7; ++vv)
-            dma16(src.get(vv) + cbase, off,
-                  lds_addr(&lds_stage[w][vv][h][0][0]));
+            dma16(src.get(vv), off, lds_addr(&lds_stage[w][vv][h][0][0]));
     }
 }
 
@@ -383,13 +357,12 @@ __device__ __forceinline__ void fetch_vecs(const BwdArgs& A, int w, int c,
 template <int M>
 __device__ __forceinline__ void fetch_state(const BwdArgs& A, int w, int c,
                                             int lane) {
-    const bf16_t* base =
-        A.ckpt + (int64_t(c / M) * A.BH + int64_t(blockIdx.x)) * NN;
-    const int ldu = lane & 7, ldseg = lane >> 3;
-    const uint32_t off = uint32_t(ldu * WN + 8 * ldseg) * sizeof(bf16_t);
+    const uint32_t off =
+        (uint32_t(c / M) * uint32_t(A.BH) + blockIdx.x) * uint32_t(NN * 2) +
+        uint32_t(((lane & 7) * WN + 8 * (lane >> 3)) * 2);
 #pragma unroll
     for (int g = 0; g < 8; ++g)
-        dma16(base + 8 * g * WN, off, lds_addr(&lds_S[w][512 * g]));
+        dma16(A.ckpt, off + 8 * g * WN * 2, lds_addr(&lds_S[w][512 * g]));
 }
 
 // The T layout read of vector vv from worker w's stage: token lr, columns
@@ -399,6 +372,19 @@ __device__ __forceinline__ uint2 read_t(int w, int vv, int kb, int lane) {
     const bf16_t* p = reinterpret_cast<const bf16_t*>(
         &lds_stage[w][vv][lr >> 3][2 * kb + (lq >> 1)][lr & 7]);
     return *reinterpret_cast<const uint2*>(p + 4 * (lq & 1));
+}
+
+// The J layout tile D(X_jb) of vector vv from worker w's stage by one
+// transposing read: lane s of each 16-lane group addresses token 4 lq + s / 4,
+// columns 16 jb + 4 (s % 4) .. + 3 (segment 2 jb + (s % 4) / 2, half s % 2),
+// and receives X[4 lq + e][16 jb + s].
+__device__ __forceinline__ i16x4_t stage_j(int w, int vv, int jb, int lane) {
+    const int s = lane & 15, q = lane >> 4;
+    const int t = 4 * q + (s >> 2);
+    const bf16_t* p = reinterpret_cast<const bf16_t*>(
+        &lds_stage[w][vv][t >> 3][2 * jb + ((s & 3) >> 1)][t & 7]);
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_i16x4_t*)(p + 4 * (s & 1)));
 }
 
 // The J layout tile D(X_kb) of a T layout tile of X: X_kb I, with the
@@ -418,10 +404,10 @@ __device__ __forceinline__ i16x4_t to_j(const i16x4_t& t, const i16x4_t& kI) {
 template <int M, bool ACC>
 __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
     const int64_t bh = blockIdx.x;
-    const int64_t hoff = A.lay.head(bh, WN);
-    const int64_t T = A.T;
-    const int nch = int((T + WL - 1) / WL);
-    const uint32_t TS = uint32_t(A.lay.ts);
+    const uint32_t hoff2 = uint32_t(A.lay.head(bh, WN)) * 2;
+    const int T = int(A.T);
+    const int nch = (T + WL - 1) / WL;
+    const uint32_t ts2 = A.ts2;
     constexpr int m = M;
     // the worker of chunk c + 1 (one position earlier in the reverse order),
     // whose start state chunk c's end state is
@@ -432,7 +418,9 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
     BMap& map = lds_map[w];
 
     if (nch - 1 - w >= 0) {
-        fetch_vecs(A, w, nch - 1 - w, lane0);
+        const int c0 = nch - 1 - w;
+        fetch_vecs(A, w, uint32_t(c0) * WL * ts2 + hoff2,
+                   T - c0 * WL < WL ? T - c0 * WL : WL, lane0);
         if ((nch - 1 - w) % m == 0) fetch_state<M>(A, w, nch - 1 - w, lane0);
     }
 
@@ -451,15 +439,16 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             for (int e = 0; e < 4; ++e) id[e] = (4 * lq + e == lr) ? 1.f : 0.f;
             kI = kq(id);
         }
+        // the zero half of a K = 16 product run as a K = 32 one
+        const i16x4_t kZero = {0, 0, 0, 0};
         const int c = nch - 1 - p;
         const int cn = c - NWORK;  // this worker's next chunk
-        const int64_t t0 = int64_t(c) * WL;
-        const int n = int(T - t0 < WL ? T - t0 : WL);
+        const int n = T - c * WL < WL ? T - c * WL : WL;
         const bool valid = lr < n;
-        // this chunk's rows of the token-major outputs: the lanes of tokens
-        // past the end (lr >= n) store at or past obytes, dropped
-        const int64_t gbase = t0 * A.lay.ts + hoff;
-        const uint32_t obytes = (uint32_t(n - 1) * TS + WN) * 2;
+        // byte offset of the chunk's first token, and of this lane's token
+        // row of the token-major outputs (kNoLane past the end: dropped)
+        const uint32_t cb2 = uint32_t(c) * WL * ts2 + hoff2;
+        const uint32_t row2 = valid ? cb2 + uint32_t(lr) * ts2 : kNoLane;
         const bool starts = c % m == 0;  // S_0 is checkpoint c / m
         const bool feeds = c % m != m - 1 && c + 1 < nch;  // S_0 of c + 1
         // the vectors.  Vector memory operations complete in issue order, and
@@ -485,15 +474,22 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         for (int vv = 0; vv < 7; ++vv)
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) raw[vv][kb] = read_t(w, vv, kb, lane);
+        // v and dy in the J layout (products over t), straight from the stage
+        i16x4_t jV[4], jdY[4];
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            jV[jb] = stage_j(w, 3, jb, lane);
+            jdY[jb] = stage_j(w, 6, jb, lane);
+        }
         lds_drain();
         // the cotangents added to this chunk's dv (value blocks ib) and dr,
         // dk (key blocks jb), at the lanes' own output offsets
         uint2 adv[4], adr[4], adk[4];
         if constexpr (ACC) {
-            const __amdgpu_buffer_rsrc_t rv = in_rsrc(A.add_dv, gbase, obytes),
-                                         rr = in_rsrc(A.add_dr, gbase, obytes),
-                                         rk = in_rsrc(A.add_dk, gbase, obytes);
-            const uint32_t lo0 = (uint32_t(lr) * TS + 4 * lq) * 2;
+            const __amdgpu_buffer_rsrc_t rv = in_rsrc(A.add_dv),
+                                         rr = in_rsrc(A.add_dr),
+                                         rk = in_rsrc(A.add_dk);
+            const uint32_t lo0 = row2 + 8 * lq;
 #pragma unroll
             for (int ib = 0; ib < 4; ++ib) adv[ib] = load8(rv, lo0 + 32 * ib);
 #pragma unroll
@@ -503,7 +499,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             }
         }
         // the stage is free: the next chunk's vectors load during this one
-        if (cn >= 0) fetch_vecs(A, w, cn, lane);
+        if (cn >= 0) fetch_vecs(A, w, cb2 - NWORK * WL * ts2, WL, lane);
         if (n < WL) {
             // padding tokens: zero vectors and w = -inf (bf16), so that
             // they decay by nothing
@@ -515,6 +511,15 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 for (int kb = 0; kb < 4; ++kb)
                     raw[vv][kb] = valid ? raw[vv][kb] : pad;
             }
+            // the J tiles hold tokens 4 lq + e
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (4 * lq + e >= n) {
+                        jV[jb][e] = 0;
+                        jdY[jb][e] = 0;
+                    }
         }
 
         // ---- factors (T layout) ------------------------------------------
@@ -676,18 +681,13 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) y[e] *= erj;
             mfma16(y, kArbA, kW);
-            map.W[jb][lane] = kW;
-            map.Q[jb][lane] = kq(y);
+            map.QW[jb][lane] = pk8(kq(y), kW);
         }
         const bf16x8_t Bhp0 = pk8(tB[0], tB[1]), Bhp1 = pk8(tB[2], tB[3]);
         map.Bh[0][lane] = Bhp0;
         map.Bh[1][lane] = Bhp1;
-        i16x4_t jdY[4];
 #pragma unroll
-        for (int ib = 0; ib < 4; ++ib) {
-            jdY[ib] = to_j(as_i16x4(raw[6][ib]), kI);
-            map.dY[ib][lane] = jdY[ib];
-        }
+        for (int ib = 0; ib < 4; ++ib) map.dY[ib][lane] = jdY[ib];
         lds_drain();
         if (lane == 0) lds_store(&fl.map_ready[w], kord + 1);
 
@@ -739,13 +739,12 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         i16x4_t kXT[4];
 #pragma unroll
         for (int ib = 0; ib < 4; ++ib) {
-            const i16x4_t jV = to_j(as_i16x4(raw[3][ib]), kI);
-            f32x4_t u = zero4(), av = zero4();
+            // Aak V as a K = 32 product with a zero half, accumulated with
+            // the K = 64 products
+            f32x4_t u = zero4();
             mfma(u, Ahp0, frag_rows(S, ib, 0, lane));
             mfma(u, Ahp1, frag_rows(S, ib, 1, lane));
-            mfma16(av, kAakA, jV);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) u[e] += av[e];
+            mfma(u, pk8(kAakA, kZero), pk8(jV[ib], jV[ib]));
             const i16x4_t kU = kq(u);  // D(U_ib): B = U, A = U^T
             f32x4_t xt = zero4();
             mfma16(xt, kU, kMinv);  // X^T = U^T Minv^T
@@ -765,8 +764,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                     f32x4_t acc;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) acc[e] = s0[e] * el[e];
-                    mfma16(acc, kBh[jpb], kXJ);
-                    mfma16(acc, kKh[jpb], jV);
+                    mfma(acc, pk8(kBh[jpb], kKh[jpb]), pk8(kXJ, jV[ib]));
                     sd_write4(Sn, 16 * ib + lr, 16 * jpb + 4 * lq, pack4(acc));
                 }
             }
@@ -784,7 +782,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                      [&](int x) { return x >= NCHAIN * (kord + 1); }) <= 0)
             break;
         const bf16x8_t Khp0 = pk8(tK[0], tK[1]), Khp1 = pk8(tK[2], tK[3]);
-        const __amdgpu_buffer_rsrc_t rs_dv = out_rsrc(A.dv + gbase, obytes);
+        const __amdgpu_buffer_rsrc_t rs_dv = whole_rsrc(A.dv);
         if constexpr (ACC) {
             // the dv cotangents: the 8 dr, dk loads and the next chunk's 14
             // vector loads (if any) came after them
@@ -799,33 +797,29 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         for (int ib = 0; ib < 4; ++ib) {
             const bf16x8_t d0 = frag_rows(D, ib, 0, lane);
             const bf16x8_t d1 = frag_rows(D, ib, 1, lane);
-            f32x4_t dx = zero4(), dxy = zero4();
+            f32x4_t dx = zero4();
             mfma(dx, Bhp0, d0);
             mfma(dx, Bhp1, d1);
-            mfma16(dxy, kArbTA, jdY[ib]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) dx[e] += dxy[e];
+            mfma(dx, pk8(kArbTA, kZero), pk8(jdY[ib], jdY[ib]));
             const i16x4_t kdX = kq(dx);
             f32x4_t du = zero4(), dut = zero4();
             mfma16(du, kMinvT, kdX);   // dU = Minv^T dX (J)
             mfma16(dut, kdX, kMinvT);  // dU^T = dX^T Minv (T)
             kdUT[ib] = kq(dut);
             const i16x4_t kdUJ = kq(du);
-            f32x4_t dv = zero4(), dv16 = zero4();
+            // D K^^T + dY^T Ark + dU^T Aak, the last two as one K = 32
+            // product
+            f32x4_t dv = zero4();
             mfma(dv, d0, Khp0);
             mfma(dv, d1, Khp1);
-            mfma16(dv16, jdY[ib], kArkB);  // dY^T Ark
-            mfma16(dv16, kdUJ, kAakB);     // dU^T Aak
-#pragma unroll
-            for (int e = 0; e < 4; ++e) dv[e] += dv16[e];
+            mfma(dv, pk8(jdY[ib], kdUJ), pk8(kArkB, kAakB));
             if constexpr (ACC) {
                 const f32x4_t ad = unpack4(adv[ib]);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) dv[e] += ad[e];
             }
             // lane: dV[t0 + lr][16 ib + 4 lq + e]
-            store8(rs_dv, (uint32_t(lr) * TS + 16 * ib + 4 * lq) * 2,
-                   pack4(dv));
+            store8(rs_dv, row2 + (16 * ib + 4 * lq) * 2, pack4(dv));
         }
 
         // ---- cotangents of the 16 x 16 matrices (K = 64 over i) -----------
@@ -858,20 +852,30 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         const i16x4_t kgAak = kq(mask4(gAak, lr, lq, true, true));
         const i16x4_t kgAakT = kq(mask4(gAakT, lr, lq, true, false));
 
-        // ---- the chains' shares of sum_i D_0 S_0 -------------------------
-        if (wait_for(A.wait, &fl.tail_cnt[w], lane,
+        // the B operands of the K = 32 products that add the 16 x 16
+        // cotangents' terms to dR~, dA~, dB~, dK~
+        const bf16x8_t kgR2 = pk8(kgArbT, kgArkT), kgA2 = pk8(kgAabT, kgAakT);
+        const bf16x8_t kgB2 = pk8(kgAab, kgArb), kgK2 = pk8(kgAak, kgArk);
+
+        // ---- the chains' shares of sum_i D_0 S_0 at the boundary they
+        // formed it: this chunk's start (even positions, worker tw = w) or
+        // its end, the start of chunk c + 1 (odd positions, tw = w - 1) ----
+        const int tw = w & ~1;
+        const bool odd = (w & 1) != 0;
+        const float oddf = odd ? 1.f : 0.f;
+        if (wait_for(A.wait, &fl.tail_cnt[tw], lane,
                      [&](int x) { return x >= NCHAIN * (kord + 1); }) <= 0)
             break;
 
         // ---- per column block: dR~, dA~, dB~, dK~ and the input gradients -
         // (tiles of the transposes: lane holds token lr, columns
         // 16 jb + 4 lq + e, the T layout)
-        const uint32_t goff = (uint32_t(lr) * TS + 4 * lq) * 2;
-        const __amdgpu_buffer_rsrc_t rs_dr = out_rsrc(A.dr + gbase, obytes),
-                                     rs_dw = out_rsrc(A.dw + gbase, obytes),
-                                     rs_dk = out_rsrc(A.dk + gbase, obytes),
-                                     rs_da = out_rsrc(A.da + gbase, obytes),
-                                     rs_db = out_rsrc(A.db + gbase, obytes);
+        const uint32_t goff = row2 + 8 * lq;
+        const __amdgpu_buffer_rsrc_t rs_dr = whole_rsrc(A.dr),
+                                     rs_dw = whole_rsrc(A.dw),
+                                     rs_dk = whole_rsrc(A.dk),
+                                     rs_da = whole_rsrc(A.da),
+                                     rs_db = whole_rsrc(A.db);
         // the products over i of column block jb, issued one block ahead
         // of their use: their latency is hidden by the previous block's
         // element-wise work
@@ -913,7 +917,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
 #pragma unroll
             for (int ch = 0; ch < NCHAIN; ++ch)
                 tl[ch] = *reinterpret_cast<const f32x4_t*>(
-                    &lds_tail[w][ch][16 * jb + 4 * lq]);
+                    &lds_tail[tw][ch][16 * jb + 4 * lq]);
             Acc4 nxt;
             if (jb < 3) nxt = products(jb + 1);
             f32x4_t tail = zero4();
@@ -929,33 +933,41 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             }
             const i16x4_t jA = to_j(tA[jb], kI), jB = to_j(tB[jb], kI);
             const i16x4_t jK = to_j(tK[jb], kI), jR = to_j(tR[jb], kI);
-            mfma16(gR, jB, kgArbT);  // + B~^T dArb^T
-            mfma16(gR, jK, kgArkT);  // + K~^T dArk^T
-            mfma16(gA, jB, kgAabT);  // + B~^T dAab^T
-            mfma16(gA, jK, kgAakT);  // + K~^T dAak^T
-            mfma16(gB, jA, kgAab);   // + A~^T dAab
-            mfma16(gB, jR, kgArb);   // + R~^T dArb
-            mfma16(gK, jA, kgAak);   // + A~^T dAak
-            mfma16(gK, jR, kgArk);   // + R~^T dArk
+            const bf16x8_t jBK = pk8(jB, jK), jAR = pk8(jA, jR);
+            mfma(gR, jBK, kgR2);  // + B~^T dArb^T + K~^T dArk^T
+            mfma(gA, jBK, kgA2);  // + B~^T dAab^T + K~^T dAak^T
+            mfma(gB, jAR, kgB2);  // + A~^T dAab + R~^T dArb
+            mfma(gK, jAR, kgK2);  // + A~^T dAak + R~^T dArk
 
             // input gradients.  The decay gradient's terms r dr, b db, k dk,
             // a da are R~ dR~, B~ dB~, K~ dK~, A~ dA~, and
-            // dlog d_t = S_t - f1_t + tail with S the inclusive prefix sum of
-            // f1 - A~ dA~ (f1 = B~ dB~ + K~ dK~ - R~ dR~)
+            // dlog d_t = S_t - f1_t + E_0 with S the inclusive prefix sum of
+            // f1 - A~ dA~ (f1 = B~ dB~ + K~ dK~ - R~ dR~) and E_0 the
+            // chunk's sum_i D_0 S_0 at its start.  The end value E_L gives
+            // it through the same identity: E_0 = E_L - S_15 (the chunk-end
+            // identity, dlog d_t = E_L - sum_{t' > t} (f1 - a da)_{t'} - f1_t)
             const f32x4_t fA = unpack_i16(tA[jb]), fR = unpack_i16(tR[jb]);
             const f32x4_t fB = unpack_i16(tB[jb]), fK = unpack_i16(tK[jb]);
             const f32x4_t eg = unpack_i16(keg[jb]), eng = unpack_i16(keng[jb]);
             const f32x4_t ep = unpack_i16(kep[jb]);
             f32x4_t drv, dwv, dkv, dav, dbv;
+            float f1[4], sc[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 drv[e] = gR[e] * eg[e];
                 dav[e] = gA[e] * ep[e];
                 dbv[e] = gB[e] * eng[e];
                 dkv[e] = gK[e] * eng[e];
-                const float f1 = fB[e] * gB[e] + fK[e] * gK[e] - fR[e] * gR[e];
-                const float sc = scan16(f1 - fA[e] * gA[e]);
-                dwv[e] = (sc - f1 + tail[e]) * lam4[jb][e];  // dlog d (-e^w)
+                f1[e] = fB[e] * gB[e] + fK[e] * gK[e] - fR[e] * gR[e];
+                sc[e] = f1[e] - fA[e] * gA[e];
+            }
+            scan16x4(sc);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // odd positions: E_0 = E_L - S_15 (the scan's last token)
+                const float e0 =
+                    tail[e] - oddf * pin_lanes(row_bcast<15>(sc[e]));
+                dwv[e] = (sc[e] - f1[e] + e0) * lam4[jb][e];  // dlog d (-e^w)
             }
             if constexpr (ACC) {
                 const f32x4_t ar = unpack4(adr[jb]), ak = unpack4(adk[jb]);
@@ -979,6 +991,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         if (lane == 0) {
             lds_store(&fl.d_done[w], kord + 1);
             lds_store(&fl.s_free[w], cn);
+            if (odd) lds_store(&fl.tail_used[w], kord + 1);
         }
         if (cn >= 0 && cn % m == 0) fetch_state<M>(A, w, cn, lane);
     }
@@ -1011,6 +1024,7 @@ wkv7_wave_bwd_kernel(BwdArgs A) {
         fl.d_cnt[tid] = 0;
         fl.d_done[tid] = 0;
         fl.tail_cnt[tid] = 0;
+        fl.tail_used[tid] = 0;
         fl.s_ready[tid] = -1;
         fl.s_free[tid] = nch - 1 - tid;
     }
@@ -1055,6 +1069,7 @@ hipError_t launch_wave_backward(const WaveBwdArgs& p, hipStream_t stream) {
     A.db = static_cast<bf16_t*>(p.db);
     A.ds0 = p.ds0;
     A.wait = p.wait;
+    A.ts2 = uint32_t(p.lay.ts * 2);
     A.add_dr = static_cast<const bf16_t*>(p.add_dr);
     A.add_dk = static_cast<const bf16_t*>(p.add_dk);
     A.add_dv = static_cast<const bf16_t*>(p.add_dv);

@@ -146,6 +146,21 @@ __device__ __forceinline__ float scan16(float x) {
     return x;
 }
 
+// scan16 of four independent values in lock step: each DPP step is issued
+// for all four before the next, so the steps' read-after-write distance is
+// covered by the other values' instructions instead of wait states.
+__device__ __forceinline__ void scan16x4(float (&x)[4]) {
+#define RWKV7M_SHR4(n)                                                      \
+    for (int e = 0; e < 4; ++e)                                             \
+        x[e] += __int_as_float(__builtin_amdgcn_update_dpp(                 \
+            0, __float_as_int(x[e]), 0x110 + (n), 0xF, 0xF, true))
+    RWKV7M_SHR4(1);
+    RWKV7M_SHR4(2);
+    RWKV7M_SHR4(4);
+    RWKV7M_SHR4(8);
+#undef RWKV7M_SHR4
+}
+
 // Sum over each row of 16 lanes, in every lane of the row (DPP row_ror).
 __device__ __forceinline__ float row_sum16(float x) {
 #define RWKV7M_ROR(n)                                                       \
@@ -212,6 +227,50 @@ __device__ __forceinline__ f32x4_t mask4(f32x4_t x, int r, int q, bool strict,
         x[e] = keep ? x[e] : 0.f;
     }
     return x;
+}
+
+// Element (i, j) of a 64 x 64 bf16 S/D buffer: 16-byte unit (i, j / 8) at
+// ((i / 8) * 8 + j / 8) * 8 + i % 8, so one global_load_lds of 64 lanes
+// (16 bytes each, at consecutive units) fills rows 8g .. 8g + 7.
+__device__ __forceinline__ int sd_off(int i, int j) {
+    return ((((i >> 3) << 3) + (j >> 3)) * 8 + (i & 7)) * 8 + (j & 7);
+}
+
+__device__ __forceinline__ uint2 sd_read4(const bf16_t* buf, int i, int j) {
+    return *reinterpret_cast<const uint2*>(buf + sd_off(i, j));
+}
+
+__device__ __forceinline__ void sd_write4(bf16_t* buf, int i, int j, uint2 v) {
+    *reinterpret_cast<uint2*>(buf + sd_off(i, j)) = v;
+}
+
+// x32 fragment of rows 16 rb .. 16 rb + 15 over the 32 columns of pair p:
+// lane (q, r) takes row 16 rb + r, columns 32p + 4q .. + 3 (slots 0..3) and
+// 32p + 16 + 4q .. + 3 (slots 4..7).  As an A operand: the rows (m = i,
+// k = j); as a B operand: their transpose (k = j, n = i).
+__device__ __forceinline__ bf16x8_t frag_rows(const bf16_t* buf, int rb,
+                                              int p, int lane) {
+    const int r = lane & 15, q = lane >> 4;
+    const int i = 16 * rb + r, j = 32 * p + 4 * q;
+    return pk8(as_i16x4(sd_read4(buf, i, j)),
+               as_i16x4(sd_read4(buf, i, j + 16)));
+}
+
+// x32 fragment of columns 16 cb .. 16 cb + 15 over the 32 rows of pair p,
+// by two transposing reads: lane (q, r) takes column 16 cb + r at rows
+// 32p + 4q + e (slots 0..3) and 32p + 16 + 4q + e (slots 4..7).  Lane
+// s = a + 4e of each 16-lane group addresses row 32p + 4q + e, columns
+// 16 cb + 4a .. + 3.  As an A operand: the transpose (m = j, k = i); as a B
+// operand: the matrix (k = i, n = j).
+__device__ __forceinline__ bf16x8_t frag_cols(const bf16_t* buf, int cb,
+                                              int p, int lane) {
+    const int s = lane & 15, q = lane >> 4;
+    const int i = 32 * p + 4 * q + (s >> 2), j = 16 * cb + 4 * (s & 3);
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_i16x4_t*)(buf + sd_off(i, j)));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_i16x4_t*)(buf + sd_off(i + 16, j)));
+    return pk8(lo, hi);
 }
 
 // LDS DMA (global_load_lds_dwordx4): lane l's 16 bytes at gbase + voff (a

@@ -129,9 +129,9 @@ int rwkv7m_timemix_wkv_output_backward_noalloc(
  * sums the two cotangents of each (nnx_model.py:695-727; the reference's
  * training step differentiates the time mix as a whole).  The sums are
  * formed in fp32 and rounded once, inside the backward's own stores, so no
- * separate pass re-reads the three gradients.  The added cotangents must
- * not overlap an output buffer (RWKV7M_ERR_INVALID_ARGUMENT when one is
- * the same pointer).
+ * separate pass re-reads the three gradients.  An added cotangent may not
+ * share a byte with an output buffer (RWKV7M_ERR_INVALID_ARGUMENT, checked
+ * over the buffers' byte ranges), and ds0 may not share a byte with ds_t.
  */
 int rwkv7m_timemix_wkv_backward(
     int dtype, int64_t T, int64_t B, int64_t H, int64_t N, const void *r,

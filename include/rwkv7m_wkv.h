@@ -148,7 +148,9 @@ int rwkv7m_wkv7_forward_with_aux(int dtype, int64_t T, int64_t B, int64_t H,
  * Replaces WKVFFIBackend.backward (wkv_ffi.py:34; called at wkv.py:216) and
  * the reference's backward kernel (wkv_pallas_gpu.py:167-282, :433-530).
  * Vector gradients are written in the vector dtype, dS0 in fp32.
- * dy may be NULL (treated as zeros) and so may ds_t.
+ * dy may be NULL (treated as zeros) and so may ds_t.  ds0 may not share a
+ * byte with ds_t (RWKV7M_ERR_INVALID_ARGUMENT): a head that needs the exact
+ * sequential pass reads dS_T again after its dS0 holds the pass's mark.
  */
 int rwkv7m_wkv7_backward(int dtype, int64_t T, int64_t B, int64_t H,
                          int64_t N, const void *r, const void *w,

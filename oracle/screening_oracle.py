@@ -254,6 +254,39 @@ def read_forward_torch(x, h_base, slots, ages, usage, P, cfg,
     return torch.stack(hs, 1), slots, usage
 
 
+# Tolerances of scalar_grad_error.  fp32: 1e-4 of the gradient's own
+# magnitude, unless the sum cancelled by more than 1000x (|grad| / sum|terms|
+# below HEAVY_CANCELLATION), where fp32 rounding of the terms alone (6e-8
+# each) can exceed 1e-4 of the result: then 1e-6 of the terms' sum (about 16
+# fp32 roundings).  bf16: 4e-3 of the terms' sum (two bf16 roundings, 2^-8).
+SCALAR_TOL_FP32 = 1e-4
+SCALAR_TOL_FP32_TERMS = 1e-6
+HEAVY_CANCELLATION = 1e-3
+SCALAR_TOL_BF16 = 4e-3
+
+
+def scalar_grad_error(got, want, term_scale, fp32):
+    """Error of a scalar parameter's gradient ``got`` against ``want``, whose
+    terms (one per output element: cotangent times derivative) have
+    magnitudes summing to ``term_scale``.
+
+    Returns ``(error, ratio, basis, tol)`` with ``ratio = |want| /
+    term_scale``, the share of the terms that survives their cancellation.
+    fp32: relative to ``|want|`` (tol 1e-4) unless ``ratio <
+    HEAVY_CANCELLATION``, then relative to ``term_scale`` (tol 1e-6).  bf16:
+    relative to ``term_scale`` (tol 4e-3).  Relative to ``term_scale``, a
+    relative error ``e`` of the gradient reads as ``e * ratio`` and a missing
+    group of terms as its share of ``term_scale``."""
+    ratio = abs(want) / term_scale if term_scale > 0 else 0.0
+    terms = abs(got - want) / term_scale if term_scale > 0 else abs(got - want)
+    if fp32 and ratio >= HEAVY_CANCELLATION:
+        return abs(got - want) / abs(want), ratio, "own magnitude", \
+            SCALAR_TOL_FP32
+    if fp32:
+        return terms, ratio, "terms", SCALAR_TOL_FP32_TERMS
+    return terms, ratio, "terms", SCALAR_TOL_BF16
+
+
 def default_config(**overrides):
     """The reference's ScreeningConfig defaults (screening.py:92-121) as a
     dict, with overrides."""

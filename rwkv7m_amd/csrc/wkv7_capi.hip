@@ -148,6 +148,15 @@ rwkv7m::VecLayout vec_layout(bool batch_major, int64_t T, int64_t B,
     return l;
 }
 
+// Whether the byte ranges [a, a + abytes) and [b, b + bbytes) share a byte
+// (a NULL pointer or an empty range shares none).
+bool overlaps(const void* a, int64_t abytes, const void* b, int64_t bbytes) {
+    if (!a || !b || abytes <= 0 || bbytes <= 0) return false;
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a);
+    const uintptr_t b0 = reinterpret_cast<uintptr_t>(b);
+    return a0 < b0 + uintptr_t(bbytes) && b0 < a0 + uintptr_t(abytes);
+}
+
 bool all_aligned16(std::initializer_list<const void*> ptrs) {
     for (const void* p : ptrs)
         if (p && !aligned16(p)) return false;
@@ -281,15 +290,23 @@ int backward_impl(const char* fn, int dtype, int64_t T, int64_t B, int64_t H,
     RWKV7M_TRY(need(ds0, st, fn, "ds0"));
     RWKV7M_TRY(need(checkpoints, vecs, fn, "checkpoints"));
     // an added cotangent is read while the gradients are written: it may
-    // not be an output buffer (a head handed to the exact pass is written
-    // twice)
+    // not share a byte with an output buffer (a head handed to the exact
+    // pass is written twice, and its second pass reads the cotangent again)
+    const int64_t vbytes =
+        d.vec_elems * (dtype == RWKV7M_DTYPE_BF16 ? 2 : 4);
     for (const void* a : {add_dr, add_dk, add_dv})
         for (const void* o : {dr, dw, dk, dv, dneg_kk, dkka})
-            if (a && a == o)
+            if (overlaps(a, vbytes, o, vbytes))
                 return fail(RWKV7M_ERR_INVALID_ARGUMENT,
                             std::string(fn) +
-                                ": an added cotangent may not be an output "
-                                "buffer");
+                                ": an added cotangent may not overlap an "
+                                "output buffer");
+    // dS_T is read again by the exact pass of a head whose dS0 already holds
+    // the pass's mark: dS0 may not share a byte with it
+    const int64_t sbytes = d.state_elems * 4;
+    if (overlaps(ds0, sbytes, ds_t, sbytes))
+        return fail(RWKV7M_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": ds0 may not overlap ds_t");
     if (d.state_elems == 0) return RWKV7M_OK;
     if (T == 0) return copy_or_clear(ds0, ds_t, d.state_elems, s);
     const rwkv7m::VecLayout lay = vec_layout(batch_major, T, B, H, N);

@@ -3,8 +3,10 @@
 
 Two checks per configuration:
 
-* Sampled (batch, head) slices at full T against the float64 oracle.  Heads
-  are independent, so each slice is an exact sub-problem of the full call.
+* Sampled (batch, head) slices at full T against the float64 oracle, for
+  every checkpoint interval of the MFMA kernels (16, the default, 32 and
+  64).  Heads are independent, so each slice is an exact sub-problem of the
+  full call.
   Tolerance: max|diff| <= 2e-2 * max|oracle| per tensor (the path's bf16
   accuracy target; the reference's accelerator tier uses the same order,
   tests/test_wkv_pallas_accelerator.py:39-71).
@@ -99,8 +101,6 @@ def _train_config(hip, index, case):
     B, H = cfg["B"], cfg["H"]
     print("case:", case, flush=True)
     inp = config_inputs(index, device="cuda", generator="torch")
-    outs, paths = _train_call(hip, inp, 32)
-    assert paths == ("wave_forward", "wave_backward"), paths
     bs, hs = _heads(B, H, seed=index)
     host = [_vec_slice(inp[n], bs, hs) for n in NAMES]
     s0 = _state_slice(inp["s0"], bs, hs)
@@ -109,14 +109,23 @@ def _train_config(hip, index, case):
                           _state_slice(inp["ds_t"], bs, hs),
                           threads=THREADS)
     expected = (ey, es, *egr)
-    for name, got, exp in zip(OUT_NAMES, outs, expected):
-        take = _state_slice if name in STATE_OUTS else _vec_slice
-        _check(name, take(got, bs, hs), exp, f"{case} sampled heads")
-        assert torch.isfinite(got).all(), f"{case} {name}: non-finite"
+    # every checkpoint interval the MFMA kernels serve, the benchmarked
+    # default (16) first, each against the oracle on the sampled heads
+    kept = {}
+    for ci in (16, 32, 64):
+        outs, paths = _train_call(hip, inp, ci)
+        assert paths == ("wave_forward", "wave_backward"), (ci, paths)
+        for name, got, exp in zip(OUT_NAMES, outs, expected):
+            take = _state_slice if name in STATE_OUTS else _vec_slice
+            _check(name, take(got, bs, hs), exp,
+                   f"{case} L{ci} sampled heads")
+            assert torch.isfinite(got).all(), f"{case} L{ci} {name}: " \
+                "non-finite"
+        if ci in (16, 32):
+            kept[ci] = outs
+        del outs
     # every head: the same call at L = 16 agrees with L = 32
-    outs16, paths16 = _train_call(hip, inp, 16)
-    assert paths16 == ("wave_forward", "wave_backward"), paths16
-    for name, a, b in zip(OUT_NAMES, outs16, outs):
+    for name, a, b in zip(OUT_NAMES, kept[16], kept[32]):
         _check_dev(name, a, b, f"{case} L16 vs L32 (all heads)")
 
 

@@ -323,8 +323,33 @@ def test_summed_backward_checks_its_arguments_before_any_device_call(lib):
         adds = [None, None, None]
         adds[i] = outs[o]
         assert fn(1, 2, 1, 1, 64, *fake, 16, *adds, *outs, None) == 1
-        assert b"may not be an output buffer" in lib.rwkv7m_last_error()
+        assert b"may not overlap an output buffer" in lib.rwkv7m_last_error()
+    # a partly overlapping view is refused as well: the check compares byte
+    # ranges (the vectors are 2 * 64 bf16 = 256 bytes here)
+    for shift in (8, -8, 248, -248):
+        adds = [None, ctypes.c_void_p(outs[4].value + shift), None]
+        assert fn(1, 2, 1, 1, 64, *fake, 16, *adds, *outs, None) == 1
+        assert b"may not overlap an output buffer" in lib.rwkv7m_last_error()
     assert lib.rwkv7m_wkv7_last_path() == b""
+
+
+def test_backward_refuses_ds0_sharing_bytes_with_ds_t(lib):
+    # The exact pass of a marked head reads dS_T after dS0 holds the mark,
+    # so dS0 may not share a byte with dS_T: the same buffer and partly
+    # overlapping views are refused before any device call (the fake
+    # addresses are never dereferenced; states are 64 * 64 * 4 bytes)
+    # r, w, k, v, neg_kk, kka, initial_state, dy; then the checkpoints
+    fake = [ctypes.c_void_p(0x1000 * (i + 1)) for i in range(9)]
+    outs = [ctypes.c_void_p(0x100000 * (i + 1)) for i in range(6)]
+    ds_t = 0x4000000
+    for entry in (lib.rwkv7m_wkv7_backward, lib.rwkv7m_wkv7_backward_bthn):
+        for shift in (0, 4, 16380, -16380):
+            ds0 = ctypes.c_void_p(ds_t + shift)
+            rc = entry(1, 2, 1, 1, 64, *fake[:8], ctypes.c_void_p(ds_t),
+                       fake[8], 16, *outs, ds0, None)
+            assert rc == 1
+            assert b"ds0 may not overlap ds_t" in lib.rwkv7m_last_error()
+        assert lib.rwkv7m_wkv7_last_path() == b""
 
 
 def test_noalloc_consumer_backward_rejects_sizes_beyond_its_scratch(lib):

@@ -516,3 +516,97 @@ def test_hand_pins_catch_planted_mistakes(monkeypatch, plant):
         monkeypatch.setattr(so, "layer_norm", lambda x, sc, b, eps=1e-6: x)
     with pytest.raises(AssertionError):
         _check_hand({}, np.array([1.0, 0.25, 0.0]), torch_too=False)
+
+
+def _scalar_grads(case, cfg_opt_cots, n):
+    """float64 autograd gradient of the loss sum(cot * output) with respect
+    to the scalar parameter n, and the sum of its terms' magnitudes."""
+    x, h, slots, ages, usage, P, cfg = case
+    cot_h, cot_s, cot_u = cfg_opt_cots
+    arrays = dict(x=x, h=h, slots=slots, ages=ages, usage=usage, **P)
+    base = {k: _t(v) for k, v in arrays.items()}
+
+    def f(theta):
+        a = dict(base)
+        a[n] = theta
+        return so.read_forward_torch(a["x"], a["h"], a["slots"], a["ages"],
+                                     a["usage"], {k: a[k] for k in P}, cfg)
+
+    theta = base[n].clone().requires_grad_(True)
+    ht, st, ut = f(theta)
+    loss = ((ht * _t(cot_h)).sum() + (st * _t(cot_s)).sum()
+            + (ut * _t(cot_u)).sum())
+    (g,) = torch.autograd.grad(loss, [theta])
+    _, jac = torch.autograd.functional.jvp(f, base[n],
+                                           torch.ones_like(base[n]))
+    scale = float(sum((j * _t(c)).abs().sum()
+                      for j, c in zip(jac, (cot_h, cot_s, cot_u))))
+    return float(g), scale
+
+
+@pytest.mark.parametrize("opt", [dict(), dict(use_age_mask=True)], ids=str)
+def test_scalar_gradient_measures_reject_planted_errors(opt):
+    # The GPU parity tests measure a scalar parameter's gradient with
+    # so.scalar_grad_error: fp32 against its own magnitude (1e-4), bf16
+    # against the sum of its terms' magnitudes (4e-3), because such a
+    # gradient is a sum over every output element that cancels heavily
+    # (|grad| / sum|terms| = 0.006 .. 0.07 at the GPU tests' shapes).
+    # Planted errors in tau_r_raw's oracle gradient (it cancels most) show
+    # what each measure rejects.  fp32 rejects every one: a dropped group of
+    # terms (the usage EMA's path, one token's h outputs) and a relative
+    # error above 1e-4.  Under the bf16 measure a relative error d reads as
+    # d * ratio and a dropped group as its share of sum|terms|, rejected
+    # above 4e-3: the usage path is, a single token's outputs (0.3 % of the
+    # terms in the first case) may not be.  The screening kernels run the
+    # same code for both compute dtypes, so such algorithmic mistakes are
+    # the fp32 checks' to catch; the bf16 checks bound the bf16 roundings.
+    case = _case(B=2, T=23, C=64, ds=80, dk=32, dv=80, M=5,
+                 seed=7 + len(str(opt)), **opt)
+    x, h, slots, ages, usage, P, cfg = case
+    rng = np.random.default_rng(3)
+    cots = (rng.normal(size=x.shape), rng.normal(size=slots.shape),
+            rng.normal(size=usage.shape))
+    want, scale = _scalar_grads(case, cots, "tau_r_raw")
+    ratio = abs(want) / scale
+    print(f"  {opt}: dtau_r_raw {want:.4e}, sum|terms| {scale:.4e}, "
+          f"ratio {ratio:.3e}")
+    assert 1e-4 < ratio < 0.2  # heavy cancellation, as on the GPU
+    t32, t16 = so.SCALAR_TOL_FP32, so.SCALAR_TOL_BF16
+
+    def measures(got):
+        e32, _, b32, s32 = so.scalar_grad_error(got, want, scale, True)
+        e16, r, b16, s16 = so.scalar_grad_error(got, want, scale, False)
+        assert (b32, b16) == ("own magnitude", "terms")
+        assert (s32, s16) == (t32, t16)
+        assert r == pytest.approx(ratio)
+        return e32, e16
+
+    # dropped groups of terms: the usage EMA's path, the last token's h
+    dropped_usage, _ = _scalar_grads(case, (cots[0], cots[1], 0 * cots[2]),
+                                     "tau_r_raw")
+    cot_h = cots[0].copy()
+    cot_h[:, -1] = 0.0
+    dropped_token, _ = _scalar_grads(case, (cot_h,) + cots[1:], "tau_r_raw")
+    for what, got in (("usage path", dropped_usage),
+                      ("last token", dropped_token)):
+        e32, e16 = measures(got)
+        print(f"  {opt}: {what} dropped: fp32 error {e32:.3e}, bf16 error "
+              f"{e16:.3e} (the group's share of sum|terms|)")
+        assert e32 > t32, what
+        assert e16 == pytest.approx(abs(got - want) / scale)
+    assert measures(dropped_usage)[1] > t16
+    # relative errors: the terms measure reads d * ratio
+    for d in (0.5 * t16 / ratio, 1.5 * t16 / ratio):
+        _, e16 = measures(want * (1 + d))
+        assert e16 == pytest.approx(d * ratio, rel=1e-9)
+        assert (e16 > t16) == (d > t16 / ratio)
+    for d, rejected in ((0.5 * t32, False), (1.5 * t32, True), (0.05, True)):
+        e32, _ = measures(want * (1 + d))
+        assert (e32 > t32) == rejected, d
+    # a gradient that cancelled by more than 1000x is measured against its
+    # terms in fp32 too, where d * ratio must stay below 1e-6
+    tiny = 0.5 * so.HEAVY_CANCELLATION * scale
+    e, r, basis, tol = so.scalar_grad_error(tiny * (1 + 0.01), tiny, scale,
+                                            True)
+    assert (basis, tol) == ("terms", so.SCALAR_TOL_FP32_TERMS)
+    assert e == pytest.approx(0.01 * r) and e > tol

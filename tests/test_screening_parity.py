@@ -8,8 +8,12 @@ Tolerances, normalised max error (max |got - want| / max |want|): 1e-4 for
 fp32 activations and parameters, 2e-2 for bf16 activations (compute dtype
 bf16, as the reference's presets run), per tensor, forward and backward (the
 bf16 oracle runs on the bf16-rounded activations); the gradient of a scalar
-parameter (a sum over every output element) is measured against the sum of
-its terms' magnitudes instead of its own.  Shapes include partial
+parameter (a sum over every output element) is measured against its own
+magnitude in fp32 (1e-4; 1e-6 of the terms' sum where the sum cancelled by
+more than 1000x, which happens), and against the sum of its terms'
+magnitudes in bf16 (4e-3) (oracle.screening_oracle.scalar_grad_error;
+tests/test_screening_oracle.py plants errors to show what each measure
+rejects).  Shapes include partial
 64-channel waves (d_slot = 80, d_v = 80), d_k < 64, several slot counts,
 every option of the read (age mask, leaky warm-up, values not normalised,
 half-life rates) and the 0.3B preset's sizes.
@@ -171,10 +175,18 @@ def _check_backward(case, name, dtype, phase="read_screening_only"):
         assert got[n] is not None, f"{name} d{n} missing"
         if w.dim() == 0:
             # a scalar parameter's gradient is a sum over every output
-            # element, often with heavy cancellation: its error is measured
-            # against the sum of the terms' magnitudes
-            e = (abs(float(got[n]) - float(w))
-                 / _term_scale(tin, n, P, cfg, phase, (cot_h, cot_s, cot_u)))
+            # element that cancels heavily (|grad| / sum|terms| is 2e-5 to
+            # 0.12 in these cases): fp32 is measured against its own
+            # magnitude unless it cancelled by more than 1000x, bf16 against
+            # the sum of its terms' magnitudes (so.scalar_grad_error); the
+            # ratio is printed for every case
+            scale = _term_scale(tin, n, P, cfg, phase, (cot_h, cot_s, cot_u))
+            e, ratio, basis, stol = so.scalar_grad_error(
+                float(got[n]), float(w), scale, dtype == torch.float32)
+            print(f"  {name} d{n}: |grad| / sum|terms| = {ratio:.3e}, "
+                  f"error {e:.3e} against {basis} (tol {stol})", flush=True)
+            assert e <= stol, f"{name} d{n}: {e:.3e} > {stol}"
+            continue
         else:
             e = _err(got[n], w.numpy())
         assert e <= tol, f"{name} d{n}: {e:.3e} > {tol}"

@@ -71,10 +71,12 @@ const char *rwkv7m_last_error(void);
  * number of times, so every wave always exits.  A wait that gives up does
  * not pass silently: the workgroup overwrites every output of its
  * (batch, head) -- y, S_T, checkpoints, gradients -- with NaN and raises a
- * per-device failure counter.  This call synchronises `stream`, then reads
- * and clears the current device's counter: RWKV7M_OK if no wait gave up
- * since the last call, RWKV7M_ERR_DEVICE (with the count in
- * rwkv7m_last_error()) otherwise.  No counterpart in the reference (its
+ * per-device failure counter.  This call takes the current device's
+ * counter in one atomic exchange with zero, ordered after the work already
+ * queued on `stream`, then synchronises `stream`: RWKV7M_OK if no wait gave
+ * up since the last call, RWKV7M_ERR_DEVICE (with the count in
+ * rwkv7m_last_error()) otherwise.  A failure that a kernel on another
+ * stream records while this call runs is kept for the next call, never lost.  No counterpart in the reference (its
  * Pallas kernels have no inter-wave hand-over); for callers that check a
  * run's health, and for the failure-path tests.
  */

@@ -638,8 +638,16 @@ int scratch_address(const char* fn, float** out) {
                         " devices the built-in scratch tracks");
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (g_scratch_ptr[dev] == nullptr) {
+        // The lookup may load this code object onto the device.  A first
+        // call made under stream capture in the global or thread-local mode
+        // would have that refused as unsafe; this thread's capture mode is
+        // relaxed for the lookup alone (it queues nothing on any stream)
+        // and restored after it.
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        RWKV7M_TRY(hip_status(fn, hipThreadExchangeStreamCaptureMode(&mode)));
         void* p = nullptr;
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        RWKV7M_TRY(hip_status(fn, hipThreadExchangeStreamCaptureMode(&mode)));
         if (e != hipSuccess || p == nullptr)
             return fail(RWKV7M_ERR_HIP,
                         std::string(fn) +

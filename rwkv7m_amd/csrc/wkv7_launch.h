@@ -21,7 +21,8 @@ hipError_t wait_config(WaitCfg* out);
 // Poll budget for later launches (0: the default); a hook for tests of the
 // failure path.
 void set_wait_limit(int64_t polls);
-// Synchronises the stream, then reads and clears the current device's count.
+// Exchanges the current device's count for zero (atomically, after the
+// stream's queued work), synchronises the stream and returns what was taken.
 hipError_t take_wait_failures(hipStream_t stream, unsigned int* count);
 
 struct SeqFwdArgs {

@@ -19,11 +19,22 @@ namespace rwkv7m {
 namespace {
 
 __device__ unsigned int g_wait_failures;
+// the count taken by the last status call (read back by the host)
+__device__ unsigned int g_wait_taken;
 
 constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 unsigned int* g_counter[kMaxDevices];
+unsigned int* g_taken[kMaxDevices];
 std::atomic<int64_t> g_limit{0};
+
+// Takes the count and clears it in one atomic exchange, so that a failure a
+// kernel on another stream adds meanwhile is kept for the next call.
+__global__ void take_failures_kernel(unsigned int* counter,
+                                     unsigned int* out) {
+    *out = __hip_atomic_exchange(counter, 0u, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+}
 
 }  // namespace
 
@@ -38,6 +49,10 @@ hipError_t wait_config(WaitCfg* out) {
             void* p = nullptr;
             e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_wait_failures));
             if (e != hipSuccess) return e;
+            void* t = nullptr;
+            e = hipGetSymbolAddress(&t, HIP_SYMBOL(g_wait_taken));
+            if (e != hipSuccess) return e;
+            g_taken[dev] = static_cast<unsigned int*>(t);
             g_counter[dev] = static_cast<unsigned int*>(p);
         }
         out->failures = g_counter[dev];
@@ -56,17 +71,25 @@ hipError_t take_wait_failures(hipStream_t stream, unsigned int* count) {
     WaitCfg cfg;
     hipError_t e = wait_config(&cfg);
     if (e != hipSuccess) return e;
+    int dev = 0;
+    e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    unsigned int* taken = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        taken = g_taken[dev];
+    }
+    // after the stream's earlier work: exchange the count for zero, then
+    // read what was taken
+    hipLaunchKernelGGL(take_failures_kernel, dim3(1), dim3(1), 0, stream,
+                       cfg.failures, taken);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
     e = hipStreamSynchronize(stream);
     if (e != hipSuccess) return e;
     unsigned int n = 0;
-    e = hipMemcpy(&n, cfg.failures, sizeof(n), hipMemcpyDeviceToHost);
+    e = hipMemcpy(&n, taken, sizeof(n), hipMemcpyDeviceToHost);
     if (e != hipSuccess) return e;
-    if (n != 0) {
-        const unsigned int zero = 0;
-        e = hipMemcpy(cfg.failures, &zero, sizeof(zero),
-                      hipMemcpyHostToDevice);
-        if (e != hipSuccess) return e;
-    }
     *count = n;
     return hipSuccess;
 }

@@ -280,7 +280,9 @@ __device__ __forceinline__ bf16x8_t frag_cols(const bf16_t* buf, int cb,
 // would wait for all outstanding vector memory operations, this load's and
 // every earlier store's, before each one): the caller orders the data's
 // use with explicit vmcnt waits.  M0 is set in the same statement; no other
-// code of these kernels uses it.
+// code of these kernels uses it.  `lds` is wave-uniform; the readfirstlane
+// only tells the compiler so where its uniformity analysis cannot see it
+// (after a loop with an early exit) and costs nothing otherwise.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(const void* gbase, uint32_t voff,
@@ -288,7 +290,7 @@ __device__ __forceinline__ void dma16(const void* gbase, uint32_t voff,
     asm volatile(
         "s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
         :
-        : "v"(voff), "s"(gbase), "s"(lds)
+        : "v"(voff), "s"(gbase), "s"(__builtin_amdgcn_readfirstlane(lds))
         : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -352,6 +354,28 @@ __device__ __forceinline__ bool poll(int* p, int limit, Pred pred) {
     }
     asm volatile("" ::: "memory");
     return ok;
+}
+
+// Poll an LDS word until pred(value) holds: 1 when it does, 0 when the word
+// *stop turned nonzero first (read on every eighth poll: another wave of
+// the workgroup gave up), -1 after `limit` polls.
+template <typename Pred>
+__device__ __forceinline__ int poll_or_stop(int* p, int limit, int* stop,
+                                            Pred pred) {
+    for (int it = 0; it < limit; ++it) {
+        if (pred(__builtin_amdgcn_readfirstlane(lds_load(p)))) {
+            asm volatile("" ::: "memory");
+            return 1;
+        }
+        if ((it & 7) == 7 &&
+            __builtin_amdgcn_readfirstlane(lds_load(stop)) != 0) {
+            asm volatile("" ::: "memory");
+            return 0;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("" ::: "memory");
+    return -1;
 }
 
 // A wait gave up: mark the workgroup failed (LDS) and count it on the device

@@ -63,8 +63,11 @@ constexpr int WTHREADS = 64 * (NCHAIN + NPROD);
 // Every hand-over wait is bounded (WaitCfg::limit polls of ~64 cycles; a
 // wave waits for at most a few other chunks, and the default bound is orders
 // of magnitude above that), so every wave exits.  A wait that gives up marks
-// the workgroup failed: its outputs are then overwritten with NaN and the
-// device's failure counter is raised (wkv7_status.hip).
+// the workgroup failed; every other wave reads that mark within eight polls
+// of its current wait and leaves its loop, so a lost hand-over costs one
+// wait's budget, not one per remaining chunk.  The workgroup's outputs are
+// then overwritten with NaN and the device's failure counter is raised
+// (wkv7_status.hip).
 
 // Per producer: the next chunk's six vectors as loaded, and, once the
 // factors are formed, the four J-layout matrices on their way through the
@@ -372,9 +375,14 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
         // ---- hand the chunk to the chains ---------------------------------
         const int s = c % NSLOT;
         const int uses = c / NSLOT;  // earlier uses of this slot
-        if (!poll(vdone + s, A.wait.limit,
-                  [&](int d) { return d >= NCHAIN * uses; }))
-            wait_failed(&sm.failed, A.wait.failures, lane);
+        // a wave that gives up marks the workgroup failed; every other wave
+        // then stops at its next wait (within eight polls)
+        const int got = poll_or_stop(vdone + s, A.wait.limit, &sm.failed,
+                                     [&](int d) { return d >= NCHAIN * uses; });
+        if (got <= 0) {
+            if (got < 0) wait_failed(&sm.failed, A.wait.failures, lane);
+            break;
+        }
         Slot& sl = sm.slot[s];
         sl.W[0][lane] = pk8(wt[0], wt[1]);
         sl.W[1][lane] = pk8(wt[2], wt[3]);
@@ -436,13 +444,20 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
         f32x4_t eL[4];
         int exact;
     };
-    auto take = [&](int c, int s, int word, SlotRegs& r) {
-        if ((word >> 1) != c &&
-            !poll(vready + s, A.wait.limit, [&](int x) {
-                word = x;
-                return (x >> 1) == c;
-            }))
-            wait_failed(&sm.failed, A.wait.failures, lane);
+    // false when the workgroup failed (this wave's wait gave up, or another
+    // wave's did)
+    auto take = [&](int c, int s, int word, SlotRegs& r) -> bool {
+        if ((word >> 1) != c) {
+            const int got = poll_or_stop(vready + s, A.wait.limit, &sm.failed,
+                                         [&](int x) {
+                                             word = x;
+                                             return (x >> 1) == c;
+                                         });
+            if (got <= 0) {
+                if (got < 0) wait_failed(&sm.failed, A.wait.failures, lane);
+                return false;
+            }
+        }
         const Slot& sl = sm.slot[s];
         r.exact = word & 1;
         r.W0 = sl.W[0][lane];
@@ -460,6 +475,7 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
         r.Q1 = sl.Q[1][lane];
         r.Arb = sl.Arb[lane];
         r.Ark = sl.Ark[lane];
+        return true;
     };
     // y of the previous chunk as its two products, added and stored one
     // iteration late (complete by then): rows of chunk yc (yc < 0: none)
@@ -496,8 +512,8 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
     int s = 0, cph = 0;
     int64_t ckoff = sbase;
     SlotRegs cur;
-    if (nch > 0) take(0, 0, -1, cur);
-    for (int c = 0; c < nch; ++c) {
+    const int nrun = nch > 0 && take(0, 0, -1, cur) ? nch : 0;
+    for (int c = 0; c < nrun; ++c) {
         const int64_t t0 = int64_t(c) * WL;
         const int n = int(T - t0 < WL ? T - t0 : WL);
         const int exact = cur.exact;
@@ -572,8 +588,9 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
             cph = 0;
             ckoff += A.BH * NN;
         }
-        if (c + 1 < nch)
-            take(c + 1, s, __builtin_amdgcn_readfirstlane(word), cur);
+        if (c + 1 < nch &&
+            !take(c + 1, s, __builtin_amdgcn_readfirstlane(word), cur))
+            break;
         if (exact) {
             // exact fp32 sequential pass over the chunk for the rows of
             // block ib (a chunk outside the factored form's range, far

@@ -63,7 +63,7 @@
 // that gives up sets every output of the head to NaN and raises the
 // device's failure counter.
 
-#include "wkv7_wave_common.h"
+#include "wkv7_wave_bwd_common.h"
 
 namespace rwkv7m {
 namespace {
@@ -108,29 +108,10 @@ __shared__ bf16_t lds_D[NWORK][NN];  // the cotangent of its end state
 __shared__ BMap lds_map[NWORK];
 // sum_i D_0 S_0 per chain, for the even positions' workers (0 and 2)
 __shared__ float lds_tail[NWORK][NCHAIN][WN];
-__shared__ float lds_eref[NWORK][WN];          // 2^{g_ref} per column
-__shared__ float lds_eLR[NWORK][WN];           // 2^{g_L - g_ref}
-__shared__ float lds_eL[NWORK][WN];            // 2^{g_L}
+// per-column factors of the chunk: [0] 2^{g_L - g_ref}, [1] 2^{g_ref},
+// [2] 2^{g_L} (written by lanes 0, 1, 2 of each 16-lane row in one store)
+__shared__ float lds_fac[NWORK][3][WN];
 __shared__ BwdFlags lds_flags;
-
-// Every byte offset into the vectors and the checkpoints is below 2^31
-// (checked by the host): addresses are a kernel-constant base plus a 32-bit
-// per-lane offset, and a lane with nothing to store or load uses the offset
-// kNoLane, past every buffer's 2^31-byte range.
-constexpr uint32_t kNoLane = 0x80000000u;
-struct BwdArgs {
-    int64_t T, BH;
-    VecLayout lay;
-    uint32_t ts2;  // bytes per token step of the vectors
-    const bf16_t *r, *w, *k, *v, *a, *b, *dy;
-    const float* ds_t;
-    const bf16_t* ckpt;
-    bf16_t *dr, *dw, *dk, *dv, *da, *db;
-    float* ds0;
-    WaitCfg wait;
-    // cotangents added to dr, dk, dv (the accumulating kernel; null: zeros)
-    const bf16_t *add_dr, *add_dk, *add_dv;
-};
 
 // Wait until pred(*p) holds: 1 when it does, 0 when the workgroup aborted
 // first, -1 when the poll budget ran out (then the workgroup is marked
@@ -162,31 +143,6 @@ __device__ __forceinline__ int wait_for(const WaitCfg& wc, int* p, int lane,
     return -1;
 }
 
-__device__ __forceinline__ f32x4_t unpack_i16(const i16x4_t& x) {
-    return unpack4(__builtin_bit_cast(uint2, x));
-}
-
-// A buffer resource over a whole input tensor (null p: an empty range, so
-// every load returns zeros); loads at offset kNoLane return zeros.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t in_rsrc(const bf16_t* p) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(p), 0,
-                                             p ? int(kNoLane) : 0,
-                                             0x00020000);
-}
-
-// A buffer resource over a whole output tensor: stores at offset kNoLane
-// are dropped.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t whole_rsrc(bf16_t* p) {
-    return __builtin_amdgcn_make_buffer_rsrc(p, 0, int(kNoLane), 0x00020000);
-}
-
-// 8 bytes at byte offset `off` of the buffer.
-__device__ __forceinline__ uint2 load8(__amdgpu_buffer_rsrc_t rs,
-                                       uint32_t off) {
-    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-    const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(rs, int(off), 0, 0);
-    return make_uint2(x[0], x[1]);
-}
 
 // ---------------------------------------------------------------------------
 // Chain ib: rows 16 ib .. 16 ib + 15 of the cotangent through every chunk.
@@ -240,7 +196,7 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
             const f32x4_t elr = *reinterpret_cast<const f32x4_t*>(
-                &lds_eLR[w][16 * jb + 4 * lq]);
+                &lds_fac[w][0][16 * jb + 4 * lq]);
             f32x4_t x;
 #pragma unroll
             for (int e = 0; e < 4; ++e) x[e] = Dt[jb][e] * elr[e];
@@ -260,7 +216,7 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
         for (int jb = 0; jb < 4; ++jb) {
             QW[jb] = mp.QW[jb][lane];
             eL[jb] = *reinterpret_cast<const f32x4_t*>(
-                &lds_eL[w][16 * jb + 4 * lq]);
+                &lds_fac[w][2][16 * jb + 4 * lq]);
         }
         const i16x4_t dYt = mp.dY[ib][lane];
         lds_drain();
@@ -387,14 +343,6 @@ __device__ __forceinline__ i16x4_t stage_j(int w, int vv, int jb, int lane) {
         (lds_i16x4_t*)(p + 4 * (s & 1)));
 }
 
-// The J layout tile D(X_kb) of a T layout tile of X: X_kb I, with the
-// identity as the B operand (exact for bf16 values).
-__device__ __forceinline__ i16x4_t to_j(const i16x4_t& t, const i16x4_t& kI) {
-    f32x4_t x = zero4();
-    mfma16(x, t, kI);
-    return kq(x);
-}
-
 // ---------------------------------------------------------------------------
 // Worker w: chunks nch - 1 - w, nch - 1 - w - NWORK, ...; checkpoints every
 // M chunks.  ACC: the cotangents add_dr, add_dk, add_dv are added to dr, dk,
@@ -501,6 +449,8 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         // the stage is free: the next chunk's vectors load during this one
         if (cn >= 0) fetch_vecs(A, w, cb2 - NWORK * WL * ts2, WL, lane);
         if (n < WL) {
+            // (a branch, not selects: only a head's last chunk is short)
+            asm volatile("" ::: "memory");
             // padding tokens: zero vectors and w = -inf (bf16), so that
             // they decay by nothing
 #pragma unroll
@@ -572,14 +522,9 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             keg[kb] = kq(eg4);
             keng[kb] = kq(eng4);
             kep[kb] = kq(ep4);
-            if (lr == 1)
-                *reinterpret_cast<f32x4_t*>(&lds_eref[w][16 * kb + 4 * lq]) =
-                    sp4;
-            if (lr == 2)
-                *reinterpret_cast<f32x4_t*>(&lds_eL[w][16 * kb + 4 * lq]) = sp4;
-            if (lr == 0)
-                *reinterpret_cast<f32x4_t*>(&lds_eLR[w][16 * kb + 4 * lq]) =
-                    lr4;
+            if (lr < 3)
+                *reinterpret_cast<f32x4_t*>(&lds_fac[w][lr][16 * kb + 4 * lq]) =
+                    lr == 0 ? lr4 : sp4;
         }
         // the factored form needs g_ref >= -H and g_L - g_ref >= -H
         if (__builtin_amdgcn_ballot_w64(lo < -kHalfRange * kLog2e) != 0) {
@@ -671,7 +616,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             break;
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
-            const float erj = lds_eref[w][16 * jb + lr];
+            const float erj = lds_fac[w][1][16 * jb + lr];
             f32x4_t x = zero4();
             mfma16(x, kMinv, to_j(tA[jb], kI));
 #pragma unroll
@@ -723,7 +668,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 break;
 #pragma unroll
             for (int jb = 0; jb < 4; ++jb) {
-                const float elr = lds_eLR[w][16 * jb + lr];
+                const float elr = lds_fac[w][0][16 * jb + lr];
                 f32x4_t bj = unpack_i16(to_j(tB[jb], kI));
                 f32x4_t kj = unpack_i16(to_j(tK[jb], kI));
 #pragma unroll
@@ -758,7 +703,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 for (int jpb = 0; jpb < 4; ++jpb) {
                     // lane: S_L[16 ib + lr][16 jpb + 4 lq + e]
                     const f32x4_t el = *reinterpret_cast<const f32x4_t*>(
-                        &lds_eL[w][16 * jpb + 4 * lq]);
+                        &lds_fac[w][2][16 * jpb + 4 * lq]);
                     const f32x4_t s0 = unpack4(
                         sd_read4(S, 16 * ib + lr, 16 * jpb + 4 * lq));
                     f32x4_t acc;
@@ -912,7 +857,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
             const f32x4_t er = *reinterpret_cast<const f32x4_t*>(
-                &lds_eref[w][16 * jb + 4 * lq]);
+                &lds_fac[w][1][16 * jb + 4 * lq]);
             f32x4_t tl[NCHAIN];
 #pragma unroll
             for (int ch = 0; ch < NCHAIN; ++ch)
@@ -997,20 +942,6 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
     }
 }
 
-// A workgroup whose wait gave up overwrites every output of its head with
-// NaN.
-__device__ __forceinline__ void poison(const BwdArgs& A, int tid) {
-    const int64_t bh = blockIdx.x;
-    const int64_t hoff = A.lay.head(bh, WN);
-    const bf16_t nan16 = 0x7fc0;
-    bf16_t* const outs[6] = {A.dr, A.dw, A.dk, A.dv, A.da, A.db};
-    for (int g = 0; g < 6; ++g)
-        for (int64_t e = tid; e < A.T * WN; e += BTHREADS)
-            outs[g][(e / WN) * A.lay.ts + hoff + e % WN] = nan16;
-    for (int e = tid; e < NN; e += BTHREADS)
-        A.ds0[bh * NN + e] = __builtin_nanf("");
-}
-
 template <int M, bool ACC>
 __global__ void __launch_bounds__(BTHREADS)
 wkv7_wave_bwd_kernel(BwdArgs A) {
@@ -1040,7 +971,7 @@ wkv7_wave_bwd_kernel(BwdArgs A) {
     // every wait is bounded, so every wave arrives here
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (lds_load(&fl.failed) != 0) poison(A, tid);
+    if (lds_load(&fl.failed) != 0) poison(A, tid, BTHREADS);
 }
 
 }  // namespace
@@ -1048,31 +979,7 @@ wkv7_wave_bwd_kernel(BwdArgs A) {
 hipError_t launch_wave_backward(const WaveBwdArgs& p, hipStream_t stream) {
     if (p.L % WL != 0 || p.L / WL < 1 || p.L / WL > 4 || p.L / WL == 3)
         return hipErrorInvalidValue;
-    BwdArgs A;
-    A.T = p.T;
-    A.BH = p.B * p.H;
-    A.lay = p.lay;
-    A.r = static_cast<const bf16_t*>(p.r);
-    A.w = static_cast<const bf16_t*>(p.w);
-    A.k = static_cast<const bf16_t*>(p.k);
-    A.v = static_cast<const bf16_t*>(p.v);
-    A.a = static_cast<const bf16_t*>(p.a);
-    A.b = static_cast<const bf16_t*>(p.b);
-    A.dy = static_cast<const bf16_t*>(p.dy);
-    A.ds_t = p.ds_t;
-    A.ckpt = static_cast<const bf16_t*>(p.ckpt);
-    A.dr = static_cast<bf16_t*>(p.dr);
-    A.dw = static_cast<bf16_t*>(p.dw);
-    A.dk = static_cast<bf16_t*>(p.dk);
-    A.dv = static_cast<bf16_t*>(p.dv);
-    A.da = static_cast<bf16_t*>(p.da);
-    A.db = static_cast<bf16_t*>(p.db);
-    A.ds0 = p.ds0;
-    A.wait = p.wait;
-    A.ts2 = uint32_t(p.lay.ts * 2);
-    A.add_dr = static_cast<const bf16_t*>(p.add_dr);
-    A.add_dk = static_cast<const bf16_t*>(p.add_dk);
-    A.add_dv = static_cast<const bf16_t*>(p.add_dv);
+    const BwdArgs A = bwd_args(p);
     if (A.BH <= 0 || A.T <= 0) return hipSuccess;
     const bool acc = A.add_dr || A.add_dk || A.add_dv;
     const dim3 grid(unsigned(A.BH)), block(BTHREADS);

@@ -1,0 +1,108 @@
+// Pieces of the MFMA backward (wkv7_wave_bwd.hip) that do not depend on its
+// wave roles: its arguments, 32-bit buffer addressing and the failure path.
+#pragma once
+
+#include "wkv7_wave_common.h"
+
+namespace rwkv7m {
+namespace wave {
+
+// Every byte offset into the vectors and the checkpoints is below 2^31
+// (checked by the host): addresses are a kernel-constant base plus a 32-bit
+// per-lane offset, and a lane with nothing to store or load uses the offset
+// kNoLane, past every buffer's 2^31-byte range.
+constexpr uint32_t kNoLane = 0x80000000u;
+struct BwdArgs {
+    int64_t T, BH;
+    VecLayout lay;
+    uint32_t ts2;  // bytes per token step of the vectors
+    const bf16_t *r, *w, *k, *v, *a, *b, *dy;
+    const float* ds_t;
+    const bf16_t* ckpt;
+    bf16_t *dr, *dw, *dk, *dv, *da, *db;
+    float* ds0;
+    WaitCfg wait;
+    // cotangents added to dr, dk, dv (the accumulating kernel; null: zeros)
+    const bf16_t *add_dr, *add_dk, *add_dv;
+};
+
+__host__ inline BwdArgs bwd_args(const WaveBwdArgs& p) {
+    BwdArgs A;
+    A.T = p.T;
+    A.BH = p.B * p.H;
+    A.lay = p.lay;
+    A.ts2 = uint32_t(p.lay.ts * 2);
+    A.r = static_cast<const bf16_t*>(p.r);
+    A.w = static_cast<const bf16_t*>(p.w);
+    A.k = static_cast<const bf16_t*>(p.k);
+    A.v = static_cast<const bf16_t*>(p.v);
+    A.a = static_cast<const bf16_t*>(p.a);
+    A.b = static_cast<const bf16_t*>(p.b);
+    A.dy = static_cast<const bf16_t*>(p.dy);
+    A.ds_t = p.ds_t;
+    A.ckpt = static_cast<const bf16_t*>(p.ckpt);
+    A.dr = static_cast<bf16_t*>(p.dr);
+    A.dw = static_cast<bf16_t*>(p.dw);
+    A.dk = static_cast<bf16_t*>(p.dk);
+    A.dv = static_cast<bf16_t*>(p.dv);
+    A.da = static_cast<bf16_t*>(p.da);
+    A.db = static_cast<bf16_t*>(p.db);
+    A.ds0 = p.ds0;
+    A.wait = p.wait;
+    A.add_dr = static_cast<const bf16_t*>(p.add_dr);
+    A.add_dk = static_cast<const bf16_t*>(p.add_dk);
+    A.add_dv = static_cast<const bf16_t*>(p.add_dv);
+    return A;
+}
+
+__device__ __forceinline__ f32x4_t unpack_i16(const i16x4_t& x) {
+    return unpack4(__builtin_bit_cast(uint2, x));
+}
+
+// A buffer resource over a whole input tensor (null p: an empty range, so
+// every load returns zeros); loads at offset kNoLane return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t in_rsrc(const bf16_t* p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(p), 0,
+                                             p ? int(kNoLane) : 0,
+                                             0x00020000);
+}
+
+// A buffer resource over a whole output tensor: stores at offset kNoLane
+// are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t whole_rsrc(bf16_t* p) {
+    return __builtin_amdgcn_make_buffer_rsrc(p, 0, int(kNoLane), 0x00020000);
+}
+
+// 8 bytes at byte offset `off` of the buffer.
+__device__ __forceinline__ uint2 load8(__amdgpu_buffer_rsrc_t rs,
+                                       uint32_t off) {
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(rs, int(off), 0, 0);
+    return make_uint2(x[0], x[1]);
+}
+
+// The J layout tile D(X_kb) of a T layout tile of X: X_kb I, with the
+// identity as the B operand (exact for bf16 values).
+__device__ __forceinline__ i16x4_t to_j(const i16x4_t& t, const i16x4_t& kI) {
+    f32x4_t x = zero4();
+    mfma16(x, t, kI);
+    return kq(x);
+}
+
+// A workgroup whose wait gave up overwrites every output of its head with
+// NaN (all `nthreads` threads of the workgroup take part).
+__device__ __forceinline__ void poison(const BwdArgs& A, int tid,
+                                       int nthreads) {
+    const int64_t bh = blockIdx.x;
+    const int64_t hoff = A.lay.head(bh, WN);
+    const bf16_t nan16 = 0x7fc0;
+    bf16_t* const outs[6] = {A.dr, A.dw, A.dk, A.dv, A.da, A.db};
+    for (int g = 0; g < 6; ++g)
+        for (int64_t e = tid; e < A.T * WN; e += nthreads)
+            outs[g][(e / WN) * A.lay.ts + hoff + e % WN] = nan16;
+    for (int e = tid; e < WN * WN; e += nthreads)
+        A.ds0[bh * WN * WN + e] = __builtin_nanf("");
+}
+
+}  // namespace wave
+}  // namespace rwkv7m

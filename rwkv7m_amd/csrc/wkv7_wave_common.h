@@ -340,22 +340,6 @@ __device__ __forceinline__ void lds_drain() {
     asm volatile("" ::: "memory");
 }
 
-// Poll an LDS word until pred(value) holds, at most `limit` times; false if
-// it never did.
-template <typename Pred>
-__device__ __forceinline__ bool poll(int* p, int limit, Pred pred) {
-    bool ok = false;
-    for (int it = 0; it < limit; ++it) {
-        if (pred(__builtin_amdgcn_readfirstlane(lds_load(p)))) {
-            ok = true;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-    asm volatile("" ::: "memory");
-    return ok;
-}
-
 // Poll an LDS word until pred(value) holds: 1 when it does, 0 when the word
 // *stop turned nonzero first (read on every eighth poll: another wave of
 // the workgroup gave up), -1 after `limit` polls.

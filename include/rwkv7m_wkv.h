@@ -93,6 +93,19 @@ int rwkv7m_device_status(void *stream);
 void rwkv7m_debug_set_wait_limit(int64_t polls);
 
 /*
+ * Workgroups per (batch, head) of the MFMA backward in later launches; 0
+ * restores the default.  By default a head's backward is split over as many
+ * workgroups as the device's CUs leave room for beside the other heads (at
+ * most 4): each takes a run of chunks and first carries the cotangent
+ * through the chunks after its own, so a call with few heads (B * H well
+ * below the CU count) uses the idle CUs.  The split changes no arithmetic:
+ * results are bit-identical for every count.  A hook for tests; not
+ * thread-safe against launches on other threads.  No counterpart in the
+ * reference.
+ */
+void rwkv7m_debug_set_backward_segments(int workgroups_per_head);
+
+/*
  * Name of the kernel path the last successful WKV-7 call on this thread
  * launched: "wave_forward" (MFMA chunked forward), "decode" (single-token
  * kernel), "seq_forward", "wave_backward" (MFMA chunked backward, with the

@@ -99,6 +99,9 @@ struct WaveBwdArgs {
 };
 
 hipError_t launch_wave_backward(const WaveBwdArgs& p, hipStream_t stream);
+// Workgroups per head for later wave backward launches (0: as many as the
+// device's idle CUs allow, at most 4).  A hook for tests.
+void set_backward_segments(int k);
 
 hipError_t launch_seq_forward(const SeqFwdArgs& p, hipStream_t stream);
 

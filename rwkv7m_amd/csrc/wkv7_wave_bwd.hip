@@ -63,6 +63,8 @@
 // that gives up sets every output of the head to NaN and raises the
 // device's failure counter.
 
+#include <atomic>
+
 #include "wkv7_wave_bwd_common.h"
 
 namespace rwkv7m {
@@ -148,8 +150,12 @@ __device__ __forceinline__ int wait_for(const WaitCfg& wc, int* p, int lane,
 // Chain ib: rows 16 ib .. 16 ib + 15 of the cotangent through every chunk.
 __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
     const int lr = lane & 15, lq = lane >> 4;
-    const int64_t bh = blockIdx.x;
+    const int64_t bh = head_of(A);
     const int nch = int((A.T + WL - 1) / WL);
+    // this workgroup's chunks [c_lo, c_hi); the later ones it only passes
+    // the cotangent through
+    const int sg = seg_of(A);
+    const int c_lo = A.seg_lo[sg], c_hi = A.seg_hi[sg];
     const int row = 16 * ib + lr;
     BwdFlags& fl = lds_flags;
     __builtin_amdgcn_s_setprio(2);  // the serial path
@@ -177,7 +183,7 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
 
     bool done = true;
-    for (int p = 0; p < nch; ++p) {
+    for (int p = 0; p < nch - c_lo; ++p) {
         const int c = nch - 1 - p;
         const int w = p % NWORK, kord = p / NWORK;
 
@@ -243,6 +249,12 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
         // its chunk's start value, and the worker of the next (odd)
         // position, one chunk earlier in time, as its chunk's end value.
         if (p & 1) continue;
+        if (c >= c_hi) {
+            // a chunk past this workgroup's own: no gradients, so no share,
+            // but the count stays in step with the worker's chunk order
+            if (lane == 0) lds_add(&fl.tail_cnt[w], 1);
+            continue;
+        }
         // this block's share for the worker.  P = D_0 * S_0 on the block's
         // tiles D(P^T) is split into bf16 parts P = P_hi + P_lo (16
         // significant bits); each part is turned into D(P) by P I and summed
@@ -277,7 +289,7 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
         lds_drain();
         if (lane == 0) lds_add(&fl.tail_cnt[w], 1);
     }
-    if (done) {
+    if (done && c_lo == 0) {
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb)
             *reinterpret_cast<f32x4_t*>(A.ds0 + bh * NN + row * WN + 16 * jb +
@@ -314,7 +326,8 @@ template <int M>
 __device__ __forceinline__ void fetch_state(const BwdArgs& A, int w, int c,
                                             int lane) {
     const uint32_t off =
-        (uint32_t(c / M) * uint32_t(A.BH) + blockIdx.x) * uint32_t(NN * 2) +
+        (uint32_t(c / M) * uint32_t(A.BH) + uint32_t(head_of(A))) *
+            uint32_t(NN * 2) +
         uint32_t(((lane & 7) * WN + 8 * (lane >> 3)) * 2);
 #pragma unroll
     for (int g = 0; g < 8; ++g)
@@ -351,7 +364,7 @@ __device__ __forceinline__ i16x4_t stage_j(int w, int vv, int jb, int lane) {
 // and count in the waits below.
 template <int M, bool ACC>
 __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
-    const int64_t bh = blockIdx.x;
+    const int64_t bh = head_of(A);
     const uint32_t hoff2 = uint32_t(A.lay.head(bh, WN)) * 2;
     const int T = int(A.T);
     const int nch = (T + WL - 1) / WL;
@@ -364,15 +377,20 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
     bf16_t* const S = lds_S[w];
     bf16_t* const D = lds_D[w];
     BMap& map = lds_map[w];
+    // this workgroup's chunks [c_lo, c_hi) (segment boundaries are interval
+    // boundaries); for a chunk at or past c_hi it only publishes the map
+    // that carries the cotangent through
+    const int sg = seg_of(A);
+    const int c_lo = A.seg_lo[sg], c_hi = A.seg_hi[sg];
 
-    if (nch - 1 - w >= 0) {
+    if (nch - 1 - w >= c_lo) {
         const int c0 = nch - 1 - w;
         fetch_vecs(A, w, uint32_t(c0) * WL * ts2 + hoff2,
                    T - c0 * WL < WL ? T - c0 * WL : WL, lane0);
-        if ((nch - 1 - w) % m == 0) fetch_state<M>(A, w, nch - 1 - w, lane0);
+        if (c0 < c_hi && c0 % m == 0) fetch_state<M>(A, w, c0, lane0);
     }
 
-    for (int kord = 0, p = w; p < nch; ++kord, p += NWORK) {
+    for (int kord = 0, p = w; p < nch - c_lo; ++kord, p += NWORK) {
         // lane-derived addresses and masks are formed inside each iteration:
         // hoisted out of the loop they would each hold a register for the
         // whole run
@@ -397,14 +415,18 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         // row of the token-major outputs (kNoLane past the end: dropped)
         const uint32_t cb2 = uint32_t(c) * WL * ts2 + hoff2;
         const uint32_t row2 = valid ? cb2 + uint32_t(lr) * ts2 : kNoLane;
-        const bool starts = c % m == 0;  // S_0 is checkpoint c / m
-        const bool feeds = c % m != m - 1 && c + 1 < nch;  // S_0 of c + 1
+        const bool skim = c >= c_hi;  // only the map (past the segment)
+        const bool more = cn >= c_lo;  // the worker has a next chunk
+        // S_0 is checkpoint c / m; S_0 of c + 1 is formed here
+        const bool starts = !skim && c % m == 0;
+        const bool feeds = !skim && c % m != m - 1 && c + 1 < c_hi;
         // the vectors.  Vector memory operations complete in issue order, and
         // since the vectors' loads this worker issued the previous chunk's 24
-        // gradient stores (4 of dv, 20 of the column blocks) and, when this
-        // chunk starts an interval, its start state's 8 loads, whose wait
-        // comes only before S_0's first use
-        if (kord == 0) {
+        // gradient stores (4 of dv, 20 of the column blocks; none after a
+        // chunk that only published its map) and, when this chunk starts an
+        // interval, its start state's 8 loads, whose wait comes only before
+        // S_0's first use
+        if (kord == 0 || c + NWORK >= c_hi) {
             if (starts)
                 __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8)
             else
@@ -433,7 +455,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         // the cotangents added to this chunk's dv (value blocks ib) and dr,
         // dk (key blocks jb), at the lanes' own output offsets
         uint2 adv[4], adr[4], adk[4];
-        if constexpr (ACC) {
+        if (ACC && !skim) {
             const __amdgpu_buffer_rsrc_t rv = in_rsrc(A.add_dv),
                                          rr = in_rsrc(A.add_dr),
                                          rk = in_rsrc(A.add_dk);
@@ -447,7 +469,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             }
         }
         // the stage is free: the next chunk's vectors load during this one
-        if (cn >= 0) fetch_vecs(A, w, cb2 - NWORK * WL * ts2, WL, lane);
+        if (more) fetch_vecs(A, w, cb2 - NWORK * WL * ts2, WL, lane);
         if (n < WL) {
             // (a branch, not selects: only a head's last chunk is short)
             asm volatile("" ::: "memory");
@@ -473,6 +495,13 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         }
 
         // ---- factors (T layout) ------------------------------------------
+        // The per-column factors and the map of this worker's previous chunk
+        // are read by every chain at that chunk's position (the factors
+        // before the map's hand-over count): overwrite neither before the
+        // count says all have been read.
+        if (wait_for(A.wait, &fl.map_taken[w], lane,
+                     [&](int x) { return x >= NCHAIN * kord; }) <= 0)
+            break;
         // lam = log2 d_t, g its running sum over the chunk, g_ref = g at
         // token 7, g_L = g at token 15 (padding tokens decay by nothing)
         i16x4_t tA[4], tR[4], tB[4], tK[4], tAh[4];
@@ -611,9 +640,6 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         }
 
         // ---- W^ = Minv A^, Q^ = R~ 2^{g_ref} + Arb W^ (J layout); the map -
-        if (wait_for(A.wait, &fl.map_taken[w], lane,
-                     [&](int x) { return x >= NCHAIN * kord; }) <= 0)
-            break;
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
             const float erj = lds_fac[w][1][16 * jb + lr];
@@ -635,6 +661,20 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         for (int ib = 0; ib < 4; ++ib) map.dY[ib][lane] = jdY[ib];
         lds_drain();
         if (lane == 0) lds_store(&fl.map_ready[w], kord + 1);
+        if (skim) {
+            // the cotangent passes through this chunk; nothing else is
+            // formed here.  Its D buffer and tail are not read: release them
+            // at once (the chains' counts stay in step), and start the next
+            // chunk's start state if it is this segment's first.
+            if (lane == 0) {
+                lds_store(&fl.d_done[w], kord + 1);
+                lds_store(&fl.s_free[w], cn);
+                if (w & 1) lds_store(&fl.tail_used[w], kord + 1);
+            }
+            if (more && cn < c_hi && cn % m == 0)
+                fetch_state<M>(A, w, cn, lane);
+            continue;
+        }
 
         // ---- U = A^ S_0^T + Aak V, X = Minv U ------------------------------
         if (starts) {
@@ -642,12 +682,12 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             // vector loads (if any) were issued
             if constexpr (ACC) {
                 // and the 12 cotangent loads
-                if (cn >= 0)
+                if (more)
                     __builtin_amdgcn_s_waitcnt(0x4f7a);  // vmcnt(26)
                 else
                     __builtin_amdgcn_s_waitcnt(0x0f7c);  // vmcnt(12)
             } else {
-                if (cn >= 0)
+                if (more)
                     __builtin_amdgcn_s_waitcnt(0x0f7e);  // vmcnt(14)
                 else
                     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
@@ -731,7 +771,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         if constexpr (ACC) {
             // the dv cotangents: the 8 dr, dk loads and the next chunk's 14
             // vector loads (if any) came after them
-            if (cn >= 0)
+            if (more)
                 __builtin_amdgcn_s_waitcnt(0x4f76);  // vmcnt(22)
             else
                 __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8)
@@ -847,7 +887,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         if constexpr (ACC) {
             // the dr and dk cotangents: the next chunk's vector loads (if
             // any) and the 4 dv stores came after them
-            if (cn >= 0)
+            if (more)
                 __builtin_amdgcn_s_waitcnt(0x4f72);  // vmcnt(18)
             else
                 __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4)
@@ -938,7 +978,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             lds_store(&fl.s_free[w], cn);
             if (odd) lds_store(&fl.tail_used[w], kord + 1);
         }
-        if (cn >= 0 && cn % m == 0) fetch_state<M>(A, w, cn, lane);
+        if (more && cn % m == 0) fetch_state<M>(A, w, cn, lane);
     }
 }
 
@@ -976,13 +1016,106 @@ wkv7_wave_bwd_kernel(BwdArgs A) {
 
 }  // namespace
 
+namespace {
+
+// Cost of a chunk whose workgroup only publishes its map (the cotangent
+// passes through it), relative to a chunk whose gradients it forms: the
+// factors, the inverse and the map, about 7,300 of 19,600 cycles per worker.
+constexpr double kPassCost = 0.4;
+
+std::atomic<int> g_force_segments{0};
+std::atomic<int> g_cu_count[64];
+
+int cu_count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int n = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount,
+                                  dev) != hipSuccess)
+            return 0;
+        g_cu_count[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+// Splits a head's nch chunks (interval m chunks) over k workgroups when the
+// heads alone leave CUs idle.  Segment j owns chunks [lo[j], hi[j]) and first
+// carries the cotangent through every later chunk, so the later segments
+// own fewer chunks: with costs 1 (own) and kPassCost (passed through), equal
+// finishing times give segment j the weight 1 - kPassCost * (the weights
+// before it).  Every boundary b is an interval boundary (b % m == 0) and
+// leaves an even number of chunks after it, so that the chunk-boundary
+// pairs of the decay gradient's identity stay inside a segment.  Returns the
+// number of segments (1 when no split satisfies that).
+int plan_segments(int nch, int m, int k, int* lo, int* hi) {
+    lo[0] = 0;
+    hi[0] = nch;
+    if (k < 2 || (m > 1 && nch % 2 != 0)) return 1;
+    if (k > kMaxSegments) k = kMaxSegments;
+    for (; k >= 2; --k) {
+        double wt[kMaxSegments], tot = 0, before = 0;
+        for (int j = 0; j < k; ++j) {
+            wt[j] = 1.0 - kPassCost * before;
+            if (wt[j] < 0.15) wt[j] = 0.15;
+            before += wt[j];
+            tot += wt[j];
+        }
+        int b[kMaxSegments + 1];
+        b[0] = nch;
+        b[k] = 0;
+        bool ok = true;
+        double cum = 0;
+        for (int j = 1; j < k && ok; ++j) {
+            cum += wt[j - 1];
+            const double target = nch * (1.0 - cum / tot);
+            // the nearest allowed boundary: nch - 2i (m = 1) or a multiple
+            // of m (m even, nch even)
+            int v;
+            if (m == 1) {
+                const int i = int((nch - target) / 2.0 + 0.5);
+                v = nch - 2 * i;
+            } else {
+                v = int(target / m + 0.5) * m;
+            }
+            const int step = m > 1 ? m : 2;
+            if (v > b[j - 1] - step) v = b[j - 1] - step;
+            if (v < step) ok = false;
+            b[j] = v;
+        }
+        if (!ok) continue;
+        for (int j = 0; j < k; ++j) {
+            hi[j] = b[j];
+            lo[j] = b[j + 1];
+        }
+        return k;
+    }
+    return 1;
+}
+
+}  // namespace
+
+void set_backward_segments(int k) {
+    g_force_segments.store(k < 0 ? 0 : k, std::memory_order_relaxed);
+}
+
 hipError_t launch_wave_backward(const WaveBwdArgs& p, hipStream_t stream) {
     if (p.L % WL != 0 || p.L / WL < 1 || p.L / WL > 4 || p.L / WL == 3)
         return hipErrorInvalidValue;
-    const BwdArgs A = bwd_args(p);
+    BwdArgs A = bwd_args(p);
     if (A.BH <= 0 || A.T <= 0) return hipSuccess;
+    // workgroups per head: as many as fit beside the other heads' on the
+    // device's CUs (one workgroup per CU), at most kMaxSegments
+    int k = g_force_segments.load(std::memory_order_relaxed);
+    if (k == 0) {
+        const int cus = cu_count();
+        k = cus > 0 && A.BH < cus ? int(cus / A.BH) : 1;
+    }
+    const int nch = int((A.T + WL - 1) / WL);
+    A.nseg = plan_segments(nch, p.L / WL, k, A.seg_lo, A.seg_hi);
+    if (A.BH * A.nseg > int64_t(UINT32_MAX)) return hipErrorInvalidValue;
     const bool acc = A.add_dr || A.add_dk || A.add_dv;
-    const dim3 grid(unsigned(A.BH)), block(BTHREADS);
+    const dim3 grid(unsigned(A.BH * A.nseg)), block(BTHREADS);
     switch (p.L / WL) {
         case 1:
             if (acc)

@@ -7,6 +7,9 @@
 namespace rwkv7m {
 namespace wave {
 
+// Most workgroups one head's backward is split over (see BwdArgs::nseg).
+constexpr int kMaxSegments = 4;
+
 // Every byte offset into the vectors and the checkpoints is below 2^31
 // (checked by the host): addresses are a kernel-constant base plus a 32-bit
 // per-lane offset, and a lane with nothing to store or load uses the offset
@@ -24,7 +27,20 @@ struct BwdArgs {
     WaitCfg wait;
     // cotangents added to dr, dk, dv (the accumulating kernel; null: zeros)
     const bf16_t *add_dr, *add_dk, *add_dv;
+    // Workgroups per head and, per segment s, the chunks [seg_lo[s],
+    // seg_hi[s]) whose gradients that workgroup writes (segment 0 ends the
+    // sequence).  Workgroup blockIdx.x serves head blockIdx.x / nseg,
+    // segment blockIdx.x % nseg.
+    int nseg;
+    int seg_lo[kMaxSegments], seg_hi[kMaxSegments];
 };
+
+__device__ __forceinline__ int64_t head_of(const BwdArgs& A) {
+    return int64_t(blockIdx.x) / A.nseg;
+}
+__device__ __forceinline__ int seg_of(const BwdArgs& A) {
+    return int(blockIdx.x % unsigned(A.nseg));
+}
 
 __host__ inline BwdArgs bwd_args(const WaveBwdArgs& p) {
     BwdArgs A;
@@ -52,6 +68,10 @@ __host__ inline BwdArgs bwd_args(const WaveBwdArgs& p) {
     A.add_dr = static_cast<const bf16_t*>(p.add_dr);
     A.add_dk = static_cast<const bf16_t*>(p.add_dk);
     A.add_dv = static_cast<const bf16_t*>(p.add_dv);
+    A.nseg = 1;
+    for (int g = 0; g < kMaxSegments; ++g) A.seg_lo[g] = A.seg_hi[g] = 0;
+    A.seg_lo[0] = 0;
+    A.seg_hi[0] = int((p.T + WL - 1) / WL);
     return A;
 }
 
@@ -89,19 +109,25 @@ __device__ __forceinline__ i16x4_t to_j(const i16x4_t& t, const i16x4_t& kI) {
     return kq(x);
 }
 
-// A workgroup whose wait gave up overwrites every output of its head with
-// NaN (all `nthreads` threads of the workgroup take part).
+// A workgroup whose wait gave up overwrites every output it writes with NaN:
+// the gradients of its segment's tokens of its head, and dS0 if its segment
+// starts the sequence (all `nthreads` threads of the workgroup take part).
 __device__ __forceinline__ void poison(const BwdArgs& A, int tid,
                                        int nthreads) {
-    const int64_t bh = blockIdx.x;
+    const int64_t bh = head_of(A);
+    const int sg = seg_of(A);
     const int64_t hoff = A.lay.head(bh, WN);
+    const int64_t t_lo = int64_t(A.seg_lo[sg]) * WL;
+    int64_t t_hi = int64_t(A.seg_hi[sg]) * WL;
+    if (t_hi > A.T) t_hi = A.T;
     const bf16_t nan16 = 0x7fc0;
     bf16_t* const outs[6] = {A.dr, A.dw, A.dk, A.dv, A.da, A.db};
     for (int g = 0; g < 6; ++g)
-        for (int64_t e = tid; e < A.T * WN; e += nthreads)
+        for (int64_t e = t_lo * WN + tid; e < t_hi * WN; e += nthreads)
             outs[g][(e / WN) * A.lay.ts + hoff + e % WN] = nan16;
-    for (int e = tid; e < WN * WN; e += nthreads)
-        A.ds0[bh * WN * WN + e] = __builtin_nanf("");
+    if (A.seg_lo[sg] == 0)
+        for (int e = tid; e < WN * WN; e += nthreads)
+            A.ds0[bh * WN * WN + e] = __builtin_nanf("");
 }
 
 }  // namespace wave

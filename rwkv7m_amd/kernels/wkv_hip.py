@@ -52,6 +52,7 @@ EXPORTED_SYMBOLS = (
     "rwkv7m_last_error",
     "rwkv7m_device_status",
     "rwkv7m_debug_set_wait_limit",
+    "rwkv7m_debug_set_backward_segments",
     "rwkv7m_wkv7_last_path",
     "rwkv7m_wkv7_checkpoint_count",
     "rwkv7m_wkv7_default_checkpoint_interval",
@@ -109,6 +110,8 @@ def load_library(path: str | None = None):
         lib.rwkv7m_device_status.argtypes = [vp]
         lib.rwkv7m_debug_set_wait_limit.restype = None
         lib.rwkv7m_debug_set_wait_limit.argtypes = [i64]
+        lib.rwkv7m_debug_set_backward_segments.restype = None
+        lib.rwkv7m_debug_set_backward_segments.argtypes = [i32]
         lib.rwkv7m_wkv7_last_path.restype = ctypes.c_char_p
         lib.rwkv7m_wkv7_last_path.argtypes = []
         lib.rwkv7m_wkv7_checkpoint_count.restype = i64
@@ -266,6 +269,13 @@ def set_wait_limit(polls: int) -> None:
     """Poll budget of the kernels' bounded waits for later launches (0: the
     library default).  For tests of the failure path."""
     load_library().rwkv7m_debug_set_wait_limit(int(polls))
+
+
+def set_backward_segments(workgroups_per_head: int) -> None:
+    """Workgroups per head of the MFMA backward for later launches (0: as
+    many as the idle CUs allow).  Results are bit-identical for every count;
+    for tests."""
+    load_library().rwkv7m_debug_set_backward_segments(int(workgroups_per_head))
 
 
 def default_checkpoint_interval(dtype: torch.dtype, head_size: int) -> int:

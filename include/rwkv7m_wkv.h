@@ -106,6 +106,14 @@ void rwkv7m_debug_set_wait_limit(int64_t polls);
 void rwkv7m_debug_set_backward_segments(int workgroups_per_head);
 
 /*
+ * The same for the MFMA forward (at most 2 workgroups per head by default):
+ * each writes y and the checkpoints of its run of chunks and first carries
+ * the state through the chunks before them.  Bit-identical results for
+ * every count.  A hook for tests; no counterpart in the reference.
+ */
+void rwkv7m_debug_set_forward_segments(int workgroups_per_head);
+
+/*
  * Name of the kernel path the last successful WKV-7 call on this thread
  * launched: "wave_forward" (MFMA chunked forward), "decode" (single-token
  * kernel), "seq_forward", "wave_backward" (MFMA chunked backward, with the

@@ -740,6 +740,10 @@ void rwkv7m_debug_set_backward_segments(int workgroups_per_head) {
     rwkv7m::set_backward_segments(workgroups_per_head);
 }
 
+void rwkv7m_debug_set_forward_segments(int workgroups_per_head) {
+    rwkv7m::set_forward_segments(workgroups_per_head);
+}
+
 int64_t rwkv7m_wkv7_checkpoint_count(int64_t T, int64_t checkpoint_interval) {
     if (T < 0 || checkpoint_interval <= 0) return -1;
     return (T + checkpoint_interval - 1) / checkpoint_interval + 1;

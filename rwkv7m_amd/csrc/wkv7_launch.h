@@ -77,6 +77,9 @@ struct ChunkFwdArgs {
 // The forward runs in 16-token chunks (wkv7_wave_fwd.hip); L in {16, 32, 64}
 // is the checkpoint interval (checkpoints every L / 16 chunks).
 hipError_t launch_wave_forward(const ChunkFwdArgs& p, hipStream_t stream);
+// Workgroups per head for later wave forward launches (0: as many as the
+// device's idle CUs allow, at most 2).  A hook for tests.
+void set_forward_segments(int k);
 
 // Wave-specialised backward (wkv7_wave_bwd.hip): 16-token chunks, bf16
 // checkpoints every L in {16, 32, 64} tokens.  A head with a chunk outside

@@ -49,6 +49,8 @@
 // 16x16x16 product never accumulates onto a 16x16x32 result or the other way
 // round: every such hand-over goes through a VALU operation.
 
+#include <atomic>
+
 #include "wkv7_wave_common.h"
 
 namespace rwkv7m {
@@ -112,6 +114,9 @@ struct WaveFwdSmem {
 };
 
 
+// Most workgroups one head's forward is split over (see FwdArgs::nseg).
+constexpr int kMaxFwdSegments = 2;
+
 struct FwdArgs {
     int64_t T, BH;
     VecLayout lay;
@@ -123,14 +128,29 @@ struct FwdArgs {
     int cstride;   // checkpoint interval / 16
     int cshift;    // log2(cstride)
     WaitCfg wait;
+    // Workgroups per head and, per segment g, the chunks [seg_lo[g],
+    // seg_hi[g]) whose y and checkpoints that workgroup writes; it carries
+    // the state through the chunks before them without writing anything.
+    // Workgroup blockIdx.x serves head blockIdx.x / nseg, segment
+    // blockIdx.x % nseg; the segment with seg_hi == the chunk count also
+    // writes S_T and the last checkpoint.
+    int nseg;
+    int seg_lo[kMaxFwdSegments], seg_hi[kMaxFwdSegments];
 };
+
+__device__ __forceinline__ int64_t head_of(const FwdArgs& A) {
+    return int64_t(blockIdx.x) / A.nseg;
+}
+__device__ __forceinline__ int seg_of(const FwdArgs& A) {
+    return int(blockIdx.x % unsigned(A.nseg));
+}
 
 // ---------------------------------------------------------------------------
 // Producer p: chunks p, p + NPROD, ...
 __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
                                         int p, int lane) {
     const int lr = lane & 15, lq = lane >> 4;
-    const int64_t bh = blockIdx.x;
+    const int64_t bh = head_of(A);
     const int64_t hoff = A.lay.head(bh, WN);
     const int64_t T = A.T;
     const int nch = int((T + WL - 1) / WL);
@@ -167,9 +187,12 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
         return *reinterpret_cast<const uint2*>(rbase + vv * (2 * 8 * 8 * 8) +
                                                kb * (2 * 8 * 8));
     };
-    if (p < nch) fetch(p);
+    // this workgroup's chunks end at c_hi (the chunks before its own it
+    // only carries the state through)
+    const int c_hi = A.seg_hi[seg_of(A)];
+    if (p < c_hi) fetch(p);
 
-    for (int c = p; c < nch; c += NPROD) {
+    for (int c = p; c < c_hi; c += NPROD) {
         const int n = int(T - int64_t(c) * WL < WL ? T - int64_t(c) * WL : WL);
         const bool valid = lr < n;
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this chunk's vectors
@@ -323,7 +346,7 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
         // vectors load during the rest of this one
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
         asm volatile("" ::: "memory");
-        if (c + NPROD < nch) fetch(c + NPROD);
+        if (c + NPROD < c_hi) fetch(c + NPROD);
 
         // 2^{g_ref} of column 16 jb + lr (W's columns in the J layout) and
         // of rows 16 jb + 4 lq + e (the T layout): folded into W and R~, so
@@ -411,7 +434,7 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
 __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
                                       int ib, int lane) {
     const int lr = lane & 15, lq = lane >> 4;
-    const int64_t bh = blockIdx.x;
+    const int64_t bh = head_of(A);
     const int64_t sbase = bh * WN * WN;
     const int64_t hoff = A.lay.head(bh, WN);
     const int64_t T = A.T;
@@ -512,11 +535,16 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
     int s = 0, cph = 0;
     int64_t ckoff = sbase;
     SlotRegs cur;
-    const int nrun = nch > 0 && take(0, 0, -1, cur) ? nch : 0;
+    // this workgroup's chunks [c_lo, c_hi); it carries the state through the
+    // chunks before c_lo without writing y or checkpoints
+    const int sg = seg_of(A);
+    const int c_lo = A.seg_lo[sg], c_hi = A.seg_hi[sg];
+    const int nrun = c_hi > 0 && take(0, 0, -1, cur) ? c_hi : 0;
     for (int c = 0; c < nrun; ++c) {
         const int64_t t0 = int64_t(c) * WL;
         const int n = int(T - t0 < WL ? T - t0 : WL);
         const int exact = cur.exact;
+        const bool own = c >= c_lo;
         const int sn = s + 1 == NSLOT ? 0 : s + 1;  // the next chunk's slot
 
         // bf16(S_0): the operand of the state step and of y, and the
@@ -550,7 +578,7 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
         yc = -1;
         if (ckp >= 0) store_ck();
         ckp = -1;
-        if (A.ckpt && cph == 0) {
+        if (A.ckpt && cph == 0 && own) {
             // rows 16 ib .. + 15 of checkpoint c / stride, and at once their
             // whole-row read-back (the same wave's LDS accesses complete in
             // order)
@@ -564,7 +592,7 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
                 &ckr[8 + (lane >> 3)][8 * (lane & 7)]);
             ckp = ckoff;
         }
-        if (!exact) {
+        if (!exact && own) {
             // Y^T_ib = bf16(S_0) Q^^T + U^T Arb^T + V^T Ark^T, lane:
             // y[t0 + lr][16 ib + 4 lq ..] (added and stored in the next
             // iteration)
@@ -576,7 +604,7 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
             mfma(yq, Sb1, cur.Q1);
             yc = c;
         } else {
-            lds_drain();  // the slot's reads (unused) have completed
+            lds_drain();  // the slot's reads (some unused) have completed
         }
         // the slot goes back to the producers: its reads completed before
         // their values were used
@@ -588,7 +616,7 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
             cph = 0;
             ckoff += A.BH * NN;
         }
-        if (c + 1 < nch &&
+        if (c + 1 < c_hi &&
             !take(c + 1, s, __builtin_amdgcn_readfirstlane(word), cur))
             break;
         if (exact) {
@@ -621,14 +649,16 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
                     }
                 acc += __shfl_xor(acc, 16);
                 acc += __shfl_xor(acc, 32);
-                if (lq == 0) A.y[off + row] = to_bf16(acc);
+                if (lq == 0 && own) A.y[off + row] = to_bf16(acc);
             }
         }
     }
     if (yc >= 0) store_y();
     if (ckp >= 0) store_ck();
 
-    // final state (fp32) and the last checkpoint
+    // final state (fp32) and the last checkpoint, from the segment that
+    // ends the sequence
+    if (c_hi < nch) return;
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
         *reinterpret_cast<float4*>(A.s_t + sbase + row * WN + 16 * jb +
@@ -644,24 +674,38 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
     }
 }
 
-// A workgroup whose hand-over failed overwrites every output of its
-// (batch, head) -- y, S_T and the checkpoints -- with NaN, so that a lost
-// hand-over can never pass as a result.
+// A workgroup whose hand-over failed overwrites every output it writes --
+// y and the checkpoints of its segment's chunks, and S_T if its segment ends
+// the sequence -- with NaN, so that a lost hand-over can never pass as a
+// result.
 __device__ __forceinline__ void poison(const FwdArgs& A, int tid) {
-    const int64_t bh = blockIdx.x;
+    const int64_t bh = head_of(A);
+    const int sg = seg_of(A);
     const int64_t hoff = A.lay.head(bh, WN);
     const int64_t NN = WN * WN;
+    const int64_t nch = (A.T + WL - 1) / WL;
+    const int64_t t_lo = int64_t(A.seg_lo[sg]) * WL;
+    int64_t t_hi = int64_t(A.seg_hi[sg]) * WL;
+    if (t_hi > A.T) t_hi = A.T;
+    const bool last = A.seg_hi[sg] == nch;
     const bf16_t nan16 = 0x7fc0;
-    for (int64_t e = tid; e < A.T * WN; e += WTHREADS)
+    for (int64_t e = t_lo * WN + tid; e < t_hi * WN; e += WTHREADS)
         A.y[(e / WN) * A.lay.ts + hoff + e % WN] = nan16;
-    for (int e = tid; e < WN * WN; e += WTHREADS)
-        A.s_t[bh * NN + e] = __builtin_nanf("");
+    if (last)
+        for (int e = tid; e < WN * WN; e += WTHREADS)
+            A.s_t[bh * NN + e] = __builtin_nanf("");
     if (A.ckpt) {
-        const int64_t nch = (A.T + WL - 1) / WL;
+        // checkpoint k holds the state before chunk k * stride (the last
+        // one S_T): those of this segment's chunks, and S_T's if last
         const int64_t nck = (nch + A.cstride - 1) / A.cstride + 1;
-        for (int64_t c = 0; c < nck; ++c)
+        for (int64_t k = 0; k < nck; ++k) {
+            const int64_t c = k * A.cstride;
+            const bool mine = (c >= A.seg_lo[sg] && c < A.seg_hi[sg]) ||
+                              (last && k == nck - 1);
+            if (!mine) continue;
             for (int e = tid; e < WN * WN; e += WTHREADS)
-                A.ckpt[c * A.BH * NN + bh * NN + e] = nan16;
+                A.ckpt[k * A.BH * NN + bh * NN + e] = nan16;
+        }
     }
 }
 
@@ -692,6 +736,75 @@ wkv7_wave_fwd_kernel(FwdArgs A) {
 
 }  // namespace
 
+namespace {
+
+// Cost of a chunk whose workgroup only carries the state through it (no y,
+// no checkpoint), relative to a chunk it writes.  A chain wave takes about
+// 1,190 against 1,850 cycles per chunk, but the whole workgroup's time also
+// has the producers' start and the chain's end; 0.8 gave the shortest
+// forwards of 0.5 .. 0.95 measured at B8 T512 H12, B4 T512 H12 and
+// B1 T2048 H8.
+constexpr double kFwdPassCost = 0.8;
+
+std::atomic<int> g_force_fwd_segments{0};
+std::atomic<int> g_fwd_cu_count[64];
+
+int fwd_cu_count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int n = g_fwd_cu_count[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount,
+                                  dev) != hipSuccess)
+            return 0;
+        g_fwd_cu_count[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+// Splits a head's nch chunks over k workgroups (at most kMaxFwdSegments):
+// segment j owns chunks [lo[j], hi[j]) and first carries the state through
+// every earlier chunk.  Equal finishing times give segment j the weight
+// 1 - kFwdPassCost * (the weights before it).  Returns the number of
+// segments (1 when a segment would own no chunk).
+int plan_fwd_segments(int nch, int k, int* lo, int* hi) {
+    lo[0] = 0;
+    hi[0] = nch;
+    if (k > kMaxFwdSegments) k = kMaxFwdSegments;
+    for (; k >= 2; --k) {
+        double wt[kMaxFwdSegments], tot = 0, before = 0;
+        for (int j = 0; j < k; ++j) {
+            wt[j] = 1.0 - kFwdPassCost * before;
+            if (wt[j] < 0.1) wt[j] = 0.1;
+            before += wt[j];
+            tot += wt[j];
+        }
+        int b[kMaxFwdSegments + 1];
+        b[0] = 0;
+        b[k] = nch;
+        bool ok = true;
+        double cum = 0;
+        for (int j = 1; j < k && ok; ++j) {
+            cum += wt[j - 1];
+            b[j] = int(nch * cum / tot + 0.5);
+            if (b[j] <= b[j - 1] || b[j] >= nch) ok = false;
+        }
+        if (!ok) continue;
+        for (int j = 0; j < k; ++j) {
+            lo[j] = b[j];
+            hi[j] = b[j + 1];
+        }
+        return k;
+    }
+    return 1;
+}
+
+}  // namespace
+
+void set_forward_segments(int k) {
+    g_force_fwd_segments.store(k < 0 ? 0 : k, std::memory_order_relaxed);
+}
+
 hipError_t launch_wave_forward(const ChunkFwdArgs& p, hipStream_t stream) {
     // p.L: the checkpoint interval, a multiple of the 16-token chunk
     if (p.L % WL != 0 || p.L / WL < 1 || p.L / WL > 4)
@@ -714,7 +827,18 @@ hipError_t launch_wave_forward(const ChunkFwdArgs& p, hipStream_t stream) {
     A.cshift = A.cstride == 4 ? 2 : A.cstride == 2 ? 1 : 0;
     A.wait = p.wait;
     if (A.BH <= 0) return hipSuccess;
-    hipLaunchKernelGGL(wkv7_wave_fwd_kernel, dim3(unsigned(A.BH)),
+    // workgroups per head: as many as fit beside the other heads' on the
+    // device's CUs (one workgroup per CU), at most kMaxFwdSegments
+    int k = g_force_fwd_segments.load(std::memory_order_relaxed);
+    if (k == 0) {
+        const int cus = fwd_cu_count();
+        k = cus > 0 && A.BH < cus ? int(cus / A.BH) : 1;
+    }
+    for (int g = 0; g < kMaxFwdSegments; ++g) A.seg_lo[g] = A.seg_hi[g] = 0;
+    A.nseg = plan_fwd_segments(int((A.T + WL - 1) / WL), k, A.seg_lo,
+                               A.seg_hi);
+    if (A.BH * A.nseg > int64_t(UINT32_MAX)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(wkv7_wave_fwd_kernel, dim3(unsigned(A.BH * A.nseg)),
                        dim3(WTHREADS), 0, stream, A);
     return hipGetLastError();
 }

@@ -53,6 +53,7 @@ EXPORTED_SYMBOLS = (
     "rwkv7m_device_status",
     "rwkv7m_debug_set_wait_limit",
     "rwkv7m_debug_set_backward_segments",
+    "rwkv7m_debug_set_forward_segments",
     "rwkv7m_wkv7_last_path",
     "rwkv7m_wkv7_checkpoint_count",
     "rwkv7m_wkv7_default_checkpoint_interval",
@@ -112,6 +113,8 @@ def load_library(path: str | None = None):
         lib.rwkv7m_debug_set_wait_limit.argtypes = [i64]
         lib.rwkv7m_debug_set_backward_segments.restype = None
         lib.rwkv7m_debug_set_backward_segments.argtypes = [i32]
+        lib.rwkv7m_debug_set_forward_segments.restype = None
+        lib.rwkv7m_debug_set_forward_segments.argtypes = [i32]
         lib.rwkv7m_wkv7_last_path.restype = ctypes.c_char_p
         lib.rwkv7m_wkv7_last_path.argtypes = []
         lib.rwkv7m_wkv7_checkpoint_count.restype = i64
@@ -276,6 +279,13 @@ def set_backward_segments(workgroups_per_head: int) -> None:
     many as the idle CUs allow).  Results are bit-identical for every count;
     for tests."""
     load_library().rwkv7m_debug_set_backward_segments(int(workgroups_per_head))
+
+
+def set_forward_segments(workgroups_per_head: int) -> None:
+    """Workgroups per head of the MFMA forward for later launches (0: as
+    many as the idle CUs allow).  Results are bit-identical for every count;
+    for tests."""
+    load_library().rwkv7m_debug_set_forward_segments(int(workgroups_per_head))
 
 
 def default_checkpoint_interval(dtype: torch.dtype, head_size: int) -> int:

@@ -1,4 +1,12 @@
-"""The MFMA backward split over several workgroups per head.
+"""The MFMA kernels split over several workgroups per head.
+
+Forward: with few heads the library splits each head's chunks over two
+workgroups: each writes y and the checkpoints of its own run of chunks and
+first carries the state through the chunks before them
+(rwkv7m_debug_set_forward_segments overrides the count).  Every count must
+give y, S_T and checkpoints bit-identical to one workgroup per head.
+
+Backward:
 
 With few heads (B * H well below the CU count) the library splits each
 head's chunks over up to four workgroups: each writes the gradients of its
@@ -28,6 +36,54 @@ def hip(hip_lib):
     from rwkv7m_amd.kernels import wkv_hip
     yield wkv_hip
     wkv_hip.set_backward_segments(0)
+    wkv_hip.set_forward_segments(0)
+
+
+def _forward(hip, dev, ci, segments):
+    hip.set_forward_segments(segments)
+    vecs = [dev[n] for n in NAMES]
+    (y, s_t), (ckpt, _) = hip.forward_with_aux(*vecs, dev["s0"],
+                                               checkpoint_interval=ci)
+    assert hip.last_path() == "wave_forward"
+    torch.cuda.synchronize()
+    return [y.clone(), s_t.clone(), ckpt.clone()]
+
+
+def _compare_forward(hip, inp, ci, counts, case):
+    print("case:", case, flush=True)
+    dev = {k: v.cuda() for k, v in inp.items()}
+    ref = _forward(hip, dev, ci, 1)
+    for k in counts:
+        got = _forward(hip, dev, ci, k)
+        for name, a, b in zip(("y", "S_T", "checkpoints"), got, ref):
+            assert torch.equal(a, b), (
+                f"{case}: {k} workgroups per head, {name} differs from one "
+                f"workgroup per head")
+    hip.set_forward_segments(0)
+
+
+@pytest.mark.parametrize("ci", [16, 32, 64])
+def test_forward_split_is_bit_identical(hip, ci):
+    for T, B, H in ((1000, 1, 2), (130, 2, 1), (40, 1, 3)):
+        inp = make_inputs(T, B, H, 64, seed=T + ci, state_std=0.1)
+        _compare_forward(hip, inp, ci, (0, 2),
+                         f"forward split T{T} B{B} H{H} L{ci}")
+
+
+def test_forward_split_with_exact_chunks(hip):
+    # decays strong in tokens 256..383 of head 1: those chunks take the
+    # chains' exact pass, in the first segment's own chunks and in the
+    # second's carried ones
+    inp = make_inputs(768, 1, 2, 64, seed=13, state_std=0.1)
+    w = inp["w"].float()
+    w[256:384, :, 1] += 3.0
+    inp["w"] = w.to(torch.bfloat16)
+    _compare_forward(hip, inp, 16, (0, 2), "forward split exact chunks")
+
+
+def test_forward_split_config1_shape(hip):
+    inp = make_inputs(512, 8, 12, 64, seed=1, generator="torch")
+    _compare_forward(hip, inp, 16, (0,), "forward split config 1")
 
 
 def _backward(hip, dev, aux, segments, layout, add=None):

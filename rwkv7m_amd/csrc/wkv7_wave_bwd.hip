@@ -308,6 +308,11 @@ __device__ __forceinline__ void fetch_vecs(const BwdArgs& A, int w,
                                            uint32_t cb2, int n, int lane) {
     const VecPtrs src{A.r, A.w, A.k, A.v, A.a, A.b, A.dy};
     const int ldu = lane & 7, ldseg = lane >> 3;
+    // the stage's LDS address, formed here and opaque to the compiler: the
+    // fourteen destinations are then sums formed at each load, instead of
+    // fourteen scalar registers held (and spilled) across the whole loop
+    uint32_t base = lds_addr(&lds_stage[w][0][0][0][0]);
+    asm volatile("" : "+s"(base));
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int t = 8 * h + ldu;
@@ -315,7 +320,9 @@ __device__ __forceinline__ void fetch_vecs(const BwdArgs& A, int w,
             cb2 + uint32_t(t < n ? t : n - 1) * A.ts2 + 16 * ldseg;
 #pragma unroll
         for (int vv = 0; vv < 7; ++vv)
-            dma16(src.get(vv), off, lds_addr(&lds_stage[w][vv][h][0][0]));
+            dma16(src.get(vv), off,
+                  base + uint32_t(sizeof(lds_stage[0][0])) * vv +
+                      uint32_t(sizeof(lds_stage[0][0][0])) * h);
     }
 }
 
@@ -329,9 +336,11 @@ __device__ __forceinline__ void fetch_state(const BwdArgs& A, int w, int c,
         (uint32_t(c / M) * uint32_t(A.BH) + uint32_t(head_of(A))) *
             uint32_t(NN * 2) +
         uint32_t(((lane & 7) * WN + 8 * (lane >> 3)) * 2);
+    uint32_t base = lds_addr(&lds_S[w][0]);
+    asm volatile("" : "+s"(base));
 #pragma unroll
     for (int g = 0; g < 8; ++g)
-        dma16(A.ckpt, off + 8 * g * WN * 2, lds_addr(&lds_S[w][512 * g]));
+        dma16(A.ckpt, off + 8 * g * WN * 2, base + 1024 * g);
 }
 
 // The T layout read of vector vv from worker w's stage: token lr, columns
@@ -421,11 +430,11 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         const bool starts = !skim && c % m == 0;
         const bool feeds = !skim && c % m != m - 1 && c + 1 < c_hi;
         // the vectors.  Vector memory operations complete in issue order, and
-        // since the vectors' loads this worker issued the previous chunk's 24
-        // gradient stores (4 of dv, 20 of the column blocks; none after a
-        // chunk that only published its map) and, when this chunk starts an
-        // interval, its start state's 8 loads, whose wait comes only before
-        // S_0's first use
+        // since the vectors' loads this worker issued the previous chunk's 12
+        // gradient stores (2 of dv, 10 of the column blocks, 16 bytes per
+        // lane; none after a chunk that only published its map) and, when
+        // this chunk starts an interval, its start state's 8 loads, whose
+        // wait comes only before S_0's first use
         if (kord == 0 || c + NWORK >= c_hi) {
             if (starts)
                 __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8)
@@ -433,9 +442,9 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
         } else {
             if (starts)
-                __builtin_amdgcn_s_waitcnt(0x8f70);  // vmcnt(32)
+                __builtin_amdgcn_s_waitcnt(0x4f74);  // vmcnt(20)
             else
-                __builtin_amdgcn_s_waitcnt(0x4f78);  // vmcnt(24)
+                __builtin_amdgcn_s_waitcnt(0x0f7c);  // vmcnt(12)
         }
         asm volatile("" ::: "memory");
 
@@ -778,6 +787,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             asm volatile("" ::: "memory");
         }
         i16x4_t kdUT[4];
+        uint2 held_dv;
 #pragma unroll
         for (int ib = 0; ib < 4; ++ib) {
             const bf16x8_t d0 = frag_rows(D, ib, 0, lane);
@@ -803,8 +813,14 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) dv[e] += ad[e];
             }
-            // lane: dV[t0 + lr][16 ib + 4 lq + e]
-            store8(rs_dv, row2 + (16 * ib + 4 * lq) * 2, pack4(dv));
+            // lane: dV[t0 + lr][16 ib + 4 lq + e]; value blocks in pairs,
+            // 16 bytes per lane (pair_rows)
+            const uint2 pv = pack4(dv);
+            if ((ib & 1) == 0)
+                held_dv = pv;
+            else
+                store16(rs_dv, row2 + 32 * (ib - 1) + pair_off(lq),
+                        pair_rows(held_dv, pv));
         }
 
         // ---- cotangents of the 16 x 16 matrices (K = 64 over i) -----------
@@ -855,7 +871,8 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         // ---- per column block: dR~, dA~, dB~, dK~ and the input gradients -
         // (tiles of the transposes: lane holds token lr, columns
         // 16 jb + 4 lq + e, the T layout)
-        const uint32_t goff = row2 + 8 * lq;
+        const uint32_t goff = row2 + pair_off(lq);
+        uint2 held[5];
         const __amdgpu_buffer_rsrc_t rs_dr = whole_rsrc(A.dr),
                                      rs_dw = whole_rsrc(A.dw),
                                      rs_dk = whole_rsrc(A.dk),
@@ -886,11 +903,11 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         };
         if constexpr (ACC) {
             // the dr and dk cotangents: the next chunk's vector loads (if
-            // any) and the 4 dv stores came after them
+            // any) and the 2 dv stores came after them
             if (more)
-                __builtin_amdgcn_s_waitcnt(0x4f72);  // vmcnt(18)
+                __builtin_amdgcn_s_waitcnt(0x4f70);  // vmcnt(16)
             else
-                __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4)
+                __builtin_amdgcn_s_waitcnt(0x0f72);  // vmcnt(2)
             asm volatile("" ::: "memory");
         }
         Acc4 cur = products(0);
@@ -962,12 +979,20 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                     dkv[e] += ak[e];
                 }
             }
-            const uint32_t o = goff + 32 * jb;
-            store8(rs_dr, o, pack4(drv));
-            store8(rs_dw, o, pack4(dwv));
-            store8(rs_dk, o, pack4(dkv));
-            store8(rs_da, o, pack4(dav));
-            store8(rs_db, o, pack4(dbv));
+            // column blocks in pairs, 16 bytes per lane (pair_rows)
+            const uint2 pv[5] = {pack4(drv), pack4(dwv), pack4(dkv),
+                                 pack4(dav), pack4(dbv)};
+            if ((jb & 1) == 0) {
+#pragma unroll
+                for (int g = 0; g < 5; ++g) held[g] = pv[g];
+            } else {
+                const uint32_t o = goff + 32 * (jb - 1);
+                store16(rs_dr, o, pair_rows(held[0], pv[0]));
+                store16(rs_dw, o, pair_rows(held[1], pv[1]));
+                store16(rs_dk, o, pair_rows(held[2], pv[2]));
+                store16(rs_da, o, pair_rows(held[3], pv[3]));
+                store16(rs_db, o, pair_rows(held[4], pv[4]));
+            }
             if (jb < 3) cur = nxt;
         }
 

@@ -311,6 +311,33 @@ __device__ __forceinline__ void store8(__amdgpu_buffer_rsrc_t rs, uint32_t off,
     __builtin_amdgcn_raw_buffer_store_b64(x, rs, int(off), 0, 0);
 }
 
+// 16 bytes at byte offset `off` of the buffer.
+__device__ __forceinline__ void store16(__amdgpu_buffer_rsrc_t rs,
+                                        uint32_t off, uint4 v) {
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    const u32x4_t x = {v.x, v.y, v.z, v.w};
+    __builtin_amdgcn_raw_buffer_store_b128(x, rs, int(off), 0, 0);
+}
+
+// Two 16-column blocks of a token-major tile as 16-byte pieces.  Lane (q, r)
+// holds 8 bytes of block p (columns 16 p + 4 q .. + 3) in `a` and of block
+// p + 1 in `b`.  v_permlane16_swap exchanges the odd 16-lane rows of its
+// first operand with the even rows of its second, so after one swap per
+// dword an even-row lane holds columns 16 p + 4 q .. + 7 (its own and its
+// odd neighbour's `a`) and an odd-row lane columns 16 (p + 1) + 4 (q - 1)
+// .. + 7 (its even neighbour's `b` and its own): every lane then stores 16
+// contiguous bytes, at byte 32 p + pair_off(q) of the token's row, instead
+// of two 8-byte pieces (a half-line write per instruction and lane, which
+// the memory path serves at about two thirds of the rate of 16-byte ones).
+__device__ __forceinline__ uint4 pair_rows(uint2 a, uint2 b) {
+    const auto lo = __builtin_amdgcn_permlane16_swap(a.x, b.x, false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap(a.y, b.y, false, false);
+    return make_uint4(lo[0], hi[0], lo[1], hi[1]);
+}
+__device__ __forceinline__ uint32_t pair_off(int q) {
+    return uint32_t(8 * q + ((q & 1) ? 24 : 0));
+}
+
 // The LDS byte address of a __shared__ object.
 template <typename T>
 __device__ __forceinline__ uint32_t lds_addr(const T* p) {

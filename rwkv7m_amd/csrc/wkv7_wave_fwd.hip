@@ -61,6 +61,7 @@ using namespace wave;
 constexpr int NCHAIN = 4;    // chain waves (16 state rows each)
 constexpr int NPROD = 8;     // producer waves
 constexpr int NSLOT = 3;     // hand-over ring
+constexpr int NYBUF = 4;     // y staging buffers (y of chunk c: c % NYBUF)
 constexpr int WTHREADS = 64 * (NCHAIN + NPROD);
 // Every hand-over wait is bounded (WaitCfg::limit polls of ~64 cycles; a
 // wave waits for at most a few other chunks, and the default bound is orders
@@ -106,6 +107,15 @@ struct WaveFwdSmem {
     ProdStage st[NPROD];
     float eref[NPROD][WN];  // per producer: 2^{g_ref} per column
     float eL[NPROD][WN];    // per producer: 2^{g_L} per column
+    // y of chunk c on its way to global memory, buffer c % NYBUF: each chain
+    // writes its 16 columns and the producer of chunk c + 4 stores the 16
+    // rows whole (the slot wait it does anyway proves the four tiles are
+    // there, and it publishes chunk c + 4 before any chain can stage
+    // chunk c + NYBUF); the last NYBUF chunks are stored after the loops.
+    // Four chains each storing their own quarter of every 128-byte row, at
+    // their own times, cost about twice what y's bytes do.
+    bf16_t ys[NYBUF][WL][XPITCH];
+    int ychunk[NYBUF];      // the chunk whose y the buffer holds (-1: none)
     int ready[NSLOT];       // 2 c + exact for the chunk c the slot holds
                             // (exact: it needs the exact sequential pass;
                             // -1: none yet)
@@ -143,6 +153,27 @@ __device__ __forceinline__ int64_t head_of(const FwdArgs& A) {
 }
 __device__ __forceinline__ int seg_of(const FwdArgs& A) {
     return int(blockIdx.x % unsigned(A.nseg));
+}
+
+// ---------------------------------------------------------------------------
+// The staged y of chunk yc (buffer yb) as whole rows: lane l stores the
+// 16-byte pieces l % 8 of tokens l / 8 and 8 + l / 8 (two stores per lane,
+// every 128-byte row written whole); tokens past the end store at or past
+// the range's bound and are dropped.
+__device__ __forceinline__ void store_y_rows(const FwdArgs& A,
+                                             WaveFwdSmem& sm, int yb, int yc,
+                                             int64_t hoff, int lane) {
+    const int64_t ty = int64_t(yc) * WL;
+    const int ny = int(A.T - ty < WL ? A.T - ty : WL);
+    const uint32_t TS = uint32_t(A.lay.ts);
+    const __amdgpu_buffer_rsrc_t rs = out_rsrc(
+        A.y + (ty * A.lay.ts + hoff), (uint32_t(ny - 1) * TS + WN) * 2);
+    const int yt = lane >> 3, yo = 8 * (lane & 7);
+    const uint4 y0 = *reinterpret_cast<const uint4*>(&sm.ys[yb][yt][yo]);
+    const uint4 y1 = *reinterpret_cast<const uint4*>(&sm.ys[yb][8 + yt][yo]);
+    lds_drain();  // the buffer may be staged again once the reads are done
+    store16(rs, (uint32_t(yt) * TS + yo) * 2, y0);
+    store16(rs, (uint32_t(8 + yt) * TS + yo) * 2, y1);
 }
 
 // ---------------------------------------------------------------------------
@@ -192,10 +223,19 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
     const int c_hi = A.seg_hi[seg_of(A)];
     if (p < c_hi) fetch(p);
 
+    // y stores issued after the next chunk's vector loads (their count: the
+    // wait for those loads lets them run on)
+    int ystores = 0;
     for (int c = p; c < c_hi; c += NPROD) {
         const int n = int(T - int64_t(c) * WL < WL ? T - int64_t(c) * WL : WL);
         const bool valid = lr < n;
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this chunk's vectors
+        // this chunk's vectors (vector memory operations complete in issue
+        // order)
+        if (ystores)
+            __builtin_amdgcn_s_waitcnt(0x0f72);  // vmcnt(2)
+        else
+            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+        ystores = 0;
         asm volatile("" ::: "memory");
         uint2 raw[6][4];
 #pragma unroll
@@ -406,6 +446,18 @@ __device__ __forceinline__ void produce(const FwdArgs& A, WaveFwdSmem& sm,
             if (got < 0) wait_failed(&sm.failed, A.wait.failures, lane);
             break;
         }
+        // y of chunk c - 4: its four tiles were staged before chunk c - 3's
+        // slot came back (done above)
+        {
+            const int yb = c & (NYBUF - 1);
+            const int ych =
+                __builtin_amdgcn_readfirstlane(lds_load(&sm.ychunk[yb]));
+            if (ych >= 0) {
+                store_y_rows(A, sm, yb, ych, hoff, lane);
+                if (lane == 0) lds_store(&sm.ychunk[yb], -1);
+                ystores = 2;
+            }
+        }
         Slot& sl = sm.slot[s];
         sl.W[0][lane] = pk8(wt[0], wt[1]);
         sl.W[1][lane] = pk8(wt[2], wt[3]);
@@ -502,18 +554,17 @@ __device__ __forceinline__ void chain(const FwdArgs& A, WaveFwdSmem& sm,
     };
     // y of the previous chunk as its two products, added and stored one
     // iteration late (complete by then): rows of chunk yc (yc < 0: none)
+    // (into y buffer yc % NYBUF, whole rows stored by a producer)
     f32x4_t yq = zero4(), yp = zero4();
     int yc = -1;
     auto store_y = [&]() {
-        const int64_t ty = int64_t(yc) * WL;
-        const int ny = int(T - ty < WL ? T - ty : WL);
         f32x4_t yy;
 #pragma unroll
         for (int e = 0; e < 4; ++e) yy[e] = yq[e] + yp[e];
-        // lanes of tokens past the end store at or past the bound: dropped
-        const __amdgpu_buffer_rsrc_t rs = out_rsrc(
-            A.y + (ty * A.lay.ts + hoff), (uint32_t(ny - 1) * TS + WN) * 2);
-        store8(rs, (uint32_t(lr) * TS + 16 * ib + 4 * lq) * 2, pack4(yy));
+        const int yb = yc & (NYBUF - 1);
+        *reinterpret_cast<uint2*>(&sm.ys[yb][lr][16 * ib + 4 * lq]) =
+            pack4(yy);
+        if (ib == 0 && lane == 0) lds_store(&sm.ychunk[yb], yc);
     };
     // this chain's rows of a checkpoint: written to its LDS rows in the
     // register layout, read back at once as whole rows (lane l: 16-byte
@@ -720,6 +771,7 @@ wkv7_wave_fwd_kernel(FwdArgs A) {
         sm.ready[tid] = -1;
         sm.done[tid] = 0;
     }
+    if (tid < NYBUF) sm.ychunk[tid] = -1;
 
     if (tid == 0) sm.failed = 0;
     __syncthreads();
@@ -731,7 +783,17 @@ wkv7_wave_fwd_kernel(FwdArgs A) {
     // in flight)
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (lds_load(&sm.failed) != 0) poison(A, tid);
+    if (lds_load(&sm.failed) != 0) {
+        poison(A, tid);
+        return;
+    }
+    // the y of the last chunks, which no later producer stored: wave b
+    // stores buffer b
+    if (wv < NYBUF) {
+        const int ych = __builtin_amdgcn_readfirstlane(lds_load(&sm.ychunk[wv]));
+        if (ych >= 0)
+            store_y_rows(A, sm, wv, ych, A.lay.head(head_of(A), WN), lane);
+    }
 }
 
 }  // namespace

@@ -28,11 +28,13 @@
 //              + E_0,   E_0 = sum_i D_0[i, :] S_0[i, :]
 //
 // and dw = dlog d * (-e^w).  E is needed at every other chunk boundary
-// only: the chunk at an even position of the reverse order takes it at its
-// start; the chunk at the next (odd) position, one chunk earlier in time,
-// takes the same value as its end value E_L and recovers its own start
-// value through the same identity, E_0 = E_L - sum over the chunk of
-// (b db + k dk - r dr - a da).  These are the reference's reverse equations
+// only: a start member (a position of the reverse order of parity tpar, or
+// position 0) takes it at its start; the chunk at the next position, one
+// chunk earlier in time, takes the same value as its end value E_L and
+// recovers its own start value through the same identity,
+// E_0 = E_L - sum over the chunk of (b db + k dk - r dr - a da).  With an
+// interval of two chunks the start members are the checkpoint chunks, so
+// that the chains never wait for a recomputed start state.  These are the reference's reverse equations
 // (src/rwkv7m/kernels/wkv_pallas_gpu.py:221-257) summed over a chunk; states
 // come from checkpoints, never from dividing by the decay.  Inside an
 // interval of m chunks, the start state of chunk c + 1 is recomputed from
@@ -108,7 +110,7 @@ __shared__ uint4 lds_stage[NWORK][7][2][8][8];
 __shared__ bf16_t lds_S[NWORK][NN];  // the chunk's start state (sd_off)
 __shared__ bf16_t lds_D[NWORK][NN];  // the cotangent of its end state
 __shared__ BMap lds_map[NWORK];
-// sum_i D_0 S_0 per chain, for the even positions' workers (0 and 2)
+// sum_i D_0 S_0 per chain, for the start members' workers (tail_start)
 __shared__ float lds_tail[NWORK][NCHAIN][WN];
 // per-column factors of the chunk: [0] 2^{g_L - g_ref}, [1] 2^{g_ref},
 // [2] 2^{g_L} (written by lanes 0, 1, 2 of each 16-lane row in one store)
@@ -145,6 +147,15 @@ __device__ __forceinline__ int wait_for(const WaitCfg& wc, int* p, int lane,
     return -1;
 }
 
+
+// Whether the chunk at reverse position p takes the decay gradient's
+// boundary sum sum_i D_0 S_0 at its start (a start member; the chains form it
+// there) or at its end, from the start member one position earlier (an end
+// member, one chunk earlier in time).  Start members are the positions of
+// parity A.tpar, and position 0 (whose end is the sequence's end).
+__device__ __forceinline__ bool tail_start(const BwdArgs& A, int p) {
+    return (p & 1) == A.tpar || p == 0;
+}
 
 // ---------------------------------------------------------------------------
 // Chain ib: rows 16 ib .. 16 ib + 15 of the cotangent through every chunk.
@@ -245,10 +256,10 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
         }
 
         // The decay gradient needs sum_i D_0[i][j] S_0[i][j] at every other
-        // chunk boundary only: the worker of an even position takes it as
-        // its chunk's start value, and the worker of the next (odd)
-        // position, one chunk earlier in time, as its chunk's end value.
-        if (p & 1) continue;
+        // chunk boundary only: a start member's worker takes it as its
+        // chunk's start value, and the worker of the next position, one
+        // chunk earlier in time, as its chunk's end value (tail_start).
+        if (!tail_start(A, p)) continue;
         if (c >= c_hi) {
             // a chunk past this workgroup's own: no gradients, so no share,
             // but the count stays in step with the worker's chunk order
@@ -262,7 +273,7 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
         // accumulation)
         if (wait_for(A.wait, &fl.s_ready[w], lane,
                      [&](int x) { return x == c; }, true) <= 0 ||
-            (kord > 0 && wait_for(A.wait, &fl.tail_used[w + 1], lane,
+            (kord > 0 && wait_for(A.wait, &fl.tail_used[(w + 1) % NWORK], lane,
                                   [&](int x) { return x >= kord; },
                                   true) <= 0)) {
             done = false;
@@ -429,6 +440,13 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         // S_0 is checkpoint c / m; S_0 of c + 1 is formed here
         const bool starts = !skim && c % m == 0;
         const bool feeds = !skim && c % m != m - 1 && c + 1 < c_hi;
+        // the decay gradient's boundary sum (tail_start): a start member
+        // takes it at its own start (worker tw = w, round tk = kord); an end
+        // member at its end, from the start member one position earlier
+        // (worker w - 1; round kord - 1 when that is worker NWORK - 1)
+        const bool endm = !tail_start(A, p);
+        const int tw = endm ? (w + NWORK - 1) % NWORK : w;
+        const int tk = (endm && w == 0) ? kord - 1 : kord;
         // the vectors.  Vector memory operations complete in issue order, and
         // since the vectors' loads this worker issued the previous chunk's 12
         // gradient stores (2 of dv, 10 of the column blocks, 16 bytes per
@@ -648,28 +666,185 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             kMinvT = kq(dM);
         }
 
-        // ---- W^ = Minv A^, Q^ = R~ 2^{g_ref} + Arb W^ (J layout); the map -
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb) {
-            const float erj = lds_fac[w][1][16 * jb + lr];
-            f32x4_t x = zero4();
-            mfma16(x, kMinv, to_j(tA[jb], kI));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) x[e] *= erj;
-            const i16x4_t kW = kq(x);
-            f32x4_t y = unpack_i16(to_j(tR[jb], kI));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] *= erj;
-            mfma16(y, kArbA, kW);
-            map.QW[jb][lane] = pk8(kq(y), kW);
+        // The phases after the factors, as calls: the map (the chains'
+        // operands), U and X (need S_0), and dX, dU, dV (need D).  At an
+        // interval of two chunks the even (checkpoint) chunk forms U, X and
+        // its successor's start state first, and the odd chunk, whose start
+        // state that is, forms dX, dU, dV before waiting for it; otherwise
+        // the odd chunk's worker waits most of a chunk for it.
+        bf16x8_t Bhp0, Bhp1;
+        i16x4_t kXT[4], kdUT[4];
+        auto publish_map = [&]() {
+            // ---- W^ = Minv A^, Q^ = R~ 2^{g_ref} + Arb W^ (J layout); the map -
+    #pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+                const float erj = lds_fac[w][1][16 * jb + lr];
+                f32x4_t x = zero4();
+                mfma16(x, kMinv, to_j(tA[jb], kI));
+    #pragma unroll
+                for (int e = 0; e < 4; ++e) x[e] *= erj;
+                const i16x4_t kW = kq(x);
+                f32x4_t y = unpack_i16(to_j(tR[jb], kI));
+    #pragma unroll
+                for (int e = 0; e < 4; ++e) y[e] *= erj;
+                mfma16(y, kArbA, kW);
+                map.QW[jb][lane] = pk8(kq(y), kW);
+            }
+            Bhp0 = pk8(tB[0], tB[1]);
+            Bhp1 = pk8(tB[2], tB[3]);
+            map.Bh[0][lane] = Bhp0;
+            map.Bh[1][lane] = Bhp1;
+    #pragma unroll
+            for (int ib = 0; ib < 4; ++ib) map.dY[ib][lane] = jdY[ib];
+            lds_drain();
+            if (lane == 0) lds_store(&fl.map_ready[w], kord + 1);
+        };
+        auto do_ux = [&]() -> bool {
+            // ---- U = A^ S_0^T + Aak V, X = Minv U ------------------------------
+            if (starts) {
+                // the start state: since its loads, only the next chunk's 14
+                // vector loads (if any) were issued
+                if constexpr (ACC) {
+                    // and the 12 cotangent loads
+                    if (more)
+                        __builtin_amdgcn_s_waitcnt(0x4f7a);  // vmcnt(26)
+                    else
+                        __builtin_amdgcn_s_waitcnt(0x0f7c);  // vmcnt(12)
+                } else {
+                    if (more)
+                        __builtin_amdgcn_s_waitcnt(0x0f7e);  // vmcnt(14)
+                    else
+                        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+                }
+                asm volatile("" ::: "memory");
+                if (lane == 0) lds_store(&fl.s_ready[w], c);
+            } else if (wait_for(A.wait, &fl.s_ready[w], lane,
+                                [&](int x) { return x == c; }) <= 0) {
+                return false;
+            }
+            // the next chunk's start state, S_L = S_0 2^{g_L} + X^T B^ + V^T K^,
+            // goes to the worker of chunk c + 1 (tiles of S_L^T, formed per i
+            // block as X is)
+            i16x4_t kBh[4], kKh[4];
+            if (feeds) {
+                if (wait_for(A.wait, &fl.s_free[wfeed], lane,
+                             [&](int x) { return x == c + 1; }) <= 0)
+                    return false;
+    #pragma unroll
+                for (int jb = 0; jb < 4; ++jb) {
+                    const float elr = lds_fac[w][0][16 * jb + lr];
+                    f32x4_t bj = unpack_i16(to_j(tB[jb], kI));
+                    f32x4_t kj = unpack_i16(to_j(tK[jb], kI));
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        bj[e] *= elr;
+                        kj[e] *= elr;
+                    }
+                    kBh[jb] = kq(bj);
+                    kKh[jb] = kq(kj);
+                }
+            }
+            const bf16x8_t Ahp0 = pk8(tAh[0], tAh[1]), Ahp1 = pk8(tAh[2], tAh[3]);
+    #pragma unroll
+            for (int ib = 0; ib < 4; ++ib) {
+                // Aak V as a K = 32 product with a zero half, accumulated with
+                // the K = 64 products
+                f32x4_t u = zero4();
+                mfma(u, Ahp0, frag_rows(S, ib, 0, lane));
+                mfma(u, Ahp1, frag_rows(S, ib, 1, lane));
+                mfma(u, pk8(kAakA, kZero), pk8(jV[ib], jV[ib]));
+                const i16x4_t kU = kq(u);  // D(U_ib): B = U, A = U^T
+                f32x4_t xt = zero4();
+                mfma16(xt, kU, kMinv);  // X^T = U^T Minv^T
+                kXT[ib] = kq(xt);
+                if (feeds) {
+                    f32x4_t xj = zero4();
+                    mfma16(xj, kMinv, kU);  // X = Minv U
+                    const i16x4_t kXJ = kq(xj);
+                    bf16_t* const Sn = lds_S[wfeed];
+    #pragma unroll
+                    for (int jpb = 0; jpb < 4; ++jpb) {
+                        // lane: S_L[16 ib + lr][16 jpb + 4 lq + e]
+                        const f32x4_t el = *reinterpret_cast<const f32x4_t*>(
+                            &lds_fac[w][2][16 * jpb + 4 * lq]);
+                        const f32x4_t s0 = unpack4(
+                            sd_read4(S, 16 * ib + lr, 16 * jpb + 4 * lq));
+                        f32x4_t acc;
+    #pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[e] = s0[e] * el[e];
+                        mfma(acc, pk8(kBh[jpb], kKh[jpb]), pk8(kXJ, jV[ib]));
+                        sd_write4(Sn, 16 * ib + lr, 16 * jpb + 4 * lq, pack4(acc));
+                    }
+                }
+            }
+            if (feeds) {
+                lds_drain();
+                if (lane == 0) lds_store(&fl.s_ready[wfeed], c + 1);
+            }
+
+            return true;
+        };
+        auto do_dx = [&]() -> bool {
+            // ---- D arrives: dX = B^ D^T + Arb^T dY, dU = Minv^T dX (J and T),
+            // dV^T = D K^^T + dY^T Ark + dU^T Aak.  The buffer holds
+            // D' = bf16(D diag(2^{g_L - g_ref})), so B^ D^T = B~ D'^T and
+            // K^ D^T = K~ D'^T -------------------------------------------------
+            if (wait_for(A.wait, &fl.d_cnt[w], lane,
+                         [&](int x) { return x >= NCHAIN * (kord + 1); }) <= 0)
+                return false;
+            const bf16x8_t Khp0 = pk8(tK[0], tK[1]), Khp1 = pk8(tK[2], tK[3]);
+            const __amdgpu_buffer_rsrc_t rs_dv = whole_rsrc(A.dv);
+            if constexpr (ACC) {
+                // the dv cotangents: the 8 dr, dk loads and the next chunk's 14
+                // vector loads (if any) came after them
+                if (more)
+                    __builtin_amdgcn_s_waitcnt(0x4f76);  // vmcnt(22)
+                else
+                    __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8)
+                asm volatile("" ::: "memory");
+            }
+            uint2 held_dv;
+    #pragma unroll
+            for (int ib = 0; ib < 4; ++ib) {
+                const bf16x8_t d0 = frag_rows(D, ib, 0, lane);
+                const bf16x8_t d1 = frag_rows(D, ib, 1, lane);
+                f32x4_t dx = zero4();
+                mfma(dx, Bhp0, d0);
+                mfma(dx, Bhp1, d1);
+                mfma(dx, pk8(kArbTA, kZero), pk8(jdY[ib], jdY[ib]));
+                const i16x4_t kdX = kq(dx);
+                f32x4_t du = zero4(), dut = zero4();
+                mfma16(du, kMinvT, kdX);   // dU = Minv^T dX (J)
+                mfma16(dut, kdX, kMinvT);  // dU^T = dX^T Minv (T)
+                kdUT[ib] = kq(dut);
+                const i16x4_t kdUJ = kq(du);
+                // D K^^T + dY^T Ark + dU^T Aak, the last two as one K = 32
+                // product
+                f32x4_t dv = zero4();
+                mfma(dv, d0, Khp0);
+                mfma(dv, d1, Khp1);
+                mfma(dv, pk8(jdY[ib], kdUJ), pk8(kArkB, kAakB));
+                if constexpr (ACC) {
+                    const f32x4_t ad = unpack4(adv[ib]);
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e) dv[e] += ad[e];
+                }
+                // lane: dV[t0 + lr][16 ib + 4 lq + e]; value blocks in pairs,
+                // 16 bytes per lane (pair_rows)
+                const uint2 pv = pack4(dv);
+                if ((ib & 1) == 0)
+                    held_dv = pv;
+                else
+                    store16(rs_dv, row2 + 32 * (ib - 1) + pair_off(lq),
+                            pair_rows(held_dv, pv));
+            }
+
+            return true;
+        };
+        if constexpr (M == 2) {
+            if (starts && !do_ux()) break;
         }
-        const bf16x8_t Bhp0 = pk8(tB[0], tB[1]), Bhp1 = pk8(tB[2], tB[3]);
-        map.Bh[0][lane] = Bhp0;
-        map.Bh[1][lane] = Bhp1;
-#pragma unroll
-        for (int ib = 0; ib < 4; ++ib) map.dY[ib][lane] = jdY[ib];
-        lds_drain();
-        if (lane == 0) lds_store(&fl.map_ready[w], kord + 1);
+        publish_map();
         if (skim) {
             // the cotangent passes through this chunk; nothing else is
             // formed here.  Its D buffer and tail are not read: release them
@@ -678,149 +853,19 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             if (lane == 0) {
                 lds_store(&fl.d_done[w], kord + 1);
                 lds_store(&fl.s_free[w], cn);
-                if (w & 1) lds_store(&fl.tail_used[w], kord + 1);
+                if (endm) lds_store(&fl.tail_used[w], tk + 1);
             }
             if (more && cn < c_hi && cn % m == 0)
                 fetch_state<M>(A, w, cn, lane);
             continue;
         }
 
-        // ---- U = A^ S_0^T + Aak V, X = Minv U ------------------------------
-        if (starts) {
-            // the start state: since its loads, only the next chunk's 14
-            // vector loads (if any) were issued
-            if constexpr (ACC) {
-                // and the 12 cotangent loads
-                if (more)
-                    __builtin_amdgcn_s_waitcnt(0x4f7a);  // vmcnt(26)
-                else
-                    __builtin_amdgcn_s_waitcnt(0x0f7c);  // vmcnt(12)
-            } else {
-                if (more)
-                    __builtin_amdgcn_s_waitcnt(0x0f7e);  // vmcnt(14)
-                else
-                    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-            }
-            asm volatile("" ::: "memory");
-            if (lane == 0) lds_store(&fl.s_ready[w], c);
-        } else if (wait_for(A.wait, &fl.s_ready[w], lane,
-                            [&](int x) { return x == c; }) <= 0) {
-            break;
+        if constexpr (M != 2) {
+            if (!do_ux()) break;
         }
-        // the next chunk's start state, S_L = S_0 2^{g_L} + X^T B^ + V^T K^,
-        // goes to the worker of chunk c + 1 (tiles of S_L^T, formed per i
-        // block as X is)
-        i16x4_t kBh[4], kKh[4];
-        if (feeds) {
-            if (wait_for(A.wait, &fl.s_free[wfeed], lane,
-                         [&](int x) { return x == c + 1; }) <= 0)
-                break;
-#pragma unroll
-            for (int jb = 0; jb < 4; ++jb) {
-                const float elr = lds_fac[w][0][16 * jb + lr];
-                f32x4_t bj = unpack_i16(to_j(tB[jb], kI));
-                f32x4_t kj = unpack_i16(to_j(tK[jb], kI));
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    bj[e] *= elr;
-                    kj[e] *= elr;
-                }
-                kBh[jb] = kq(bj);
-                kKh[jb] = kq(kj);
-            }
-        }
-        const bf16x8_t Ahp0 = pk8(tAh[0], tAh[1]), Ahp1 = pk8(tAh[2], tAh[3]);
-        i16x4_t kXT[4];
-#pragma unroll
-        for (int ib = 0; ib < 4; ++ib) {
-            // Aak V as a K = 32 product with a zero half, accumulated with
-            // the K = 64 products
-            f32x4_t u = zero4();
-            mfma(u, Ahp0, frag_rows(S, ib, 0, lane));
-            mfma(u, Ahp1, frag_rows(S, ib, 1, lane));
-            mfma(u, pk8(kAakA, kZero), pk8(jV[ib], jV[ib]));
-            const i16x4_t kU = kq(u);  // D(U_ib): B = U, A = U^T
-            f32x4_t xt = zero4();
-            mfma16(xt, kU, kMinv);  // X^T = U^T Minv^T
-            kXT[ib] = kq(xt);
-            if (feeds) {
-                f32x4_t xj = zero4();
-                mfma16(xj, kMinv, kU);  // X = Minv U
-                const i16x4_t kXJ = kq(xj);
-                bf16_t* const Sn = lds_S[wfeed];
-#pragma unroll
-                for (int jpb = 0; jpb < 4; ++jpb) {
-                    // lane: S_L[16 ib + lr][16 jpb + 4 lq + e]
-                    const f32x4_t el = *reinterpret_cast<const f32x4_t*>(
-                        &lds_fac[w][2][16 * jpb + 4 * lq]);
-                    const f32x4_t s0 = unpack4(
-                        sd_read4(S, 16 * ib + lr, 16 * jpb + 4 * lq));
-                    f32x4_t acc;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[e] = s0[e] * el[e];
-                    mfma(acc, pk8(kBh[jpb], kKh[jpb]), pk8(kXJ, jV[ib]));
-                    sd_write4(Sn, 16 * ib + lr, 16 * jpb + 4 * lq, pack4(acc));
-                }
-            }
-        }
-        if (feeds) {
-            lds_drain();
-            if (lane == 0) lds_store(&fl.s_ready[wfeed], c + 1);
-        }
-
-        // ---- D arrives: dX = B^ D^T + Arb^T dY, dU = Minv^T dX (J and T),
-        // dV^T = D K^^T + dY^T Ark + dU^T Aak.  The buffer holds
-        // D' = bf16(D diag(2^{g_L - g_ref})), so B^ D^T = B~ D'^T and
-        // K^ D^T = K~ D'^T -------------------------------------------------
-        if (wait_for(A.wait, &fl.d_cnt[w], lane,
-                     [&](int x) { return x >= NCHAIN * (kord + 1); }) <= 0)
-            break;
-        const bf16x8_t Khp0 = pk8(tK[0], tK[1]), Khp1 = pk8(tK[2], tK[3]);
-        const __amdgpu_buffer_rsrc_t rs_dv = whole_rsrc(A.dv);
-        if constexpr (ACC) {
-            // the dv cotangents: the 8 dr, dk loads and the next chunk's 14
-            // vector loads (if any) came after them
-            if (more)
-                __builtin_amdgcn_s_waitcnt(0x4f76);  // vmcnt(22)
-            else
-                __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8)
-            asm volatile("" ::: "memory");
-        }
-        i16x4_t kdUT[4];
-        uint2 held_dv;
-#pragma unroll
-        for (int ib = 0; ib < 4; ++ib) {
-            const bf16x8_t d0 = frag_rows(D, ib, 0, lane);
-            const bf16x8_t d1 = frag_rows(D, ib, 1, lane);
-            f32x4_t dx = zero4();
-            mfma(dx, Bhp0, d0);
-            mfma(dx, Bhp1, d1);
-            mfma(dx, pk8(kArbTA, kZero), pk8(jdY[ib], jdY[ib]));
-            const i16x4_t kdX = kq(dx);
-            f32x4_t du = zero4(), dut = zero4();
-            mfma16(du, kMinvT, kdX);   // dU = Minv^T dX (J)
-            mfma16(dut, kdX, kMinvT);  // dU^T = dX^T Minv (T)
-            kdUT[ib] = kq(dut);
-            const i16x4_t kdUJ = kq(du);
-            // D K^^T + dY^T Ark + dU^T Aak, the last two as one K = 32
-            // product
-            f32x4_t dv = zero4();
-            mfma(dv, d0, Khp0);
-            mfma(dv, d1, Khp1);
-            mfma(dv, pk8(jdY[ib], kdUJ), pk8(kArkB, kAakB));
-            if constexpr (ACC) {
-                const f32x4_t ad = unpack4(adv[ib]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) dv[e] += ad[e];
-            }
-            // lane: dV[t0 + lr][16 ib + 4 lq + e]; value blocks in pairs,
-            // 16 bytes per lane (pair_rows)
-            const uint2 pv = pack4(dv);
-            if ((ib & 1) == 0)
-                held_dv = pv;
-            else
-                store16(rs_dv, row2 + 32 * (ib - 1) + pair_off(lq),
-                        pair_rows(held_dv, pv));
+        if (!do_dx()) break;
+        if constexpr (M == 2) {
+            if (!starts && !do_ux()) break;
         }
 
         // ---- cotangents of the 16 x 16 matrices (K = 64 over i) -----------
@@ -861,11 +906,9 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         // ---- the chains' shares of sum_i D_0 S_0 at the boundary they
         // formed it: this chunk's start (even positions, worker tw = w) or
         // its end, the start of chunk c + 1 (odd positions, tw = w - 1) ----
-        const int tw = w & ~1;
-        const bool odd = (w & 1) != 0;
-        const float oddf = odd ? 1.f : 0.f;
+        const float oddf = endm ? 1.f : 0.f;
         if (wait_for(A.wait, &fl.tail_cnt[tw], lane,
-                     [&](int x) { return x >= NCHAIN * (kord + 1); }) <= 0)
+                     [&](int x) { return x >= NCHAIN * (tk + 1); }) <= 0)
             break;
 
         // ---- per column block: dR~, dA~, dB~, dK~ and the input gradients -
@@ -1001,7 +1044,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         if (lane == 0) {
             lds_store(&fl.d_done[w], kord + 1);
             lds_store(&fl.s_free[w], cn);
-            if (odd) lds_store(&fl.tail_used[w], kord + 1);
+            if (endm) lds_store(&fl.tail_used[w], tk + 1);
         }
         if (more && cn % m == 0) fetch_state<M>(A, w, cn, lane);
     }
@@ -1076,7 +1119,11 @@ int cu_count() {
 int plan_segments(int nch, int m, int k, int* lo, int* hi) {
     lo[0] = 0;
     hi[0] = nch;
-    if (k < 2 || (m > 1 && nch % 2 != 0)) return 1;
+    // (an interval of two chunks is not split: one workgroup per head puts
+    // the decay gradient's boundary sums at the checkpoint chunks (tpar),
+    // which a segment's first own chunk cannot follow, and every count must
+    // give the same bits)
+    if (k < 2 || m == 2 || (m > 1 && nch % 2 != 0)) return 1;
     if (k > kMaxSegments) k = kMaxSegments;
     for (; k >= 2; --k) {
         double wt[kMaxSegments], tot = 0, before = 0;
@@ -1139,6 +1186,9 @@ hipError_t launch_wave_backward(const WaveBwdArgs& p, hipStream_t stream) {
     const int nch = int((A.T + WL - 1) / WL);
     A.nseg = plan_segments(nch, p.L / WL, k, A.seg_lo, A.seg_hi);
     if (A.BH * A.nseg > int64_t(UINT32_MAX)) return hipErrorInvalidValue;
+    // an interval of two chunks (never split): the boundary sums at the even
+    // (checkpoint) chunks, reverse positions of parity nch - 1
+    A.tpar = (p.L / WL == 2) ? ((nch - 1) & 1) : 0;
     const bool acc = A.add_dr || A.add_dk || A.add_dv;
     const dim3 grid(unsigned(A.BH * A.nseg)), block(BTHREADS);
     switch (p.L / WL) {

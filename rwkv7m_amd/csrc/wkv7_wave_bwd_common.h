@@ -33,6 +33,12 @@ struct BwdArgs {
     // segment blockIdx.x % nseg.
     int nseg;
     int seg_lo[kMaxSegments], seg_hi[kMaxSegments];
+    // Parity of the reverse positions whose chunks take the decay
+    // gradient's boundary sum at their start (see tail_start): 0, or, for
+    // an interval of two chunks in one workgroup per head, the parity that
+    // puts those sums at the checkpoint chunks, whose start states are
+    // loaded, not recomputed by a neighbouring worker.
+    int tpar;
 };
 
 __device__ __forceinline__ int64_t head_of(const BwdArgs& A) {
@@ -69,6 +75,7 @@ __host__ inline BwdArgs bwd_args(const WaveBwdArgs& p) {
     A.add_dk = static_cast<const bf16_t*>(p.add_dk);
     A.add_dv = static_cast<const bf16_t*>(p.add_dv);
     A.nseg = 1;
+    A.tpar = 0;
     for (int g = 0; g < kMaxSegments; ++g) A.seg_lo[g] = A.seg_hi[g] = 0;
     A.seg_lo[0] = 0;
     A.seg_hi[0] = int((p.T + WL - 1) / WL);

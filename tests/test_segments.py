@@ -13,7 +13,10 @@ head's chunks over up to four workgroups: each writes the gradients of its
 own run of chunks and first carries the cotangent through the chunks after
 them (rwkv7m_debug_set_backward_segments overrides the count).  The split
 changes no arithmetic, so every count must give results bit-identical to one
-workgroup per head: for every checkpoint interval, a ragged final chunk,
+workgroup per head (an interval of 32 tokens is never split: one workgroup
+per head takes the decay gradient's boundary sums at the checkpoint chunks,
+which a segment's first chunk cannot follow): for every checkpoint interval,
+a ragged final chunk,
 nonzero initial state and state cotangent, the summing (time-mix) instance,
 heads that the exact sequential pass takes over, and the automatic count at
 config 1's shape (B8 T512 H12: 96 heads on 256 CUs).  The oracle parity of

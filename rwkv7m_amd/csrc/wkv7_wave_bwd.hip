@@ -34,9 +34,10 @@
 // recovers its own start value through the same identity,
 // E_0 = E_L - sum over the chunk of (b db + k dk - r dr - a da).  With an
 // interval of two chunks the start members are the checkpoint chunks, so
-// that the chains never wait for a recomputed start state.  These are the reference's reverse equations
-// (src/rwkv7m/kernels/wkv_pallas_gpu.py:221-257) summed over a chunk; states
-// come from checkpoints, never from dividing by the decay.  Inside an
+// that the chains never wait for a recomputed start state.  These are the
+// reference's reverse equations (src/rwkv7m/kernels/wkv_pallas_gpu.py:
+// 221-257) summed over a chunk; states come from checkpoints, never from
+// dividing by the decay.  Inside an
 // interval of m chunks, the start state of chunk c + 1 is recomputed from
 // chunk c's: S_L = S_0 2^{g_L} + X^T B^ + V^T K^.
 //
@@ -675,17 +676,17 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         bf16x8_t Bhp0, Bhp1;
         i16x4_t kXT[4], kdUT[4];
         auto publish_map = [&]() {
-            // ---- W^ = Minv A^, Q^ = R~ 2^{g_ref} + Arb W^ (J layout); the map -
-    #pragma unroll
+            // ---- W^ = Minv A^, Q^ = R~ 2^{g_ref} + Arb W^ (J layout); map
+#pragma unroll
             for (int jb = 0; jb < 4; ++jb) {
                 const float erj = lds_fac[w][1][16 * jb + lr];
                 f32x4_t x = zero4();
                 mfma16(x, kMinv, to_j(tA[jb], kI));
-    #pragma unroll
+#pragma unroll
                 for (int e = 0; e < 4; ++e) x[e] *= erj;
                 const i16x4_t kW = kq(x);
                 f32x4_t y = unpack_i16(to_j(tR[jb], kI));
-    #pragma unroll
+#pragma unroll
                 for (int e = 0; e < 4; ++e) y[e] *= erj;
                 mfma16(y, kArbA, kW);
                 map.QW[jb][lane] = pk8(kq(y), kW);
@@ -694,13 +695,13 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             Bhp1 = pk8(tB[2], tB[3]);
             map.Bh[0][lane] = Bhp0;
             map.Bh[1][lane] = Bhp1;
-    #pragma unroll
+#pragma unroll
             for (int ib = 0; ib < 4; ++ib) map.dY[ib][lane] = jdY[ib];
             lds_drain();
             if (lane == 0) lds_store(&fl.map_ready[w], kord + 1);
         };
         auto do_ux = [&]() -> bool {
-            // ---- U = A^ S_0^T + Aak V, X = Minv U ------------------------------
+            // ---- U = A^ S_0^T + Aak V, X = Minv U --------------------------
             if (starts) {
                 // the start state: since its loads, only the next chunk's 14
                 // vector loads (if any) were issued
@@ -722,7 +723,8 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                                 [&](int x) { return x == c; }) <= 0) {
                 return false;
             }
-            // the next chunk's start state, S_L = S_0 2^{g_L} + X^T B^ + V^T K^,
+            // the next chunk's start state, S_L = S_0 2^{g_L} + X^T B^ +
+            // V^T K^,
             // goes to the worker of chunk c + 1 (tiles of S_L^T, formed per i
             // block as X is)
             i16x4_t kBh[4], kKh[4];
@@ -730,12 +732,12 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 if (wait_for(A.wait, &fl.s_free[wfeed], lane,
                              [&](int x) { return x == c + 1; }) <= 0)
                     return false;
-    #pragma unroll
+#pragma unroll
                 for (int jb = 0; jb < 4; ++jb) {
                     const float elr = lds_fac[w][0][16 * jb + lr];
                     f32x4_t bj = unpack_i16(to_j(tB[jb], kI));
                     f32x4_t kj = unpack_i16(to_j(tK[jb], kI));
-    #pragma unroll
+#pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         bj[e] *= elr;
                         kj[e] *= elr;
@@ -744,8 +746,9 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                     kKh[jb] = kq(kj);
                 }
             }
-            const bf16x8_t Ahp0 = pk8(tAh[0], tAh[1]), Ahp1 = pk8(tAh[2], tAh[3]);
-    #pragma unroll
+            const bf16x8_t Ahp0 = pk8(tAh[0], tAh[1]),
+                           Ahp1 = pk8(tAh[2], tAh[3]);
+#pragma unroll
             for (int ib = 0; ib < 4; ++ib) {
                 // Aak V as a K = 32 product with a zero half, accumulated with
                 // the K = 64 products
@@ -762,19 +765,34 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                     mfma16(xj, kMinv, kU);  // X = Minv U
                     const i16x4_t kXJ = kq(xj);
                     bf16_t* const Sn = lds_S[wfeed];
-    #pragma unroll
+                    // lane: S_L[16 ib + lr][16 jpb + 4 lq + e].  The block's
+                    // four S_0 tiles are read before any S_L tile is
+                    // written: the compiler cannot tell the two buffers
+                    // apart, and read after each write the sixteen tiles
+                    // would take one LDS round trip each.
+                    uint2 s0r[4];
+                    f32x4_t el[4];  // 2^{g_L} per column
+#pragma unroll
                     for (int jpb = 0; jpb < 4; ++jpb) {
-                        // lane: S_L[16 ib + lr][16 jpb + 4 lq + e]
-                        const f32x4_t el = *reinterpret_cast<const f32x4_t*>(
+                        s0r[jpb] =
+                            sd_read4(S, 16 * ib + lr, 16 * jpb + 4 * lq);
+                        el[jpb] = *reinterpret_cast<const f32x4_t*>(
                             &lds_fac[w][2][16 * jpb + 4 * lq]);
-                        const f32x4_t s0 = unpack4(
-                            sd_read4(S, 16 * ib + lr, 16 * jpb + 4 * lq));
-                        f32x4_t acc;
-    #pragma unroll
-                        for (int e = 0; e < 4; ++e) acc[e] = s0[e] * el[e];
-                        mfma(acc, pk8(kBh[jpb], kKh[jpb]), pk8(kXJ, jV[ib]));
-                        sd_write4(Sn, 16 * ib + lr, 16 * jpb + 4 * lq, pack4(acc));
                     }
+                    f32x4_t acc[4];
+#pragma unroll
+                    for (int jpb = 0; jpb < 4; ++jpb) {
+                        const f32x4_t s0 = unpack4(s0r[jpb]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            acc[jpb][e] = s0[e] * el[jpb][e];
+                        mfma(acc[jpb], pk8(kBh[jpb], kKh[jpb]),
+                             pk8(kXJ, jV[ib]));
+                    }
+#pragma unroll
+                    for (int jpb = 0; jpb < 4; ++jpb)
+                        sd_write4(Sn, 16 * ib + lr, 16 * jpb + 4 * lq,
+                                  pack4(acc[jpb]));
                 }
             }
             if (feeds) {
@@ -788,7 +806,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             // ---- D arrives: dX = B^ D^T + Arb^T dY, dU = Minv^T dX (J and T),
             // dV^T = D K^^T + dY^T Ark + dU^T Aak.  The buffer holds
             // D' = bf16(D diag(2^{g_L - g_ref})), so B^ D^T = B~ D'^T and
-            // K^ D^T = K~ D'^T -------------------------------------------------
+            // K^ D^T = K~ D'^T ---------------------------------------------
             if (wait_for(A.wait, &fl.d_cnt[w], lane,
                          [&](int x) { return x >= NCHAIN * (kord + 1); }) <= 0)
                 return false;
@@ -804,7 +822,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 asm volatile("" ::: "memory");
             }
             uint2 held_dv;
-    #pragma unroll
+#pragma unroll
             for (int ib = 0; ib < 4; ++ib) {
                 const bf16x8_t d0 = frag_rows(D, ib, 0, lane);
                 const bf16x8_t d1 = frag_rows(D, ib, 1, lane);
@@ -826,7 +844,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 mfma(dv, pk8(jdY[ib], kdUJ), pk8(kArkB, kAakB));
                 if constexpr (ACC) {
                     const f32x4_t ad = unpack4(adv[ib]);
-    #pragma unroll
+#pragma unroll
                     for (int e = 0; e < 4; ++e) dv[e] += ad[e];
                 }
                 // lane: dV[t0 + lr][16 ib + 4 lq + e]; value blocks in pairs,

@@ -391,6 +391,11 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
     const int nch = (T + WL - 1) / WL;
     const uint32_t ts2 = A.ts2;
     constexpr int m = M;
+    // Blocks of four independent 16-column tiles go through some phases
+    // stage by stage, GW blocks at a time: all four for the plain interval-16
+    // instance; one at a time where the registers of four in flight would
+    // spill (longer intervals, the summing instance).
+    constexpr int GW = (M == 1 && !ACC) ? 4 : 1;
     // the worker of chunk c + 1 (one position earlier in the reverse order),
     // whose start state chunk c's end state is
     const int wfeed = (w + NWORK - 1) % NWORK;
@@ -536,7 +541,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         // kept for the input gradients: 2^{g_t - g_ref}, 2^{g_ref - g_t},
         // 2^{g_{t-1} - g_ref} (bf16) and -e^w (the decay gradient's factor)
         i16x4_t keg[4], keng[4], kep[4];
-        f32x4_t lam4[4];
+        f32x4_t lam4[4], facv[4];
         float lo = 0.f;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
@@ -579,9 +584,22 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             keg[kb] = kq(eg4);
             keng[kb] = kq(eng4);
             kep[kb] = kq(ep4);
-            if (lr < 3)
+            if constexpr (GW == 4)
+                facv[kb] = lr == 0 ? lr4 : sp4;
+            else if (lr < 3)
                 *reinterpret_cast<f32x4_t*>(&lds_fac[w][lr][16 * kb + 4 * lq]) =
                     lr == 0 ? lr4 : sp4;
+        }
+        if constexpr (GW == 4) {
+            // (stored after the loop: a store under a lane condition inside
+            // it splits the four column blocks' chains into separate blocks;
+            // the other instances keep it inside, where its registers fit)
+            if (lr < 3) {
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+                    *reinterpret_cast<f32x4_t*>(
+                        &lds_fac[w][lr][16 * kb + 4 * lq]) = facv[kb];
+            }
         }
         // the factored form needs g_ref >= -H and g_L - g_ref >= -H
         if (__builtin_amdgcn_ballot_w64(lo < -kHalfRange * kLog2e) != 0) {
@@ -677,19 +695,47 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         i16x4_t kXT[4], kdUT[4];
         auto publish_map = [&]() {
             // ---- W^ = Minv A^, Q^ = R~ 2^{g_ref} + Arb W^ (J layout); map
+            // (each stage for GW key blocks before the next)
 #pragma unroll
-            for (int jb = 0; jb < 4; ++jb) {
-                const float erj = lds_fac[w][1][16 * jb + lr];
-                f32x4_t x = zero4();
-                mfma16(x, kMinv, to_j(tA[jb], kI));
+            for (int jb0 = 0; jb0 < 4; jb0 += GW) {
+                float erj[GW];
+                f32x4_t xa[GW], xr[GW];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) x[e] *= erj;
-                const i16x4_t kW = kq(x);
-                f32x4_t y = unpack_i16(to_j(tR[jb], kI));
+                for (int g = 0; g < GW; ++g) {
+                    erj[g] = lds_fac[w][1][16 * (jb0 + g) + lr];
+                    xa[g] = zero4();
+                    xr[g] = zero4();
+                    mfma16(xa[g], tA[jb0 + g], kI);  // D(A~_jb), J layout
+                    mfma16(xr[g], tR[jb0 + g], kI);  // D(R~_jb)
+                }
+                i16x4_t jAt[GW];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) y[e] *= erj;
-                mfma16(y, kArbA, kW);
-                map.QW[jb][lane] = pk8(kq(y), kW);
+                for (int g = 0; g < GW; ++g) jAt[g] = kq(xa[g]);
+                f32x4_t xw[GW];
+#pragma unroll
+                for (int g = 0; g < GW; ++g) {
+                    xw[g] = zero4();
+                    mfma16(xw[g], kMinv, jAt[g]);
+                }
+                i16x4_t kW[GW];
+                f32x4_t yq[GW];
+#pragma unroll
+                for (int g = 0; g < GW; ++g) {
+                    // R~ as the products take it (bf16), times 2^{g_ref}
+                    const f32x4_t rj = unpack_i16(kq(xr[g]));
+                    f32x4_t xs = xw[g];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        xs[e] *= erj[g];
+                        yq[g][e] = rj[e] * erj[g];
+                    }
+                    kW[g] = kq(xs);
+                }
+#pragma unroll
+                for (int g = 0; g < GW; ++g) mfma16(yq[g], kArbA, kW[g]);
+#pragma unroll
+                for (int g = 0; g < GW; ++g)
+                    map.QW[jb0 + g][lane] = pk8(kq(yq[g]), kW[g]);
             }
             Bhp0 = pk8(tB[0], tB[1]);
             Bhp1 = pk8(tB[2], tB[3]);
@@ -748,6 +794,29 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             }
             const bf16x8_t Ahp0 = pk8(tAh[0], tAh[1]),
                            Ahp1 = pk8(tAh[2], tAh[3]);
+            if constexpr (GW == 4) {
+                // (interval 16, no next start state: each stage for all four
+                // value blocks before the next, as for dX, dU, dV)
+                f32x4_t u[4], xt[4];
+#pragma unroll
+                for (int ib = 0; ib < 4; ++ib) {
+                    u[ib] = zero4();
+                    mfma(u[ib], Ahp0, frag_rows(S, ib, 0, lane));
+                    mfma(u[ib], Ahp1, frag_rows(S, ib, 1, lane));
+                    mfma(u[ib], pk8(kAakA, kZero), pk8(jV[ib], jV[ib]));
+                }
+                i16x4_t kU[4];
+#pragma unroll
+                for (int ib = 0; ib < 4; ++ib) kU[ib] = kq(u[ib]);
+#pragma unroll
+                for (int ib = 0; ib < 4; ++ib) {
+                    xt[ib] = zero4();
+                    mfma16(xt[ib], kU[ib], kMinv);  // X^T = U^T Minv^T
+                }
+#pragma unroll
+                for (int ib = 0; ib < 4; ++ib) kXT[ib] = kq(xt[ib]);
+                return true;
+            }
 #pragma unroll
             for (int ib = 0; ib < 4; ++ib) {
                 // Aak V as a K = 32 product with a zero half, accumulated with
@@ -770,29 +839,38 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                     // written: the compiler cannot tell the two buffers
                     // apart, and read after each write the sixteen tiles
                     // would take one LDS round trip each.
-                    uint2 s0r[4];
-                    f32x4_t el[4];  // 2^{g_L} per column
+                    // (The summing instance, short of registers, goes tile
+                    // by tile.)
+                    constexpr int GS = ACC ? 1 : 4;
 #pragma unroll
-                    for (int jpb = 0; jpb < 4; ++jpb) {
-                        s0r[jpb] =
-                            sd_read4(S, 16 * ib + lr, 16 * jpb + 4 * lq);
-                        el[jpb] = *reinterpret_cast<const f32x4_t*>(
-                            &lds_fac[w][2][16 * jpb + 4 * lq]);
+                    for (int jp0 = 0; jp0 < 4; jp0 += GS) {
+                        uint2 s0r[GS];
+                        f32x4_t el[GS];  // 2^{g_L} per column
+#pragma unroll
+                        for (int g = 0; g < GS; ++g) {
+                            const int jpb = jp0 + g;
+                            s0r[g] =
+                                sd_read4(S, 16 * ib + lr, 16 * jpb + 4 * lq);
+                            el[g] = *reinterpret_cast<const f32x4_t*>(
+                                &lds_fac[w][2][16 * jpb + 4 * lq]);
+                        }
+                        f32x4_t acc[GS];
+#pragma unroll
+                        for (int g = 0; g < GS; ++g) {
+                            const int jpb = jp0 + g;
+                            const f32x4_t s0 = unpack4(s0r[g]);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                acc[g][e] = s0[e] * el[g][e];
+                            mfma(acc[g], pk8(kBh[jpb], kKh[jpb]),
+                                 pk8(kXJ, jV[ib]));
+                        }
+#pragma unroll
+                        for (int g = 0; g < GS; ++g)
+                            sd_write4(Sn, 16 * ib + lr,
+                                      16 * (jp0 + g) + 4 * lq,
+                                      pack4(acc[g]));
                     }
-                    f32x4_t acc[4];
-#pragma unroll
-                    for (int jpb = 0; jpb < 4; ++jpb) {
-                        const f32x4_t s0 = unpack4(s0r[jpb]);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            acc[jpb][e] = s0[e] * el[jpb][e];
-                        mfma(acc[jpb], pk8(kBh[jpb], kKh[jpb]),
-                             pk8(kXJ, jV[ib]));
-                    }
-#pragma unroll
-                    for (int jpb = 0; jpb < 4; ++jpb)
-                        sd_write4(Sn, 16 * ib + lr, 16 * jpb + 4 * lq,
-                                  pack4(acc[jpb]));
                 }
             }
             if (feeds) {
@@ -821,40 +899,68 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                     __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8)
                 asm volatile("" ::: "memory");
             }
+            // The four value blocks are independent: each stage is issued
+            // for GW of them before the next, so that one block's products
+            // cover another's latency (block by block, the compiler keeps
+            // each block's chain of products and conversions in sequence).
             uint2 held_dv;
 #pragma unroll
-            for (int ib = 0; ib < 4; ++ib) {
-                const bf16x8_t d0 = frag_rows(D, ib, 0, lane);
-                const bf16x8_t d1 = frag_rows(D, ib, 1, lane);
-                f32x4_t dx = zero4();
-                mfma(dx, Bhp0, d0);
-                mfma(dx, Bhp1, d1);
-                mfma(dx, pk8(kArbTA, kZero), pk8(jdY[ib], jdY[ib]));
-                const i16x4_t kdX = kq(dx);
-                f32x4_t du = zero4(), dut = zero4();
-                mfma16(du, kMinvT, kdX);   // dU = Minv^T dX (J)
-                mfma16(dut, kdX, kMinvT);  // dU^T = dX^T Minv (T)
-                kdUT[ib] = kq(dut);
-                const i16x4_t kdUJ = kq(du);
-                // D K^^T + dY^T Ark + dU^T Aak, the last two as one K = 32
-                // product
-                f32x4_t dv = zero4();
-                mfma(dv, d0, Khp0);
-                mfma(dv, d1, Khp1);
-                mfma(dv, pk8(jdY[ib], kdUJ), pk8(kArkB, kAakB));
-                if constexpr (ACC) {
-                    const f32x4_t ad = unpack4(adv[ib]);
+            for (int ib0 = 0; ib0 < 4; ib0 += GW) {
+                f32x4_t dx[GW], dv[GW];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) dv[e] += ad[e];
+                for (int g = 0; g < GW; ++g) {
+                    const int ib = ib0 + g;
+                    const bf16x8_t d0 = frag_rows(D, ib, 0, lane);
+                    const bf16x8_t d1 = frag_rows(D, ib, 1, lane);
+                    dx[g] = zero4();
+                    mfma(dx[g], Bhp0, d0);
+                    mfma(dx[g], Bhp1, d1);
+                    mfma(dx[g], pk8(kArbTA, kZero), pk8(jdY[ib], jdY[ib]));
+                    // D K^^T (dY^T Ark + dU^T Aak follow, once dU is formed)
+                    dv[g] = zero4();
+                    mfma(dv[g], d0, Khp0);
+                    mfma(dv[g], d1, Khp1);
                 }
-                // lane: dV[t0 + lr][16 ib + 4 lq + e]; value blocks in pairs,
-                // 16 bytes per lane (pair_rows)
-                const uint2 pv = pack4(dv);
-                if ((ib & 1) == 0)
-                    held_dv = pv;
-                else
-                    store16(rs_dv, row2 + 32 * (ib - 1) + pair_off(lq),
-                            pair_rows(held_dv, pv));
+                i16x4_t kdX[GW];
+#pragma unroll
+                for (int g = 0; g < GW; ++g) kdX[g] = kq(dx[g]);
+                f32x4_t du[GW], dut[GW];
+#pragma unroll
+                for (int g = 0; g < GW; ++g) {
+                    du[g] = zero4();
+                    dut[g] = zero4();
+                    mfma16(du[g], kMinvT, kdX[g]);   // dU = Minv^T dX (J)
+                    mfma16(dut[g], kdX[g], kMinvT);  // dU^T = dX^T Minv (T)
+                }
+                i16x4_t kdUJ[GW];
+#pragma unroll
+                for (int g = 0; g < GW; ++g) {
+                    kdUT[ib0 + g] = kq(dut[g]);
+                    kdUJ[g] = kq(du[g]);
+                }
+                // + dY^T Ark + dU^T Aak as one K = 32 product
+#pragma unroll
+                for (int g = 0; g < GW; ++g)
+                    mfma(dv[g], pk8(jdY[ib0 + g], kdUJ[g]),
+                         pk8(kArkB, kAakB));
+#pragma unroll
+                for (int g = 0; g < GW; ++g) {
+                    const int ib = ib0 + g;
+                    f32x4_t o = dv[g];
+                    if constexpr (ACC) {
+                        const f32x4_t ad = unpack4(adv[ib]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) o[e] += ad[e];
+                    }
+                    // lane: dV[t0 + lr][16 ib + 4 lq + e]; value blocks in
+                    // pairs, 16 bytes per lane (pair_rows)
+                    const uint2 pv = pack4(o);
+                    if ((ib & 1) == 0)
+                        held_dv = pv;
+                    else
+                        store16(rs_dv, row2 + 32 * (ib - 1) + pair_off(lq),
+                                pair_rows(held_dv, pv));
+                }
             }
 
             return true;

@@ -52,8 +52,9 @@
 //   * waves 4..7, the workers: worker w takes chunks nch - 1 - w,
 //     nch - 1 - w - 4, ...  It loads the chunk's vectors, forms the factors,
 //     the 16 x 16 matrices and the inverse in registers, publishes the map,
-//     recomputes the next chunk's start state if the interval continues,
-//     then, once D has arrived, forms every gradient in registers and writes
+//     recomputes the next chunk's start state if the interval continues
+//     (at an interval of two chunks it hands X, V, B^ and K^ to the chains,
+//     which form that state between their steps), then, once D has arrived, forms every gradient in registers and writes
 //     them.  Four chunks are in flight at once; only D is serial.
 // Register layouts are those of wkv7_wave_common.h.  The S and D buffers are
 // bf16 64 x 64 in 16-byte units (sd_off), read as row fragments (plain
@@ -97,6 +98,10 @@ struct BwdFlags {
     int tail_used[NWORK];  // odd workers' reads of the even tail (count)
     int s_ready[NWORK];    // chunk whose start state the S buffer holds
     int s_free[NWORK];     // chunk whose start state the S buffer takes next
+    // interval of two chunks: the chains form the odd chunk's start state
+    int h_ready[NWORK];    // chunk whose step operands the buffers hold
+    int h_read[NWORK];     // chain reads of the worker's shared operands
+    int s_cnt[NWORK];      // chain writes of start-state rows (NCHAIN each)
     int abort;             // a chunk needs the exact pass: every wave stops
     int failed;            // a bounded wait gave up
 };
@@ -160,6 +165,10 @@ __device__ __forceinline__ bool tail_start(const BwdArgs& A, int p) {
 
 // ---------------------------------------------------------------------------
 // Chain ib: rows 16 ib .. 16 ib + 15 of the cotangent through every chunk.
+// Intervals of two chunks: at the odd chunk c it also forms rows 16 ib ..
+// + 15 of that chunk's start state from chunk c - 1's checkpoint and step
+// operands (see work()).
+template <int M>
 __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
     const int lr = lane & 15, lq = lane >> 4;
     const int64_t bh = head_of(A);
@@ -256,6 +265,51 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
             Dt[jb] = acc;
         }
 
+        // An odd chunk of an interval of two: its start state, rows 16 ib ..
+        // + 15, S_L = S_0 2^{g_L} + X^T B^ + V^T K^ of chunk c - 1 (worker
+        // we, position p + 1).  B^ and K^ (J layout, all key blocks) are in
+        // that worker's D buffer, which the chains write only after its map
+        // (published once every chain has read them); X and V of value block
+        // ib (J layout) in this chain's own 16 rows of this worker's S
+        // buffer, which it reads before writing its rows there.
+        const bool fed = M == 2 && (c & 1) && c < c_hi;
+        if (fed) {
+            const int we = (w + 1) % NWORK;
+            if (wait_for(A.wait, &fl.h_ready[w], lane,
+                         [&](int x) { return x == c; }, true) <= 0) {
+                done = false;
+                break;
+            }
+            const i16x4_t* const hs = reinterpret_cast<const i16x4_t*>(lds_D[we]);
+            const i16x4_t* const hp = reinterpret_cast<const i16x4_t*>(lds_S[w]);
+            i16x4_t kB[4], kK[4];
+            uint2 s0r[4];
+            f32x4_t el[4];
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+                kB[jb] = hs[64 * jb + lane];
+                kK[jb] = hs[64 * (4 + jb) + lane];
+                s0r[jb] = sd_read4(lds_S[we], row, 16 * jb + 4 * lq);
+                el[jb] = *reinterpret_cast<const f32x4_t*>(
+                    &lds_fac[we][2][16 * jb + 4 * lq]);
+            }
+            const bf16x8_t XV = pk8(hp[64 * (4 * ib) + lane],
+                                    hp[64 * (4 * ib + 1) + lane]);
+            lds_drain();
+            if (lane == 0) lds_add(&fl.h_read[we], 1);
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+                const f32x4_t s0 = unpack4(s0r[jb]);
+                f32x4_t acc;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] = s0[e] * el[jb][e];
+                mfma(acc, pk8(kB[jb], kK[jb]), XV);
+                sd_write4(lds_S[w], row, 16 * jb + 4 * lq, pack4(acc));
+            }
+            lds_drain();
+            if (lane == 0) lds_add(&fl.s_cnt[w], 1);
+        }
+
         // The decay gradient needs sum_i D_0[i][j] S_0[i][j] at every other
         // chunk boundary only: a start member's worker takes it as its
         // chunk's start value, and the worker of the next position, one
@@ -272,8 +326,9 @@ __device__ __forceinline__ void chain(const BwdArgs& A, int ib, int lane) {
         // significant bits); each part is turned into D(P) by P I and summed
         // over i by a product with ones (exact for bf16 values, fp32
         // accumulation)
-        if (wait_for(A.wait, &fl.s_ready[w], lane,
-                     [&](int x) { return x == c; }, true) <= 0 ||
+        // (rows of a start state this chain formed itself need no wait)
+        if ((!fed && wait_for(A.wait, &fl.s_ready[w], lane,
+                              [&](int x) { return x == c; }, true) <= 0) ||
             (kord > 0 && wait_for(A.wait, &fl.tail_used[(w + 1) % NWORK], lane,
                                   [&](int x) { return x >= kord; },
                                   true) <= 0)) {
@@ -416,6 +471,9 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         if (c0 < c_hi && c0 % m == 0) fetch_state<M>(A, w, c0, lane0);
     }
 
+    // interval of two: this worker's chunks so far whose start states the
+    // chains formed, and whose successors' step operands it handed over
+    int nfed = 0, nfeed = 0;
     for (int kord = 0, p = w; p < nch - c_lo; ++kord, p += NWORK) {
         // lane-derived addresses and masks are formed inside each iteration:
         // hoisted out of the loop they would each hold a register for the
@@ -446,6 +504,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         // S_0 is checkpoint c / m; S_0 of c + 1 is formed here
         const bool starts = !skim && c % m == 0;
         const bool feeds = !skim && c % m != m - 1 && c + 1 < c_hi;
+        if (M == 2 && !skim && !starts) ++nfed;
         // the decay gradient's boundary sum (tail_start): a start member
         // takes it at its own start (worker tw = w, round tk = kord); an end
         // member at its end, from the start member one position earlier
@@ -688,12 +747,13 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         // The phases after the factors, as calls: the map (the chains'
         // operands), U and X (need S_0), and dX, dU, dV (need D).  At an
         // interval of two chunks the even (checkpoint) chunk forms U, X and
-        // its successor's start state first, and the odd chunk, whose start
-        // state that is, forms dX, dU, dV before waiting for it; otherwise
-        // the odd chunk's worker waits most of a chunk for it.
+        // hands its successor's start-state operands to the chains first,
+        // and the odd chunk, whose start state that is, forms dX, dU, dV
+        // before waiting for it; otherwise the odd chunk's worker waits most
+        // of a chunk for it.
         bf16x8_t Bhp0, Bhp1;
         i16x4_t kXT[4], kdUT[4];
-        auto publish_map = [&]() {
+        auto publish_map = [&]() -> bool {
             // ---- W^ = Minv A^, Q^ = R~ 2^{g_ref} + Arb W^ (J layout); map
             // (each stage for GW key blocks before the next)
 #pragma unroll
@@ -744,7 +804,16 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
 #pragma unroll
             for (int ib = 0; ib < 4; ++ib) map.dY[ib][lane] = jdY[ib];
             lds_drain();
+            // (interval of two: the chains write D into the buffer that
+            // holds their step operands only after this map; every chain
+            // has read them first)
+            if constexpr (M == 2) {
+                if (feeds && wait_for(A.wait, &fl.h_read[w], lane,
+                                      [&](int x) { return x >= NCHAIN * nfeed; }) <= 0)
+                    return false;
+            }
             if (lane == 0) lds_store(&fl.map_ready[w], kord + 1);
+            return true;
         };
         auto do_ux = [&]() -> bool {
             // ---- U = A^ S_0^T + Aak V, X = Minv U --------------------------
@@ -765,6 +834,11 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 }
                 asm volatile("" ::: "memory");
                 if (lane == 0) lds_store(&fl.s_ready[w], c);
+            } else if constexpr (M == 2) {
+                // formed by the four chains
+                if (wait_for(A.wait, &fl.s_cnt[w], lane,
+                             [&](int x) { return x >= NCHAIN * nfed; }) <= 0)
+                    return false;
             } else if (wait_for(A.wait, &fl.s_ready[w], lane,
                                 [&](int x) { return x == c; }) <= 0) {
                 return false;
@@ -790,6 +864,16 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                     }
                     kBh[jb] = kq(bj);
                     kKh[jb] = kq(kj);
+                }
+                if constexpr (M == 2) {
+                    // the chains' shared step operands, in this worker's
+                    // D buffer (free until its map is published)
+                    i16x4_t* const hs = reinterpret_cast<i16x4_t*>(D);
+#pragma unroll
+                    for (int jb = 0; jb < 4; ++jb) {
+                        hs[64 * jb + lane] = kBh[jb];
+                        hs[64 * (4 + jb) + lane] = kKh[jb];
+                    }
                 }
             }
             const bf16x8_t Ahp0 = pk8(tAh[0], tAh[1]),
@@ -829,7 +913,15 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 f32x4_t xt = zero4();
                 mfma16(xt, kU, kMinv);  // X^T = U^T Minv^T
                 kXT[ib] = kq(xt);
-                if (feeds) {
+                if (feeds && M == 2) {
+                    // X and V of value block ib for chain ib, in its own
+                    // rows of the S buffer of chunk c + 1's worker
+                    f32x4_t xj = zero4();
+                    mfma16(xj, kMinv, kU);  // X = Minv U
+                    i16x4_t* const hp = reinterpret_cast<i16x4_t*>(lds_S[wfeed]);
+                    hp[64 * (4 * ib) + lane] = kq(xj);
+                    hp[64 * (4 * ib + 1) + lane] = jV[ib];
+                } else if (feeds) {
                     f32x4_t xj = zero4();
                     mfma16(xj, kMinv, kU);  // X = Minv U
                     const i16x4_t kXJ = kq(xj);
@@ -875,7 +967,12 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             }
             if (feeds) {
                 lds_drain();
-                if (lane == 0) lds_store(&fl.s_ready[wfeed], c + 1);
+                if constexpr (M == 2) {
+                    ++nfeed;
+                    if (lane == 0) lds_store(&fl.h_ready[wfeed], c + 1);
+                } else {
+                    if (lane == 0) lds_store(&fl.s_ready[wfeed], c + 1);
+                }
             }
 
             return true;
@@ -968,7 +1065,7 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
         if constexpr (M == 2) {
             if (starts && !do_ux()) break;
         }
-        publish_map();
+        if (!publish_map()) break;
         if (skim) {
             // the cotangent passes through this chunk; nothing else is
             // formed here.  Its D buffer and tail are not read: release them
@@ -1190,6 +1287,9 @@ wkv7_wave_bwd_kernel(BwdArgs A) {
         fl.tail_used[tid] = 0;
         fl.s_ready[tid] = -1;
         fl.s_free[tid] = nch - 1 - tid;
+        fl.h_ready[tid] = -1;
+        fl.h_read[tid] = 0;
+        fl.s_cnt[tid] = 0;
     }
     if (tid == 0) {
         fl.abort = 0;
@@ -1197,7 +1297,7 @@ wkv7_wave_bwd_kernel(BwdArgs A) {
     }
     __syncthreads();
     if (wv < NCHAIN)
-        chain(A, wv, lane);
+        chain<M>(A, wv, lane);
     else
         work<M, ACC>(A, wv - NCHAIN, lane);
     // every wait is bounded, so every wave arrives here

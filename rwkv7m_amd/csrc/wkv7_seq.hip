@@ -26,6 +26,15 @@ struct SeqShape {
     static constexpr int NWAVES = (THREADS + 63) / 64;
     static constexpr int SUB = (N >= 128) ? 4 : (N >= 64 ? 8 : 16);
     static constexpr int TB = 16;
+    // The backward's LDS besides the saved states (bytes): the staged
+    // vectors, the reduction buffers and dv.
+    static constexpr int BWD_LDS =
+        4 * (8 * SUB * N + 2 * NWAVES * 5 * N + SUB * N);
+    // Sub-interval start states the backward keeps in LDS (fp32, N x N
+    // each) so that it recomputes each from the nearest saved one instead of
+    // from the interval's checkpoint; 0 where not even one fits.
+    static constexpr int KS_FIT = (163840 - 512 - BWD_LDS) / (4 * N * N);
+    static constexpr int KSAVE = KS_FIT > 16 ? 16 : KS_FIT;
 };
 
 // Forward.  ckpt == nullptr: no aux.  s_t may alias s0.  CT is the
@@ -150,9 +159,12 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
     constexpr int G = Sh::G, C = Sh::C, SUB = Sh::SUB, TH = Sh::THREADS;
     constexpr int WL = Sh::WAVE_LANES, NW = Sh::NWAVES;
     constexpr int64_t NN = int64_t(N) * N;
+    constexpr int KS = Sh::KSAVE;
     __shared__ float sh[8][SUB][N];
     __shared__ float red[2][NW][5][N];
     __shared__ float sh_dv[SUB][N];
+    // saved sub-interval start states, each thread's own C values
+    __shared__ float saved[KS > 0 ? KS : 1][KS > 0 ? TH * C : 1];
 
     const int64_t bh = blockIdx.x;
     // marked_only: serve only the heads another kernel left to this exact
@@ -173,37 +185,57 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
 
     const int64_t nint = (T + ci - 1) / ci;
     int buf = 0;
+    // one full sub-interval of steps on Sx, from token t0 (the staging
+    // buffers are free on entry and on exit)
+    auto advance = [&](float (&Sx)[C], int64_t t0) {
+        stage_bwd<N, VT>(sh, t0, SUB, lay.ts, hoff, r, w, k, v, a, b,
+                         nullptr);
+        __syncthreads();
+        for (int u = 0; u < SUB; ++u) {
+            float sa = 0.f;
+#pragma unroll
+            for (int cc = 0; cc < C; ++cc) sa += Sx[cc] * sh[4][u][col0 + cc];
+            sa = group_sum<G>(sa);
+            const float vi = sh[3][u][row];
+#pragma unroll
+            for (int cc = 0; cc < C; ++cc)
+                Sx[cc] = Sx[cc] * sh[1][u][col0 + cc] +
+                         sa * sh[5][u][col0 + cc] + vi * sh[2][u][col0 + cc];
+        }
+        __syncthreads();
+    };
     for (int64_t c = nint - 1; c >= 0; --c) {
         const int64_t ta = c * ci;
         const int64_t tb = (ta + ci < T) ? ta + ci : T;
         const int64_t nsub = (tb - ta + SUB - 1) / SUB;
-        for (int64_t s = nsub - 1; s >= 0; --s) {
+        // Sub-intervals in reverse, in blocks of KS: each block's start
+        // states are formed once, from the checkpoint, and saved; each
+        // sub-interval then starts from its saved state (KS = 0: every
+        // sub-interval from the checkpoint).  The same steps in the same
+        // order either way.
+        const int64_t per = KS > 0 ? KS : 1;
+        for (int64_t s_lo = ((nsub - 1) / per) * per; s_lo >= 0; s_lo -= per) {
+        const int64_t s_hi = s_lo + per < nsub ? s_lo + per : nsub;
+        float Sx[C];
+#pragma unroll
+        for (int cc = 0; cc < C; ++cc)
+            Sx[cc] = load_f(ckpt + c * BH * NN + my + cc);
+        for (int64_t t0 = ta; t0 < ta + s_lo * SUB; t0 += SUB) advance(Sx, t0);
+        if constexpr (KS > 0) {
+            for (int64_t s = s_lo; s < s_hi; ++s) {
+#pragma unroll
+                for (int cc = 0; cc < C; ++cc)
+                    saved[s - s_lo][tid * C + cc] = Sx[cc];
+                if (s + 1 < s_hi) advance(Sx, ta + s * SUB);
+            }
+        }
+        for (int64_t s = s_hi - 1; s >= s_lo; --s) {
             float St[SUB + 1][C];
             float sa_r[SUB];
 #pragma unroll
             for (int cc = 0; cc < C; ++cc)
-                St[0][cc] = load_f(ckpt + c * BH * NN + my + cc);
+                St[0][cc] = KS > 0 ? saved[s - s_lo][tid * C + cc] : Sx[cc];
             const int64_t ts = ta + s * SUB;
-            // advance from the interval checkpoint to the sub-interval start
-            for (int64_t t0 = ta; t0 < ts; t0 += SUB) {
-                stage_bwd<N, VT>(sh, t0, SUB, lay.ts, hoff, r, w, k, v, a,
-                                 b, nullptr);
-                __syncthreads();
-                for (int u = 0; u < SUB; ++u) {
-                    float sa = 0.f;
-#pragma unroll
-                    for (int cc = 0; cc < C; ++cc)
-                        sa += St[0][cc] * sh[4][u][col0 + cc];
-                    sa = group_sum<G>(sa);
-                    const float vi = sh[3][u][row];
-#pragma unroll
-                    for (int cc = 0; cc < C; ++cc)
-                        St[0][cc] = St[0][cc] * sh[1][u][col0 + cc] +
-                                    sa * sh[5][u][col0 + cc] +
-                                    vi * sh[2][u][col0 + cc];
-                }
-                __syncthreads();
-            }
             const int nt = int(tb - ts < SUB ? tb - ts : SUB);
             stage_bwd<N, VT>(sh, ts, nt, lay.ts, hoff, r, w, k, v, a, b,
                              dy);
@@ -243,21 +275,55 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
                     dsa = group_sum<G>(dsa);
                     dvv = group_sum<G>(dvv);
                     if (col0 == 0) sh_dv[u][row] = dvv;
+                    // this lane's terms of the five column sums (over the
+                    // state rows i), value q * C + cc
+                    float pv[5 * C];
 #pragma unroll
                     for (int cc = 0; cc < C; ++cc) {
-                        float p[5];
-                        p[0] = St[u + 1][cc] * dyi;   // dr
-                        p[1] = Gc[cc] * St[u][cc];    // d decay
-                        p[2] = Gc[cc] * sa;           // dkka
-                        p[3] = Gc[cc] * vi;           // dk
-                        p[4] = St[u][cc] * dsa;       // dneg_kk
-#pragma unroll
-                        for (int q = 0; q < 5; ++q) {
-                            p[q] = cross_group_sum<G, WL>(p[q]);
-                            if (lane < G) red[buf][wave][q][col0 + cc] = p[q];
-                        }
+                        pv[0 * C + cc] = St[u + 1][cc] * dyi;  // dr
+                        pv[1 * C + cc] = Gc[cc] * St[u][cc];   // d decay
+                        pv[2 * C + cc] = Gc[cc] * sa;          // dkka
+                        pv[3 * C + cc] = Gc[cc] * vi;          // dk
+                        pv[4 * C + cc] = St[u][cc] * dsa;      // dneg_kk
                         dS[cc] = Gc[cc] * sh[1][u][col0 + cc] +
                                  dsa * sh[4][u][col0 + cc];
+                    }
+                    constexpr int V = 5 * C;
+                    if constexpr (G == 16 && WL == 64 && V % 4 == 0) {
+                        // Sums over the wave's four rows as a reduce-scatter:
+                        // a permlane16 swap of values j and j + V/2 leaves
+                        // value j summed over rows {0, 1} in row 0 and over
+                        // {2, 3} in row 2, value j + V/2 likewise in rows 1
+                        // and 3; a permlane32 swap of those results j and
+                        // j + V/4 completes j and j + V/2 in rows 0 and 1,
+                        // j + V/4 and j + 3V/4 in rows 2 and 3.  V/2 + V/4
+                        // swaps instead of 2V, and every lane stores.
+                        constexpr int H1 = V / 2, H2 = V / 4;
+                        float w1[H1];
+#pragma unroll
+                        for (int j = 0; j < H1; ++j) {
+                            const auto x = __builtin_amdgcn_permlane16_swap(
+                                __float_as_uint(pv[j]),
+                                __float_as_uint(pv[j + H1]), false, false);
+                            w1[j] = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+                        }
+                        const int rw = lane >> 4;
+                        const int vo = ((rw & 1) ? H1 : 0) + ((rw & 2) ? H2 : 0);
+#pragma unroll
+                        for (int j = 0; j < H2; ++j) {
+                            const auto x = __builtin_amdgcn_permlane32_swap(
+                                __float_as_uint(w1[j]),
+                                __float_as_uint(w1[j + H2]), false, false);
+                            const int vi2 = j + vo;
+                            red[buf][wave][vi2 / C][col0 + vi2 % C] =
+                                __uint_as_float(x[0]) + __uint_as_float(x[1]);
+                        }
+                    } else {
+#pragma unroll
+                        for (int vv = 0; vv < V; ++vv) {
+                            const float x = cross_group_sum<G, WL>(pv[vv]);
+                            if (lane < G) red[buf][wave][vv / C][col0 + vv % C] = x;
+                        }
                     }
                     __syncthreads();
                     const int64_t t = ts + u;
@@ -285,6 +351,7 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
                         sh_dv[u][i] + (add_dv ? load_f(add_dv + off) : 0.f));
             }
             __syncthreads();
+        }
         }
     }
 #pragma unroll

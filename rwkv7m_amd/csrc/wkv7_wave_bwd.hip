@@ -447,10 +447,10 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
     const uint32_t ts2 = A.ts2;
     constexpr int m = M;
     // Blocks of four independent 16-column tiles go through some phases
-    // stage by stage, GW blocks at a time: all four for the plain interval-16
-    // instance; one at a time where the registers of four in flight would
-    // spill (longer intervals, the summing instance).
-    constexpr int GW = (M == 1 && !ACC) ? 4 : 1;
+    // stage by stage, GW blocks at a time: all four for the plain instances
+    // at intervals 16 and 32; one at a time where the registers of four in
+    // flight would spill (interval 64, the summing instance).
+    constexpr int GW = (M <= 2 && !ACC) ? 4 : 1;
     // the worker of chunk c + 1 (one position earlier in the reverse order),
     // whose start state chunk c's end state is
     const int wfeed = (w + NWORK - 1) % NWORK;
@@ -879,8 +879,8 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
             const bf16x8_t Ahp0 = pk8(tAh[0], tAh[1]),
                            Ahp1 = pk8(tAh[2], tAh[3]);
             if constexpr (GW == 4) {
-                // (interval 16, no next start state: each stage for all four
-                // value blocks before the next, as for dX, dU, dV)
+                // (each stage for all four value blocks before the next, as
+                // for dX, dU, dV)
                 f32x4_t u[4], xt[4];
 #pragma unroll
                 for (int ib = 0; ib < 4; ++ib) {
@@ -899,6 +899,25 @@ __device__ __forceinline__ void work(const BwdArgs& A, int w, int lane0) {
                 }
 #pragma unroll
                 for (int ib = 0; ib < 4; ++ib) kXT[ib] = kq(xt[ib]);
+                if (M == 2 && feeds) {
+                    // X and V of value block ib for chain ib, in its own
+                    // rows of the S buffer of chunk c + 1's worker
+                    f32x4_t xj[4];
+#pragma unroll
+                    for (int ib = 0; ib < 4; ++ib) {
+                        xj[ib] = zero4();
+                        mfma16(xj[ib], kMinv, kU[ib]);  // X = Minv U
+                    }
+                    i16x4_t* const hp = reinterpret_cast<i16x4_t*>(lds_S[wfeed]);
+#pragma unroll
+                    for (int ib = 0; ib < 4; ++ib) {
+                        hp[64 * (4 * ib) + lane] = kq(xj[ib]);
+                        hp[64 * (4 * ib + 1) + lane] = jV[ib];
+                    }
+                    lds_drain();
+                    ++nfeed;
+                    if (lane == 0) lds_store(&fl.h_ready[wfeed], c + 1);
+                }
                 return true;
             }
 #pragma unroll

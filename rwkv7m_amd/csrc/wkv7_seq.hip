@@ -68,18 +68,53 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, VecLayout lay,
     }
     const VT* srcs[6] = {r, w, k, v, a, b};
 
-    for (int64_t t0 = 0; t0 < T; t0 += TB) {
+    // Each block's vectors are loaded into registers (this thread's
+    // elements e = tid + i * TH) during the previous block's steps, where
+    // that takes a few registers (PF); small heads load them in place.
+    constexpr int PF = (6 * TB * N + TH - 1) / TH;
+    constexpr bool AHEAD = PF <= 8;
+    float pf[AHEAD ? PF : 1];
+    auto load_block = [&](int64_t t0) __attribute__((always_inline)) {
         const int nt = int(T - t0 < TB ? T - t0 : TB);
-        for (int e = tid; e < 6 * TB * N; e += TH) {
+#pragma unroll
+        for (int i = 0; i < PF; ++i) {
+            const int e = tid + i * TH;
             const int vec = e / (TB * N), rem = e - vec * TB * N;
             const int u = rem / N, j = rem - u * N;
-            if (u < nt) {
-                float x = load_f(srcs[vec] + (t0 + u) * lay.ts + hoff + j);
-                if (vec == 1) x = expf(-expf(x));
-                sh[vec][u][j] = x;
+            pf[i] = 0.f;
+            if (e < 6 * TB * N && u < nt)
+                pf[i] = load_f(srcs[vec] + (t0 + u) * lay.ts + hoff + j);
+        }
+    };
+    if constexpr (AHEAD) {
+        if (T > 0) load_block(0);
+    }
+    for (int64_t t0 = 0; t0 < T; t0 += TB) {
+        const int nt = int(T - t0 < TB ? T - t0 : TB);
+        if constexpr (AHEAD) {
+#pragma unroll
+            for (int i = 0; i < PF; ++i) {
+                const int e = tid + i * TH;
+                const int vec = e / (TB * N), rem = e - vec * TB * N;
+                const int u = rem / N, j = rem - u * N;
+                if (e < 6 * TB * N && u < nt)
+                    sh[vec][u][j] = vec == 1 ? expf(-expf(pf[i])) : pf[i];
+            }
+        } else {
+            for (int e = tid; e < 6 * TB * N; e += TH) {
+                const int vec = e / (TB * N), rem = e - vec * TB * N;
+                const int u = rem / N, j = rem - u * N;
+                if (u < nt) {
+                    float x = load_f(srcs[vec] + (t0 + u) * lay.ts + hoff + j);
+                    if (vec == 1) x = expf(-expf(x));
+                    sh[vec][u][j] = x;
+                }
             }
         }
         __syncthreads();
+        if constexpr (AHEAD) {
+            if (t0 + TB < T) load_block(t0 + TB);
+        }
         for (int u = 0; u < nt; ++u) {
             float sa = 0.f;
 #pragma unroll
@@ -114,29 +149,88 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, VecLayout lay,
     for (int c = 0; c < C; ++c) s_t[my + c] = S[c];
 }
 
-// Stage `count` tokens starting at t0 into sh[8][SUB][N]:
-// 0 r, 1 decay, 2 k, 3 v, 4 a, 5 b, 6 dy, 7 exp(w).
+// The backward's staged vectors, sh[8][SUB][N]: 0 r, 1 decay, 2 k, 3 v,
+// 4 a, 5 b, 6 dy, 7 exp(w), for `count` tokens from t0.  Loaded into each
+// thread's registers first (its elements e = tid + i * THREADS of the
+// seven vectors), so that the loads of the next block can be issued before
+// the current one is used, then written to LDS.
+// Small heads (more than 8 elements per thread) load in place instead:
+// stage_load only records the block and stage_write loads it.
+template <int N>
+struct StageRegs {
+    static constexpr int PF =
+        (7 * SeqShape<N>::SUB * N + SeqShape<N>::THREADS - 1) /
+        SeqShape<N>::THREADS;
+    static constexpr bool AHEAD = PF <= 8;
+    float x[AHEAD ? PF : 1];
+    int64_t t0 = -1;
+    int count = 0;
+    const void* dy = nullptr;
+};
+
 template <int N, typename VT>
-__device__ __forceinline__ void stage_bwd(
-    float (*sh)[SeqShape<N>::SUB][N], int64_t t0, int count, int64_t tstr,
-    int64_t hoff, const VT* r, const VT* w, const VT* k, const VT* v,
-    const VT* a, const VT* b, const VT* dy) {
+__device__ __forceinline__ void stage_load(
+    StageRegs<N>& R, int64_t t0, int count, int64_t tstr, int64_t hoff,
+    const VT* r, const VT* w, const VT* k, const VT* v, const VT* a,
+    const VT* b, const VT* dy) {
     using Sh = SeqShape<N>;
     constexpr int SUB = Sh::SUB, TH = Sh::THREADS;
-    const VT* srcs[7] = {r, w, k, v, a, b, dy};
-    for (int e = threadIdx.x; e < 7 * SUB * N; e += TH) {
+    if constexpr (StageRegs<N>::AHEAD) {
+        const VT* srcs[7] = {r, w, k, v, a, b, dy};
+#pragma unroll
+        for (int i = 0; i < StageRegs<N>::PF; ++i) {
+            const int e = threadIdx.x + i * TH;
+            const int vec = e / (SUB * N), rem = e - vec * SUB * N;
+            const int u = rem / N, j = rem - u * N;
+            R.x[i] = 0.f;
+            if (e < 7 * SUB * N && u < count && (vec != 6 || dy))
+                R.x[i] = load_f(srcs[vec] + (t0 + u) * tstr + hoff + j);
+        }
+    }
+    R.t0 = t0;
+    R.count = count;
+    R.dy = dy;
+}
+
+template <int N, typename VT>
+__device__ __forceinline__ void stage_write(
+    const StageRegs<N>& R, float (*sh)[SeqShape<N>::SUB][N], int64_t tstr,
+    int64_t hoff, const VT* r, const VT* w, const VT* k, const VT* v,
+    const VT* a, const VT* b) {
+    using Sh = SeqShape<N>;
+    constexpr int SUB = Sh::SUB, TH = Sh::THREADS;
+    if constexpr (!StageRegs<N>::AHEAD) {
+        const VT* dy = static_cast<const VT*>(R.dy);
+        const VT* srcs[7] = {r, w, k, v, a, b, dy};
+        for (int e = threadIdx.x; e < 7 * SUB * N; e += TH) {
+            const int vec = e / (SUB * N), rem = e - vec * SUB * N;
+            const int u = rem / N, j = rem - u * N;
+            if (u < R.count) {
+                const int64_t off = (R.t0 + u) * tstr + hoff + j;
+                if (vec == 1) {
+                    const float ew = expf(load_f(w + off));
+                    sh[1][u][j] = expf(-ew);
+                    sh[7][u][j] = ew;
+                } else {
+                    sh[vec][u][j] =
+                        vec == 6 && !dy ? 0.f : load_f(srcs[vec] + off);
+                }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < StageRegs<N>::PF; ++i) {
+        const int e = threadIdx.x + i * TH;
         const int vec = e / (SUB * N), rem = e - vec * SUB * N;
         const int u = rem / N, j = rem - u * N;
-        if (u < count) {
-            const int64_t off = (t0 + u) * tstr + hoff + j;
+        if (e < 7 * SUB * N && u < R.count) {
             if (vec == 1) {
-                const float ew = expf(load_f(w + off));
+                const float ew = expf(R.x[i]);
                 sh[1][u][j] = expf(-ew);
                 sh[7][u][j] = ew;
-            } else if (vec == 6) {
-                sh[6][u][j] = dy ? load_f(dy + off) : 0.f;
             } else {
-                sh[vec][u][j] = load_f(srcs[vec] + off);
+                sh[vec][u][j] = R.x[i];
             }
         }
     }
@@ -185,12 +279,9 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
 
     const int64_t nint = (T + ci - 1) / ci;
     int buf = 0;
-    // one full sub-interval of steps on Sx, from token t0 (the staging
-    // buffers are free on entry and on exit)
-    auto advance = [&](float (&Sx)[C], int64_t t0) {
-        stage_bwd<N, VT>(sh, t0, SUB, lay.ts, hoff, r, w, k, v, a, b,
-                         nullptr);
-        __syncthreads();
+    // one full sub-interval of steps on Sx with the staged vectors (the
+    // staging buffers are free again on exit)
+    auto advance = [&](float (&Sx)[C]) __attribute__((always_inline)) {
         for (int u = 0; u < SUB; ++u) {
             float sa = 0.f;
 #pragma unroll
@@ -220,15 +311,37 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
 #pragma unroll
         for (int cc = 0; cc < C; ++cc)
             Sx[cc] = load_f(ckpt + c * BH * NN + my + cc);
-        for (int64_t t0 = ta; t0 < ta + s_lo * SUB; t0 += SUB) advance(Sx, t0);
-        if constexpr (KS > 0) {
-            for (int64_t s = s_lo; s < s_hi; ++s) {
+        {
+            // The advances of this block, sub-intervals 0 .. s_lo - 1 to
+            // reach its start, then (saving each start state) s_lo ..
+            // s_hi - 2: each sub-interval's vectors are loaded into
+            // registers while the previous one's steps run.
+            const int64_t n_adv = KS > 0 ? s_hi - 1 : s_lo;
+            StageRegs<N> pf;
+            if (n_adv > 0)
+                stage_load<N, VT>(pf, ta, SUB, lay.ts, hoff, r, w, k, v, a, b,
+                                  nullptr);
+            for (int64_t q = 0; q < n_adv; ++q) {
+                if (KS > 0 && q >= s_lo) {
+#pragma unroll
+                    for (int cc = 0; cc < C; ++cc)
+                        saved[q - s_lo][tid * C + cc] = Sx[cc];
+                }
+                stage_write<N, VT>(pf, sh, lay.ts, hoff, r, w, k, v, a, b);
+                __syncthreads();
+                if (q + 1 < n_adv)
+                    stage_load<N, VT>(pf, ta + (q + 1) * SUB, SUB, lay.ts,
+                                      hoff, r, w, k, v, a, b, nullptr);
+                advance(Sx);
+            }
+            // the start state of the block's last sub-interval
+            if constexpr (KS > 0) {
 #pragma unroll
                 for (int cc = 0; cc < C; ++cc)
-                    saved[s - s_lo][tid * C + cc] = Sx[cc];
-                if (s + 1 < s_hi) advance(Sx, ta + s * SUB);
+                    saved[s_hi - 1 - s_lo][tid * C + cc] = Sx[cc];
             }
         }
+        StageRegs<N> rp;  // the reverse's next sub-interval, loaded ahead
         for (int64_t s = s_hi - 1; s >= s_lo; --s) {
             float St[SUB + 1][C];
             float sa_r[SUB];
@@ -237,9 +350,14 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
                 St[0][cc] = KS > 0 ? saved[s - s_lo][tid * C + cc] : Sx[cc];
             const int64_t ts = ta + s * SUB;
             const int nt = int(tb - ts < SUB ? tb - ts : SUB);
-            stage_bwd<N, VT>(sh, ts, nt, lay.ts, hoff, r, w, k, v, a, b,
-                             dy);
+            if (s == s_hi - 1)
+                stage_load<N, VT>(rp, ts, nt, lay.ts, hoff, r, w, k, v, a, b,
+                                  dy);
+            stage_write<N, VT>(rp, sh, lay.ts, hoff, r, w, k, v, a, b);
             __syncthreads();
+            if (s > s_lo)
+                stage_load<N, VT>(rp, ts - SUB, SUB, lay.ts, hoff, r, w, k, v,
+                                  a, b, dy);
             // recompute the sub-interval's states: St[u] = S before token u
 #pragma unroll
             for (int u = 0; u < SUB; ++u) {

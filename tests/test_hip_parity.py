@@ -110,6 +110,26 @@ def test_forward_backward_match_oracle(hip, case, dtype):
         _assert_close(name, g, e, tol, tag)
 
 
+@pytest.mark.parametrize("n", [32, 64, 128])
+def test_sequential_backward_saved_states_long_interval(hip, n):
+    """One interval of 300 tokens: the sequential backward's sub-interval
+    start states are saved in LDS several at a time (16 at N = 32, 6 at
+    N = 64) or, at N = 128, recomputed from the checkpoint each time; every
+    grouping, the partial last sub-interval and the prefetched vector blocks
+    against the oracle."""
+    print("case: sequential backward, T = 300, interval 256, N =", n,
+          flush=True)
+    inp = make_inputs(300, 1, 2, n, dtype=torch.float32, seed=91,
+                      state_std=0.1, dstate_std=0.1)
+    ey, es, egrads = _oracle_all(inp)
+    y, s_t, aux, grads, _, _ = _run_hip(hip, _to_dev(inp), ci=256)
+    assert aux[0].shape[0] == 3
+    _assert_close("y", y, ey, 1e-4, f"N={n}")
+    _assert_close("s_t", s_t, es, 1e-4, f"N={n}")
+    for name, g, e in zip(GRAD_NAMES, grads, egrads):
+        _assert_close(name, g, e, 1e-4, f"N={n}")
+
+
 @pytest.mark.parametrize("ci", [1, 3, 16, 64, 200])
 def test_checkpoint_interval_does_not_change_results(hip, ci):
     print("case: checkpoint interval", ci, flush=True)

@@ -11,6 +11,8 @@
 // Reverse equations (reference src/rwkv7m/kernels/wkv_pallas_gpu.py:221-257),
 // with S_{t-1} recomputed forward from checkpoints instead of divided out.
 
+#include <mutex>
+
 #include "wkv7_common.h"
 #include "wkv7_launch.h"
 
@@ -19,22 +21,38 @@ namespace {
 
 template <int N>
 struct SeqShape {
-    static constexpr int G = (N >= 128) ? 8 : (N >= 16 ? 16 : N);
+    // A head's N state rows over RS workgroups, each owning NR consecutive
+    // rows: rows are independent in the recurrence, and only the backward's
+    // five column sums cross them (each workgroup's partial sums are added
+    // by a second kernel).  Split where one workgroup would hold more than
+    // 64 x 64 state values: the register file then holds C = 8 per lane.
+    static constexpr int RS = (N >= 128) ? 2 : 1;
+    static constexpr int NR = N / RS;
+    static constexpr int G = N >= 16 ? 16 : N;
     static constexpr int C = N / G;
-    static constexpr int THREADS = N * G;
+    static constexpr int THREADS = NR * G;
     static constexpr int WAVE_LANES = THREADS < 64 ? THREADS : 64;
     static constexpr int NWAVES = (THREADS + 63) / 64;
     static constexpr int SUB = (N >= 128) ? 4 : (N >= 64 ? 8 : 16);
     static constexpr int TB = 16;
-    // The backward's LDS besides the saved states (bytes): the staged
-    // vectors, the reduction buffers and dv.
-    static constexpr int BWD_LDS =
-        4 * (8 * SUB * N + 2 * NWAVES * 5 * N + SUB * N);
-    // Sub-interval start states the backward keeps in LDS (fp32, N x N
-    // each) so that it recomputes each from the nearest saved one instead of
-    // from the interval's checkpoint; 0 where not even one fits.
-    static constexpr int KS_FIT = (163840 - 512 - BWD_LDS) / (4 * N * N);
-    static constexpr int KSAVE = KS_FIT > 16 ? 16 : KS_FIT;
+    // The backward's LDS besides the saved states (bytes) with RB
+    // reduction buffers: the staged vectors, the reduction buffers and dv.
+    static constexpr int bwd_lds(int rb) {
+        return 4 * (8 * SUB * N + rb * NWAVES * 5 * N + SUB * N);
+    }
+    static constexpr int ks_fit(int rb) {
+        return (163840 - 512 - bwd_lds(rb)) / (4 * NR * N);
+    }
+    // Reduction buffers: two (a token's sums are written while the
+    // previous token's are read), or one and a second barrier per token
+    // where that makes room for two saved states.
+    static constexpr int RB = (ks_fit(2) < 2 && ks_fit(1) >= 2) ? 1 : 2;
+    // Sub-interval start states the backward keeps in LDS (fp32, the
+    // workgroup's NR x N each) so that it recomputes each from the nearest
+    // saved one instead of from the interval's checkpoint; 0 where fewer
+    // than two fit (one saves no advance).
+    static constexpr int KS_FIT = ks_fit(RB);
+    static constexpr int KSAVE = KS_FIT < 2 ? 0 : (KS_FIT > 16 ? 16 : KS_FIT);
 };
 
 // Forward.  ckpt == nullptr: no aux.  s_t may alias s0.  CT is the
@@ -53,9 +71,11 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, VecLayout lay,
     __shared__ float sh[6][TB][N];  // r, decay, k, v, a, b
     __shared__ float sh_y[TB][N];
 
-    const int64_t bh = blockIdx.x;
+    constexpr int NR = Sh::NR;
+    const int64_t bh = blockIdx.x / Sh::RS;
+    const int split = int(blockIdx.x % Sh::RS);
     const int tid = threadIdx.x;
-    const int row = tid / G, col0 = (tid % G) * C;
+    const int row = split * NR + tid / G, col0 = (tid % G) * C;
     const int64_t my = bh * NN + int64_t(row) * N + col0;
     const int64_t hoff = lay.head(bh, N);
 
@@ -72,7 +92,7 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, VecLayout lay,
     // elements e = tid + i * TH) during the previous block's steps, where
     // that takes a few registers (PF); small heads load them in place.
     constexpr int PF = (6 * TB * N + TH - 1) / TH;
-    constexpr bool AHEAD = PF <= 8;
+    constexpr bool AHEAD = PF <= 12;
     float pf[AHEAD ? PF : 1];
     auto load_block = [&](int64_t t0) __attribute__((always_inline)) {
         const int nt = int(T - t0 < TB ? T - t0 : TB);
@@ -140,8 +160,8 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, VecLayout lay,
             }
         }
         __syncthreads();
-        for (int e = tid; e < nt * N; e += TH) {
-            const int u = e / N, i = e - u * N;
+        for (int e = tid; e < nt * NR; e += TH) {
+            const int u = e / NR, i = split * NR + (e - u * NR);
             store_f(y + (t0 + u) * lay.ts + hoff + i, sh_y[u][i]);
         }
     }
@@ -243,31 +263,36 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
                     const VT* __restrict__ w, const VT* __restrict__ k,
                     const VT* __restrict__ v, const VT* __restrict__ a,
                     const VT* __restrict__ b, const VT* __restrict__ dy,
-                    const float* __restrict__ ds_t,
+                    const float* ds_t,
                     const CT* __restrict__ ckpt, int64_t ci, VT* dr,
                     VT* dw, VT* dk, VT* dv, VT* da, VT* db, float* ds0,
                     int marked_only, const VT* __restrict__ add_dr,
                     const VT* __restrict__ add_dk,
-                    const VT* __restrict__ add_dv) {
+                    const VT* __restrict__ add_dv, int64_t c_lo,
+                    int64_t c_hi, float* __restrict__ part, int64_t pt0,
+                    int64_t pT) {
     using Sh = SeqShape<N>;
     constexpr int G = Sh::G, C = Sh::C, SUB = Sh::SUB, TH = Sh::THREADS;
     constexpr int WL = Sh::WAVE_LANES, NW = Sh::NWAVES;
     constexpr int64_t NN = int64_t(N) * N;
     constexpr int KS = Sh::KSAVE;
     __shared__ float sh[8][SUB][N];
-    __shared__ float red[2][NW][5][N];
+    __shared__ float red[Sh::RB][NW][5][N];
     __shared__ float sh_dv[SUB][N];
     // saved sub-interval start states, each thread's own C values
     __shared__ float saved[KS > 0 ? KS : 1][KS > 0 ? TH * C : 1];
 
-    const int64_t bh = blockIdx.x;
-    // marked_only: serve only the heads another kernel left to this exact
-    // pass (their dS0 holds kExactPassMark); every other head is complete
+    constexpr int NR = Sh::NR;
+    const int64_t bh = blockIdx.x / Sh::RS;
+    const int split = int(blockIdx.x % Sh::RS);
+    // marked_only (one workgroup per head): serve only the heads another
+    // kernel left to this exact pass (their dS0 holds kExactPassMark);
+    // every other head is complete
     if (marked_only &&
         __float_as_uint(ds0[bh * NN]) != kExactPassMark)
         return;
     const int tid = threadIdx.x;
-    const int row = tid / G, col0 = (tid % G) * C;
+    const int row = split * NR + tid / G, col0 = (tid % G) * C;
     const int wave = tid / 64, lane = tid % 64;
     const int64_t my = bh * NN + int64_t(row) * N + col0;
     const int64_t hoff = lay.head(bh, N);
@@ -277,7 +302,6 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
 #pragma unroll
     for (int c = 0; c < C; ++c) dS[c] = ds_t ? ds_t[my + c] : 0.f;
 
-    const int64_t nint = (T + ci - 1) / ci;
     int buf = 0;
     // one full sub-interval of steps on Sx with the staged vectors (the
     // staging buffers are free again on exit)
@@ -295,18 +319,24 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
         }
         __syncthreads();
     };
-    for (int64_t c = nint - 1; c >= 0; --c) {
+    // intervals c_lo .. c_hi - 1 (a time segment of the whole backward when
+    // the column sums go through `part`), the last first
+    for (int64_t c = c_hi - 1; c >= c_lo; --c) {
         const int64_t ta = c * ci;
         const int64_t tb = (ta + ci < T) ? ta + ci : T;
         const int64_t nsub = (tb - ta + SUB - 1) / SUB;
-        // Sub-intervals in reverse, in blocks of KS: each block's start
-        // states are formed once, from the checkpoint, and saved; each
-        // sub-interval then starts from its saved state (KS = 0: every
-        // sub-interval from the checkpoint).  The same steps in the same
-        // order either way.
+        // Sub-intervals in reverse, in blocks of KS counted from the
+        // interval's end (a partial block holds the first sub-intervals,
+        // the cheapest to reach): each block's start states are formed
+        // once, from the checkpoint, and saved; each sub-interval then
+        // starts from its saved state (KS = 0: every sub-interval from the
+        // checkpoint).  The same steps in the same order either way.
         const int64_t per = KS > 0 ? KS : 1;
-        for (int64_t s_lo = ((nsub - 1) / per) * per; s_lo >= 0; s_lo -= per) {
-        const int64_t s_hi = s_lo + per < nsub ? s_lo + per : nsub;
+        const int64_t skew = (per - nsub % per) % per;
+        for (int64_t s_lo = ((nsub - 1 + skew) / per) * per - skew;
+             s_lo > -per; s_lo -= per) {
+        const int64_t s_hi = s_lo + per;
+        if (s_lo < 0) s_lo = 0;  // the partial first block (then the last)
         float Sx[C];
 #pragma unroll
         for (int cc = 0; cc < C; ++cc)
@@ -394,55 +424,64 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
                     dvv = group_sum<G>(dvv);
                     if (col0 == 0) sh_dv[u][row] = dvv;
                     // this lane's terms of the five column sums (over the
-                    // state rows i), value q * C + cc
-                    float pv[5 * C];
-#pragma unroll
-                    for (int cc = 0; cc < C; ++cc) {
-                        pv[0 * C + cc] = St[u + 1][cc] * dyi;  // dr
-                        pv[1 * C + cc] = Gc[cc] * St[u][cc];   // d decay
-                        pv[2 * C + cc] = Gc[cc] * sa;          // dkka
-                        pv[3 * C + cc] = Gc[cc] * vi;          // dk
-                        pv[4 * C + cc] = St[u][cc] * dsa;      // dneg_kk
-                        dS[cc] = Gc[cc] * sh[1][u][col0 + cc] +
-                                 dsa * sh[4][u][col0 + cc];
-                    }
-                    constexpr int V = 5 * C;
-                    if constexpr (G == 16 && WL == 64 && V % 4 == 0) {
+                    // state rows i): q 0 dr, 1 d decay, 2 dkka, 3 dk,
+                    // 4 dneg_kk, each summed over the wave's rows into
+                    // red[buf][wave][q] one sum at a time (so that only one
+                    // sum's C terms are live)
+                    auto term = [&](int q, int cc) __attribute__((always_inline)) {
+                        return q == 0   ? St[u + 1][cc] * dyi
+                               : q == 1 ? Gc[cc] * St[u][cc]
+                               : q == 2 ? Gc[cc] * sa
+                               : q == 3 ? Gc[cc] * vi
+                                        : St[u][cc] * dsa;
+                    };
+                    if constexpr (G == 16 && WL == 64 && C % 4 == 0) {
                         // Sums over the wave's four rows as a reduce-scatter:
-                        // a permlane16 swap of values j and j + V/2 leaves
-                        // value j summed over rows {0, 1} in row 0 and over
-                        // {2, 3} in row 2, value j + V/2 likewise in rows 1
+                        // a permlane16 swap of terms j and j + C/2 leaves
+                        // term j summed over rows {0, 1} in row 0 and over
+                        // {2, 3} in row 2, term j + C/2 likewise in rows 1
                         // and 3; a permlane32 swap of those results j and
-                        // j + V/4 completes j and j + V/2 in rows 0 and 1,
-                        // j + V/4 and j + 3V/4 in rows 2 and 3.  V/2 + V/4
-                        // swaps instead of 2V, and every lane stores.
-                        constexpr int H1 = V / 2, H2 = V / 4;
-                        float w1[H1];
-#pragma unroll
-                        for (int j = 0; j < H1; ++j) {
-                            const auto x = __builtin_amdgcn_permlane16_swap(
-                                __float_as_uint(pv[j]),
-                                __float_as_uint(pv[j + H1]), false, false);
-                            w1[j] = __uint_as_float(x[0]) + __uint_as_float(x[1]);
-                        }
+                        // j + C/4 completes j and j + C/2 in rows 0 and 1,
+                        // j + C/4 and j + 3C/4 in rows 2 and 3.  3C/4 swaps
+                        // per sum instead of 2C, and every lane stores.
+                        constexpr int H1 = C / 2, H2 = C / 4;
                         const int rw = lane >> 4;
                         const int vo = ((rw & 1) ? H1 : 0) + ((rw & 2) ? H2 : 0);
 #pragma unroll
-                        for (int j = 0; j < H2; ++j) {
-                            const auto x = __builtin_amdgcn_permlane32_swap(
-                                __float_as_uint(w1[j]),
-                                __float_as_uint(w1[j + H2]), false, false);
-                            const int vi2 = j + vo;
-                            red[buf][wave][vi2 / C][col0 + vi2 % C] =
-                                __uint_as_float(x[0]) + __uint_as_float(x[1]);
+                        for (int q = 0; q < 5; ++q) {
+                            float w1[H1];
+#pragma unroll
+                            for (int jj = 0; jj < H1; ++jj) {
+                                const auto x = __builtin_amdgcn_permlane16_swap(
+                                    __float_as_uint(term(q, jj)),
+                                    __float_as_uint(term(q, jj + H1)), false,
+                                    false);
+                                w1[jj] = __uint_as_float(x[0]) +
+                                         __uint_as_float(x[1]);
+                            }
+#pragma unroll
+                            for (int jj = 0; jj < H2; ++jj) {
+                                const auto x = __builtin_amdgcn_permlane32_swap(
+                                    __float_as_uint(w1[jj]),
+                                    __float_as_uint(w1[jj + H2]), false, false);
+                                red[buf][wave][q][col0 + jj + vo] =
+                                    __uint_as_float(x[0]) + __uint_as_float(x[1]);
+                            }
                         }
                     } else {
 #pragma unroll
-                        for (int vv = 0; vv < V; ++vv) {
-                            const float x = cross_group_sum<G, WL>(pv[vv]);
-                            if (lane < G) red[buf][wave][vv / C][col0 + vv % C] = x;
-                        }
+                        for (int q = 0; q < 5; ++q)
+#pragma unroll
+                            for (int cc = 0; cc < C; ++cc) {
+                                const float x =
+                                    cross_group_sum<G, WL>(term(q, cc));
+                                if (lane < G) red[buf][wave][q][col0 + cc] = x;
+                            }
                     }
+#pragma unroll
+                    for (int cc = 0; cc < C; ++cc)
+                        dS[cc] = Gc[cc] * sh[1][u][col0 + cc] +
+                                 dsa * sh[4][u][col0 + cc];
                     __syncthreads();
                     const int64_t t = ts + u;
                     for (int e = tid; e < 5 * N; e += TH) {
@@ -450,6 +489,13 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
                         float acc = 0.f;
 #pragma unroll
                         for (int ww = 0; ww < NW; ++ww) acc += red[buf][ww][q][j];
+                        if constexpr (Sh::RS > 1) {
+                            // this workgroup's rows' share, for the sum
+                            // kernel: part[split][t - pt0][bh][q][j]
+                            part[((split * pT + (t - pt0)) * BH + bh) * 5 * N +
+                                 e] = acc;
+                            continue;
+                        }
                         if (q == 1) acc *= -sh[7][u][j] * sh[1][u][j];
                         const int64_t off = t * lay.ts + hoff + j;
                         // cotangents of r and k from other uses, added in
@@ -458,12 +504,15 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
                         if (q == 3 && add_dk) acc += load_f(add_dk + off);
                         store_f(gout[q] + off, acc);
                     }
-                    buf ^= 1;
+                    if constexpr (Sh::RB == 2)
+                        buf ^= 1;
+                    else
+                        __syncthreads();
                 }
             }
             __syncthreads();
-            for (int e = tid; e < nt * N; e += TH) {
-                const int u = e / N, i = e - u * N;
+            for (int e = tid; e < nt * NR; e += TH) {
+                const int u = e / NR, i = split * NR + (e - u * NR);
                 const int64_t off = (ts + u) * lay.ts + hoff + i;
                 store_f(dv + off,
                         sh_dv[u][i] + (add_dv ? load_f(add_dv + off) : 0.f));
@@ -476,10 +525,87 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
     for (int c = 0; c < C; ++c) ds0[my + c] = dS[c];
 }
 
+// The column sums of a row-split backward: for each of nt tokens from t0,
+// head and column, the RS workgroups' shares from part[RS][nt][BH][5][N]
+// added, then, as in the one-workgroup backward, the decay gradient's
+// factor -e^w d applied, the added cotangents summed in and the result
+// rounded and stored (q: 0 dr, 1 dw, 2 db, 3 dk, 4 da).
+template <int N, typename VT>
+__global__ void __launch_bounds__(256)
+wkv7_seq_colsum_kernel(int64_t nt, int64_t t0, int64_t BH, VecLayout lay,
+                       const float* __restrict__ part,
+                       const VT* __restrict__ w,
+                       const VT* __restrict__ add_dr,
+                       const VT* __restrict__ add_dk, VT* dr, VT* dw, VT* db,
+                       VT* dk, VT* da) {
+    constexpr int RS = SeqShape<N>::RS;
+    const int64_t per = BH * 5 * N;  // values per token
+    const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (e >= nt * per) return;
+    const int64_t tl = e / per;
+    const int64_t rem = e - tl * per;
+    const int64_t bh = rem / (5 * N);
+    const int qj = int(rem - bh * (5 * N));
+    const int q = qj / N, j = qj - q * N;
+    float acc = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < RS; ++sp) acc += part[sp * nt * per + e];
+    const int64_t off = (t0 + tl) * lay.ts + lay.head(bh, N) + j;
+    if (q == 1) {
+        const float ew = expf(load_f(w + off));
+        acc *= -ew * expf(-ew);
+    }
+    if (q == 0 && add_dr) acc += load_f(add_dr + off);
+    if (q == 3 && add_dk) acc += load_f(add_dk + off);
+    VT* gout[5] = {dr, dw, db, dk, da};
+    store_f(gout[q] + off, acc);
+}
+
+// Device memory for the row-split backward's partial column sums: a
+// stream-ordered pool per device that keeps what it has reserved (so
+// repeated calls reuse it instead of mapping new memory each time).
+constexpr int kPoolDevices = 64;
+std::mutex g_pool_mu;
+hipMemPool_t g_pool[kPoolDevices];
+
+hipError_t part_alloc(float** out, size_t bytes, hipStream_t stream) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kPoolDevices) return hipErrorInvalidDevice;
+    {
+        std::lock_guard<std::mutex> lock(g_pool_mu);
+        if (g_pool[dev] == nullptr) {
+            hipMemPoolProps props{};
+            props.allocType = hipMemAllocationTypePinned;
+            props.location.type = hipMemLocationTypeDevice;
+            props.location.id = dev;
+            hipMemPool_t pool = nullptr;
+            e = hipMemPoolCreate(&pool, &props);
+            if (e != hipSuccess) return e;
+            uint64_t keep = UINT64_MAX;
+            e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold,
+                                       &keep);
+            if (e != hipSuccess) {
+                hipMemPoolDestroy(pool);
+                return e;
+            }
+            g_pool[dev] = pool;
+        }
+    }
+    return hipMallocFromPoolAsync(reinterpret_cast<void**>(out), bytes,
+                                  g_pool[dev], stream);
+}
+
+// Partial column sums held at once by a row-split backward (bytes): the
+// backward runs in time segments of whole intervals that fit it.
+constexpr int64_t kPartBytes = int64_t(128) << 20;
+
 template <int N, typename VT, typename CT>
 hipError_t launch_fwd_nc(const SeqFwdArgs& p, hipStream_t stream) {
     const int64_t BH = p.B * p.H;
-    hipLaunchKernelGGL((wkv7_seq_fwd_kernel<N, VT, CT>), dim3(unsigned(BH)),
+    hipLaunchKernelGGL((wkv7_seq_fwd_kernel<N, VT, CT>),
+                       dim3(unsigned(BH * SeqShape<N>::RS)),
                        dim3(SeqShape<N>::THREADS), 0, stream, p.T, BH, p.lay,
                        static_cast<const VT*>(p.r),
                        static_cast<const VT*>(p.w),
@@ -499,9 +625,12 @@ hipError_t launch_fwd_n(const SeqFwdArgs& p, hipStream_t stream) {
 }
 
 template <int N, typename VT, typename CT>
-hipError_t launch_bwd_nc(const SeqBwdArgs& p, hipStream_t stream) {
+hipError_t launch_bwd_seg(const SeqBwdArgs& p, const float* ds_in,
+                          int64_t c_lo, int64_t c_hi, float* part, int64_t pt0,
+                          int64_t pT, hipStream_t stream) {
     const int64_t BH = p.B * p.H;
-    hipLaunchKernelGGL((wkv7_seq_bwd_kernel<N, VT, CT>), dim3(unsigned(BH)),
+    hipLaunchKernelGGL((wkv7_seq_bwd_kernel<N, VT, CT>),
+                       dim3(unsigned(BH * SeqShape<N>::RS)),
                        dim3(SeqShape<N>::THREADS), 0, stream, p.T, BH, p.lay,
                        static_cast<const VT*>(p.r),
                        static_cast<const VT*>(p.w),
@@ -509,7 +638,7 @@ hipError_t launch_bwd_nc(const SeqBwdArgs& p, hipStream_t stream) {
                        static_cast<const VT*>(p.v),
                        static_cast<const VT*>(p.a),
                        static_cast<const VT*>(p.b),
-                       static_cast<const VT*>(p.dy), p.ds_t,
+                       static_cast<const VT*>(p.dy), ds_in,
                        static_cast<const CT*>(p.ckpt), p.ci,
                        static_cast<VT*>(p.dr), static_cast<VT*>(p.dw),
                        static_cast<VT*>(p.dk), static_cast<VT*>(p.dv),
@@ -517,8 +646,58 @@ hipError_t launch_bwd_nc(const SeqBwdArgs& p, hipStream_t stream) {
                        p.ds0, p.marked_only ? 1 : 0,
                        static_cast<const VT*>(p.add_dr),
                        static_cast<const VT*>(p.add_dk),
-                       static_cast<const VT*>(p.add_dv));
+                       static_cast<const VT*>(p.add_dv), c_lo, c_hi, part,
+                       pt0, pT);
     return hipGetLastError();
+}
+
+template <int N, typename VT, typename CT>
+hipError_t launch_bwd_nc(const SeqBwdArgs& p, hipStream_t stream) {
+    const int64_t nint = (p.T + p.ci - 1) / p.ci;
+    constexpr int RS = SeqShape<N>::RS;
+    if constexpr (RS == 1) {
+        return launch_bwd_seg<N, VT, CT>(p, p.ds_t, 0, nint, nullptr, 0, 0,
+                                         stream);
+    } else {
+        // (the exact pass's marks live in one head's dS0, which every split
+        // of the head would read while another writes its rows)
+        if (p.marked_only) return hipErrorInvalidValue;
+        const int64_t BH = p.B * p.H;
+        const int64_t tok_bytes = int64_t(RS) * BH * 5 * N * 4;
+        int64_t seg = kPartBytes / (tok_bytes * p.ci);
+        if (seg < 1) seg = 1;
+        if (seg > nint) seg = nint;
+        const int64_t seg_tok = seg * p.ci < p.T ? seg * p.ci : p.T;
+        float* part = nullptr;
+        hipError_t e = part_alloc(&part, size_t(seg_tok * tok_bytes), stream);
+        if (e != hipSuccess) return e;
+        // segments of `seg` intervals, the last first; dS passes from one to
+        // the next through dS0 (each lane reads its own values before it
+        // writes them)
+        for (int64_t c_hi = nint; c_hi > 0 && e == hipSuccess;) {
+            const int64_t c_lo = c_hi - seg > 0 ? c_hi - seg : 0;
+            const int64_t t0 = c_lo * p.ci;
+            const int64_t t1 = c_hi * p.ci < p.T ? c_hi * p.ci : p.T;
+            e = launch_bwd_seg<N, VT, CT>(p, c_hi == nint ? p.ds_t : p.ds0,
+                                          c_lo, c_hi, part, t0, t1 - t0,
+                                          stream);
+            if (e != hipSuccess) break;
+            const int64_t n = (t1 - t0) * BH * 5 * N;
+            hipLaunchKernelGGL((wkv7_seq_colsum_kernel<N, VT>),
+                               dim3(unsigned((n + 255) / 256)), dim3(256), 0,
+                               stream, t1 - t0, t0, BH, p.lay, part,
+                               static_cast<const VT*>(p.w),
+                               static_cast<const VT*>(p.add_dr),
+                               static_cast<const VT*>(p.add_dk),
+                               static_cast<VT*>(p.dr), static_cast<VT*>(p.dw),
+                               static_cast<VT*>(p.db), static_cast<VT*>(p.dk),
+                               static_cast<VT*>(p.da));
+            e = hipGetLastError();
+            c_hi = c_lo;
+        }
+        const hipError_t f = hipFreeAsync(part, stream);
+        return e != hipSuccess ? e : f;
+    }
 }
 
 template <int N, typename VT>

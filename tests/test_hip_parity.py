@@ -130,6 +130,23 @@ def test_sequential_backward_saved_states_long_interval(hip, n):
         _assert_close(name, g, e, 1e-4, f"N={n}")
 
 
+def test_sequential_backward_row_split_time_segments(hip):
+    """N = 128 splits each head's rows over two workgroups, whose shares of
+    the column sums (dr, dw, dk, da, db) a second kernel adds; the shares of
+    8 heads fit 3264 tokens at a time, so 3500 tokens run as two time
+    segments that pass dS through dS0."""
+    print("case: sequential backward, B2 T3500 H4 N128, interval 16",
+          flush=True)
+    inp = make_inputs(3500, 2, 4, 128, dtype=torch.float32, seed=93,
+                      state_std=0.1, dstate_std=0.1)
+    ey, es, egrads = _oracle_all(inp)
+    y, s_t, aux, grads, _, _ = _run_hip(hip, _to_dev(inp), ci=16)
+    _assert_close("y", y, ey, 1e-4, "N=128")
+    _assert_close("s_t", s_t, es, 1e-4, "N=128")
+    for name, g, e in zip(GRAD_NAMES, grads, egrads):
+        _assert_close(name, g, e, 1e-4, "N=128")
+
+
 @pytest.mark.parametrize("ci", [1, 3, 16, 64, 200])
 def test_checkpoint_interval_does_not_change_results(hip, ci):
     print("case: checkpoint interval", ci, flush=True)

@@ -58,6 +58,13 @@ def parse_args():
     p.add_argument("--chunk", type=int, default=0,
                    help="checkpoint interval / chunk length (0 = library "
                         "default)")
+    p.add_argument("--head-size", type=int, default=0,
+                   help="run the configuration at this head size, with H "
+                        "scaled to keep H * N (0 = the configuration's N); "
+                        "sizes other than 64 take the sequential kernels")
+    p.add_argument("--fp32", action="store_true",
+                   help="fp32 vectors instead of the configuration's bf16 "
+                        "(the sequential kernels)")
     p.add_argument("--layout", choices=("tbhn", "bthn"), default="tbhn",
                    help="vector layout: time-major [T,B,H,N] (the "
                         "reference's WKV contract) or batch-major "
@@ -831,6 +838,15 @@ def main():
         sys.exit(1)
     wkv_hip.load_library()
     cfg = dict(CONFIGS[args.config])
+    variant = bool(args.head_size or args.fp32)
+    if args.head_size:
+        cfg["H"] = cfg["H"] * cfg["N"] // args.head_size
+        cfg["N"] = args.head_size
+    if args.fp32:
+        cfg["dtype"] = torch.float32
+    if variant and args.path != "wkv":
+        print("--head-size and --fp32 apply to --path wkv", file=sys.stderr)
+        sys.exit(2)
     if args.path == "timemix":
         return bench_timemix(args, cfg)
     if args.path == "screening":
@@ -934,11 +950,12 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": measured_traffic(dominant, args.config, ci,
-                                        args.layout),
+            "traffic": None if variant else measured_traffic(
+                dominant, args.config, ci, args.layout),
             "algorithmic_bytes": dom_bytes,
             "avg_ms": dom_ms,
-            "mfma": mfma_diagnostic(dominant, args.config, ci),
+            "mfma": None if variant else mfma_diagnostic(dominant,
+                                                         args.config, ci),
         },
         "kernels_ms": {"forward": fwd_ms, "backward": bwd_ms},
         "step_roofline_frac": step_gbs / HBM_PEAK_GBS,

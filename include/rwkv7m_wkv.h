@@ -174,6 +174,9 @@ int rwkv7m_wkv7_forward_with_aux(int dtype, int64_t T, int64_t B, int64_t H,
  * dy may be NULL (treated as zeros) and so may ds_t.  ds0 may not share a
  * byte with ds_t (RWKV7M_ERR_INVALID_ARGUMENT): a head that needs the exact
  * sequential pass reads dS_T again after its dS0 holds the pass's mark.
+ * At N = 128 the backward takes up to 128 MiB of stream-ordered device
+ * memory for the row-split workgroups' partial column sums, from a pool
+ * of the library's own that keeps it reserved for later calls.
  */
 int rwkv7m_wkv7_backward(int dtype, int64_t T, int64_t B, int64_t H,
                          int64_t N, const void *r, const void *w,

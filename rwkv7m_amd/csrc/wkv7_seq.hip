@@ -12,6 +12,7 @@
 // with S_{t-1} recomputed forward from checkpoints instead of divided out.
 
 #include <mutex>
+#include <type_traits>
 
 #include "wkv7_common.h"
 #include "wkv7_launch.h"
@@ -55,6 +56,24 @@ struct SeqShape {
     static constexpr int KSAVE = KS_FIT < 2 ? 0 : (KS_FIT > 16 ? 16 : KS_FIT);
 };
 
+// A prefetched vector element as loaded (its bits), converted to fp32 only
+// when written to LDS, so that no instruction waits for the load before
+// then.  Loads go through the global address space.
+template <typename VT>
+struct RawOf {
+    using type = VT;
+};
+__device__ __forceinline__ float raw_load(const float* p) {
+    return *(const __attribute__((address_space(1))) float*)p;
+}
+__device__ __forceinline__ bf16_t raw_load(const bf16_t* p) {
+    return *(const __attribute__((address_space(1))) bf16_t*)p;
+}
+__device__ __forceinline__ float raw_to_f(float x) { return x; }
+__device__ __forceinline__ float raw_to_f(bf16_t x) {
+    return __uint_as_float(uint32_t(x) << 16);
+}
+
 // Forward.  ckpt == nullptr: no aux.  s_t may alias s0.  CT is the
 // checkpoint element type (float or bf16_t).
 template <int N, typename VT, typename CT>
@@ -91,9 +110,12 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, VecLayout lay,
     // Each block's vectors are loaded into registers (this thread's
     // elements e = tid + i * TH) during the previous block's steps, where
     // that takes a few registers (PF); small heads load them in place.
+    // Elements past the block load token 0 of r instead (every load is
+    // unconditional, so none is waited for before its use) and are not
+    // written.
     constexpr int PF = (6 * TB * N + TH - 1) / TH;
     constexpr bool AHEAD = PF <= 12;
-    float pf[AHEAD ? PF : 1];
+    typename RawOf<VT>::type pf[AHEAD ? PF : 1];
     auto load_block = [&](int64_t t0) __attribute__((always_inline)) {
         const int nt = int(T - t0 < TB ? T - t0 : TB);
 #pragma unroll
@@ -101,9 +123,10 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, VecLayout lay,
             const int e = tid + i * TH;
             const int vec = e / (TB * N), rem = e - vec * TB * N;
             const int u = rem / N, j = rem - u * N;
-            pf[i] = 0.f;
-            if (e < 6 * TB * N && u < nt)
-                pf[i] = load_f(srcs[vec] + (t0 + u) * lay.ts + hoff + j);
+            const bool ok = e < 6 * TB * N && u < nt;
+            pf[i] = raw_load(ok ? srcs[ok ? vec : 0] + (t0 + u) * lay.ts +
+                                      hoff + j
+                                : r + hoff);
         }
     };
     if constexpr (AHEAD) {
@@ -117,8 +140,10 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, VecLayout lay,
                 const int e = tid + i * TH;
                 const int vec = e / (TB * N), rem = e - vec * TB * N;
                 const int u = rem / N, j = rem - u * N;
-                if (e < 6 * TB * N && u < nt)
-                    sh[vec][u][j] = vec == 1 ? expf(-expf(pf[i])) : pf[i];
+                if (e < 6 * TB * N && u < nt) {
+                    const float x = raw_to_f(pf[i]);
+                    sh[vec][u][j] = vec == 1 ? expf(-expf(x)) : x;
+                }
             }
         } else {
             for (int e = tid; e < 6 * TB * N; e += TH) {
@@ -135,28 +160,46 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, VecLayout lay,
         if constexpr (AHEAD) {
             if (t0 + TB < T) load_block(t0 + TB);
         }
-        for (int u = 0; u < nt; ++u) {
-            float sa = 0.f;
+        // The block's steps.  Where checkpoints fall only on a block's last
+        // token (intervals that are multiples of TB, and the end of the
+        // sequence), they are stored after the loop, so that the loop holds
+        // no global store (one makes the compiler wait for the next block's
+        // loads before it).
+        auto steps = [&](auto ck_in_loop) __attribute__((always_inline)) {
+            for (int u = 0; u < nt; ++u) {
+                float sa = 0.f;
 #pragma unroll
-            for (int c = 0; c < C; ++c) sa += S[c] * sh[4][u][col0 + c];
-            sa = group_sum<G>(sa);
-            const float vi = sh[3][u][row];
-            float acc = 0.f;
+                for (int c = 0; c < C; ++c) sa += S[c] * sh[4][u][col0 + c];
+                sa = group_sum<G>(sa);
+                const float vi = sh[3][u][row];
+                float acc = 0.f;
 #pragma unroll
-            for (int c = 0; c < C; ++c) {
-                S[c] = S[c] * sh[1][u][col0 + c] + sa * sh[5][u][col0 + c] +
-                       vi * sh[2][u][col0 + c];
-                acc += S[c] * sh[0][u][col0 + c];
-            }
-            acc = group_sum<G>(acc);
-            if (col0 == 0) sh_y[u][row] = acc;
-            if (ckpt) {
-                const int64_t t = t0 + u;
-                if ((t + 1) % ci == 0 || t + 1 == T) {
-                    CT* dst = ckpt + ((t + ci) / ci) * BH * NN + my;
-#pragma unroll
-                    for (int c = 0; c < C; ++c) store_f(dst + c, S[c]);
+                for (int c = 0; c < C; ++c) {
+                    S[c] = S[c] * sh[1][u][col0 + c] +
+                           sa * sh[5][u][col0 + c] + vi * sh[2][u][col0 + c];
+                    acc += S[c] * sh[0][u][col0 + c];
                 }
+                acc = group_sum<G>(acc);
+                if (col0 == 0) sh_y[u][row] = acc;
+                if constexpr (decltype(ck_in_loop)::value) {
+                    const int64_t t = t0 + u;
+                    if ((t + 1) % ci == 0 || t + 1 == T) {
+                        CT* dst = ckpt + ((t + ci) / ci) * BH * NN + my;
+#pragma unroll
+                        for (int c = 0; c < C; ++c) store_f(dst + c, S[c]);
+                    }
+                }
+            }
+        };
+        if (ckpt && ci % TB != 0) {
+            steps(std::true_type{});
+        } else {
+            steps(std::false_type{});
+            const int64_t t = t0 + nt - 1;
+            if (ckpt && ((t + 1) % ci == 0 || t + 1 == T)) {
+                CT* dst = ckpt + ((t + ci) / ci) * BH * NN + my;
+#pragma unroll
+                for (int c = 0; c < C; ++c) store_f(dst + c, S[c]);
             }
         }
         __syncthreads();
@@ -176,13 +219,13 @@ wkv7_seq_fwd_kernel(int64_t T, int64_t BH, VecLayout lay,
 // the current one is used, then written to LDS.
 // Small heads (more than 8 elements per thread) load in place instead:
 // stage_load only records the block and stage_write loads it.
-template <int N>
+template <int N, typename VT>
 struct StageRegs {
     static constexpr int PF =
         (7 * SeqShape<N>::SUB * N + SeqShape<N>::THREADS - 1) /
         SeqShape<N>::THREADS;
     static constexpr bool AHEAD = PF <= 8;
-    float x[AHEAD ? PF : 1];
+    typename RawOf<VT>::type x[AHEAD ? PF : 1];  // raw bits (see RawOf)
     int64_t t0 = -1;
     int count = 0;
     const void* dy = nullptr;
@@ -190,21 +233,24 @@ struct StageRegs {
 
 template <int N, typename VT>
 __device__ __forceinline__ void stage_load(
-    StageRegs<N>& R, int64_t t0, int count, int64_t tstr, int64_t hoff,
+    StageRegs<N, VT>& R, int64_t t0, int count, int64_t tstr, int64_t hoff,
     const VT* r, const VT* w, const VT* k, const VT* v, const VT* a,
     const VT* b, const VT* dy) {
     using Sh = SeqShape<N>;
     constexpr int SUB = Sh::SUB, TH = Sh::THREADS;
-    if constexpr (StageRegs<N>::AHEAD) {
+    if constexpr (StageRegs<N, VT>::AHEAD) {
         const VT* srcs[7] = {r, w, k, v, a, b, dy};
+        // (unconditional loads: elements outside the block, and dy when
+        // there is none, load token 0 of r and are not written as loaded)
 #pragma unroll
-        for (int i = 0; i < StageRegs<N>::PF; ++i) {
+        for (int i = 0; i < StageRegs<N, VT>::PF; ++i) {
             const int e = threadIdx.x + i * TH;
             const int vec = e / (SUB * N), rem = e - vec * SUB * N;
             const int u = rem / N, j = rem - u * N;
-            R.x[i] = 0.f;
-            if (e < 7 * SUB * N && u < count && (vec != 6 || dy))
-                R.x[i] = load_f(srcs[vec] + (t0 + u) * tstr + hoff + j);
+            const bool ok = e < 7 * SUB * N && u < count && (vec != 6 || dy);
+            R.x[i] = raw_load(ok ? srcs[ok ? vec : 0] + (t0 + u) * tstr +
+                                       hoff + j
+                                 : r + hoff);
         }
     }
     R.t0 = t0;
@@ -214,12 +260,12 @@ __device__ __forceinline__ void stage_load(
 
 template <int N, typename VT>
 __device__ __forceinline__ void stage_write(
-    const StageRegs<N>& R, float (*sh)[SeqShape<N>::SUB][N], int64_t tstr,
+    const StageRegs<N, VT>& R, float (*sh)[SeqShape<N>::SUB][N], int64_t tstr,
     int64_t hoff, const VT* r, const VT* w, const VT* k, const VT* v,
     const VT* a, const VT* b) {
     using Sh = SeqShape<N>;
     constexpr int SUB = Sh::SUB, TH = Sh::THREADS;
-    if constexpr (!StageRegs<N>::AHEAD) {
+    if constexpr (!StageRegs<N, VT>::AHEAD) {
         const VT* dy = static_cast<const VT*>(R.dy);
         const VT* srcs[7] = {r, w, k, v, a, b, dy};
         for (int e = threadIdx.x; e < 7 * SUB * N; e += TH) {
@@ -240,17 +286,18 @@ __device__ __forceinline__ void stage_write(
         return;
     }
 #pragma unroll
-    for (int i = 0; i < StageRegs<N>::PF; ++i) {
+    for (int i = 0; i < StageRegs<N, VT>::PF; ++i) {
         const int e = threadIdx.x + i * TH;
         const int vec = e / (SUB * N), rem = e - vec * SUB * N;
         const int u = rem / N, j = rem - u * N;
         if (e < 7 * SUB * N && u < R.count) {
+            const float x = raw_to_f(R.x[i]);
             if (vec == 1) {
-                const float ew = expf(R.x[i]);
+                const float ew = expf(x);
                 sh[1][u][j] = expf(-ew);
                 sh[7][u][j] = ew;
             } else {
-                sh[vec][u][j] = R.x[i];
+                sh[vec][u][j] = vec == 6 && !R.dy ? 0.f : x;
             }
         }
     }
@@ -347,7 +394,7 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
             // s_hi - 2: each sub-interval's vectors are loaded into
             // registers while the previous one's steps run.
             const int64_t n_adv = KS > 0 ? s_hi - 1 : s_lo;
-            StageRegs<N> pf;
+            StageRegs<N, VT> pf;
             if (n_adv > 0)
                 stage_load<N, VT>(pf, ta, SUB, lay.ts, hoff, r, w, k, v, a, b,
                                   nullptr);
@@ -371,7 +418,7 @@ wkv7_seq_bwd_kernel(int64_t T, int64_t BH, VecLayout lay,
                     saved[s_hi - 1 - s_lo][tid * C + cc] = Sx[cc];
             }
         }
-        StageRegs<N> rp;  // the reverse's next sub-interval, loaded ahead
+        StageRegs<N, VT> rp;  // the reverse's next sub-interval, loaded ahead
         for (int64_t s = s_hi - 1; s >= s_lo; --s) {
             float St[SUB + 1][C];
             float sa_r[SUB];

@@ -46,11 +46,15 @@ def _replay_check(step, leaves, case):
             assert torch.equal(a, b), f"{case}: replay {i} gradient {k}"
 
 
-def test_wkv7_operator_graph_replay(hip_lib):
+@pytest.mark.parametrize("n", [64, 128])
+def test_wkv7_operator_graph_replay(hip_lib, n):
+    # N = 128: the sequential kernels over row-split workgroups, whose
+    # partial column sums take stream-ordered memory from the library's pool
+    # (a memory node in the captured graph)
     import rwkv7m_amd
     from rwkv7m_amd.kernels.wkv_ffi import unregister_wkv_ffi_backend
-    print("case: wkv7 graph replay T70 B2 H2 N64 bf16", flush=True)
-    inp = make_inputs(70, 2, 2, 64, seed=41, state_std=0.1)
+    print(f"case: wkv7 graph replay T70 B2 H2 N{n} bf16", flush=True)
+    inp = make_inputs(70, 2, 2, n, seed=41, state_std=0.1)
     leaves = [inp[n].cuda().requires_grad_(True) for n in NAMES]
     s0 = inp["s0"].cuda().requires_grad_(True)
     dy = inp["dy"].cuda()
@@ -62,7 +66,7 @@ def test_wkv7_operator_graph_replay(hip_lib):
             ((y.float() * dy.float()).sum() + s_t.sum()).backward()
             return [y, s_t]
 
-        _replay_check(step, leaves + [s0], "wkv7")
+        _replay_check(step, leaves + [s0], f"wkv7 N{n}")
     finally:
         unregister_wkv_ffi_backend()
 

@@ -1,4 +1,5 @@
-// Sequential WKV-7 kernels for gfx950: one workgroup per (batch, head).
+// Sequential WKV-7 kernels for gfx950: one workgroup per (batch, head), or
+// at N = 128 two, each owning half the state rows.
 //
 // Each state row i is owned by G consecutive lanes, each holding C = N / G
 // contiguous columns in VGPRs, so the row-local parts of the recurrence

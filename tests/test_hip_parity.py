@@ -114,9 +114,9 @@ def test_forward_backward_match_oracle(hip, case, dtype):
 def test_sequential_backward_saved_states_long_interval(hip, n):
     """One interval of 300 tokens: the sequential backward's sub-interval
     start states are saved in LDS several at a time (16 at N = 32, 6 at
-    N = 64) or, at N = 128, recomputed from the checkpoint each time; every
-    grouping, the partial last sub-interval and the prefetched vector blocks
-    against the oracle."""
+    N = 64, 3 at N = 128 over two row-split workgroups); every grouping (the
+    partial group first), the partial last sub-interval and the prefetched
+    vector blocks against the oracle."""
     print("case: sequential backward, T = 300, interval 256, N =", n,
           flush=True)
     inp = make_inputs(300, 1, 2, n, dtype=torch.float32, seed=91,
